@@ -1,0 +1,168 @@
+/*
+ * mko.h -- C ABI of the MI355X (gfx950) SSM scan library, libmko.so.
+ *
+ * Plain pointers and sizes only: no torch or C++ types cross this boundary.  Every
+ * entry point takes a POD parameter block and a HIP stream (passed as void*, a
+ * hipStream_t; NULL is the default stream), launches asynchronously on that
+ * stream and returns MKO_OK or an error code; mko_last_error() then describes
+ * the failure (thread-local).
+ *
+ * Ownership: the caller allocates every input, output and workspace; the
+ * library never allocates or frees device memory.  Inputs are never written.
+ * All tensors are dense row-major (contiguous) in the layouts documented per
+ * field.  dtype fields take MKO_F32 / MKO_F16 / MKO_BF16; every kernel computes
+ * in float32 and rounds once when it stores a 16-bit output.
+ *
+ * The reference (dbydd/metal-kernelops) has no native ABI: its Python launches
+ * Metal kernels through torch.mps.compile_shader.  Each entry point below names
+ * the reference function it replaces (paths relative to src/metal_kernelops/).
+ */
+#ifndef MKO_H
+#define MKO_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MKO_ABI_VERSION 1
+
+enum mko_dtype { MKO_F32 = 0, MKO_F16 = 1, MKO_BF16 = 2 };
+
+enum mko_status {
+  MKO_OK = 0,
+  MKO_EINVAL = 1,       /* bad shape, pointer, dtype or flag */
+  MKO_ELAUNCH = 2,      /* the HIP runtime refused a launch */
+  MKO_EUNSUPPORTED = 3, /* valid request outside what the kernels implement */
+  MKO_EWORKSPACE = 4    /* workspace missing or smaller than *_workspace_size() */
+};
+
+/* MKO_ABI_VERSION of the loaded library. */
+int mko_abi_version(void);
+/* Message for the last non-zero status returned on this thread ("" if none). */
+const char* mko_last_error(void);
+/* sizeof() of the parameter blocks, so a binding can check its mirror of them. */
+size_t mko_sizeof_selscan_params(void);
+size_t mko_sizeof_state_update_params(void);
+
+/* ======================================================================== */
+/* Mamba-1 selective scan                                                     */
+/* ======================================================================== */
+
+#define MKO_SS_SOFTPLUS 1u /* delta = softplus(delta + delta_bias) (threshold 20) */
+
+/* Steps between two saved scan states (the forward writes one state per 64
+ * steps; the backward restarts its recompute from them). */
+#define MKO_SS_CHECKPOINT 64
+
+typedef struct mko_selscan_params {
+  /* forward inputs (also read by the backward) */
+  const void* u;            /* (batch, dim, length)            u_dtype            */
+  const void* delta;        /* (batch, dim, length)            delta_dtype, raw   */
+  const float* A;           /* (dim, dstate)                   float32            */
+  const void* B;            /* (batch, ngroups, dstate, length) bc_dtype          */
+  const void* C;            /* (batch, ngroups, dstate, length) bc_dtype          */
+  const float* D;           /* (dim,) or NULL                                     */
+  const void* z;            /* (batch, dim, length) u_dtype, or NULL              */
+  const float* delta_bias;  /* (dim,) or NULL                                     */
+  /* forward outputs */
+  void* out;                /* (batch, dim, length) u_dtype                        */
+  float* states;            /* (batch, dim, mko_selscan_num_checkpoints(length), dstate):
+                               the state entering every 64-step block; written by the
+                               forward, read by the backward                        */
+  /* backward input */
+  const void* dout;         /* (batch, dim, length) u_dtype                        */
+  /* backward outputs (any may be NULL when that gradient is not wanted, except
+     du and ddelta which are always written) */
+  void* du;                 /* (batch, dim, length) u_dtype                        */
+  void* ddelta;             /* (batch, dim, length) delta_dtype: grad of raw delta */
+  float* dA;                /* (dim, dstate)                                       */
+  void* dB;                 /* (batch, ngroups, dstate, length) bc_dtype           */
+  void* dC;                 /* (batch, ngroups, dstate, length) bc_dtype           */
+  float* dD;                /* (dim,), needs D                                     */
+  void* dz;                 /* (batch, dim, length) u_dtype, needs z               */
+  float* ddelta_bias;       /* (dim,), needs delta_bias                            */
+  void* workspace;
+  size_t workspace_bytes;
+  int64_t batch, dim, length, dstate, ngroups;
+  int32_t u_dtype, delta_dtype, bc_dtype;
+  uint32_t flags;
+} mko_selscan_params;
+
+/* ceil(length / MKO_SS_CHECKPOINT): the third extent of params.states. */
+int64_t mko_selscan_num_checkpoints(int64_t length);
+
+/* Replaces _Scan.forward (scan.py:237-255) together with the pointwise pre/post
+ * ops of selective_scan (scan.py:311-319): out = (scan(u, softplus(delta +
+ * delta_bias), A, B, C) + u*D) * silu(z), each stage optional as in the
+ * reference.  dstate <= 32 (the reference kernels assume the same). */
+size_t mko_selscan_fwd_workspace_size(const mko_selscan_params* p);
+int mko_selscan_fwd(const mko_selscan_params* p, void* stream);
+
+/* Replaces _Scan.backward (scan.py:257-280) and the autograd of the pre/post
+ * ops: given dout and the forward's inputs and states, writes the gradients
+ * listed above.  Deterministic when dim/ngroups is a multiple of 64; otherwise
+ * dB/dC are accumulated with float atomics. */
+size_t mko_selscan_bwd_workspace_size(const mko_selscan_params* p);
+int mko_selscan_bwd(const mko_selscan_params* p, void* stream);
+
+/* ======================================================================== */
+/* Mamba-2 decode state update                                                */
+/* ======================================================================== */
+
+#define MKO_SU_SOFTPLUS 1u   /* delta = softplus(dt + dt_bias) */
+#define MKO_SU_DT_PER_ROW 2u /* dt is (batch, nheads, headdim) instead of (batch, nheads) */
+#define MKO_SU_D_PER_ROW 4u  /* D is (nheads, headdim) instead of (nheads,) */
+
+typedef struct mko_state_update_params {
+  const void* state;        /* (batch, nheads, headdim, dstate) state_dtype        */
+  const void* x;            /* (batch, nheads, headdim)        x_dtype             */
+  const void* dt;           /* (batch, nheads) or (batch, nheads, headdim) dt_dtype */
+  const float* A;           /* (nheads,)                                           */
+  const void* B;            /* (batch, ngroups, dstate)        bc_dtype            */
+  const void* C;            /* (batch, ngroups, dstate)        bc_dtype            */
+  const float* D;           /* (nheads,) or (nheads, headdim), or NULL             */
+  const void* z;            /* (batch, nheads, headdim) x_dtype, or NULL           */
+  const float* dt_bias;     /* (nheads,) or NULL                                   */
+  /* forward outputs */
+  void* new_state;          /* (batch, nheads, headdim, dstate) state_dtype; may alias
+                               state (in-place decode)                             */
+  void* y;                  /* (batch, nheads, headdim) state_dtype                */
+  /* backward inputs: upstream grads of y and new_state (either may be NULL) */
+  const float* dy;          /* (batch, nheads, headdim) float32                    */
+  const float* dnew_state;  /* (batch, nheads, headdim, dstate) float32            */
+  /* backward outputs, float32 (dz/dD/ddt_bias only with z/D/dt_bias) */
+  float* grad_state;        /* (batch, nheads, headdim, dstate)                    */
+  float* dx;                /* (batch, nheads, headdim)                            */
+  float* ddt;               /* shape of dt                                         */
+  float* dA;                /* (nheads,)                                           */
+  float* dB;                /* (batch, ngroups, dstate)                            */
+  float* dC;                /* (batch, ngroups, dstate)                            */
+  float* dD;                /* shape of D                                          */
+  float* dz;                /* (batch, nheads, headdim)                            */
+  float* ddt_bias;          /* (nheads,)                                           */
+  void* workspace;
+  size_t workspace_bytes;
+  int64_t batch, nheads, headdim, dstate, ngroups;
+  int32_t state_dtype, x_dtype, dt_dtype, bc_dtype;
+  uint32_t flags;
+} mko_state_update_params;
+
+/* Replaces the Metal state_update_{f32,f16,bf16} kernel and _launch
+ * (cv/mamba2_state.py:184-267, 601-637): one fused read-modify-write of the
+ * state per decode step. */
+int mko_state_update_fwd(const mko_state_update_params* p, void* stream);
+
+/* Replaces _StateUpdate.backward (cv/mamba2_state.py:653-756) and its Metal
+ * state_update_backward / state_update_reduce kernels (:269-536): every
+ * gradient has one writer, so repeated runs are bit-identical. */
+size_t mko_state_update_bwd_workspace_size(const mko_state_update_params* p);
+int mko_state_update_bwd(const mko_state_update_params* p, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MKO_H */

@@ -1,0 +1,908 @@
+// Mamba-1 selective scan, forward and backward, for gfx950.
+//
+// Mapping: one lane per channel row (batch, d).  A wavefront holds 64 channels of
+// one (batch, group) whenever dim/ngroups is a multiple of 64, so B_t and C_t are
+// wave-uniform (scalar loads) and the dB/dC sums over channels are cross-lane
+// reductions.  Each lane walks time sequentially with its N states in registers.
+//
+// Time parallelism: the sequence is cut into `nchunks` coarse chunks of `lc`
+// steps (a multiple of 64).  The forward is three launches:
+//   1. fwd_summary: per chunk, the state it leaves from a zero entry and the sum
+//      of its steps (its decay is exp(A * sum));
+//   2. chain: per (row, state), the exact entering state of every chunk;
+//   3. fwd_replay: replays every chunk from its entering state, writes
+//      out = (C.x + D u) * silu(z) and the state entering every 64-step block.
+// The backward mirrors it: bwd_summary (each chunk's adjoint from a zero exit),
+// a reverse chain, then bwd_main, which walks every chunk backwards in 16-step
+// quarters, recomputing the forward states of a quarter from the saved 64-step
+// state, and finally small reduction kernels for dB/dC, dA, dD and ddelta_bias.
+//
+// Per-step inputs of the state-inner loops (one lane, all states, one step at a
+// time) are staged through LDS so the step loop is a real loop and B_t/C_t are
+// fetched one step at a time.
+#include "common.hpp"
+#include "io.hpp"
+
+namespace mko {
+namespace ss {
+
+constexpr int CK = MKO_SS_CHECKPOINT;  // steps between saved states
+constexpr int HS = 16;                 // steps held in registers / staged at a time
+
+struct Geo {
+  int64_t batch, dim, length, dstate, ngroups;
+  int64_t rows;      // batch * dim
+  int64_t dg;        // channels per group
+  int64_t nwr;       // wave rows = ceil(rows / 64)
+  int lc;            // coarse chunk length (multiple of CK)
+  int nchunks;       // number of coarse chunks
+  int nck;           // saved states per row = ceil(length / CK)
+  int wpg;           // wavefronts per workgroup
+  int ncb;           // channel blocks (of 64*wpg channels) per group, uniform mode
+  int u_dtype, d_dtype, bc_dtype;
+  int softplus;
+  int vec;           // per-element rows may use 16-byte vector accesses
+};
+
+struct Ptrs {
+  const void* u;
+  const void* delta;
+  const float* A;
+  const void* B;
+  const void* C;
+  const float* D;
+  const void* z;
+  const float* bias;
+  const void* dout;
+  void* out;
+  float* states;
+  void* du;
+  void* ddelta;
+  void* dz;
+  // workspace
+  float* bt;     // (batch*G, L, NS) B, time-major, fp32, zero-padded states
+  float* ct;     // (batch*G, L, NS) C
+  float* bn;     // (batch*G, NS, L) B, state-major (backward)
+  float* cn;     // (batch*G, NS, L) C
+  float* drive;  // (rows, nchunks, N) chunk summaries
+  float* sumd;   // (rows, nchunks) sum of steps per chunk
+  float* adj;    // (rows, nchunks, N) adjoint entering each chunk from the right
+  float* pbc;    // (batch*G, ncb, L, NS, 2) dB/dC partial sums
+  float* dap;    // (nchunks, NS, rows) dA partials
+  float* hcs;    // (nchunks, NS, rows) adjoint carried between quarters
+  float* qx;     // (nchunks, 3, NS, rows) states entering quarters 1..3 of a 64-block
+  float* ddp;    // (nchunks, rows) dD partials
+  float* dbp;    // (nchunks, rows) ddelta_bias partials
+};
+
+struct LaneInfo {
+  int64_t row;   // clamped to a valid row
+  bool active;
+  int64_t d;
+  int64_t bg;    // batch * G + group
+  int64_t wave_row;
+};
+
+__device__ __forceinline__ LaneInfo lane_info(const Geo& g, bool uni) {
+  LaneInfo li;
+  const int wave = uniform(static_cast<int>(threadIdx.x >> 6));
+  const int lane = threadIdx.x & 63;
+  li.wave_row = static_cast<int64_t>(blockIdx.x) * g.wpg + wave;
+  const int64_t row = li.wave_row * kWave + lane;
+  li.active = row < g.rows;
+  li.row = li.active ? row : g.rows - 1;
+  li.d = li.row % g.dim;
+  if (uni) {
+    const int64_t r0 = li.wave_row * kWave;
+    const int64_t b0 = r0 / g.dim;
+    const int64_t g0 = (r0 % g.dim) / g.dg;
+    li.bg = __builtin_amdgcn_readfirstlane(static_cast<int>(b0 * g.ngroups + g0));
+  } else {
+    li.bg = (li.row / g.dim) * g.ngroups + li.d / g.dg;
+  }
+  return li;
+}
+
+__device__ __forceinline__ float step_of(const Geo& g, float raw, float bias) {
+  const float v = raw + bias;
+  return g.softplus ? softplus(v) : v;
+}
+
+// ---------------------------------------------------------------- layout prep
+
+// B, C (bg, N, L) any dtype -> time-major fp32 (bg, L, NS), states >= N zeroed.
+template <int NS>
+__global__ void __launch_bounds__(256) prep_time_major(Geo g, const void* B, const void* C,
+                                                       float* bt, float* ct) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t total = g.batch * g.ngroups * g.length;
+  if (i >= total) return;
+  const int64_t bg = i / g.length, t = i % g.length;
+  const int N = static_cast<int>(g.dstate);
+#pragma unroll
+  for (int n = 0; n < NS; ++n) {
+    float vb = 0.0f, vc = 0.0f;
+    if (n < N) {
+      const int64_t src = (bg * N + n) * g.length + t;
+      if (B) vb = load_one(B, g.bc_dtype, src);
+      if (C) vc = load_one(C, g.bc_dtype, src);
+    }
+    if (bt) bt[i * NS + n] = vb;
+    if (ct) ct[i * NS + n] = vc;
+  }
+}
+
+// B, C (bg, N, L) any dtype -> state-major fp32 (bg, NS, L), padded states zeroed.
+__global__ void __launch_bounds__(256) prep_state_major(Geo g, int ns, const void* B, const void* C,
+                                                        float* bn, float* cn) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t total = g.batch * g.ngroups * ns * g.length;
+  if (i >= total) return;
+  const int64_t t = i % g.length;
+  const int64_t n = (i / g.length) % ns;
+  const int64_t bg = i / (g.length * ns);
+  float vb = 0.0f, vc = 0.0f;
+  if (n < g.dstate) {
+    const int64_t src = (bg * g.dstate + n) * g.length + t;
+    vb = load_one(B, g.bc_dtype, src);
+    vc = load_one(C, g.bc_dtype, src);
+  }
+  bn[i] = vb;
+  cn[i] = vc;
+}
+
+// ---------------------------------------------------------------- forward
+
+// LDS staging used by the state-inner kernels: per wavefront [3][HS][64] floats.
+constexpr int kStage = 3 * HS * kWave;
+
+template <int NS, bool UNI>
+__global__ void __launch_bounds__(256) fwd_summary(Geo g, Ptrs p) {
+  __shared__ float stage_all[4 * kStage];
+  const LaneInfo li = lane_info(g, UNI);
+  const int lane = threadIdx.x & 63;
+  float* st_d = stage_all + uniform(static_cast<int>(threadIdx.x >> 6)) * kStage;
+  float* st_u = st_d + HS * kWave;
+  const int N = static_cast<int>(g.dstate);
+  const int c = blockIdx.y;
+  const int t_begin = c * g.lc;
+  const int t_end = min(t_begin + g.lc, static_cast<int>(g.length));
+  float A2[NS];
+#pragma unroll
+  for (int n = 0; n < NS; ++n) A2[n] = n < N ? p.A[li.d * N + n] * kLog2e : 0.0f;
+  const float bias = p.bias ? p.bias[li.d] : 0.0f;
+  float x[NS];
+#pragma unroll
+  for (int n = 0; n < NS; ++n) x[n] = 0.0f;
+  float sd = 0.0f;
+  const int64_t rbase = li.row * g.length;
+  for (int t0 = t_begin; t0 < t_end; t0 += HS) {
+    const int nv = min(HS, t_end - t0);
+    float dl[HS], uu[HS];
+    load_run<HS>(p.delta, g.d_dtype, rbase + t0, nv, g.vec, dl);
+    load_run<HS>(p.u, g.u_dtype, rbase + t0, nv, g.vec, uu);
+#pragma unroll
+    for (int i = 0; i < HS; ++i) {
+      const float del = i < nv ? step_of(g, dl[i], bias) : 0.0f;
+      sd += del;
+      st_d[i * kWave + lane] = del;
+      st_u[i * kWave + lane] = del * uu[i];
+    }
+    wave_lds_sync();
+    for (int i = 0; i < nv; ++i) {
+      const float del = st_d[i * kWave + lane];
+      const float du = st_u[i * kWave + lane];
+      const float* bp = p.bt + (li.bg * g.length + t0 + i) * NS;
+#pragma unroll
+      for (int n = 0; n < NS; ++n) x[n] = fmaf(fast_exp2(A2[n] * del), x[n], du * bp[n]);
+    }
+    wave_lds_sync();
+  }
+  if (li.active) {
+    const int64_t o = (li.row * g.nchunks + c) * N;
+#pragma unroll
+    for (int n = 0; n < NS; ++n)
+      if (n < N) p.drive[o + n] = x[n];
+    p.sumd[li.row * g.nchunks + c] = sd;
+  }
+}
+
+// Forward: state entering chunk c (written at saved-state slot c*lc/CK).
+// Reverse: adjoint entering chunk c from the right.
+template <bool REV>
+__global__ void __launch_bounds__(256) chain(Geo g, const float* __restrict__ A,
+                                             const float* __restrict__ drive,
+                                             const float* __restrict__ sumd, float* __restrict__ out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int N = static_cast<int>(g.dstate);
+  if (i >= g.rows * N) return;
+  const int64_t row = i / N;
+  const int n = static_cast<int>(i % N);
+  const float a2 = A[(row % g.dim) * N + n] * kLog2e;
+  const int k = g.nchunks;
+  if (!REV) {
+    const int per = g.lc / CK;
+    float x = 0.0f;
+    for (int c = 0; c < k; ++c) {
+      out[(row * g.nck + static_cast<int64_t>(c) * per) * N + n] = x;
+      if (c + 1 < k) x = fmaf(fast_exp2(a2 * sumd[row * k + c]), x, drive[(row * k + c) * N + n]);
+    }
+  } else {
+    float h = 0.0f;
+    for (int c = k - 1; c >= 0; --c) {
+      out[(row * k + c) * N + n] = h;
+      if (c > 0) h = fmaf(fast_exp2(a2 * sumd[row * k + c]), h, drive[(row * k + c) * N + n]);
+    }
+  }
+}
+
+template <int NS, bool UNI>
+__global__ void __launch_bounds__(256) fwd_replay(Geo g, Ptrs p) {
+  __shared__ float stage_all[4 * kStage];
+  const LaneInfo li = lane_info(g, UNI);
+  const int lane = threadIdx.x & 63;
+  float* st_d = stage_all + uniform(static_cast<int>(threadIdx.x >> 6)) * kStage;
+  float* st_u = st_d + HS * kWave;
+  float* st_y = st_u + HS * kWave;
+  const int N = static_cast<int>(g.dstate);
+  const int c = blockIdx.y;
+  const int t_begin = c * g.lc;
+  const int t_end = min(t_begin + g.lc, static_cast<int>(g.length));
+  float A2[NS];
+#pragma unroll
+  for (int n = 0; n < NS; ++n) A2[n] = n < N ? p.A[li.d * N + n] * kLog2e : 0.0f;
+  const float bias = p.bias ? p.bias[li.d] : 0.0f;
+  const float Dd = p.D ? p.D[li.d] : 0.0f;
+  const bool has_z = p.z != nullptr;
+  float* srow = p.states + li.row * g.nck * N;
+  float x[NS];
+#pragma unroll
+  for (int n = 0; n < NS; ++n) x[n] = n < N ? srow[(t_begin / CK) * N + n] : 0.0f;
+  const int64_t rbase = li.row * g.length;
+  for (int t0 = t_begin; t0 < t_end; t0 += HS) {
+    if (t0 != t_begin && (t0 % CK) == 0 && li.active) {
+#pragma unroll
+      for (int n = 0; n < NS; ++n)
+        if (n < N) srow[(t0 / CK) * N + n] = x[n];
+    }
+    const int nv = min(HS, t_end - t0);
+    float uu[HS];
+    {
+      float dl[HS];
+      load_run<HS>(p.delta, g.d_dtype, rbase + t0, nv, g.vec, dl);
+      load_run<HS>(p.u, g.u_dtype, rbase + t0, nv, g.vec, uu);
+#pragma unroll
+      for (int i = 0; i < HS; ++i) {
+        const float del = i < nv ? step_of(g, dl[i], bias) : 0.0f;
+        st_d[i * kWave + lane] = del;
+        st_u[i * kWave + lane] = del * uu[i];
+      }
+    }
+    wave_lds_sync();
+    for (int i = 0; i < nv; ++i) {
+      const float del = st_d[i * kWave + lane];
+      const float du = st_u[i * kWave + lane];
+      const float* bp = p.bt + (li.bg * g.length + t0 + i) * NS;
+      const float* cp = p.ct + (li.bg * g.length + t0 + i) * NS;
+      float acc = 0.0f;
+#pragma unroll
+      for (int n = 0; n < NS; ++n) {
+        x[n] = fmaf(fast_exp2(A2[n] * del), x[n], du * bp[n]);
+        acc = fmaf(cp[n], x[n], acc);
+      }
+      st_y[i * kWave + lane] = acc;
+    }
+    wave_lds_sync();
+    float y[HS];
+#pragma unroll
+    for (int i = 0; i < HS; ++i) y[i] = fmaf(Dd, uu[i], st_y[i * kWave + lane]);
+    if (has_z) {
+      float zz[HS];
+      load_run<HS>(p.z, g.u_dtype, rbase + t0, nv, g.vec, zz);
+#pragma unroll
+      for (int i = 0; i < HS; ++i) y[i] *= zz[i] * sigmoid(zz[i]);
+    }
+    if (li.active) store_run<HS>(p.out, g.u_dtype, rbase + t0, nv, g.vec, y);
+  }
+}
+
+// ---------------------------------------------------------------- backward
+
+template <int NS, bool UNI>
+__global__ void __launch_bounds__(256) bwd_summary(Geo g, Ptrs p) {
+  __shared__ float stage_all[4 * kStage];
+  const LaneInfo li = lane_info(g, UNI);
+  const int lane = threadIdx.x & 63;
+  float* st_d = stage_all + uniform(static_cast<int>(threadIdx.x >> 6)) * kStage;
+  float* st_g = st_d + HS * kWave;
+  const int N = static_cast<int>(g.dstate);
+  const int c = blockIdx.y + 1;  // chunk 0's adjoint summary is never needed
+  const int t_begin = c * g.lc;
+  const int t_end = min(t_begin + g.lc, static_cast<int>(g.length));
+  float A2[NS];
+#pragma unroll
+  for (int n = 0; n < NS; ++n) A2[n] = n < N ? p.A[li.d * N + n] * kLog2e : 0.0f;
+  const float bias = p.bias ? p.bias[li.d] : 0.0f;
+  const bool has_z = p.z != nullptr;
+  float hc[NS];
+#pragma unroll
+  for (int n = 0; n < NS; ++n) hc[n] = 0.0f;
+  float sd = 0.0f;
+  const int64_t rbase = li.row * g.length;
+  const int nblk = (t_end - t_begin + HS - 1) / HS;
+  for (int blk = nblk - 1; blk >= 0; --blk) {
+    const int t0 = t_begin + blk * HS;
+    const int nv = min(HS, t_end - t0);
+    {
+      float dl[HS], gy[HS];
+      load_run<HS>(p.delta, g.d_dtype, rbase + t0, nv, g.vec, dl);
+      load_run<HS>(p.dout, g.u_dtype, rbase + t0, nv, g.vec, gy);
+      if (has_z) {
+        float zz[HS];
+        load_run<HS>(p.z, g.u_dtype, rbase + t0, nv, g.vec, zz);
+#pragma unroll
+        for (int i = 0; i < HS; ++i) gy[i] *= zz[i] * sigmoid(zz[i]);
+      }
+#pragma unroll
+      for (int i = 0; i < HS; ++i) {
+        const float del = i < nv ? step_of(g, dl[i], bias) : 0.0f;
+        sd += del;
+        st_d[i * kWave + lane] = del;
+        st_g[i * kWave + lane] = gy[i];
+      }
+    }
+    wave_lds_sync();
+    for (int i = nv - 1; i >= 0; --i) {
+      const float del = st_d[i * kWave + lane];
+      const float gy = st_g[i * kWave + lane];
+      const float* cp = p.ct + (li.bg * g.length + t0 + i) * NS;
+#pragma unroll
+      for (int n = 0; n < NS; ++n) hc[n] = fast_exp2(A2[n] * del) * fmaf(gy, cp[n], hc[n]);
+    }
+    wave_lds_sync();
+  }
+  if (li.active) {
+    const int64_t o = (li.row * g.nchunks + c) * N;
+#pragma unroll
+    for (int n = 0; n < NS; ++n)
+      if (n < N) p.drive[o + n] = hc[n];
+    p.sumd[li.row * g.nchunks + c] = sd;
+  }
+}
+
+// bwd_main LDS (floats): per wavefront a staging area [2][HS][64] and a
+// transposition buffer [64][2*HS+1]; per workgroup the dB/dC sums [NS][2*HS].
+constexpr int kTransPitch = 2 * HS + 1;
+constexpr int kMainWave = 2 * HS * kWave + kWave * kTransPitch;
+
+template <int NS, bool UNI>
+__global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
+  __shared__ float lds[4 * kMainWave + NS * 2 * HS];
+  const LaneInfo li = lane_info(g, UNI);
+  const int N = static_cast<int>(g.dstate);
+  const int lane = threadIdx.x & 63;
+  const int wave = uniform(static_cast<int>(threadIdx.x >> 6));
+  float* st_d = lds + wave * kMainWave;  // [HS][64]
+  float* st_u = st_d + HS * kWave;       // [HS][64]
+  float* trans = st_u + HS * kWave;      // [64][kTransPitch]
+  float* acc = lds + 4 * kMainWave;      // [NS][2*HS]
+
+  const int c = blockIdx.y;
+  const int t_begin = c * g.lc;
+  const int t_end = min(t_begin + g.lc, static_cast<int>(g.length));
+  const float bias = p.bias ? p.bias[li.d] : 0.0f;
+  const float Dd = p.D ? p.D[li.d] : 0.0f;
+  const bool has_z = p.z != nullptr;
+  const int64_t rbase = li.row * g.length;
+  const float* arow = p.A + li.d * N;
+  const float act = li.active ? 1.0f : 0.0f;
+  const int64_t R = g.rows;
+  // Per-(chunk, state, row) carries in the workspace, state-major so a
+  // wavefront's 64 lanes touch 256 contiguous bytes.
+  float* hcs = p.hcs + static_cast<int64_t>(c) * NS * R;
+  float* dap = p.dap + static_cast<int64_t>(c) * NS * R;
+  float* qx = p.qx + static_cast<int64_t>(c) * 3 * NS * R;
+
+  if (li.active) {
+    for (int n = 0; n < N; ++n) {
+      hcs[n * R + li.row] = p.adj[(li.row * g.nchunks + c) * N + n];
+      dap[n * R + li.row] = 0.0f;
+    }
+  }
+  for (int i = threadIdx.x; i < NS * 2 * HS; i += blockDim.x) acc[i] = 0.0f;
+  __syncthreads();
+
+  int64_t cb = 0;
+  if (UNI) {
+    const int64_t r0 = static_cast<int64_t>(blockIdx.x) * g.wpg * kWave;
+    cb = ((r0 % g.dim) % g.dg) / (static_cast<int64_t>(g.wpg) * kWave);
+  }
+  const bool vec_bc = (g.length % 4) == 0;
+  float A2[NS];
+#pragma unroll
+  for (int n = 0; n < NS; ++n) A2[n] = n < N ? arow[n] * kLog2e : 0.0f;
+  float dD_acc = 0.0f, db_acc = 0.0f;
+
+  const int jb = t_begin / CK;
+  const int je = (t_end + CK - 1) / CK;
+  for (int j = je - 1; j >= jb; --j) {
+    const int tb = j * CK;
+    const int te = min(tb + CK, t_end);
+    const int nq = (te - tb + HS - 1) / HS;
+    const float* srow = p.states + (li.row * g.nck + j) * N;
+    // ---- states entering quarters 1..nq-1, state-inner sweep from the saved state
+    if (nq > 1) {
+      float x[NS];
+#pragma unroll
+      for (int n = 0; n < NS; ++n) x[n] = n < N ? srow[n] : 0.0f;
+      for (int q = 0; q < nq - 1; ++q) {
+        const int qs = tb + q * HS;
+        {
+          float dl[HS], uu[HS];
+          load_run<HS>(p.delta, g.d_dtype, rbase + qs, HS, g.vec, dl);
+          load_run<HS>(p.u, g.u_dtype, rbase + qs, HS, g.vec, uu);
+#pragma unroll
+          for (int i = 0; i < HS; ++i) {
+            const float del = step_of(g, dl[i], bias);
+            st_d[i * kWave + lane] = del;
+            st_u[i * kWave + lane] = del * uu[i];
+          }
+        }
+        wave_lds_sync();
+        for (int i = 0; i < HS; ++i) {
+          const float del = st_d[i * kWave + lane];
+          const float du = st_u[i * kWave + lane];
+          const float* bp = p.bt + (li.bg * g.length + qs + i) * NS;
+#pragma unroll
+          for (int n = 0; n < NS; ++n) x[n] = fmaf(fast_exp2(A2[n] * del), x[n], du * bp[n]);
+        }
+        wave_lds_sync();
+#pragma unroll
+        for (int n = 0; n < NS; ++n)
+          if (n < N) qx[(q * NS + n) * R + li.row] = x[n];
+      }
+    }
+    // ---- quarters in reverse, states one at a time
+    for (int q = nq - 1; q >= 0; --q) {
+      const int qs = tb + q * HS;
+      const int nv = min(HS, te - qs);
+      float del[HS], du[HS], gy[HS];
+      {
+        float uu[HS];
+        load_run<HS>(p.delta, g.d_dtype, rbase + qs, nv, g.vec, del);
+        load_run<HS>(p.u, g.u_dtype, rbase + qs, nv, g.vec, uu);
+        load_run<HS>(p.dout, g.u_dtype, rbase + qs, nv, g.vec, gy);
+        if (has_z) {
+          float zz[HS];
+          load_run<HS>(p.z, g.u_dtype, rbase + qs, nv, g.vec, zz);
+#pragma unroll
+          for (int i = 0; i < HS; ++i) gy[i] *= zz[i] * sigmoid(zz[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < HS; ++i) {
+          del[i] = i < nv ? step_of(g, del[i], bias) : 0.0f;
+          du[i] = del[i] * uu[i] * act;
+          gy[i] *= act;
+        }
+      }
+      float s1[HS], s2[HS], ya[HS];
+#pragma unroll
+      for (int i = 0; i < HS; ++i) s1[i] = s2[i] = ya[i] = 0.0f;
+
+      for (int n = 0; n < N; ++n) {
+        const float an = arow[n];
+        const float a2 = an * kLog2e;
+        const float xin = q == 0 ? srow[n] : qx[((q - 1) * NS + n) * R + li.row];
+        float hc = hcs[n * R + li.row];
+        float bv[HS], cv[HS];
+        const int64_t bco = (li.bg * NS + n) * g.length + qs;
+        load_run_t<float, HS>(p.bn + bco, nv, vec_bc, bv);
+        load_run_t<float, HS>(p.cn + bco, nv, vec_bc, cv);
+        float xh[HS], ah[HS];
+        float x = xin;
+#pragma unroll
+        for (int i = 0; i < HS; ++i) {
+          ah[i] = fast_exp2(a2 * del[i]);
+          x = fmaf(ah[i], x, du[i] * bv[i]);
+          xh[i] = x;
+        }
+        float dan = 0.0f;
+#pragma unroll
+        for (int i = HS - 1; i >= 0; --i) {
+          const float h = fmaf(gy[i], cv[i], hc);
+          s1[i] = fmaf(h, bv[i], s1[i]);
+          const float xp = i > 0 ? xh[i - 1] : xin;
+          const float pr = h * ah[i] * xp;
+          s2[i] = fmaf(an, pr, s2[i]);
+          dan = fmaf(del[i], pr, dan);
+          ya[i] = fmaf(cv[i], xh[i], ya[i]);
+          trans[lane * kTransPitch + i] = h * du[i];
+          trans[lane * kTransPitch + HS + i] = gy[i] * xh[i];
+          hc = ah[i] * h;
+        }
+        if (li.active) {
+          hcs[n * R + li.row] = hc;
+          dap[n * R + li.row] += dan;
+        }
+        wave_lds_sync();
+        if (UNI) {
+          // lane l sums column (l mod 32) over half of the 64 rows.
+          const int col = lane & (2 * HS - 1);
+          const int r0 = (lane >> 5) * 32;
+          float s = 0.0f;
+#pragma unroll 8
+          for (int r = 0; r < 32; ++r) s += trans[(r0 + r) * kTransPitch + col];
+          atomicAdd(&acc[n * 2 * HS + col], s);
+        } else if (li.active) {
+          float* dst = p.pbc + (li.bg * g.length + qs) * NS * 2;
+          for (int i = 0; i < nv; ++i) {
+            atomicAdd(dst + (static_cast<int64_t>(i) * NS + n) * 2 + 0, trans[lane * kTransPitch + i]);
+            atomicAdd(dst + (static_cast<int64_t>(i) * NS + n) * 2 + 1, trans[lane * kTransPitch + HS + i]);
+          }
+        }
+        wave_lds_sync();
+      }
+      // ---- per-step gradients of the quarter
+      {
+        float raw[HS], uu[HS], o1[HS], o2[HS];
+        load_run<HS>(p.delta, g.d_dtype, rbase + qs, nv, g.vec, raw);
+        load_run<HS>(p.u, g.u_dtype, rbase + qs, nv, g.vec, uu);
+#pragma unroll
+        for (int i = 0; i < HS; ++i) {
+          o1[i] = fmaf(del[i], s1[i], Dd * gy[i]);  // du
+          float dd = fmaf(uu[i], s1[i], s2[i]);      // d loss / d step
+          if (g.softplus) dd *= softplus_grad(raw[i] + bias);
+          o2[i] = dd;
+          if (i < nv) {
+            dD_acc = fmaf(gy[i], uu[i], dD_acc);
+            db_acc += dd * act;
+          }
+        }
+        if (li.active) {
+          store_run<HS>(p.du, g.u_dtype, rbase + qs, nv, g.vec, o1);
+          store_run<HS>(p.ddelta, g.d_dtype, rbase + qs, nv, g.vec, o2);
+        }
+        if (has_z && p.dz) {
+          float zz[HS], dy[HS];
+          load_run<HS>(p.z, g.u_dtype, rbase + qs, nv, g.vec, zz);
+          load_run<HS>(p.dout, g.u_dtype, rbase + qs, nv, g.vec, dy);
+#pragma unroll
+          for (int i = 0; i < HS; ++i) {
+            const float sg = sigmoid(zz[i]);
+            const float yfull = fmaf(Dd, uu[i], ya[i]);
+            o1[i] = dy[i] * yfull * sg * (1.0f + zz[i] * (1.0f - sg));
+          }
+          if (li.active) store_run<HS>(p.dz, g.u_dtype, rbase + qs, nv, g.vec, o1);
+        }
+      }
+      if (UNI) {
+        // The workgroup's dB/dC sums of this quarter: acc[n][k*HS + i].
+        __syncthreads();
+        float* dst = p.pbc + ((li.bg * g.ncb + cb) * g.length + qs) * NS * 2;
+        for (int e = threadIdx.x; e < NS * 2 * HS; e += blockDim.x) {
+          const int i = e % HS;
+          const int k = (e / HS) % 2;
+          const int n = e / (2 * HS);
+          if (i < nv) dst[(static_cast<int64_t>(i) * NS + n) * 2 + k] = acc[e];
+        }
+        __syncthreads();
+        for (int e = threadIdx.x; e < NS * 2 * HS; e += blockDim.x) acc[e] = 0.0f;
+        __syncthreads();
+      }
+    }
+  }
+  if (li.active) {
+    p.ddp[static_cast<int64_t>(c) * g.rows + li.row] = dD_acc;
+    p.dbp[static_cast<int64_t>(c) * g.rows + li.row] = db_acc;
+  }
+}
+
+// dB/dC (bg, N, L) = sum over channel blocks of the partials.
+template <int NS>
+__global__ void __launch_bounds__(256) reduce_bc(Geo g, int ncb, const float* __restrict__ pbc,
+                                                 void* dB, void* dC) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t total = g.batch * g.ngroups * g.dstate * g.length;
+  if (i >= total) return;
+  const int64_t t = i % g.length;
+  const int64_t n = (i / g.length) % g.dstate;
+  const int64_t bg = i / (g.length * g.dstate);
+  float sb = 0.0f, sc = 0.0f;
+  for (int cbk = 0; cbk < ncb; ++cbk) {
+    const float* q = pbc + (((bg * ncb + cbk) * g.length + t) * NS + n) * 2;
+    sb += q[0];
+    sc += q[1];
+  }
+  if (dB) store_one(dB, g.bc_dtype, i, sb);
+  if (dC) store_one(dC, g.bc_dtype, i, sc);
+}
+
+// dA (dim, N) = sum over (chunk, batch) of partials; dD, ddelta_bias likewise.
+__global__ void __launch_bounds__(256) reduce_params(Geo g, int ns, const float* __restrict__ dap,
+                                                     const float* __restrict__ ddp,
+                                                     const float* __restrict__ dbp, float* dA,
+                                                     float* dD, float* dbias) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int N = static_cast<int>(g.dstate);
+  if (i < g.dim * N) {
+    const int64_t d = i / N, n = i % N;
+    float s = 0.0f;
+    for (int c = 0; c < g.nchunks; ++c)
+      for (int64_t b = 0; b < g.batch; ++b)
+        s += dap[(static_cast<int64_t>(c) * ns + n) * g.rows + b * g.dim + d];
+    if (dA) dA[i] = s;
+  }
+  if (i < g.dim) {
+    float s1 = 0.0f, s2 = 0.0f;
+    for (int c = 0; c < g.nchunks; ++c)
+      for (int64_t b = 0; b < g.batch; ++b) {
+        s1 += ddp[static_cast<int64_t>(c) * g.rows + b * g.dim + i];
+        s2 += dbp[static_cast<int64_t>(c) * g.rows + b * g.dim + i];
+      }
+    if (dD) dD[i] = s1;
+    if (dbias) dbias[i] = s2;
+  }
+}
+
+__global__ void zero_f32(float* p, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0.0f;
+}
+
+// ---------------------------------------------------------------- host plan
+
+struct Plan {
+  Geo g;
+  int ns;
+  bool uni;
+  size_t off_bt, off_ct, off_bn, off_cn, off_drive, off_sumd, off_adj, off_pbc, off_dap, off_ddp,
+      off_dbp, off_hcs, off_qx;
+  size_t fwd_bytes, bwd_bytes;
+};
+
+inline size_t align_up(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+static int make_plan(const mko_selscan_params* p, Plan* pl) {
+  if (!p) {
+    mko_set_error("selscan: null params");
+    return MKO_EINVAL;
+  }
+  Geo& g = pl->g;
+  g.batch = p->batch;
+  g.dim = p->dim;
+  g.length = p->length;
+  g.dstate = p->dstate;
+  g.ngroups = p->ngroups;
+  if (g.batch < 0 || g.dim < 0 || g.length < 0 || g.dstate < 1 || g.ngroups < 1) {
+    mko_set_error("selscan: bad sizes batch=%lld dim=%lld length=%lld dstate=%lld ngroups=%lld",
+                  (long long)g.batch, (long long)g.dim, (long long)g.length, (long long)g.dstate,
+                  (long long)g.ngroups);
+    return MKO_EINVAL;
+  }
+  if (g.dim % g.ngroups) {
+    mko_set_error("selscan: dim=%lld not divisible by ngroups=%lld", (long long)g.dim, (long long)g.ngroups);
+    return MKO_EINVAL;
+  }
+  if (g.dstate > 32) {
+    mko_set_error("selscan: dstate=%lld > 32 is not supported", (long long)g.dstate);
+    return MKO_EUNSUPPORTED;
+  }
+  if (g.length > (int64_t)1 << 30 || g.batch * g.dim > (int64_t)1 << 31) {
+    mko_set_error("selscan: problem too large");
+    return MKO_EUNSUPPORTED;
+  }
+  for (int dt : {p->u_dtype, p->delta_dtype, p->bc_dtype}) {
+    if (dt != MKO_F32 && dt != MKO_F16 && dt != MKO_BF16) {
+      mko_set_error("selscan: unknown dtype %d", dt);
+      return MKO_EINVAL;
+    }
+  }
+  pl->ns = g.dstate <= 16 ? 16 : 32;
+  g.rows = g.batch * g.dim;
+  g.dg = g.dim / g.ngroups;
+  g.nwr = (g.rows + kWave - 1) / kWave;
+  g.u_dtype = p->u_dtype;
+  g.d_dtype = p->delta_dtype;
+  g.bc_dtype = p->bc_dtype;
+  g.softplus = (p->flags & MKO_SS_SOFTPLUS) ? 1 : 0;
+  g.nck = static_cast<int>((g.length + CK - 1) / CK);
+  pl->uni = (g.dg % kWave) == 0;
+  if (pl->uni) {
+    const int64_t blocks = g.dg / kWave;
+    g.wpg = blocks % 4 == 0 ? 4 : (blocks % 2 == 0 ? 2 : 1);
+    g.ncb = static_cast<int>(g.dg / (static_cast<int64_t>(g.wpg) * kWave));
+  } else {
+    g.wpg = 4;
+    g.ncb = 1;
+  }
+  // Coarse chunks: enough wavefronts to cover the chip (>= 2048), chunk a
+  // multiple of the save interval.
+  int64_t want = (2048 + g.nwr - 1) / (g.nwr > 0 ? g.nwr : 1);
+  int64_t k = 1;
+  while (k < want) k <<= 1;
+  int64_t lc = (g.length + k - 1) / k;
+  lc = ((lc + CK - 1) / CK) * CK;
+  if (lc < CK) lc = CK;
+  g.lc = static_cast<int>(lc);
+  g.nchunks = static_cast<int>(g.length > 0 ? (g.length + lc - 1) / lc : 0);
+  g.vec = 0;
+  const size_t ns = static_cast<size_t>(pl->ns);
+  const size_t bgl = static_cast<size_t>(g.batch * g.ngroups * g.length);
+  const size_t rk = static_cast<size_t>(g.rows) * g.nchunks;
+  size_t o = 0;
+  // forward workspace
+  pl->off_bt = o; o = align_up(o + bgl * ns * 4);
+  pl->off_ct = o; o = align_up(o + bgl * ns * 4);
+  pl->off_drive = o; o = align_up(o + rk * g.dstate * 4);
+  pl->off_sumd = o; o = align_up(o + rk * 4);
+  pl->fwd_bytes = o;
+  // backward workspace (extends the forward layout: bt/ct are used by both)
+  pl->off_bn = o; o = align_up(o + bgl * ns * 4);
+  pl->off_cn = o; o = align_up(o + bgl * ns * 4);
+  pl->off_adj = o; o = align_up(o + rk * g.dstate * 4);
+  pl->off_pbc = o; o = align_up(o + bgl * g.ncb * ns * 2 * 4);
+  pl->off_dap = o; o = align_up(o + rk * ns * 4);
+  pl->off_ddp = o; o = align_up(o + rk * 4);
+  pl->off_dbp = o; o = align_up(o + rk * 4);
+  pl->off_hcs = o; o = align_up(o + rk * ns * 4);
+  pl->off_qx = o; o = align_up(o + rk * 3 * ns * 4);
+  pl->bwd_bytes = o;
+  return MKO_OK;
+}
+
+static bool rows_vectorisable(const Geo& g, std::initializer_list<std::pair<const void*, int>> arrays) {
+  for (auto& a : arrays) {
+    if (!a.first) continue;
+    const int bytes = dtype_size(a.second);
+    if ((g.length * bytes) % 16 != 0) return false;
+    if (!aligned16(a.first)) return false;
+  }
+  return true;
+}
+
+static Ptrs make_ptrs(const mko_selscan_params* p, const Plan& pl) {
+  Ptrs q{};
+  q.u = p->u;
+  q.delta = p->delta;
+  q.A = p->A;
+  q.B = p->B;
+  q.C = p->C;
+  q.D = p->D;
+  q.z = p->z;
+  q.bias = p->delta_bias;
+  q.dout = p->dout;
+  q.out = p->out;
+  q.states = p->states;
+  q.du = p->du;
+  q.ddelta = p->ddelta;
+  q.dz = p->dz;
+  char* ws = static_cast<char*>(p->workspace);
+  q.bt = reinterpret_cast<float*>(ws + pl.off_bt);
+  q.ct = reinterpret_cast<float*>(ws + pl.off_ct);
+  q.drive = reinterpret_cast<float*>(ws + pl.off_drive);
+  q.sumd = reinterpret_cast<float*>(ws + pl.off_sumd);
+  q.bn = reinterpret_cast<float*>(ws + pl.off_bn);
+  q.cn = reinterpret_cast<float*>(ws + pl.off_cn);
+  q.adj = reinterpret_cast<float*>(ws + pl.off_adj);
+  q.pbc = reinterpret_cast<float*>(ws + pl.off_pbc);
+  q.dap = reinterpret_cast<float*>(ws + pl.off_dap);
+  q.ddp = reinterpret_cast<float*>(ws + pl.off_ddp);
+  q.dbp = reinterpret_cast<float*>(ws + pl.off_dbp);
+  q.hcs = reinterpret_cast<float*>(ws + pl.off_hcs);
+  q.qx = reinterpret_cast<float*>(ws + pl.off_qx);
+  return q;
+}
+
+static inline unsigned blocks_for(int64_t n, int per = 256) {
+  return static_cast<unsigned>((n + per - 1) / per);
+}
+
+template <int NS, bool UNI>
+static int launch_fwd(const Plan& pl, const Ptrs& q, hipStream_t s) {
+  const Geo& g = pl.g;
+  const dim3 block(g.wpg * kWave);
+  const unsigned gx = static_cast<unsigned>((g.nwr + g.wpg - 1) / g.wpg);
+  const int64_t bgl = g.batch * g.ngroups * g.length;
+  prep_time_major<NS><<<blocks_for(bgl), 256, 0, s>>>(g, q.B, q.C, q.bt, q.ct);
+  if (g.nchunks > 1) {
+    fwd_summary<NS, UNI><<<dim3(gx, g.nchunks - 1), block, 0, s>>>(g, q);
+  }
+  chain<false><<<blocks_for(g.rows * g.dstate), 256, 0, s>>>(g, q.A, q.drive, q.sumd, q.states);
+  fwd_replay<NS, UNI><<<dim3(gx, g.nchunks), block, 0, s>>>(g, q);
+  return mko_check_launch("selscan_fwd");
+}
+
+template <int NS, bool UNI>
+static int launch_bwd(const Plan& pl, const Ptrs& q, const mko_selscan_params* p, hipStream_t s) {
+  const Geo& g = pl.g;
+  const dim3 block(g.wpg * kWave);
+  const unsigned gx = static_cast<unsigned>((g.nwr + g.wpg - 1) / g.wpg);
+  const int64_t bgl = g.batch * g.ngroups * g.length;
+  prep_time_major<NS><<<blocks_for(bgl), 256, 0, s>>>(g, q.B, q.C, q.bt, q.ct);
+  prep_state_major<<<blocks_for(bgl * NS), 256, 0, s>>>(g, NS, q.B, q.C, q.bn, q.cn);
+  if (g.nchunks > 1) {
+    bwd_summary<NS, UNI><<<dim3(gx, g.nchunks - 1), block, 0, s>>>(g, q);
+  }
+  chain<true><<<blocks_for(g.rows * g.dstate), 256, 0, s>>>(g, q.A, q.drive, q.sumd, q.adj);
+  if (!UNI) {
+    const int64_t n = bgl * NS * 2;
+    zero_f32<<<blocks_for(n), 256, 0, s>>>(q.pbc, n);
+  }
+  bwd_main<NS, UNI><<<dim3(gx, g.nchunks), block, 0, s>>>(g, q);
+  reduce_bc<NS><<<blocks_for(g.batch * g.ngroups * g.dstate * g.length), 256, 0, s>>>(
+      g, UNI ? g.ncb : 1, q.pbc, p->dB, p->dC);
+  reduce_params<<<blocks_for(g.dim * g.dstate), 256, 0, s>>>(g, NS, q.dap, q.ddp, q.dbp, p->dA, p->dD,
+                                                             p->ddelta_bias);
+  return mko_check_launch("selscan_bwd");
+}
+
+}  // namespace ss
+}  // namespace mko
+
+using namespace mko;
+using namespace mko::ss;
+
+extern "C" int64_t mko_selscan_num_checkpoints(int64_t length) {
+  return length <= 0 ? 0 : (length + CK - 1) / CK;
+}
+
+extern "C" size_t mko_selscan_fwd_workspace_size(const mko_selscan_params* p) {
+  Plan pl;
+  if (make_plan(p, &pl) != MKO_OK) return 0;
+  return pl.fwd_bytes;
+}
+
+extern "C" size_t mko_selscan_bwd_workspace_size(const mko_selscan_params* p) {
+  Plan pl;
+  if (make_plan(p, &pl) != MKO_OK) return 0;
+  return pl.bwd_bytes;
+}
+
+extern "C" int mko_selscan_fwd(const mko_selscan_params* p, void* stream) {
+  Plan pl;
+  int st = make_plan(p, &pl);
+  if (st != MKO_OK) return st;
+  if (pl.g.rows == 0 || pl.g.length == 0) return MKO_OK;
+  if (!p->u || !p->delta || !p->A || !p->B || !p->C || !p->out || !p->states) {
+    mko_set_error("selscan_fwd: u, delta, A, B, C, out and states are required");
+    return MKO_EINVAL;
+  }
+  if (!p->workspace || p->workspace_bytes < pl.fwd_bytes) {
+    mko_set_error("selscan_fwd: workspace of %zu bytes needed, %zu given", pl.fwd_bytes, p->workspace_bytes);
+    return MKO_EWORKSPACE;
+  }
+  pl.g.vec = rows_vectorisable(pl.g, {{p->u, p->u_dtype}, {p->delta, p->delta_dtype}, {p->z, p->u_dtype},
+                                      {p->out, p->u_dtype}}) ? 1 : 0;
+  Ptrs q = make_ptrs(p, pl);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (pl.ns == 16) return pl.uni ? launch_fwd<16, true>(pl, q, s) : launch_fwd<16, false>(pl, q, s);
+  return pl.uni ? launch_fwd<32, true>(pl, q, s) : launch_fwd<32, false>(pl, q, s);
+}
+
+extern "C" int mko_selscan_bwd(const mko_selscan_params* p, void* stream) {
+  Plan pl;
+  int st = make_plan(p, &pl);
+  if (st != MKO_OK) return st;
+  if (!p->du || !p->ddelta) {
+    mko_set_error("selscan_bwd: du and ddelta are required");
+    return MKO_EINVAL;
+  }
+  if (pl.g.rows == 0 || pl.g.length == 0) return MKO_OK;  // caller zero-fills parameter grads
+  if (!p->u || !p->delta || !p->A || !p->B || !p->C || !p->states || !p->dout) {
+    mko_set_error("selscan_bwd: u, delta, A, B, C, states and dout are required");
+    return MKO_EINVAL;
+  }
+  if (!p->workspace || p->workspace_bytes < pl.bwd_bytes) {
+    mko_set_error("selscan_bwd: workspace of %zu bytes needed, %zu given", pl.bwd_bytes, p->workspace_bytes);
+    return MKO_EWORKSPACE;
+  }
+  pl.g.vec = rows_vectorisable(pl.g, {{p->u, p->u_dtype}, {p->delta, p->delta_dtype}, {p->z, p->u_dtype},
+                                      {p->dout, p->u_dtype}, {p->du, p->u_dtype}, {p->ddelta, p->delta_dtype},
+                                      {p->dz, p->u_dtype}}) ? 1 : 0;
+  Ptrs q = make_ptrs(p, pl);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (pl.ns == 16) return pl.uni ? launch_bwd<16, true>(pl, q, p, s) : launch_bwd<16, false>(pl, q, p, s);
+  return pl.uni ? launch_bwd<32, true>(pl, q, p, s) : launch_bwd<32, false>(pl, q, p, s);
+}

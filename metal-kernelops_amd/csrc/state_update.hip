@@ -1,0 +1,518 @@
+// Mamba-2 decode step (selective state update), forward and backward, for gfx950.
+//
+// One workgroup per (batch, head): its headdim rows of dstate states are one
+// contiguous block of the state tensor.  TPR lanes share a row and stride over
+// it in 4-element vectors, so a wavefront's loads are contiguous 16-byte runs;
+// the row's <new_state, C> is a butterfly over those TPR lanes.  delta and the
+// decay are per (batch, head) (or per row when dt has a headdim axis).
+//
+// Backward: the same workgroup recomputes the new state (instead of re-reading it
+// from memory), writes the row-local gradients, and reduces dB/dC over its rows
+// and dA/dD/ddt over its rows in a fixed order; a second kernel sums the
+// per-head partials over heads (dB/dC) or batch (dA/dD/ddt_bias).  Every output
+// has one writer, so the backward is bit-deterministic.
+#include "common.hpp"
+
+namespace mko {
+namespace su {
+
+constexpr int kThreads = 256;
+constexpr int kMaxPerThread = 16;  // states per lane: dstate / TPR <= 16
+
+struct Geo {
+  int64_t batch, nheads, headdim, dstate, ngroups;
+  int tpr;  // lanes per row (power of two, <= 64)
+  int vec;  // 4 if rows can use 4-element vector accesses, else 1
+  int state_dtype, x_dtype, dt_dtype, bc_dtype;
+  int softplus, dt_per_row, d_per_row;
+};
+
+struct Args {
+  Geo g;
+  const void* state;
+  const void* x;
+  const void* dt;
+  const float* A;
+  const void* B;
+  const void* C;
+  const float* D;
+  const void* z;
+  const float* dt_bias;
+  void* new_state;
+  void* y;
+  const float* dy;
+  const float* dnew;
+  float* gstate;
+  float* dx;
+  float* ddt;
+  float* dz;
+  float* pb;    // (batch, nheads, dstate) dB partials per head
+  float* pc;    // (batch, nheads, dstate) dC partials
+  float* pa;    // (batch, nheads) dA partials
+  float* pd;    // (batch, nheads) or (batch, nheads, headdim) dD partials
+  float* pbias; // (batch, nheads) ddt_bias partials
+};
+
+template <typename T>
+__device__ __forceinline__ void load4(const void* base, int64_t i, float (&v)[4]) {
+  if constexpr (sizeof(T) == 4) {
+    const float4 q = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + i);
+    v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+  } else {
+    const uint2 q = *reinterpret_cast<const uint2*>(static_cast<const T*>(base) + i);
+    if constexpr (__is_same(T, bf16)) {
+      v[0] = __uint_as_float(q.x << 16); v[1] = __uint_as_float(q.x & 0xffff0000u);
+      v[2] = __uint_as_float(q.y << 16); v[3] = __uint_as_float(q.y & 0xffff0000u);
+    } else {
+      v[0] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(q.x & 0xffffu)));
+      v[1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(q.x >> 16)));
+      v[2] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(q.y & 0xffffu)));
+      v[3] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(q.y >> 16)));
+    }
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void store4(void* base, int64_t i, const float (&v)[4]) {
+  if constexpr (sizeof(T) == 4) {
+    *reinterpret_cast<float4*>(static_cast<float*>(base) + i) = make_float4(v[0], v[1], v[2], v[3]);
+  } else {
+    uint32_t w0, w1;
+    if constexpr (__is_same(T, bf16)) {
+      w0 = from_f32<bf16>(v[0]).bits | (static_cast<uint32_t>(from_f32<bf16>(v[1]).bits) << 16);
+      w1 = from_f32<bf16>(v[2]).bits | (static_cast<uint32_t>(from_f32<bf16>(v[3]).bits) << 16);
+    } else {
+      w0 = __builtin_bit_cast(uint16_t, static_cast<_Float16>(v[0])) |
+           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(v[1]))) << 16);
+      w1 = __builtin_bit_cast(uint16_t, static_cast<_Float16>(v[2])) |
+           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(v[3]))) << 16);
+    }
+    *reinterpret_cast<uint2*>(static_cast<T*>(base) + i) = make_uint2(w0, w1);
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ float ld(const void* base, int64_t i) {
+  return to_f32(static_cast<const T*>(base)[i]);
+}
+
+__device__ __forceinline__ float ld_any(const void* base, int dtype, int64_t i) {
+  if (dtype == MKO_F32) return static_cast<const float*>(base)[i];
+  if (dtype == MKO_BF16) return to_f32(static_cast<const bf16*>(base)[i]);
+  return to_f32(static_cast<const _Float16*>(base)[i]);
+}
+
+// Elements of a row handled by lane j of its TPR lanes: vector chunks j, j+TPR, ...
+// (VEC = 4) or single elements (VEC = 1).
+template <int VEC, typename F>
+__device__ __forceinline__ void for_row_chunks(int n_states, int tpr, int j, F&& f) {
+#pragma unroll
+  for (int k = 0; k < kMaxPerThread / VEC; ++k) {
+    const int n0 = (j + k * tpr) * VEC;
+    if (n0 < n_states) f(k, n0);
+  }
+}
+
+__device__ __forceinline__ float row_sum(float v, int tpr) {
+  for (int off = tpr >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+template <typename TS, int VEC>
+__global__ void __launch_bounds__(kThreads) fwd(Args a) {
+  const Geo& g = a.g;
+  const int64_t bh = blockIdx.x;
+  const int64_t b = bh / g.nheads, h = bh % g.nheads;
+  const int64_t bg = b * g.ngroups + h / (g.nheads / g.ngroups);
+  const int N = static_cast<int>(g.dstate);
+  const int tpr = g.tpr;
+  const int j = threadIdx.x % tpr;
+  const int rows_per_pass = kThreads / tpr;
+  const float Ah = a.A[h];
+  const float bias = a.dt_bias ? a.dt_bias[h] : 0.0f;
+  for (int p = threadIdx.x / tpr; p < g.headdim; p += rows_per_pass) {
+    const int64_t row = bh * g.headdim + p;
+    float del = ld_any(a.dt, g.dt_dtype, g.dt_per_row ? row : bh) + bias;
+    if (g.softplus) del = softplus(del);
+    const float decay = expf(Ah * del);
+    const float xv = ld_any(a.x, g.x_dtype, row);
+    const float dx = del * xv;
+    float acc = 0.0f;
+    for_row_chunks<VEC>(N, tpr, j, [&](int, int n0) {
+      if constexpr (VEC == 4) {
+        float s[4], bv[4], cv[4], nv[4];
+        load4<TS>(a.state, row * N + n0, s);
+        if (g.bc_dtype == MKO_F32) { load4<float>(a.B, bg * N + n0, bv); load4<float>(a.C, bg * N + n0, cv); }
+        else if (g.bc_dtype == MKO_BF16) { load4<bf16>(a.B, bg * N + n0, bv); load4<bf16>(a.C, bg * N + n0, cv); }
+        else { load4<_Float16>(a.B, bg * N + n0, bv); load4<_Float16>(a.C, bg * N + n0, cv); }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          nv[e] = fmaf(decay, s[e], dx * bv[e]);
+          acc = fmaf(nv[e], cv[e], acc);
+        }
+        store4<TS>(a.new_state, row * N + n0, nv);
+      } else {
+        const float s = ld<TS>(a.state, row * N + n0);
+        const float nv = fmaf(decay, s, dx * ld_any(a.B, g.bc_dtype, bg * N + n0));
+        static_cast<TS*>(a.new_state)[row * N + n0] = from_f32<TS>(nv);
+        acc = fmaf(nv, ld_any(a.C, g.bc_dtype, bg * N + n0), acc);
+      }
+    });
+    acc = row_sum(acc, tpr);
+    if (j == 0) {
+      float out = acc;
+      if (a.D) out = fmaf(g.d_per_row ? a.D[h * g.headdim + p] : a.D[h], xv, out);
+      if (a.z) {
+        const float zv = ld_any(a.z, g.x_dtype, row);
+        out *= zv * sigmoid(zv);
+      }
+      static_cast<TS*>(a.y)[row] = from_f32<TS>(out);
+    }
+  }
+}
+
+template <typename TS, int VEC>
+__global__ void __launch_bounds__(kThreads) bwd(Args a) {
+  __shared__ float red[kThreads * kMaxPerThread];  // [rows_per_pass][dstate] fold buffer
+  __shared__ float rowv[3][kThreads];
+  const Geo& g = a.g;
+  const int64_t bh = blockIdx.x;
+  const int64_t b = bh / g.nheads, h = bh % g.nheads;
+  const int64_t bg = b * g.ngroups + h / (g.nheads / g.ngroups);
+  const int N = static_cast<int>(g.dstate);
+  const int tpr = g.tpr;
+  const int j = threadIdx.x % tpr;
+  const int slot = threadIdx.x / tpr;
+  const int rows_per_pass = kThreads / tpr;
+  const float Ah = a.A[h];
+  const float bias = a.dt_bias ? a.dt_bias[h] : 0.0f;
+  float pb[kMaxPerThread], pc[kMaxPerThread];
+#pragma unroll
+  for (int k = 0; k < kMaxPerThread; ++k) pb[k] = pc[k] = 0.0f;
+  float sum_a = 0.0f, sum_d = 0.0f, sum_t = 0.0f;  // thread 0: per-head folds
+
+  // Passes are uniform over the workgroup (every thread runs every pass), so the
+  // barriers below are reached by all threads.
+  for (int p0 = 0; p0 < g.headdim; p0 += rows_per_pass) {
+    const int p = p0 + slot;
+    if (p < g.headdim) {
+      const int64_t row = bh * g.headdim + p;
+      const float raw = ld_any(a.dt, g.dt_dtype, g.dt_per_row ? row : bh) + bias;
+      const float del = g.softplus ? softplus(raw) : raw;
+      const float decay = expf(Ah * del);
+      const float xv = ld_any(a.x, g.x_dtype, row);
+      const float dxv = del * xv;
+      const float dv = a.D ? (g.d_per_row ? a.D[h * g.headdim + p] : a.D[h]) : 0.0f;
+      const float dyv = a.dy ? a.dy[row] : 0.0f;
+      float zv = 0.0f, sg = 1.0f, gate = 1.0f;
+      if (a.z) {
+        zv = ld_any(a.z, g.x_dtype, row);
+        sg = sigmoid(zv);
+        gate = zv * sg;
+      }
+      const float dyp = dyv * gate;  // grad of the pre-gate output
+      float sx = 0.0f, sa = 0.0f, sy = 0.0f;
+      for_row_chunks<VEC>(N, tpr, j, [&](int k, int n0) {
+        float s[VEC], bv[VEC], cv[VEC], dn[VEC], gs[VEC];
+        if constexpr (VEC == 4) {
+          load4<TS>(a.state, row * N + n0, s);
+          if (g.bc_dtype == MKO_F32) { load4<float>(a.B, bg * N + n0, bv); load4<float>(a.C, bg * N + n0, cv); }
+          else if (g.bc_dtype == MKO_BF16) { load4<bf16>(a.B, bg * N + n0, bv); load4<bf16>(a.C, bg * N + n0, cv); }
+          else { load4<_Float16>(a.B, bg * N + n0, bv); load4<_Float16>(a.C, bg * N + n0, cv); }
+          if (a.dnew) load4<float>(a.dnew, row * N + n0, dn);
+          else { dn[0] = dn[1] = dn[2] = dn[3] = 0.0f; }
+        } else {
+          s[0] = ld<TS>(a.state, row * N + n0);
+          bv[0] = ld_any(a.B, g.bc_dtype, bg * N + n0);
+          cv[0] = ld_any(a.C, g.bc_dtype, bg * N + n0);
+          dn[0] = a.dnew ? a.dnew[row * N + n0] : 0.0f;
+        }
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const float nv = fmaf(decay, s[e], dxv * bv[e]);
+          const float q = fmaf(dyp, cv[e], dn[e]);  // grad of the new state
+          gs[e] = q * decay;
+          pb[k * VEC + e] = fmaf(q, dxv, pb[k * VEC + e]);
+          pc[k * VEC + e] = fmaf(dyp, nv, pc[k * VEC + e]);
+          sx = fmaf(q, bv[e], sx);
+          sa = fmaf(q, s[e], sa);
+          sy = fmaf(nv, cv[e], sy);
+        }
+        if constexpr (VEC == 4) {
+          *reinterpret_cast<float4*>(a.gstate + row * N + n0) = make_float4(gs[0], gs[1], gs[2], gs[3]);
+        } else {
+          a.gstate[row * N + n0] = gs[0];
+        }
+      });
+      sx = row_sum(sx, tpr);
+      sa = row_sum(sa, tpr);
+      sy = row_sum(sy, tpr);
+      if (j == 0) {
+        a.dx[row] = fmaf(del, sx, dyp * dv);
+        // delta enters through the drive (del x B) and the decay (exp(A del)).
+        float dd = fmaf(xv, sx, sa * decay * Ah);
+        if (g.softplus) dd *= softplus_grad(raw);
+        if (g.dt_per_row) a.ddt[row] = dd;
+        if (a.z && a.dz) {
+          const float ypre = fmaf(xv, dv, sy);
+          a.dz[row] = dyv * ypre * sg * (1.0f + zv * (1.0f - sg));
+        }
+        const float dD = dyp * xv;
+        if (a.D && g.d_per_row) a.pd[row] = dD;
+        rowv[0][slot] = sa * decay * del;  // dA contribution
+        rowv[1][slot] = dD;
+        rowv[2][slot] = dd;
+      }
+    }
+    // Fold this pass's per-row values in row order.
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const int pend = min(static_cast<int>(g.headdim) - p0, rows_per_pass);
+      for (int r = 0; r < pend; ++r) {
+        sum_a += rowv[0][r];
+        sum_d += rowv[1][r];
+        sum_t += rowv[2][r];
+      }
+    }
+    __syncthreads();
+  }
+  // dB/dC: fold the lanes' per-state partials over the row slots in a fixed order.
+  for (int which = 0; which < 2; ++which) {
+    float* src = which == 0 ? pb : pc;
+#pragma unroll
+    for (int k = 0; k < kMaxPerThread; ++k) red[slot * kMaxPerThread * tpr + k * tpr + j] = src[k];
+    __syncthreads();
+    for (int n = threadIdx.x; n < N; n += kThreads) {
+      // state n lives at chunk k = n / (tpr*VEC), lane j = (n / VEC) % tpr, element e = n % VEC
+      const int k = n / (tpr * VEC);
+      const int jj = (n / VEC) % tpr;
+      const int e = n % VEC;
+      float s = 0.0f;
+      const int nslots = min(rows_per_pass, static_cast<int>(g.headdim));
+      for (int r = 0; r < nslots; ++r) s += red[r * kMaxPerThread * tpr + (k * VEC + e) * tpr + jj];
+      (which == 0 ? a.pb : a.pc)[bh * N + n] = s;
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    a.pa[bh] = sum_a;
+    if (a.D && !g.d_per_row) a.pd[bh] = sum_d;
+    if (a.pbias) a.pbias[bh] = sum_t;
+    if (!g.dt_per_row) a.ddt[bh] = sum_t;
+  }
+}
+
+// Sum the per-head partials: dB/dC over the heads of a group, dA/dD/ddt_bias over batch.
+__global__ void __launch_bounds__(256) reduce(Args a, float* dB, float* dC, float* dA, float* dD,
+                                              float* dbias) {
+  const Geo& g = a.g;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t N = g.dstate;
+  const int64_t hpg = g.nheads / g.ngroups;
+  if (i < g.batch * g.ngroups * N) {
+    const int64_t n = i % N, bgi = i / N;
+    const int64_t b = bgi / g.ngroups, gi = bgi % g.ngroups;
+    float sb = 0.0f, sc = 0.0f;
+    for (int64_t k = 0; k < hpg; ++k) {
+      const int64_t bh = b * g.nheads + gi * hpg + k;
+      sb += a.pb[bh * N + n];
+      sc += a.pc[bh * N + n];
+    }
+    dB[i] = sb;
+    dC[i] = sc;
+  }
+  if (i < g.nheads) {
+    float s = 0.0f, t = 0.0f, d = 0.0f;
+    for (int64_t b = 0; b < g.batch; ++b) {
+      s += a.pa[b * g.nheads + i];
+      if (a.pbias) t += a.pbias[b * g.nheads + i];
+      if (a.D && !g.d_per_row) d += a.pd[b * g.nheads + i];
+    }
+    dA[i] = s;
+    if (dbias) dbias[i] = t;
+    if (a.D && !g.d_per_row && dD) dD[i] = d;
+  }
+  if (a.D && g.d_per_row && dD && i < g.nheads * g.headdim) {
+    float d = 0.0f;
+    for (int64_t b = 0; b < g.batch; ++b) d += a.pd[b * g.nheads * g.headdim + i];
+    dD[i] = d;
+  }
+}
+
+inline size_t align_up(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
+
+static int make_geo(const mko_state_update_params* p, Geo* g) {
+  if (!p) {
+    mko_set_error("state_update: null params");
+    return MKO_EINVAL;
+  }
+  g->batch = p->batch;
+  g->nheads = p->nheads;
+  g->headdim = p->headdim;
+  g->dstate = p->dstate;
+  g->ngroups = p->ngroups;
+  if (g->batch < 0 || g->nheads < 1 || g->headdim < 0 || g->dstate < 1 || g->ngroups < 1 ||
+      g->nheads % g->ngroups) {
+    mko_set_error("state_update: bad sizes");
+    return MKO_EINVAL;
+  }
+  if (g->dstate > kMaxPerThread * 64) {
+    mko_set_error("state_update: dstate=%lld > %d is not supported", (long long)g->dstate, kMaxPerThread * 64);
+    return MKO_EUNSUPPORTED;
+  }
+  for (int dt : {p->state_dtype, p->x_dtype, p->dt_dtype, p->bc_dtype}) {
+    if (dt != MKO_F32 && dt != MKO_F16 && dt != MKO_BF16) {
+      mko_set_error("state_update: unknown dtype %d", dt);
+      return MKO_EINVAL;
+    }
+  }
+  int tpr = 1;
+  while (tpr < 64 && tpr * kMaxPerThread < g->dstate) tpr <<= 1;
+  g->tpr = tpr;
+  g->state_dtype = p->state_dtype;
+  g->x_dtype = p->x_dtype;
+  g->dt_dtype = p->dt_dtype;
+  g->bc_dtype = p->bc_dtype;
+  g->softplus = (p->flags & MKO_SU_SOFTPLUS) ? 1 : 0;
+  g->dt_per_row = (p->flags & MKO_SU_DT_PER_ROW) ? 1 : 0;
+  g->d_per_row = (p->flags & MKO_SU_D_PER_ROW) ? 1 : 0;
+  return MKO_OK;
+}
+
+static bool al(const void* q, int bytes) { return (reinterpret_cast<uintptr_t>(q) % bytes) == 0; }
+
+static int pick_vec(const Geo& g, const mko_state_update_params* p, bool bwd) {
+  const int ss = g.state_dtype == MKO_F32 ? 4 : 2;
+  const int bs = g.bc_dtype == MKO_F32 ? 4 : 2;
+  if (g.dstate % 4) return 1;
+  if (!al(p->state, 4 * ss) || !al(p->B, 4 * bs) || !al(p->C, 4 * bs)) return 1;
+  if (!bwd && !al(p->new_state, 4 * ss)) return 1;
+  if (bwd && (!al(p->grad_state, 16) || (p->dnew_state && !al(p->dnew_state, 16)))) return 1;
+  return 4;
+}
+
+}  // namespace su
+}  // namespace mko
+
+using namespace mko;
+using namespace mko::su;
+
+namespace {
+
+template <typename TS>
+void launch_fwd_t(const Args& a, int vec, hipStream_t s, unsigned grid) {
+  if (vec == 4) fwd<TS, 4><<<grid, kThreads, 0, s>>>(a);
+  else fwd<TS, 1><<<grid, kThreads, 0, s>>>(a);
+}
+
+template <typename TS>
+void launch_bwd_t(const Args& a, int vec, hipStream_t s, unsigned grid) {
+  if (vec == 4) bwd<TS, 4><<<grid, kThreads, 0, s>>>(a);
+  else bwd<TS, 1><<<grid, kThreads, 0, s>>>(a);
+}
+
+Args base_args(const mko_state_update_params* p, const Geo& g) {
+  Args a{};
+  a.g = g;
+  a.state = p->state;
+  a.x = p->x;
+  a.dt = p->dt;
+  a.A = p->A;
+  a.B = p->B;
+  a.C = p->C;
+  a.D = p->D;
+  a.z = p->z;
+  a.dt_bias = p->dt_bias;
+  return a;
+}
+
+struct BwdLayout {
+  size_t pb, pc, pa, pd, pbias, total;
+};
+
+BwdLayout bwd_layout(const Geo& g) {
+  BwdLayout l{};
+  const size_t bh = static_cast<size_t>(g.batch * g.nheads);
+  size_t o = 0;
+  l.pb = o; o = align_up(o + bh * g.dstate * 4);
+  l.pc = o; o = align_up(o + bh * g.dstate * 4);
+  l.pa = o; o = align_up(o + bh * 4);
+  l.pd = o; o = align_up(o + bh * (g.headdim > 0 ? g.headdim : 1) * 4);
+  l.pbias = o; o = align_up(o + bh * 4);
+  l.total = o;
+  return l;
+}
+
+}  // namespace
+
+extern "C" int mko_state_update_fwd(const mko_state_update_params* p, void* stream) {
+  Geo g;
+  int st = make_geo(p, &g);
+  if (st != MKO_OK) return st;
+  if (g.batch == 0 || g.headdim == 0) return MKO_OK;
+  if (!p->state || !p->x || !p->dt || !p->A || !p->B || !p->C || !p->new_state || !p->y) {
+    mko_set_error("state_update_fwd: state, x, dt, A, B, C, new_state and y are required");
+    return MKO_EINVAL;
+  }
+  g.vec = pick_vec(g, p, false);
+  Args a = base_args(p, g);
+  a.new_state = p->new_state;
+  a.y = p->y;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const unsigned grid = static_cast<unsigned>(g.batch * g.nheads);
+  if (g.state_dtype == MKO_F32) launch_fwd_t<float>(a, g.vec, s, grid);
+  else if (g.state_dtype == MKO_BF16) launch_fwd_t<bf16>(a, g.vec, s, grid);
+  else launch_fwd_t<_Float16>(a, g.vec, s, grid);
+  return mko_check_launch("state_update_fwd");
+}
+
+extern "C" size_t mko_state_update_bwd_workspace_size(const mko_state_update_params* p) {
+  Geo g;
+  if (make_geo(p, &g) != MKO_OK) return 0;
+  return bwd_layout(g).total;
+}
+
+extern "C" int mko_state_update_bwd(const mko_state_update_params* p, void* stream) {
+  Geo g;
+  int st = make_geo(p, &g);
+  if (st != MKO_OK) return st;
+  if (!p->grad_state || !p->dx || !p->ddt || !p->dA || !p->dB || !p->dC) {
+    mko_set_error("state_update_bwd: grad_state, dx, ddt, dA, dB and dC are required");
+    return MKO_EINVAL;
+  }
+  if ((p->D && !p->dD) || (p->z && !p->dz) || (p->dt_bias && !p->ddt_bias)) {
+    mko_set_error("state_update_bwd: dD/dz/ddt_bias are required when D/z/dt_bias are given");
+    return MKO_EINVAL;
+  }
+  if (g.batch == 0 || g.headdim == 0) return MKO_OK;  // caller zero-fills
+  const BwdLayout l = bwd_layout(g);
+  if (!p->workspace || p->workspace_bytes < l.total) {
+    mko_set_error("state_update_bwd: workspace of %zu bytes needed, %zu given", l.total, p->workspace_bytes);
+    return MKO_EWORKSPACE;
+  }
+  g.vec = pick_vec(g, p, true);
+  Args a = base_args(p, g);
+  a.dy = p->dy;
+  a.dnew = p->dnew_state;
+  a.gstate = p->grad_state;
+  a.dx = p->dx;
+  a.ddt = p->ddt;
+  a.dz = p->dz;
+  char* ws = static_cast<char*>(p->workspace);
+  a.pb = reinterpret_cast<float*>(ws + l.pb);
+  a.pc = reinterpret_cast<float*>(ws + l.pc);
+  a.pa = reinterpret_cast<float*>(ws + l.pa);
+  a.pd = reinterpret_cast<float*>(ws + l.pd);
+  a.pbias = p->dt_bias ? reinterpret_cast<float*>(ws + l.pbias) : nullptr;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const unsigned grid = static_cast<unsigned>(g.batch * g.nheads);
+  if (g.state_dtype == MKO_F32) launch_bwd_t<float>(a, g.vec, s, grid);
+  else if (g.state_dtype == MKO_BF16) launch_bwd_t<bf16>(a, g.vec, s, grid);
+  else launch_bwd_t<_Float16>(a, g.vec, s, grid);
+  const int64_t nred = g.batch * g.ngroups * g.dstate;
+  int64_t total = nred > g.nheads * g.headdim ? nred : g.nheads * g.headdim;
+  if (total < g.nheads) total = g.nheads;
+  reduce<<<static_cast<unsigned>((total + 255) / 256), 256, 0, s>>>(a, p->dB, p->dC, p->dA, p->dD,
+                                                                     p->ddt_bias);
+  return mko_check_launch("state_update_bwd");
+}

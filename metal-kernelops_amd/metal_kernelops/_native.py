@@ -1,0 +1,134 @@
+"""ctypes binding of libmko.so, the C ABI declared in ``include/mko.h``.
+
+The library is loaded on first use from ``_lib/libmko.so`` next to this file (or
+from ``$MKO_LIBRARY``).  There is no fallback: if the library is missing or was
+built against another ABI version, every GPU entry point raises ``RuntimeError``.
+Tensors cross the boundary as raw device pointers; the current torch HIP stream
+is passed as the launch stream.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+ABI_VERSION = 1
+
+F32, F16, BF16 = 0, 1, 2
+_DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
+
+_LIB_PATH = os.environ.get(
+    "MKO_LIBRARY", os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libmko.so"))
+
+_lock = threading.Lock()
+_lib = None
+
+_vp = ctypes.c_void_p
+
+
+class SelscanParams(ctypes.Structure):
+    """Mirror of ``mko_selscan_params``."""
+
+    _fields_ = [
+        ("u", _vp), ("delta", _vp), ("A", _vp), ("B", _vp), ("C", _vp), ("D", _vp), ("z", _vp),
+        ("delta_bias", _vp), ("out", _vp), ("states", _vp), ("dout", _vp), ("du", _vp),
+        ("ddelta", _vp), ("dA", _vp), ("dB", _vp), ("dC", _vp), ("dD", _vp), ("dz", _vp),
+        ("ddelta_bias", _vp), ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
+        ("batch", ctypes.c_int64), ("dim", ctypes.c_int64), ("length", ctypes.c_int64),
+        ("dstate", ctypes.c_int64), ("ngroups", ctypes.c_int64),
+        ("u_dtype", ctypes.c_int32), ("delta_dtype", ctypes.c_int32), ("bc_dtype", ctypes.c_int32),
+        ("flags", ctypes.c_uint32),
+    ]
+
+
+class StateUpdateParams(ctypes.Structure):
+    """Mirror of ``mko_state_update_params``."""
+
+    _fields_ = [
+        ("state", _vp), ("x", _vp), ("dt", _vp), ("A", _vp), ("B", _vp), ("C", _vp), ("D", _vp),
+        ("z", _vp), ("dt_bias", _vp), ("new_state", _vp), ("y", _vp), ("dy", _vp),
+        ("dnew_state", _vp), ("grad_state", _vp), ("dx", _vp), ("ddt", _vp), ("dA", _vp),
+        ("dB", _vp), ("dC", _vp), ("dD", _vp), ("dz", _vp), ("ddt_bias", _vp),
+        ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
+        ("batch", ctypes.c_int64), ("nheads", ctypes.c_int64), ("headdim", ctypes.c_int64),
+        ("dstate", ctypes.c_int64), ("ngroups", ctypes.c_int64),
+        ("state_dtype", ctypes.c_int32), ("x_dtype", ctypes.c_int32), ("dt_dtype", ctypes.c_int32),
+        ("bc_dtype", ctypes.c_int32), ("flags", ctypes.c_uint32),
+    ]
+
+
+_SIGNATURES = {
+    "mko_abi_version": ([], ctypes.c_int),
+    "mko_last_error": ([], ctypes.c_char_p),
+    "mko_sizeof_selscan_params": ([], ctypes.c_size_t),
+    "mko_sizeof_state_update_params": ([], ctypes.c_size_t),
+    "mko_selscan_num_checkpoints": ([ctypes.c_int64], ctypes.c_int64),
+    "mko_selscan_fwd_workspace_size": ([ctypes.POINTER(SelscanParams)], ctypes.c_size_t),
+    "mko_selscan_fwd": ([ctypes.POINTER(SelscanParams), _vp], ctypes.c_int),
+    "mko_selscan_bwd_workspace_size": ([ctypes.POINTER(SelscanParams)], ctypes.c_size_t),
+    "mko_selscan_bwd": ([ctypes.POINTER(SelscanParams), _vp], ctypes.c_int),
+    "mko_state_update_fwd": ([ctypes.POINTER(StateUpdateParams), _vp], ctypes.c_int),
+    "mko_state_update_bwd_workspace_size": ([ctypes.POINTER(StateUpdateParams)], ctypes.c_size_t),
+    "mko_state_update_bwd": ([ctypes.POINTER(StateUpdateParams), _vp], ctypes.c_int),
+}
+
+
+def library_path():
+    return _LIB_PATH
+
+
+def lib():
+    """The loaded library; raises ``RuntimeError`` when it is missing or mismatched."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(_LIB_PATH):
+            raise RuntimeError(
+                f"libmko.so not found at {_LIB_PATH}: build it with "
+                "`python metal-kernelops_amd/build.py` (hipcc, gfx950)")
+        handle = ctypes.CDLL(_LIB_PATH)
+        for name, (args, res) in _SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = args
+            fn.restype = res
+        version = handle.mko_abi_version()
+        if version != ABI_VERSION:
+            raise RuntimeError(f"libmko.so ABI version {version}, this binding expects {ABI_VERSION}")
+        for struct, fn in ((SelscanParams, handle.mko_sizeof_selscan_params),
+                           (StateUpdateParams, handle.mko_sizeof_state_update_params)):
+            if ctypes.sizeof(struct) != fn():
+                raise RuntimeError(f"{struct.__name__} layout does not match libmko.so")
+        _lib = handle
+        return _lib
+
+
+def exported_symbols():
+    return list(_SIGNATURES)
+
+
+def check(status, what):
+    if status != 0:
+        msg = lib().mko_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed (status {status}): {msg}")
+
+
+def ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def code(dtype):
+    return _DTYPE_CODE[dtype]
+
+
+def stream_of(device):
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def workspace(nbytes, device):
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)

@@ -1,0 +1,233 @@
+"""Mamba-1 selective scan on MI355X: fused forward, analytic backward, HIP kernels.
+
+Public surface, as in dbydd/metal-kernelops ``scan.py:283-329``:
+
+* ``selective_scan(u, dt, A, B, C, D=None, z=None, delta_bias=None,
+  delta_softplus=False)`` and its alias ``selective_scan_fn``;
+* ``scan_mps(u, dt, A, B, C)``: the bare scan, kept under the reference's name so
+  callers switch without edits (it runs on the ROCm GPU, not on MPS);
+* ``scan_reference(u, dt, A, B, C)``: the pure-torch recurrence;
+* ``CHUNK``, ``BLOCK``.
+
+Differences from the reference, all widenings: the discretisation, the ``D`` skip
+and the ``silu(z)`` gate run inside the kernel instead of as separate torch ops
+(``scan.py:311-319``); u/z/B/C may be float16 or bfloat16 (computed in float32,
+rounded once on the store); B/C/dB/dC are reduced deterministically (the
+reference uses float atomics, ``scan.py:226-227``) whenever ``dim / ngroups`` is a
+multiple of 64.  The backward is once-differentiable, as in the reference
+(``scan.py:258``).  Tensors must live on a ROCm GPU; there is no CPU path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Tuple
+
+import torch
+from torch import Tensor
+
+from . import _native as nat
+
+CHUNK = 64
+"""Steps between the scan states the forward saves for the backward."""
+
+BLOCK = 64
+"""Channels per wavefront: the lanes that share one B_t/C_t and reduce dB/dC together."""
+
+_SOFTPLUS = 1
+_FLOATS = (torch.float32, torch.float16, torch.bfloat16)
+
+
+def _params(u, delta, A, B, C, D, z, bias, softplus):
+    batch, dim, length = u.shape
+    p = nat.SelscanParams()
+    p.u, p.delta, p.A, p.B, p.C = (nat.ptr(t) for t in (u, delta, A, B, C))
+    p.D, p.z, p.delta_bias = nat.ptr(D), nat.ptr(z), nat.ptr(bias)
+    p.batch, p.dim, p.length = batch, dim, length
+    p.dstate, p.ngroups = A.shape[1], B.shape[1]
+    p.u_dtype, p.delta_dtype, p.bc_dtype = nat.code(u.dtype), nat.code(delta.dtype), nat.code(B.dtype)
+    p.flags = _SOFTPLUS if softplus else 0
+    return p
+
+
+def _num_checkpoints(length):
+    return (length + CHUNK - 1) // CHUNK
+
+
+@torch.library.custom_op("mko::selscan_fwd", mutates_args=(), device_types="cuda")
+def _selscan_fwd(u: Tensor, delta: Tensor, A: Tensor, B: Tensor, C: Tensor, D: Optional[Tensor],
+                 z: Optional[Tensor], delta_bias: Optional[Tensor], softplus: bool
+                 ) -> Tuple[Tensor, Tensor]:
+    batch, dim, length = u.shape
+    out = torch.empty_like(u)
+    states = torch.empty(batch, dim, _num_checkpoints(length), A.shape[1], dtype=torch.float32,
+                         device=u.device)
+    if out.numel() == 0:
+        return out, states
+    lib = nat.lib()
+    p = _params(u, delta, A, B, C, D, z, delta_bias, softplus)
+    p.out, p.states = out.data_ptr(), states.data_ptr()
+    ws = nat.workspace(lib.mko_selscan_fwd_workspace_size(ctypes.byref(p)), u.device)
+    p.workspace, p.workspace_bytes = ws.data_ptr(), ws.numel()
+    nat.check(lib.mko_selscan_fwd(ctypes.byref(p), nat.stream_of(u.device)), "mko_selscan_fwd")
+    return out, states
+
+
+@_selscan_fwd.register_fake
+def _(u, delta, A, B, C, D, z, delta_bias, softplus):
+    batch, dim, length = u.shape
+    return torch.empty_like(u), u.new_empty(batch, dim, _num_checkpoints(length), A.shape[1],
+                                            dtype=torch.float32)
+
+
+@torch.library.custom_op("mko::selscan_bwd", mutates_args=(), device_types="cuda")
+def _selscan_bwd(dout: Tensor, u: Tensor, delta: Tensor, A: Tensor, B: Tensor, C: Tensor,
+                 D: Optional[Tensor], z: Optional[Tensor], delta_bias: Optional[Tensor],
+                 softplus: bool, states: Tensor
+                 ) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    dim = u.shape[1]
+    f32 = dict(dtype=torch.float32, device=u.device)
+    du, ddelta = torch.empty_like(u), torch.empty_like(delta)
+    dA = torch.zeros(A.shape, **f32)
+    dB, dC = torch.zeros_like(B), torch.zeros_like(C)
+    dD = torch.zeros(dim if D is not None else 0, **f32)
+    dz = torch.zeros_like(z) if z is not None else torch.empty(0, dtype=u.dtype, device=u.device)
+    dbias = torch.zeros(dim if delta_bias is not None else 0, **f32)
+    if u.numel() == 0:
+        return du, ddelta, dA, dB, dC, dD, dz, dbias
+    lib = nat.lib()
+    p = _params(u, delta, A, B, C, D, z, delta_bias, softplus)
+    p.states, p.dout = states.data_ptr(), dout.data_ptr()
+    p.du, p.ddelta, p.dA, p.dB, p.dC = (t.data_ptr() for t in (du, ddelta, dA, dB, dC))
+    p.dD = dD.data_ptr() if D is not None else None
+    p.dz = dz.data_ptr() if z is not None else None
+    p.ddelta_bias = dbias.data_ptr() if delta_bias is not None else None
+    ws = nat.workspace(lib.mko_selscan_bwd_workspace_size(ctypes.byref(p)), u.device)
+    p.workspace, p.workspace_bytes = ws.data_ptr(), ws.numel()
+    nat.check(lib.mko_selscan_bwd(ctypes.byref(p), nat.stream_of(u.device)), "mko_selscan_bwd")
+    return du, ddelta, dA, dB, dC, dD, dz, dbias
+
+
+@_selscan_bwd.register_fake
+def _(dout, u, delta, A, B, C, D, z, delta_bias, softplus, states):
+    dim = u.shape[1]
+    return (torch.empty_like(u), torch.empty_like(delta), A.new_empty(A.shape, dtype=torch.float32),
+            torch.empty_like(B), torch.empty_like(C), u.new_empty(dim if D is not None else 0,
+                                                                  dtype=torch.float32),
+            torch.empty_like(z) if z is not None else u.new_empty(0),
+            u.new_empty(dim if delta_bias is not None else 0, dtype=torch.float32))
+
+
+def _setup(ctx, inputs, output):
+    u, delta, A, B, C, D, z, delta_bias, softplus = inputs
+    ctx.save_for_backward(u, delta, A, B, C, D, z, delta_bias, output[1])
+    ctx.softplus = softplus
+
+
+def _backward(ctx, dout, _dstates):
+    u, delta, A, B, C, D, z, bias, states = ctx.saved_tensors
+    du, ddelta, dA, dB, dC, dD, dz, dbias = torch.ops.mko.selscan_bwd(
+        dout.contiguous(), u, delta, A, B, C, D, z, bias, ctx.softplus, states)
+    return (du, ddelta, dA, dB, dC, dD if D is not None else None, dz if z is not None else None,
+            dbias if bias is not None else None, None)
+
+
+torch.library.register_autograd("mko::selscan_fwd", _backward, setup_context=_setup)
+
+
+def _require_gpu(t):
+    if t.device.type != "cuda" or torch.version.hip is None:
+        raise ValueError("HIP kernels need tensors on a ROCm GPU (torch device 'cuda'), "
+                         f"got {t.device}")
+
+
+def _check_shapes(u, dt, A, B, C, D, z, delta_bias):
+    if u.dim() != 3:
+        raise ValueError(f"u must be (batch, dim, length), got {tuple(u.shape)}")
+    batch, dim, length = u.shape
+    if tuple(dt.shape) != (batch, dim, length):
+        raise ValueError(f"dt must be {(batch, dim, length)}, got {tuple(dt.shape)}")
+    if A.dim() != 2 or A.shape[0] != dim:
+        raise ValueError(f"A must be ({dim}, dstate), got {tuple(A.shape)}")
+    dstate = A.shape[1]
+    if B.dim() != 4 or tuple(C.shape) != tuple(B.shape):
+        raise ValueError(f"B and C must both be (batch, groups, dstate, length), got "
+                         f"{tuple(B.shape)} and {tuple(C.shape)}")
+    if B.shape[0] != batch or B.shape[2] != dstate or B.shape[3] != length:
+        raise ValueError(f"B/C must be ({batch}, groups, {dstate}, {length}), got {tuple(B.shape)}")
+    groups = B.shape[1]
+    if groups < 1 or dim % groups:
+        raise ValueError(f"dim={dim} must be divisible by groups={groups}")
+    if dstate < 1 or dstate > 32:
+        raise ValueError(f"dstate must be in [1, 32], got {dstate}")
+    if D is not None and tuple(D.shape) != (dim,):
+        raise ValueError(f"D must be ({dim},), got {tuple(D.shape)}")
+    if z is not None and tuple(z.shape) != (batch, dim, length):
+        raise ValueError(f"z must be {(batch, dim, length)}, got {tuple(z.shape)}")
+    if delta_bias is not None and tuple(delta_bias.shape) != (dim,):
+        raise ValueError(f"delta_bias must be ({dim},), got {tuple(delta_bias.shape)}")
+    for name, t in (("u", u), ("dt", dt), ("A", A), ("B", B), ("C", C), ("D", D), ("z", z),
+                    ("delta_bias", delta_bias)):
+        if t is None:
+            continue
+        if t.dtype not in _FLOATS:
+            raise ValueError(f"{name} must be float32, float16 or bfloat16, got {t.dtype}")
+        if t.device != u.device:
+            raise ValueError(f"{name} is on {t.device}, u is on {u.device}")
+
+
+def _run(u, dt, A, B, C, D, z, delta_bias, softplus):
+    _require_gpu(u)
+    _check_shapes(u, dt, A, B, C, D, z, delta_bias)
+    if dt.dtype not in (torch.float32, u.dtype):
+        dt = dt.float()
+    if B.dtype != C.dtype:
+        B, C = B.float(), C.float()
+    if z is not None and z.dtype != u.dtype:
+        z = z.to(u.dtype)
+    f32 = [None if t is None else (t if t.dtype == torch.float32 else t.float()) for t in (A, D, delta_bias)]
+    A, D, delta_bias = (None if t is None else t.contiguous() for t in f32)
+    u, dt, B, C = (t.contiguous() for t in (u, dt, B, C))
+    z = None if z is None else z.contiguous()
+    out, _ = torch.ops.mko.selscan_fwd(u, dt, A, B, C, D, z, delta_bias, bool(softplus))
+    return out
+
+
+def scan_mps(u, dt, A, B, C):
+    """Bare selective scan on the ROCm GPU (name kept from the reference's Metal entry).
+
+    Follows ``scan.py:283-292``: a ``ValueError`` for tensors off the GPU or not
+    contiguous.  float16/bfloat16 are accepted in addition to float32.
+    """
+    _require_gpu(u)
+    for name, tensor in (("u", u), ("dt", dt), ("A", A), ("B", B), ("C", C)):
+        if not tensor.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+    return _run(u, dt, A, B, C, None, None, None, False)
+
+
+def selective_scan(u, dt, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False):
+    """Drop-in selective scan matching mamba_ssm's ``selective_scan_fn``.
+
+    Args:
+        u, dt: (batch, dim, length)
+        A: (dim, dstate), negative; dstate <= 32
+        B, C: (batch, groups, dstate, length), groups dividing dim
+        D: (dim,) skip connection
+        z: (batch, dim, length) gate, applied as ``out * silu(z)``
+        delta_bias: (dim,) added to dt
+        delta_softplus: apply softplus (threshold 20) to dt + delta_bias
+
+    Returns:
+        (batch, dim, length) in u's dtype.
+    """
+    return _run(u, dt, A, B, C, D, z, delta_bias, delta_softplus)
+
+
+selective_scan_fn = selective_scan
+
+
+def scan_reference(u, dt, A, B, C):
+    """Pure torch selective scan, evaluated step by step."""
+    from .reference import selective_scan as reference_scan
+    return reference_scan(u, dt, A, B, C)

@@ -1,0 +1,102 @@
+"""Seeded input builders shared by the oracle tests, the GPU parity tests and the bench.
+
+Draw order and distributions follow the configs of the hot-path benchmark:
+one CPU generator per problem, draws in the order listed, fp32 first and then
+cast; ``dt_bias = log(expm1(U(1e-3, 1e-1)))``.
+"""
+
+from __future__ import annotations
+
+import torch
+
+
+def uniform(gen, shape, lo, hi):
+    return lo + (hi - lo) * torch.rand(shape, generator=gen)
+
+
+def inv_softplus_bias(gen, n):
+    return torch.log(torch.expm1(uniform(gen, (n,), 1e-3, 1e-1)))
+
+
+def mamba1_c1(seed=0):
+    """Config 1: batch 2, d_inner 8, seqlen 64, d_state 16, ngroups 2, fp32."""
+    g = torch.Generator().manual_seed(seed)
+    b, d, l, n, grp = 2, 8, 64, 16, 2
+    u = torch.randn(b, d, l, generator=g)
+    dt = torch.randn(b, d, l, generator=g)
+    dt_bias = inv_softplus_bias(g, d)
+    A = -torch.arange(1, n + 1, dtype=torch.float32).expand(d, n).contiguous()
+    B = torch.randn(b, grp, n, l, generator=g)
+    C = torch.randn(b, grp, n, l, generator=g)
+    D = torch.ones(d)
+    z = torch.randn(b, d, l, generator=g)
+    dy = torch.randn(b, d, l, generator=g)
+    return dict(u=u, dt=dt, A=A, B=B, C=C, D=D, z=z, delta_bias=dt_bias), dy
+
+
+def mamba1_layer(batch, dim, length, dstate=16, groups=1, seed=0, act=torch.bfloat16):
+    """Configs 2-3: u/z/B/C in ``act``; dt, A, D, dt_bias fp32; A = -exp(log(1..N))."""
+    g = torch.Generator().manual_seed(seed)
+    u = torch.randn(batch, dim, length, generator=g)
+    dt = torch.randn(batch, dim, length, generator=g)
+    dt_bias = inv_softplus_bias(g, dim)
+    A = -torch.exp(torch.log(torch.arange(1, dstate + 1, dtype=torch.float32)))
+    A = A.expand(dim, dstate).contiguous()
+    B = torch.randn(batch, groups, dstate, length, generator=g)
+    C = torch.randn(batch, groups, dstate, length, generator=g)
+    D = 1.0 + 0.1 * torch.randn(dim, generator=g)
+    z = torch.randn(batch, dim, length, generator=g)
+    dy = torch.randn(batch, dim, length, generator=g)
+    return dict(u=u.to(act), dt=dt, A=A, B=B.to(act), C=C.to(act), D=D, z=z.to(act),
+                delta_bias=dt_bias), dy.to(act)
+
+
+def ssd_problem(batch, length, nheads, headdim, ngroups, dstate, seed=0, act=torch.float32,
+                init=True, d_per_head=False):
+    """Config 4 draws: x, dt, dt_bias, A=-U(1,16), B, C, D=ones, z, initial states."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(batch, length, nheads, headdim, generator=g)
+    dt = torch.randn(batch, length, nheads, generator=g)
+    dt_bias = inv_softplus_bias(g, nheads)
+    A = -uniform(g, (nheads,), 1.0, 16.0)
+    B = torch.randn(batch, length, ngroups, dstate, generator=g)
+    C = torch.randn(batch, length, ngroups, dstate, generator=g)
+    D = torch.ones(nheads, headdim) if d_per_head else torch.ones(nheads)
+    z = torch.randn(batch, length, nheads, headdim, generator=g)
+    initial = 0.1 * torch.randn(batch, nheads, headdim, dstate, generator=g) if init else None
+    return dict(x=x.to(act), dt=dt, A=A, B=B.to(act), C=C.to(act), D=D, z=z.to(act),
+                dt_bias=dt_bias, initial_states=None if initial is None else initial.to(act))
+
+
+def decode_problem(batch, nheads, headdim, dstate, ngroups, seed=0, act=torch.bfloat16,
+                   state_dtype=torch.float32, dt_per_row=False):
+    """Config 5 draws: state=0.1*N(0,1), x, dt, dt_bias, A=-U(1,16), B, C, D=ones, z."""
+    g = torch.Generator().manual_seed(seed)
+    state = 0.1 * torch.randn(batch, nheads, headdim, dstate, generator=g)
+    x = torch.randn(batch, nheads, headdim, generator=g)
+    dt = torch.randn(*((batch, nheads, headdim) if dt_per_row else (batch, nheads)), generator=g)
+    dt_bias = inv_softplus_bias(g, nheads)
+    A = -uniform(g, (nheads,), 1.0, 16.0)
+    B = torch.randn(batch, ngroups, dstate, generator=g)
+    C = torch.randn(batch, ngroups, dstate, generator=g)
+    D = torch.ones(nheads)
+    z = torch.randn(batch, nheads, headdim, generator=g)
+    return dict(state=state.to(state_dtype), x=x.to(act), dt=dt, A=A, B=B.to(act),
+                C=C.to(act), D=D, z=z.to(act), dt_bias=dt_bias)
+
+
+def max_rel(actual, expected):
+    """Max absolute error over the largest expected magnitude (the reference's metric)."""
+    actual = actual.detach().double().cpu()
+    expected = expected.detach().double().cpu()
+    scale = max(expected.abs().max().item() if expected.numel() else 0.0, 1e-30)
+    if actual.numel() == 0:
+        return 0.0
+    return (actual - expected).abs().max().item() / scale
+
+
+def norm_rel(actual, expected):
+    """Relative error of a gradient, normalised by that gradient's norm."""
+    actual = actual.detach().double().cpu()
+    expected = expected.detach().double().cpu()
+    return (actual - expected).norm().item() / max(expected.norm().item(), 1e-30)

@@ -1,0 +1,62 @@
+"""The C ABI library loads on the CPU host and exports what include/mko.h declares.
+
+No kernel is launched here: only host-side entry points (version, sizes, argument
+validation) are called.
+"""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mko.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mko_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def native():
+    from metal_kernelops import _native
+    return _native
+
+
+def test_library_exports_every_declared_symbol(native):
+    lib = native.lib()
+    declared = _declared()
+    assert len(declared) >= 10
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert set(declared) <= set(native.exported_symbols()) | {"mko_last_error"}
+
+
+def test_abi_version_and_struct_layouts(native):
+    lib = native.lib()
+    assert lib.mko_abi_version() == native.ABI_VERSION
+    assert ctypes.sizeof(native.SelscanParams) == lib.mko_sizeof_selscan_params()
+    assert ctypes.sizeof(native.StateUpdateParams) == lib.mko_sizeof_state_update_params()
+
+
+def test_host_side_validation_without_gpu(native):
+    lib = native.lib()
+    p = native.SelscanParams()
+    p.batch, p.dim, p.length, p.dstate, p.ngroups = 2, 8, 64, 16, 3  # 8 % 3 != 0
+    assert lib.mko_selscan_fwd(ctypes.byref(p), None) == 1
+    assert b"divisible" in lib.mko_last_error()
+    p.ngroups, p.dstate = 2, 40
+    assert lib.mko_selscan_fwd(ctypes.byref(p), None) == 3
+    p.dstate = 16
+    assert lib.mko_selscan_fwd_workspace_size(ctypes.byref(p)) > 0
+    assert lib.mko_selscan_num_checkpoints(130) == 3
+    p.workspace, p.workspace_bytes = None, 0
+    for name in ("u", "delta", "A", "B", "C", "out", "states"):
+        setattr(p, name, 16)  # never dereferenced: the workspace check fails first
+    assert lib.mko_selscan_fwd(ctypes.byref(p), None) == 4
+    q = native.StateUpdateParams()
+    q.batch, q.nheads, q.headdim, q.dstate, q.ngroups = 1, 4, 8, 16, 3
+    assert lib.mko_state_update_fwd(ctypes.byref(q), None) == 1

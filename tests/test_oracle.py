@@ -1,0 +1,332 @@
+"""Pins the CPU oracle before anything is checked against it.
+
+Every oracle function is checked against something that does not share its code:
+a closed form, an independent formulation, a brute-force loop, or central finite
+differences.  Each check is chosen so that a plausible slip (a dropped term, a wrong
+sign or index, a transposed operand, an off-by-one in time) fails it.
+"""
+
+import pytest
+import torch
+
+import oracle
+from cases import decode_problem, mamba1_c1, max_rel, ssd_problem
+
+F64 = torch.float64
+
+
+def _g(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+# ----------------------------------------------------------------------- softplus
+
+
+def test_softplus_threshold_rule():
+    v = torch.tensor([-30.0, -5.0, -1e-3, 0.0, 1e-3, 5.0, 19.999, 20.0, 20.001, 50.0], dtype=F64)
+    expect = torch.tensor([float(x) if x > 20 else torch.log1p(torch.exp(torch.tensor(x, dtype=F64))).item()
+                           for x in v.tolist()], dtype=F64)
+    assert torch.allclose(oracle.softplus(v), expect, rtol=0, atol=1e-15)
+    # torch's own softplus follows the same rule (threshold 20, beta 1)
+    assert torch.allclose(oracle.softplus(v), torch.nn.functional.softplus(v), rtol=0, atol=1e-15)
+
+
+# ----------------------------------------------------------------------- Mamba-1
+
+
+def test_selscan_functional_matches_literal_loop():
+    inputs, _ = mamba1_c1()
+    args = [inputs[k] for k in ("u", "dt", "A", "B", "C")]
+    args[1] = torch.nn.functional.softplus(args[1].double()).float()  # positive steps
+    loop = oracle.selective_scan_loop(*args)
+    func = oracle.selective_scan(*args)
+    assert max_rel(func, loop) < 1e-13
+
+
+def test_selscan_single_step_closed_form():
+    g = _g(3)
+    b, d, n, grp = 2, 6, 5, 3
+    u, dt = torch.randn(b, d, 1, generator=g, dtype=F64), torch.rand(b, d, 1, generator=g, dtype=F64)
+    A = -torch.rand(d, n, generator=g, dtype=F64)
+    B, C = torch.randn(b, grp, n, 1, generator=g, dtype=F64), torch.randn(b, grp, n, 1, generator=g, dtype=F64)
+    D, z = torch.randn(d, generator=g, dtype=F64), torch.randn(b, d, 1, generator=g, dtype=F64)
+    y = oracle.selective_scan(u, dt, A, B, C, D=D, z=z)
+    Bc = B.repeat_interleave(d // grp, dim=1)[..., 0]
+    Cc = C.repeat_interleave(d // grp, dim=1)[..., 0]
+    expect = (dt[..., 0] * u[..., 0] * (Bc * Cc).sum(-1) + D * u[..., 0]) * (z[..., 0] * torch.sigmoid(z[..., 0]))
+    assert max_rel(y[..., 0], expect) < 1e-14
+
+
+def test_selscan_cumulative_sum_degeneration():
+    # A = 0, dt = 1, B = C = 1: the scan is a running sum along the sequence.
+    g = _g(4)
+    u = torch.randn(2, 3, 37, generator=g, dtype=F64)
+    y = oracle.selective_scan(u, torch.ones_like(u), torch.zeros(3, 1, dtype=F64),
+                              torch.ones(2, 1, 1, 37, dtype=F64), torch.ones(2, 1, 1, 37, dtype=F64))
+    assert max_rel(y, u.cumsum(-1)) < 1e-14
+
+
+def test_selscan_constant_inputs_geometric_series():
+    # Constant dt, u, B, C: x_t = dt u B (1 - a^(t+1)) / (1 - a) with a = exp(dt A).
+    d, n, length = 3, 4, 25
+    dt_v, u_v = 0.3, 1.7
+    A = -torch.linspace(0.2, 2.0, d * n, dtype=F64).view(d, n)
+    Bv = torch.linspace(-1, 1, n, dtype=F64)
+    Cv = torch.linspace(0.5, 1.5, n, dtype=F64)
+    u = torch.full((1, d, length), u_v, dtype=F64)
+    dt = torch.full((1, d, length), dt_v, dtype=F64)
+    B = Bv.view(1, 1, n, 1).expand(1, 1, n, length)
+    C = Cv.view(1, 1, n, 1).expand(1, 1, n, length)
+    y = oracle.selective_scan(u, dt, A, B, C)
+    a = torch.exp(dt_v * A)  # (d, n)
+    t = torch.arange(length, dtype=F64)
+    x = dt_v * u_v * Bv[:, None] * (1 - a[..., None] ** (t + 1)) / (1 - a[..., None])  # (d, n, L)
+    expect = (x * Cv[None, :, None]).sum(1)
+    assert max_rel(y[0], expect) < 1e-13
+
+
+def test_selscan_zero_B_leaves_skip_and_gate():
+    inputs, _ = mamba1_c1()
+    inputs = {k: v.double() for k, v in inputs.items()}
+    inputs["B"] = torch.zeros_like(inputs["B"])
+    y = oracle.selective_scan(**inputs, delta_softplus=True)
+    z = inputs["z"]
+    expect = inputs["u"] * inputs["D"][:, None] * z * torch.sigmoid(z)
+    assert max_rel(y, expect) < 1e-15
+
+
+def test_selscan_pre_ops_order():
+    # delta_bias is added before the softplus, not after.
+    inputs, _ = mamba1_c1()
+    inputs = {k: v.double() for k, v in inputs.items()}
+    fused = oracle.selective_scan(**inputs, delta_softplus=True)
+    manual = dict(inputs)
+    manual["dt"] = torch.nn.functional.softplus(inputs["dt"] + inputs["delta_bias"][:, None])
+    manual["delta_bias"] = None
+    assert max_rel(fused, oracle.selective_scan(**manual)) < 1e-15
+
+
+def test_selscan_finite_differences():
+    g = _g(5)
+    b, d, length, n, grp = 1, 4, 6, 3, 2
+    tensors = dict(
+        u=torch.randn(b, d, length, generator=g, dtype=F64),
+        dt=torch.randn(b, d, length, generator=g, dtype=F64),
+        A=-torch.rand(d, n, generator=g, dtype=F64) - 0.1,
+        B=torch.randn(b, grp, n, length, generator=g, dtype=F64),
+        C=torch.randn(b, grp, n, length, generator=g, dtype=F64),
+        D=torch.randn(d, generator=g, dtype=F64),
+        z=torch.randn(b, d, length, generator=g, dtype=F64),
+        delta_bias=0.1 * torch.randn(d, generator=g, dtype=F64),
+    )
+    names = list(tensors)
+    leaves = [tensors[k].clone().requires_grad_(True) for k in names]
+
+    def fn(*args):
+        return oracle.selective_scan(*args[:5], D=args[5], z=args[6], delta_bias=args[7],
+                                     delta_softplus=True)
+    assert torch.autograd.gradcheck(fn, leaves, eps=1e-6, atol=1e-7, rtol=1e-6)
+
+
+# ----------------------------------------------------------------------- Mamba-2 SSD
+
+SSD_SHAPES = [
+    (2, 13, 4, 6, 2, 5),  # length not a multiple of the chunk size
+    (1, 16, 4, 4, 1, 4),  # one group for all heads
+    (2, 9, 4, 3, 4, 3),   # one group per head
+    (1, 5, 2, 2, 1, 3),   # chunk larger than the sequence
+]
+
+
+def _ssd_inputs(shape, seed, d_per_head=False):
+    p = ssd_problem(*shape, seed=seed, act=F64, d_per_head=d_per_head)
+    return {k: (v.double() if v is not None else None) for k, v in p.items()}
+
+
+@pytest.mark.parametrize("shape", SSD_SHAPES)
+@pytest.mark.parametrize("chunk", [1, 4, 16, 64])
+def test_ssd_composition_matches_recurrence(shape, chunk):
+    p = _ssd_inputs(shape, seed=sum(shape) + chunk)
+    y_ref, s_ref = oracle.mamba2_chunk_scan_recurrence(**p, dt_softplus=True)
+    y, s = oracle.mamba2_chunk_scan_composition(chunk_size=chunk, **p, dt_softplus=True)
+    assert max_rel(y, y_ref) < 1e-12
+    assert max_rel(s, s_ref) < 1e-12
+
+
+def test_ssd_minimal_matches_recurrence():
+    g = _g(11)
+    b, length, h, pdim, grp, n = 1, 16, 2, 3, 1, 4
+    x = torch.randn(b, length, h, pdim, generator=g, dtype=F64)
+    dt = torch.nn.functional.softplus(torch.randn(b, length, h, generator=g, dtype=F64) - 2)
+    A = -torch.exp(torch.rand(h, generator=g, dtype=F64))
+    B = torch.randn(b, length, grp, n, generator=g, dtype=F64)
+    C = torch.randn(b, length, grp, n, generator=g, dtype=F64)
+    init = 0.1 * torch.randn(b, h, pdim, n, generator=g, dtype=F64)
+    y_min, s_min = oracle.ssd_minimal_discrete(x * dt[..., None], A * dt, B, C, 4, init[:, None])
+    y_ref, s_ref = oracle.mamba2_chunk_scan_recurrence(x, dt, A, B, C, initial_states=init)
+    assert max_rel(y_min, y_ref) < 1e-13
+    assert max_rel(s_min, s_ref) < 1e-13
+
+
+def test_ssd_equals_mamba1_with_expanded_channels():
+    # One SSD head is Mamba-1 over P channels with A broadcast over N and dt over P.
+    b, length, h, pdim, grp, n = 2, 11, 4, 3, 2, 5
+    p = _ssd_inputs((b, length, h, pdim, grp, n), seed=12)
+    y2, _ = oracle.mamba2_chunk_scan_recurrence(p["x"], p["dt"], p["A"], p["B"], p["C"],
+                                                D=p["D"], z=p["z"], dt_bias=p["dt_bias"],
+                                                dt_softplus=True)
+    u = p["x"].permute(0, 2, 3, 1).reshape(b, h * pdim, length)
+    dt = p["dt"].permute(0, 2, 1).repeat_interleave(pdim, dim=1)
+    A = p["A"].repeat_interleave(pdim)[:, None].expand(h * pdim, n)
+    B = p["B"].permute(0, 2, 3, 1)
+    C = p["C"].permute(0, 2, 3, 1)
+    z = p["z"].permute(0, 2, 3, 1).reshape(b, h * pdim, length)
+    y1 = oracle.selective_scan(u, dt, A, B, C, D=p["D"].repeat_interleave(pdim), z=z,
+                               delta_bias=p["dt_bias"].repeat_interleave(pdim),
+                               delta_softplus=True)
+    assert max_rel(y1.reshape(b, h, pdim, length).permute(0, 3, 1, 2), y2) < 1e-13
+
+
+def test_ssd_initial_state_linearity():
+    p = _ssd_inputs((2, 9, 4, 3, 2, 5), seed=13)
+    base = dict(x=p["x"], dt=p["dt"], A=p["A"], B=p["B"], C=p["C"], dt_bias=p["dt_bias"],
+                dt_softplus=True)
+    y_full, s_full = oracle.mamba2_chunk_scan_recurrence(**base, initial_states=p["initial_states"])
+    y_zero, s_zero = oracle.mamba2_chunk_scan_recurrence(**base)
+    base["x"] = torch.zeros_like(p["x"])
+    y_init, s_init = oracle.mamba2_chunk_scan_recurrence(**base, initial_states=p["initial_states"])
+    assert max_rel(y_full, y_zero + y_init) < 1e-13
+    assert max_rel(s_full, s_zero + s_init) < 1e-13
+
+
+def test_ssd_initial_state_spellings():
+    p = _ssd_inputs((2, 13, 4, 6, 2, 5), seed=14)
+    init = p.pop("initial_states")
+    y_a, s_a = oracle.mamba2_chunk_scan_composition(chunk_size=5, **p, initial_states=init)
+    y_b, s_b = oracle.mamba2_chunk_scan_composition(chunk_size=5, **p, initial_states=init.transpose(-1, -2))
+    y_c, s_c = oracle.mamba2_chunk_scan_composition(chunk_size=5, **p, initial_states=init[:, None])
+    assert torch.equal(y_a, y_b) and torch.equal(y_a, y_c) and torch.equal(s_a, s_c)
+    with pytest.raises(ValueError):
+        oracle.mamba2_chunk_scan_composition(chunk_size=5, **p, initial_states=torch.zeros(2, 4, 5, 5))
+
+
+def test_ssd_options_each_alone():
+    p = _ssd_inputs((2, 9, 4, 6, 2, 5), seed=15)
+    core = {k: p[k] for k in ("x", "dt", "A", "B", "C")}
+    dp = torch.randn(4, 6, generator=_g(3), dtype=F64)
+    for extra in ({}, {"D": p["D"]}, {"D": dp}, {"z": p["z"]}, {"dt_bias": p["dt_bias"]},
+                  {"dt_softplus": True}, {"initial_states": p["initial_states"]}):
+        y_ref, s_ref = oracle.mamba2_chunk_scan_recurrence(**core, **extra)
+        y, s = oracle.mamba2_chunk_scan_composition(chunk_size=4, **core, **extra)
+        assert max_rel(y, y_ref) < 1e-12 and max_rel(s, s_ref) < 1e-12, extra.keys()
+
+
+def test_ssd_finite_differences():
+    g = _g(16)
+    b, length, h, pdim, grp, n = 1, 6, 2, 2, 1, 3
+    leaves = [
+        torch.randn(b, length, h, pdim, generator=g, dtype=F64),
+        torch.randn(b, length, h, generator=g, dtype=F64),
+        -torch.exp(torch.rand(h, generator=g, dtype=F64)),
+        torch.randn(b, length, grp, n, generator=g, dtype=F64),
+        torch.randn(b, length, grp, n, generator=g, dtype=F64),
+        torch.randn(h, generator=g, dtype=F64),
+        torch.randn(b, length, h, pdim, generator=g, dtype=F64),
+        0.1 * torch.randn(h, generator=g, dtype=F64),
+        0.1 * torch.randn(b, h, pdim, n, generator=g, dtype=F64),
+    ]
+    leaves = [t.requires_grad_(True) for t in leaves]
+
+    def fn(x, dt, A, B, C, D, z, bias, init):
+        return oracle.mamba2_chunk_scan_recurrence(x, dt, A, B, C, D=D, z=z, dt_bias=bias,
+                                                   dt_softplus=True, initial_states=init)
+    assert torch.autograd.gradcheck(fn, leaves, eps=1e-6, atol=1e-7, rtol=1e-6)
+
+
+def test_ssd_composition_gradients_match_recurrence():
+    p = _ssd_inputs((2, 10, 4, 3, 2, 5), seed=17)
+    keys = ["x", "dt", "A", "B", "C", "D", "z", "dt_bias", "initial_states"]
+    g = _g(18)
+    wy = torch.randn(2, 10, 4, 3, generator=g, dtype=F64)
+    ws = torch.randn(2, 4, 3, 5, generator=g, dtype=F64)
+
+    def grads(fn, **kw):
+        leaves = {k: p[k].clone().requires_grad_(True) for k in keys}
+        y, s = fn(**leaves, dt_softplus=True, **kw)
+        ((y * wy).sum() + (s * ws).sum()).backward()
+        return [leaves[k].grad for k in keys]
+
+    ref = grads(oracle.mamba2_chunk_scan_recurrence)
+    comp = grads(oracle.mamba2_chunk_scan_composition, chunk_size=4)
+    for name, a, e in zip(keys, comp, ref):
+        assert max_rel(a, e) < 1e-11, name
+
+
+# ----------------------------------------------------------------------- decode
+
+
+def test_decode_step_elementwise_closed_form():
+    p = decode_problem(2, 4, 3, 5, 2, seed=19, act=F64, state_dtype=F64)
+    p = {k: v.double() for k, v in p.items()}
+    y, s = oracle.mamba2_state_update(**p, dt_softplus=True)
+    b, h, pd, n = p["state"].shape
+    for bi in range(b):
+        for hi in range(h):
+            g = hi // (h // p["B"].shape[1])
+            delta = torch.nn.functional.softplus(p["dt"][bi, hi] + p["dt_bias"][hi])
+            a = torch.exp(p["A"][hi] * delta)
+            for pi in range(pd):
+                xv = p["x"][bi, hi, pi]
+                new = a * p["state"][bi, hi, pi] + delta * xv * p["B"][bi, g]
+                assert torch.allclose(s[bi, hi, pi], new, rtol=0, atol=1e-14)
+                out = (new * p["C"][bi, g]).sum() + p["D"][hi] * xv
+                out = out * p["z"][bi, hi, pi] * torch.sigmoid(p["z"][bi, hi, pi])
+                assert abs(float(out - y[bi, hi, pi])) < 1e-13
+
+
+@pytest.mark.parametrize("dt_per_row", [False, True])
+def test_decode_equals_chunk_scan_of_length_one(dt_per_row):
+    p = decode_problem(2, 4, 3, 5, 2, seed=20, act=F64, state_dtype=F64, dt_per_row=dt_per_row)
+    y, s = oracle.mamba2_state_update(**p, dt_softplus=True)
+    dt = p["dt"] if not dt_per_row else p["dt"][..., 0]
+    if dt_per_row:  # the chunk scan has dt per head; use a per-head dt for both
+        p["dt"] = p["dt"][..., :1].expand_as(p["dt"]).contiguous()
+        y, s = oracle.mamba2_state_update(**p, dt_softplus=True)
+    y2, s2 = oracle.mamba2_chunk_scan_recurrence(
+        p["x"][:, None], dt[:, None], p["A"], p["B"][:, None], p["C"][:, None], D=p["D"],
+        z=p["z"][:, None], dt_bias=p["dt_bias"], dt_softplus=True, initial_states=p["state"])
+    assert max_rel(y, y2[:, 0]) < 1e-14
+    assert max_rel(s, s2) < 1e-14
+
+
+def test_decode_k_steps_equal_chunk_scan():
+    g = _g(21)
+    b, h, pdim, n, grp, k = 2, 4, 3, 5, 2, 7
+    prob = decode_problem(b, h, pdim, n, grp, seed=21, act=F64, state_dtype=F64)
+    xs = torch.randn(b, k, h, pdim, generator=g, dtype=F64)
+    dts = torch.randn(b, k, h, generator=g, dtype=F64)
+    Bs = torch.randn(b, k, grp, n, generator=g, dtype=F64)
+    Cs = torch.randn(b, k, grp, n, generator=g, dtype=F64)
+    zs = torch.randn(b, k, h, pdim, generator=g, dtype=F64)
+    state = prob["state"]
+    ys = []
+    for t in range(k):
+        y, state = oracle.mamba2_state_update(state, xs[:, t], dts[:, t], prob["A"], Bs[:, t], Cs[:, t],
+                                              D=prob["D"], z=zs[:, t], dt_bias=prob["dt_bias"],
+                                              dt_softplus=True)
+        ys.append(y)
+    y_c, s_c = oracle.mamba2_chunk_scan_composition(
+        xs, dts, prob["A"], Bs, Cs, chunk_size=3, D=prob["D"], z=zs, dt_bias=prob["dt_bias"],
+        dt_softplus=True, initial_states=prob["state"])
+    assert max_rel(torch.stack(ys, 1), y_c) < 1e-12
+    assert max_rel(state, s_c) < 1e-12
+
+
+def test_decode_finite_differences():
+    p = decode_problem(1, 2, 2, 3, 1, seed=22, act=F64, state_dtype=F64)
+    keys = ["state", "x", "dt", "A", "B", "C", "D", "z", "dt_bias"]
+    leaves = [p[k].double().clone().requires_grad_(True) for k in keys]
+
+    def fn(*args):
+        return oracle.mamba2_state_update(*args[:8], dt_bias=args[8], dt_softplus=True)
+    assert torch.autograd.gradcheck(fn, leaves, eps=1e-6, atol=1e-7, rtol=1e-6)

@@ -1,0 +1,189 @@
+"""Mamba-1 selective scan: HIP kernels against the float64 CPU oracle.
+
+Tolerances (north star): fp32 outputs <= 1e-5 max relative error (max abs error
+over the largest reference magnitude), bf16 outputs <= 2e-2, gradient norms
+<= 1e-4 relative (fp32), 2e-2 for bf16 inputs.
+"""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from cases import mamba1_c1, mamba1_layer, max_rel, norm_rel
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+NAMES = ("u", "dt", "A", "B", "C", "D", "z", "delta_bias")
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "mamba1_c1.npz")
+
+
+def _selective_scan():
+    from metal_kernelops import selective_scan
+    return selective_scan
+
+
+def _gpu(inputs, dy, softplus=True):
+    leaves = {k: (None if v is None else v.to(DEV).requires_grad_(True)) for k, v in inputs.items()}
+    out = _selective_scan()(**leaves, delta_softplus=softplus)
+    out.backward(dy.to(DEV))
+    torch.cuda.synchronize()
+    return out.detach(), {k: (None if v is None else v.grad) for k, v in leaves.items()}
+
+
+def _ref(inputs, dy, softplus=True):
+    leaves = {k: (None if v is None else v.double().requires_grad_(True)) for k, v in inputs.items()}
+    out = oracle.selective_scan(**leaves, delta_softplus=softplus)
+    out.backward(dy.double())
+    return out.detach(), {k: (None if v is None else v.grad) for k, v in leaves.items()}
+
+
+def _compare(inputs, dy, softplus, out_tol, grad_tol):
+    out, grads = _gpu(inputs, dy, softplus)
+    ref, rgrads = _ref(inputs, dy, softplus)
+    assert out.dtype == inputs["u"].dtype
+    err = max_rel(out, ref)
+    assert err <= out_tol, f"forward max rel {err:.3e}"
+    for name in NAMES:
+        if inputs.get(name) is None:
+            continue
+        assert grads[name] is not None and grads[name].dtype == inputs[name].dtype, name
+        e = norm_rel(grads[name], rgrads[name])
+        assert e <= grad_tol, f"grad {name}: norm rel {e:.3e}"
+
+
+def test_config1_fp32_forward_backward():
+    inputs, dy = mamba1_c1()
+    _compare(inputs, dy, True, 1e-5, 1e-4)
+
+
+def test_config1_matches_golden_fixture():
+    data = np.load(GOLDEN)
+    inputs = {k: torch.from_numpy(data["in_" + k]).float() for k in NAMES}
+    dy = torch.from_numpy(data["dy"]).float()
+    out, grads = _gpu(inputs, dy, True)
+    assert max_rel(out, torch.from_numpy(data["out"])) <= 1e-5
+    for k in NAMES:
+        assert norm_rel(grads[k], torch.from_numpy(data["grad_" + k])) <= 1e-4, k
+
+
+def _random_problem(batch, dim, length, dstate, groups, seed, act=torch.float32, d=True, z=True,
+                    bias=True):
+    g = torch.Generator().manual_seed(seed)
+    inputs = dict(
+        u=torch.randn(batch, dim, length, generator=g).to(act),
+        dt=torch.randn(batch, dim, length, generator=g),
+        A=-torch.rand(dim, dstate, generator=g) * 4 - 0.05,
+        B=torch.randn(batch, groups, dstate, length, generator=g).to(act),
+        C=torch.randn(batch, groups, dstate, length, generator=g).to(act),
+        D=torch.randn(dim, generator=g) if d else None,
+        z=torch.randn(batch, dim, length, generator=g).to(act) if z else None,
+        delta_bias=0.5 * torch.randn(dim, generator=g) - 1.0 if bias else None,
+    )
+    dy = torch.randn(batch, dim, length, generator=g).to(act)
+    return inputs, dy
+
+
+SHAPES = [
+    (2, 8, 64, 16, 2),      # config 1 geometry, lanes span groups (atomic dB/dC path)
+    (2, 128, 200, 16, 2),   # one 64-channel wavefront per group, ragged length
+    (1, 256, 300, 16, 1),   # four wavefronts per workgroup, several coarse chunks
+    (2, 64, 97, 5, 1),      # dstate padded to 16
+    (1, 128, 130, 32, 2),   # dstate 32
+    (3, 24, 77, 20, 3),     # dstate 20, ragged everything
+]
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_shapes_fp32(shape):
+    inputs, dy = _random_problem(*shape, seed=sum(shape))
+    _compare(inputs, dy, True, 1e-5, 1e-4)
+
+
+@pytest.mark.parametrize("opts", [dict(d=False), dict(z=False), dict(bias=False),
+                                  dict(d=False, z=False, bias=False)],
+                         ids=["noD", "noz", "nobias", "bare"])
+@pytest.mark.parametrize("softplus", [True, False])
+def test_options(opts, softplus):
+    inputs, dy = _random_problem(2, 128, 150, 16, 1, seed=7, **opts)
+    if not softplus:
+        inputs["dt"] = torch.rand(inputs["dt"].shape) * 0.3
+    _compare(inputs, dy, softplus, 1e-5, 1e-4)
+
+
+def test_bf16_activations():
+    inputs, dy = _random_problem(2, 256, 512, 16, 1, seed=9, act=torch.bfloat16)
+    _compare(inputs, dy, True, 2e-2, 2e-2)
+
+
+def test_bf16_delta_and_fp16():
+    inputs, dy = _random_problem(1, 128, 200, 16, 1, seed=10, act=torch.float16)
+    _compare(inputs, dy, True, 2e-3 * 10, 2e-2)
+    inputs, dy = _random_problem(1, 128, 200, 16, 1, seed=11, act=torch.bfloat16)
+    inputs["dt"] = inputs["dt"].bfloat16()
+    _compare(inputs, dy, True, 2e-2, 2e-2)
+
+
+def test_deterministic_backward():
+    inputs, dy = _random_problem(2, 256, 300, 16, 1, seed=12)
+    runs = [_gpu(inputs, dy, True) for _ in range(2)]
+    assert torch.equal(runs[0][0], runs[1][0])
+    for k in NAMES:
+        assert torch.equal(runs[0][1][k], runs[1][1][k]), k
+
+
+def test_config3_full_size_channel_subset():
+    # Config 3 at full size: channels are independent in the forward, and with the
+    # upstream gradient zero outside a subset the dB/dC sums only see that subset,
+    # so the oracle only needs the subset.
+    inputs, dy = mamba1_layer(4, 5120, 4096, seed=0)
+    sel = torch.arange(0, 5120, 80)  # 64 channels spread over the width
+    mask = torch.zeros(5120, dtype=torch.bool)
+    mask[sel] = True
+    dy = dy * mask[None, :, None].to(dy.dtype)
+    out, grads = _gpu(inputs, dy, True)
+    sub = {k: (v[:, sel] if k in ("u", "dt", "z") else v[sel] if k in ("A", "D", "delta_bias") else v)
+           for k, v in inputs.items()}
+    ref, rgrads = _ref(sub, dy[:, sel], True)
+    assert max_rel(out[:, sel], ref) <= 2e-2
+    for k in ("u", "dt", "z"):
+        assert norm_rel(grads[k][:, sel], rgrads[k]) <= 2e-2, k
+    for k in ("B", "C"):
+        assert norm_rel(grads[k], rgrads[k]) <= 2e-2, k
+    for k in ("A", "D", "delta_bias"):
+        assert norm_rel(grads[k][sel], rgrads[k]) <= 1e-3, k
+    assert torch.isfinite(out).all()
+
+
+def test_empty_inputs():
+    ss = _selective_scan()
+    for shape in ((2, 8, 0), (0, 8, 16)):
+        b, d, length = shape
+        u = torch.zeros(b, d, length, device=DEV, requires_grad=True)
+        A = -torch.ones(d, 4, device=DEV, requires_grad=True)
+        B = torch.zeros(b, 2, 4, length, device=DEV, requires_grad=True)
+        out = ss(u, torch.zeros_like(u), A, B, B.detach().clone(), D=torch.ones(d, device=DEV))
+        assert out.shape == shape
+        out.sum().backward()
+        assert torch.equal(A.grad, torch.zeros_like(A))
+
+
+def test_errors():
+    from metal_kernelops import scan_mps
+    ss = _selective_scan()
+    inputs, _ = mamba1_c1()
+    cpu = [inputs[k] for k in ("u", "dt", "A", "B", "C")]
+    with pytest.raises(ValueError):
+        ss(*cpu)
+    gpu = [t.to(DEV) for t in cpu]
+    with pytest.raises(ValueError):
+        ss(gpu[0], gpu[1], gpu[2], gpu[3][:, :1].repeat(1, 3, 1, 1), gpu[4][:, :1].repeat(1, 3, 1, 1))
+    with pytest.raises(ValueError):
+        ss(gpu[0], gpu[1], torch.zeros(8, 40, device=DEV), gpu[3], gpu[4])
+    with pytest.raises(ValueError):
+        scan_mps(gpu[0].transpose(0, 1).contiguous().transpose(0, 1), *gpu[1:])
+    y = scan_mps(*gpu)
+    ref = oracle.selective_scan(*cpu)
+    assert max_rel(y, ref) <= 1e-5
