@@ -47,6 +47,15 @@ const char* mko_last_error(void);
 size_t mko_sizeof_selscan_params(void);
 size_t mko_sizeof_state_update_params(void);
 
+/* Kernel timing (observability).  While enabled, every kernel the library
+ * launches is bracketed by HIP events on its launch stream; the per-kernel totals
+ * are resolved (synchronising on those events) when read.  No reference
+ * counterpart: the reference times whole calls with wall clocks. */
+int mko_profile_enable(int on);   /* returns the previous setting */
+void mko_profile_reset(void);
+int mko_profile_count(void);      /* number of distinct kernels timed */
+int mko_profile_entry(int index, char* name, size_t name_len, double* total_ms, int64_t* launches);
+
 /* ======================================================================== */
 /* Mamba-1 selective scan                                                     */
 /* ======================================================================== */

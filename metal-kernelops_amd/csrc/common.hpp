@@ -50,19 +50,39 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 
 constexpr float kLog2e = 1.4426950408889634f;
 
-// torch's softplus rule (beta 1, threshold 20) in float32.  log1p(exp(v)) is
-// evaluated with the library routines so a step of 1e-3 keeps its relative
-// accuracy.
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+
+// exp(v) on the transcendental unit; relative error a few ulp for |v| <= 80.
+__device__ __forceinline__ float fast_exp(float v) { return fast_exp2(v * kLog2e); }
+
+// torch's softplus rule (beta 1, threshold 20): v above 20, else log1p(exp(v)).
+// log1p(e) is Goldberg's log(u) * e / (u - 1) with u = fl(1 + e), which keeps the
+// relative accuracy of small steps (v = -7 gives 1e-3) to a few ulp using the
+// hardware log2/rcp.
 __device__ __forceinline__ float softplus(float v) {
-  return v > 20.0f ? v : log1pf(expf(v));
+  const float e = fast_exp(v);
+  const float u = 1.0f + e;
+  const float r = (u == 1.0f) ? e : fast_log2(u) * kLn2 * (e * fast_rcp(u - 1.0f));
+  return v > 20.0f ? v : r;
 }
+
+__device__ __forceinline__ float sigmoid(float v) { return fast_rcp(1.0f + fast_exp(-v)); }
 
 // d softplus / dv with the same threshold: sigmoid(v), or 1 above 20.
-__device__ __forceinline__ float softplus_grad(float v) {
-  return v > 20.0f ? 1.0f : 1.0f / (1.0f + expf(-v));
-}
+__device__ __forceinline__ float softplus_grad(float v) { return v > 20.0f ? 1.0f : sigmoid(v); }
 
-__device__ __forceinline__ float sigmoid(float v) { return 1.0f / (1.0f + expf(-v)); }
+// Pointer into the constant address space: loads through it with a wave-uniform
+// address compile to scalar (SMEM) loads.
+typedef const float __attribute__((address_space(4)))* cfptr;
+__device__ __forceinline__ cfptr as_const(const float* p) { return (cfptr)(p); }
+
+// s_waitcnt lgkmcnt(0) with vmcnt/expcnt left alone: retires outstanding scalar
+// and LDS loads.  Issued before a prefetch, it keeps the compiler's own wait for
+// the data in use from also waiting on the prefetch that follows.
+__device__ __forceinline__ void wait_lgkm() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
 // Wave-uniform copy of a value (makes the compiler keep it in an SGPR).
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
@@ -74,7 +94,29 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Records HIP events around the launches in its scope when kernel timing is on
+// (mko_profile_enable); a no-op otherwise.
+class ProfScope {
+ public:
+  ProfScope(const char* name, hipStream_t stream);
+  ~ProfScope();
+  ProfScope(const ProfScope&) = delete;
+  ProfScope& operator=(const ProfScope&) = delete;
+
+ private:
+  hipStream_t stream_;
+  hipEvent_t start_ = nullptr, stop_ = nullptr;
+  int slot_ = -1;
+};
+
 }  // namespace mko
+
+// Launch statement(s) timed under `name` when kernel timing is enabled.
+#define MKO_TIMED(name, stream, ...)        \
+  do {                                      \
+    ::mko::ProfScope mko_scope_(name, stream); \
+    __VA_ARGS__;                            \
+  } while (0)
 
 // Error reporting for the C ABI (defined in abi.hip).
 void mko_set_error(const char* fmt, ...);

@@ -153,16 +153,105 @@ __global__ void __launch_bounds__(256) prep_state_major(Geo g, int ns, const voi
 
 // ---------------------------------------------------------------- forward
 
-// LDS staging used by the state-inner kernels: per wavefront [3][HS][64] floats.
-constexpr int kStage = 3 * HS * kWave;
+// One step's B_t (and C_t) for a lane: scalar loads when the wavefront shares
+// (batch, group), vector loads otherwise.  WITH_B / WITH_C select the rows.
+template <int NS, bool UNI, bool WITH_B, bool WITH_C>
+struct StepBC {
+  float b[NS], c[NS];
+  __device__ __forceinline__ void load(const float* __restrict__ bt, const float* __restrict__ ct,
+                                       int64_t off) {
+    if (UNI) {
+      if (WITH_B) {
+        const cfptr pb = as_const(bt + off);
+#pragma unroll
+        for (int n = 0; n < NS; ++n) b[n] = pb[n];
+      }
+      if (WITH_C) {
+        const cfptr pc = as_const(ct + off);
+#pragma unroll
+        for (int n = 0; n < NS; ++n) c[n] = pc[n];
+      }
+    } else {
+      if (WITH_B) {
+        const float4* qb = reinterpret_cast<const float4*>(bt + off);
+#pragma unroll
+        for (int v = 0; v < NS / 4; ++v) {
+          const float4 w = qb[v];
+          b[4 * v] = w.x; b[4 * v + 1] = w.y; b[4 * v + 2] = w.z; b[4 * v + 3] = w.w;
+        }
+      }
+      if (WITH_C) {
+        const float4* qc = reinterpret_cast<const float4*>(ct + off);
+#pragma unroll
+        for (int v = 0; v < NS / 4; ++v) {
+          const float4 w = qc[v];
+          c[4 * v] = w.x; c[4 * v + 1] = w.y; c[4 * v + 2] = w.z; c[4 * v + 3] = w.w;
+        }
+      }
+    }
+  }
+};
+
+// One state-inner step: x <- exp(A del) x + du B; returns <C, x> when WITH_Y.
+template <int NS, bool WITH_Y>
+__device__ __forceinline__ float advance(const float (&A2)[NS], float del, float du, const float (&b)[NS],
+                                         const float (&c)[NS], float (&x)[NS]) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int n = 0; n < NS; ++n) {
+    x[n] = fmaf(fast_exp2(A2[n] * del), x[n], du * b[n]);
+    if (WITH_Y) acc = fmaf(c[n], x[n], acc);
+  }
+  return acc;
+}
+
+// Advances the states over the first nv steps of a block starting at t0 (per-step
+// del/du in registers, indexed by the wave-uniform step).  Two B/C buffers
+// alternate: each half-iteration retires the outstanding loads, requests the
+// next step's B/C, then computes the current step, so a load has a whole step of
+// work to arrive.  With WITH_Y, y[i] = <C_t, x_t>.
+template <int NS, bool UNI, bool WITH_Y>
+__device__ __forceinline__ void forward_block(const float* __restrict__ bt, const float* __restrict__ ct,
+                                              int64_t row0, int t0, int nv, const float (&del)[HS],
+                                              const float (&du)[HS], const float (&A2)[NS], float (&x)[NS],
+                                              float (&y)[HS]) {
+  StepBC<NS, UNI, true, WITH_Y> e0, e1;
+  e0.load(bt, ct, (row0 + t0) * NS);
+  for (int i = 0; i < nv; i += 2) {
+    const bool two = i + 1 < nv;
+    wait_lgkm();
+    if (two) e1.load(bt, ct, (row0 + t0 + i + 1) * NS);
+    float acc = advance<NS, WITH_Y>(A2, del[i], du[i], e0.b, e0.c, x);
+    if (WITH_Y) y[i] = acc;
+    if (two) {
+      wait_lgkm();
+      if (i + 2 < nv) e0.load(bt, ct, (row0 + t0 + i + 2) * NS);
+      acc = advance<NS, WITH_Y>(A2, del[i + 1], du[i + 1], e1.b, e1.c, x);
+      if (WITH_Y) y[i + 1] = acc;
+    }
+  }
+}
+
+// Per-step inputs of one block: del = step size (0 past the end), du = del * u.
+// Returns the sum of the steps.
+__device__ __forceinline__ float load_steps(const Geo& g, const Ptrs& p, int64_t off, int nv, float bias,
+                                            float (&del)[HS], float (&du)[HS]) {
+  float uu[HS];
+  load_run<HS>(p.delta, g.d_dtype, off, nv, g.vec, del);
+  load_run<HS>(p.u, g.u_dtype, off, nv, g.vec, uu);
+  float sd = 0.0f;
+#pragma unroll
+  for (int i = 0; i < HS; ++i) {
+    del[i] = i < nv ? step_of(g, del[i], bias) : 0.0f;
+    du[i] = del[i] * uu[i];
+    sd += del[i];
+  }
+  return sd;
+}
 
 template <int NS, bool UNI>
 __global__ void __launch_bounds__(256) fwd_summary(Geo g, Ptrs p) {
-  __shared__ float stage_all[4 * kStage];
   const LaneInfo li = lane_info(g, UNI);
-  const int lane = threadIdx.x & 63;
-  float* st_d = stage_all + uniform(static_cast<int>(threadIdx.x >> 6)) * kStage;
-  float* st_u = st_d + HS * kWave;
   const int N = static_cast<int>(g.dstate);
   const int c = blockIdx.y;
   const int t_begin = c * g.lc;
@@ -171,32 +260,16 @@ __global__ void __launch_bounds__(256) fwd_summary(Geo g, Ptrs p) {
 #pragma unroll
   for (int n = 0; n < NS; ++n) A2[n] = n < N ? p.A[li.d * N + n] * kLog2e : 0.0f;
   const float bias = p.bias ? p.bias[li.d] : 0.0f;
-  float x[NS];
+  float x[NS], unused[HS];
 #pragma unroll
   for (int n = 0; n < NS; ++n) x[n] = 0.0f;
   float sd = 0.0f;
   const int64_t rbase = li.row * g.length;
   for (int t0 = t_begin; t0 < t_end; t0 += HS) {
     const int nv = min(HS, t_end - t0);
-    float dl[HS], uu[HS];
-    load_run<HS>(p.delta, g.d_dtype, rbase + t0, nv, g.vec, dl);
-    load_run<HS>(p.u, g.u_dtype, rbase + t0, nv, g.vec, uu);
-#pragma unroll
-    for (int i = 0; i < HS; ++i) {
-      const float del = i < nv ? step_of(g, dl[i], bias) : 0.0f;
-      sd += del;
-      st_d[i * kWave + lane] = del;
-      st_u[i * kWave + lane] = del * uu[i];
-    }
-    wave_lds_sync();
-    for (int i = 0; i < nv; ++i) {
-      const float del = st_d[i * kWave + lane];
-      const float du = st_u[i * kWave + lane];
-      const float* bp = p.bt + (li.bg * g.length + t0 + i) * NS;
-#pragma unroll
-      for (int n = 0; n < NS; ++n) x[n] = fmaf(fast_exp2(A2[n] * del), x[n], du * bp[n]);
-    }
-    wave_lds_sync();
+    float del[HS], du[HS];
+    sd += load_steps(g, p, rbase + t0, nv, bias, del, du);
+    forward_block<NS, UNI, false>(p.bt, nullptr, li.bg * g.length, t0, nv, del, du, A2, x, unused);
   }
   if (li.active) {
     const int64_t o = (li.row * g.nchunks + c) * N;
@@ -238,12 +311,7 @@ __global__ void __launch_bounds__(256) chain(Geo g, const float* __restrict__ A,
 
 template <int NS, bool UNI>
 __global__ void __launch_bounds__(256) fwd_replay(Geo g, Ptrs p) {
-  __shared__ float stage_all[4 * kStage];
   const LaneInfo li = lane_info(g, UNI);
-  const int lane = threadIdx.x & 63;
-  float* st_d = stage_all + uniform(static_cast<int>(threadIdx.x >> 6)) * kStage;
-  float* st_u = st_d + HS * kWave;
-  float* st_y = st_u + HS * kWave;
   const int N = static_cast<int>(g.dstate);
   const int c = blockIdx.y;
   const int t_begin = c * g.lc;
@@ -266,36 +334,13 @@ __global__ void __launch_bounds__(256) fwd_replay(Geo g, Ptrs p) {
         if (n < N) srow[(t0 / CK) * N + n] = x[n];
     }
     const int nv = min(HS, t_end - t0);
+    float del[HS], du[HS], y[HS];
+    load_steps(g, p, rbase + t0, nv, bias, del, du);
+    forward_block<NS, UNI, true>(p.bt, p.ct, li.bg * g.length, t0, nv, del, du, A2, x, y);
     float uu[HS];
-    {
-      float dl[HS];
-      load_run<HS>(p.delta, g.d_dtype, rbase + t0, nv, g.vec, dl);
-      load_run<HS>(p.u, g.u_dtype, rbase + t0, nv, g.vec, uu);
+    load_run<HS>(p.u, g.u_dtype, rbase + t0, nv, g.vec, uu);
 #pragma unroll
-      for (int i = 0; i < HS; ++i) {
-        const float del = i < nv ? step_of(g, dl[i], bias) : 0.0f;
-        st_d[i * kWave + lane] = del;
-        st_u[i * kWave + lane] = del * uu[i];
-      }
-    }
-    wave_lds_sync();
-    for (int i = 0; i < nv; ++i) {
-      const float del = st_d[i * kWave + lane];
-      const float du = st_u[i * kWave + lane];
-      const float* bp = p.bt + (li.bg * g.length + t0 + i) * NS;
-      const float* cp = p.ct + (li.bg * g.length + t0 + i) * NS;
-      float acc = 0.0f;
-#pragma unroll
-      for (int n = 0; n < NS; ++n) {
-        x[n] = fmaf(fast_exp2(A2[n] * del), x[n], du * bp[n]);
-        acc = fmaf(cp[n], x[n], acc);
-      }
-      st_y[i * kWave + lane] = acc;
-    }
-    wave_lds_sync();
-    float y[HS];
-#pragma unroll
-    for (int i = 0; i < HS; ++i) y[i] = fmaf(Dd, uu[i], st_y[i * kWave + lane]);
+    for (int i = 0; i < HS; ++i) y[i] = fmaf(Dd, uu[i], y[i]);
     if (has_z) {
       float zz[HS];
       load_run<HS>(p.z, g.u_dtype, rbase + t0, nv, g.vec, zz);
@@ -310,11 +355,7 @@ __global__ void __launch_bounds__(256) fwd_replay(Geo g, Ptrs p) {
 
 template <int NS, bool UNI>
 __global__ void __launch_bounds__(256) bwd_summary(Geo g, Ptrs p) {
-  __shared__ float stage_all[4 * kStage];
   const LaneInfo li = lane_info(g, UNI);
-  const int lane = threadIdx.x & 63;
-  float* st_d = stage_all + uniform(static_cast<int>(threadIdx.x >> 6)) * kStage;
-  float* st_g = st_d + HS * kWave;
   const int N = static_cast<int>(g.dstate);
   const int c = blockIdx.y + 1;  // chunk 0's adjoint summary is never needed
   const int t_begin = c * g.lc;
@@ -329,37 +370,44 @@ __global__ void __launch_bounds__(256) bwd_summary(Geo g, Ptrs p) {
   for (int n = 0; n < NS; ++n) hc[n] = 0.0f;
   float sd = 0.0f;
   const int64_t rbase = li.row * g.length;
+  const int64_t row0 = li.bg * g.length;
   const int nblk = (t_end - t_begin + HS - 1) / HS;
   for (int blk = nblk - 1; blk >= 0; --blk) {
     const int t0 = t_begin + blk * HS;
     const int nv = min(HS, t_end - t0);
-    {
-      float dl[HS], gy[HS];
-      load_run<HS>(p.delta, g.d_dtype, rbase + t0, nv, g.vec, dl);
-      load_run<HS>(p.dout, g.u_dtype, rbase + t0, nv, g.vec, gy);
-      if (has_z) {
-        float zz[HS];
-        load_run<HS>(p.z, g.u_dtype, rbase + t0, nv, g.vec, zz);
+    float del[HS], gy[HS];
+    load_run<HS>(p.delta, g.d_dtype, rbase + t0, nv, g.vec, del);
+    load_run<HS>(p.dout, g.u_dtype, rbase + t0, nv, g.vec, gy);
+    if (has_z) {
+      float zz[HS];
+      load_run<HS>(p.z, g.u_dtype, rbase + t0, nv, g.vec, zz);
 #pragma unroll
-        for (int i = 0; i < HS; ++i) gy[i] *= zz[i] * sigmoid(zz[i]);
+      for (int i = 0; i < HS; ++i) gy[i] *= zz[i] * sigmoid(zz[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < HS; ++i) {
+      del[i] = i < nv ? step_of(g, del[i], bias) : 0.0f;
+      sd += del[i];
+    }
+    StepBC<NS, UNI, false, true> e0, e1;
+    e0.load(nullptr, p.ct, (row0 + t0 + nv - 1) * NS);
+    for (int i = nv - 1; i >= 0; i -= 2) {
+      const bool two = i > 0;
+      wait_lgkm();
+      if (two) e1.load(nullptr, p.ct, (row0 + t0 + i - 1) * NS);
+      {
+        const float d = del[i], gv = gy[i];
+#pragma unroll
+        for (int n = 0; n < NS; ++n) hc[n] = fast_exp2(A2[n] * d) * fmaf(gv, e0.c[n], hc[n]);
       }
+      if (two) {
+        wait_lgkm();
+        if (i > 1) e0.load(nullptr, p.ct, (row0 + t0 + i - 2) * NS);
+        const float d = del[i - 1], gv = gy[i - 1];
 #pragma unroll
-      for (int i = 0; i < HS; ++i) {
-        const float del = i < nv ? step_of(g, dl[i], bias) : 0.0f;
-        sd += del;
-        st_d[i * kWave + lane] = del;
-        st_g[i * kWave + lane] = gy[i];
+        for (int n = 0; n < NS; ++n) hc[n] = fast_exp2(A2[n] * d) * fmaf(gv, e1.c[n], hc[n]);
       }
     }
-    wave_lds_sync();
-    for (int i = nv - 1; i >= 0; --i) {
-      const float del = st_d[i * kWave + lane];
-      const float gy = st_g[i * kWave + lane];
-      const float* cp = p.ct + (li.bg * g.length + t0 + i) * NS;
-#pragma unroll
-      for (int n = 0; n < NS; ++n) hc[n] = fast_exp2(A2[n] * del) * fmaf(gy, cp[n], hc[n]);
-    }
-    wave_lds_sync();
   }
   if (li.active) {
     const int64_t o = (li.row * g.nchunks + c) * N;
@@ -370,22 +418,53 @@ __global__ void __launch_bounds__(256) bwd_summary(Geo g, Ptrs p) {
   }
 }
 
-// bwd_main LDS (floats): per wavefront a staging area [2][HS][64] and a
-// transposition buffer [64][2*HS+1]; per workgroup the dB/dC sums [NS][2*HS].
+// bwd_main LDS (floats): per wavefront a transposition buffer [64][2*HS+1] and
+// its dB/dC half-column sums [NS][64]; per workgroup the quarter's B and C rows
+// [2][NS][HS] when the workgroup shares (batch, group).
 constexpr int kTransPitch = 2 * HS + 1;
-constexpr int kMainWave = 2 * HS * kWave + kWave * kTransPitch;
+
+template <int NS>
+struct MainLds {
+  static constexpr int kWaveFloats = kWave * kTransPitch + NS * kWave;
+  static constexpr int kRows = 2 * NS * HS;
+};
+
+// One state's B and C over the HS steps of a quarter (state-major rows).
+template <bool UNI>
+__device__ __forceinline__ void load_state_rows(const float* __restrict__ bn, const float* __restrict__ cn,
+                                                int64_t off, float (&bv)[HS], float (&cv)[HS]) {
+  if (UNI) {
+    const cfptr pb = as_const(bn + off);
+    const cfptr pc = as_const(cn + off);
+#pragma unroll
+    for (int i = 0; i < HS; ++i) {
+      bv[i] = pb[i];
+      cv[i] = pc[i];
+    }
+  } else {
+    const float4* qb = reinterpret_cast<const float4*>(bn + off);
+    const float4* qc = reinterpret_cast<const float4*>(cn + off);
+#pragma unroll
+    for (int v = 0; v < HS / 4; ++v) {
+      const float4 wb = qb[v], wc = qc[v];
+      bv[4 * v] = wb.x; bv[4 * v + 1] = wb.y; bv[4 * v + 2] = wb.z; bv[4 * v + 3] = wb.w;
+      cv[4 * v] = wc.x; cv[4 * v + 1] = wc.y; cv[4 * v + 2] = wc.z; cv[4 * v + 3] = wc.w;
+    }
+  }
+}
 
 template <int NS, bool UNI>
 __global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
-  __shared__ float lds[4 * kMainWave + NS * 2 * HS];
+  __shared__ float lds[4 * MainLds<NS>::kWaveFloats + MainLds<NS>::kRows];
   const LaneInfo li = lane_info(g, UNI);
   const int N = static_cast<int>(g.dstate);
   const int lane = threadIdx.x & 63;
   const int wave = uniform(static_cast<int>(threadIdx.x >> 6));
-  float* st_d = lds + wave * kMainWave;  // [HS][64]
-  float* st_u = st_d + HS * kWave;       // [HS][64]
-  float* trans = st_u + HS * kWave;      // [64][kTransPitch]
-  float* acc = lds + 4 * kMainWave;      // [NS][2*HS]
+  float* trans = lds + wave * kWave * kTransPitch;                // [64][kTransPitch]
+  float* acc_all = lds + 4 * kWave * kTransPitch;                 // [wave][NS][64]
+  float* acc = acc_all + wave * NS * kWave;
+  float* rows_b = lds + 4 * MainLds<NS>::kWaveFloats;  // [NS][HS]
+  float* rows_c = rows_b + NS * HS;                    // [NS][HS]
 
   const int c = blockIdx.y;
   const int t_begin = c * g.lc;
@@ -409,19 +488,17 @@ __global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
       dap[n * R + li.row] = 0.0f;
     }
   }
-  for (int i = threadIdx.x; i < NS * 2 * HS; i += blockDim.x) acc[i] = 0.0f;
-  __syncthreads();
 
   int64_t cb = 0;
   if (UNI) {
     const int64_t r0 = static_cast<int64_t>(blockIdx.x) * g.wpg * kWave;
     cb = ((r0 % g.dim) % g.dg) / (static_cast<int64_t>(g.wpg) * kWave);
   }
-  const bool vec_bc = (g.length % 4) == 0;
   float A2[NS];
 #pragma unroll
   for (int n = 0; n < NS; ++n) A2[n] = n < N ? arow[n] * kLog2e : 0.0f;
   float dD_acc = 0.0f, db_acc = 0.0f;
+  const int64_t brow0 = li.bg * g.length;
 
   const int jb = t_begin / CK;
   const int je = (t_end + CK - 1) / CK;
@@ -437,26 +514,9 @@ __global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
       for (int n = 0; n < NS; ++n) x[n] = n < N ? srow[n] : 0.0f;
       for (int q = 0; q < nq - 1; ++q) {
         const int qs = tb + q * HS;
-        {
-          float dl[HS], uu[HS];
-          load_run<HS>(p.delta, g.d_dtype, rbase + qs, HS, g.vec, dl);
-          load_run<HS>(p.u, g.u_dtype, rbase + qs, HS, g.vec, uu);
-#pragma unroll
-          for (int i = 0; i < HS; ++i) {
-            const float del = step_of(g, dl[i], bias);
-            st_d[i * kWave + lane] = del;
-            st_u[i * kWave + lane] = del * uu[i];
-          }
-        }
-        wave_lds_sync();
-        for (int i = 0; i < HS; ++i) {
-          const float del = st_d[i * kWave + lane];
-          const float du = st_u[i * kWave + lane];
-          const float* bp = p.bt + (li.bg * g.length + qs + i) * NS;
-#pragma unroll
-          for (int n = 0; n < NS; ++n) x[n] = fmaf(fast_exp2(A2[n] * del), x[n], du * bp[n]);
-        }
-        wave_lds_sync();
+        float sdel[HS], sdu[HS], unused[HS];
+        load_steps(g, p, rbase + qs, HS, bias, sdel, sdu);
+        forward_block<NS, UNI, false>(p.bt, nullptr, brow0, qs, HS, sdel, sdu, A2, x, unused);
 #pragma unroll
         for (int n = 0; n < NS; ++n)
           if (n < N) qx[(q * NS + n) * R + li.row] = x[n];
@@ -489,29 +549,62 @@ __global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
 #pragma unroll
       for (int i = 0; i < HS; ++i) s1[i] = s2[i] = ya[i] = 0.0f;
 
+      if (UNI) {
+        // The quarter's B/C rows, shared by the workgroup (the previous quarter's
+        // flush barrier orders this write after every read of the old rows).
+        for (int e = threadIdx.x; e < NS * HS; e += blockDim.x) {
+          const int n = e / HS, i = e % HS;
+          const int64_t src = (li.bg * NS + n) * g.length + qs + i;
+          rows_b[e] = p.bn[src];
+          rows_c[e] = p.cn[src];
+        }
+        __syncthreads();
+      }
+      // per-lane carries, state-major: element (n, row) at n * R + row
+      const float* xin_p = q == 0 ? srow : qx + ((q - 1) * NS) * R + li.row;
+      const int xin_stride = q == 0 ? 1 : static_cast<int>(R);
+      float* hc_p = hcs + li.row;
+      float* da_p = dap + li.row;
+      const float* bn_p = p.bn + (li.bg * NS) * g.length + qs;
+      const float* cn_p = p.cn + (li.bg * NS) * g.length + qs;
+      const int rstride = static_cast<int>(R);
+      float xin_n = xin_p[0];
+      float hc_n = hc_p[0];
       for (int n = 0; n < N; ++n) {
+        const bool more = n + 1 < N;
+        float xin_x = 0.0f, hc_x = 0.0f;
+        if (more) {
+          xin_x = xin_p[(n + 1) * xin_stride];
+          hc_x = hc_p[(n + 1) * rstride];
+        }
+        float bv[HS], cv[HS];
+        if (UNI) {
+#pragma unroll
+          for (int i = 0; i < HS; ++i) {
+            bv[i] = rows_b[n * HS + i];
+            cv[i] = rows_c[n * HS + i];
+          }
+        } else {
+          load_run_t<float, HS>(bn_p + n * static_cast<int64_t>(g.length), HS, (g.length % 4) == 0, bv);
+          load_run_t<float, HS>(cn_p + n * static_cast<int64_t>(g.length), HS, (g.length % 4) == 0, cv);
+        }
         const float an = arow[n];
         const float a2 = an * kLog2e;
-        const float xin = q == 0 ? srow[n] : qx[((q - 1) * NS + n) * R + li.row];
-        float hc = hcs[n * R + li.row];
-        float bv[HS], cv[HS];
-        const int64_t bco = (li.bg * NS + n) * g.length + qs;
-        load_run_t<float, HS>(p.bn + bco, nv, vec_bc, bv);
-        load_run_t<float, HS>(p.cn + bco, nv, vec_bc, cv);
         float xh[HS], ah[HS];
-        float x = xin;
+        float x = xin_n;
 #pragma unroll
         for (int i = 0; i < HS; ++i) {
           ah[i] = fast_exp2(a2 * del[i]);
           x = fmaf(ah[i], x, du[i] * bv[i]);
           xh[i] = x;
         }
+        float hc = hc_n;
         float dan = 0.0f;
 #pragma unroll
         for (int i = HS - 1; i >= 0; --i) {
           const float h = fmaf(gy[i], cv[i], hc);
           s1[i] = fmaf(h, bv[i], s1[i]);
-          const float xp = i > 0 ? xh[i - 1] : xin;
+          const float xp = i > 0 ? xh[i - 1] : xin_n;
           const float pr = h * ah[i] * xp;
           s2[i] = fmaf(an, pr, s2[i]);
           dan = fmaf(del[i], pr, dan);
@@ -521,18 +614,19 @@ __global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
           hc = ah[i] * h;
         }
         if (li.active) {
-          hcs[n * R + li.row] = hc;
-          dap[n * R + li.row] += dan;
+          hc_p[n * rstride] = hc;
+          da_p[n * rstride] += dan;
         }
         wave_lds_sync();
         if (UNI) {
-          // lane l sums column (l mod 32) over half of the 64 rows.
+          // lane l sums column (l mod 32) over one half of the 64 rows; the
+          // halves and the wavefronts are added in a fixed order at the flush.
           const int col = lane & (2 * HS - 1);
           const int r0 = (lane >> 5) * 32;
-          float s = 0.0f;
+          float sum = 0.0f;
 #pragma unroll 8
-          for (int r = 0; r < 32; ++r) s += trans[(r0 + r) * kTransPitch + col];
-          atomicAdd(&acc[n * 2 * HS + col], s);
+          for (int r = 0; r < 32; ++r) sum += trans[(r0 + r) * kTransPitch + col];
+          acc[n * kWave + lane] = sum;
         } else if (li.active) {
           float* dst = p.pbc + (li.bg * g.length + qs) * NS * 2;
           for (int i = 0; i < nv; ++i) {
@@ -541,6 +635,10 @@ __global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
           }
         }
         wave_lds_sync();
+        if (more) {
+          xin_n = xin_x;
+          hc_n = hc_x;
+        }
       }
       // ---- per-step gradients of the quarter
       {
@@ -576,17 +674,22 @@ __global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
         }
       }
       if (UNI) {
-        // The workgroup's dB/dC sums of this quarter: acc[n][k*HS + i].
+        // The workgroup's dB/dC sums of this quarter, column k*HS + i of state n:
+        // wavefronts in order, each as (first half of rows) + (second half).
         __syncthreads();
         float* dst = p.pbc + ((li.bg * g.ncb + cb) * g.length + qs) * NS * 2;
-        for (int e = threadIdx.x; e < NS * 2 * HS; e += blockDim.x) {
-          const int i = e % HS;
-          const int k = (e / HS) % 2;
+        for (int e = threadIdx.x; e < N * 2 * HS; e += blockDim.x) {
+          const int col = e % (2 * HS);
           const int n = e / (2 * HS);
-          if (i < nv) dst[(static_cast<int64_t>(i) * NS + n) * 2 + k] = acc[e];
+          const int i = col % HS;
+          const int k = col / HS;
+          float sum = 0.0f;
+          for (int w = 0; w < g.wpg; ++w) {
+            const float* aw = acc_all + (w * NS + n) * kWave;
+            sum += aw[col] + aw[col + 2 * HS];
+          }
+          if (i < nv) dst[(static_cast<int64_t>(i) * NS + n) * 2 + k] = sum;
         }
-        __syncthreads();
-        for (int e = threadIdx.x; e < NS * 2 * HS; e += blockDim.x) acc[e] = 0.0f;
         __syncthreads();
       }
     }
@@ -717,9 +820,10 @@ static int make_plan(const mko_selscan_params* p, Plan* pl) {
     g.wpg = 4;
     g.ncb = 1;
   }
-  // Coarse chunks: enough wavefronts to cover the chip (>= 2048), chunk a
-  // multiple of the save interval.
-  int64_t want = (2048 + g.nwr - 1) / (g.nwr > 0 ? g.nwr : 1);
+  // Coarse chunks: about eight wavefronts per SIMD over the chip's 1024 SIMDs
+  // (the state-inner loops hide their scalar-load waits with other waves), the
+  // chunk a multiple of the save interval.
+  int64_t want = (8192 + g.nwr - 1) / (g.nwr > 0 ? g.nwr : 1);
   int64_t k = 1;
   while (k < want) k <<= 1;
   int64_t lc = (g.length + k - 1) / k;
@@ -739,8 +843,8 @@ static int make_plan(const mko_selscan_params* p, Plan* pl) {
   pl->off_sumd = o; o = align_up(o + rk * 4);
   pl->fwd_bytes = o;
   // backward workspace (extends the forward layout: bt/ct are used by both)
-  pl->off_bn = o; o = align_up(o + bgl * ns * 4);
-  pl->off_cn = o; o = align_up(o + bgl * ns * 4);
+  pl->off_bn = o; o = align_up(o + (bgl * ns + HS) * 4);  // + one row tail: quarters read HS steps
+  pl->off_cn = o; o = align_up(o + (bgl * ns + HS) * 4);
   pl->off_adj = o; o = align_up(o + rk * g.dstate * 4);
   pl->off_pbc = o; o = align_up(o + bgl * g.ncb * ns * 2 * 4);
   pl->off_dap = o; o = align_up(o + rk * ns * 4);
@@ -805,12 +909,12 @@ static int launch_fwd(const Plan& pl, const Ptrs& q, hipStream_t s) {
   const dim3 block(g.wpg * kWave);
   const unsigned gx = static_cast<unsigned>((g.nwr + g.wpg - 1) / g.wpg);
   const int64_t bgl = g.batch * g.ngroups * g.length;
-  prep_time_major<NS><<<blocks_for(bgl), 256, 0, s>>>(g, q.B, q.C, q.bt, q.ct);
+  MKO_TIMED("selscan_prep", s, prep_time_major<NS><<<blocks_for(bgl), 256, 0, s>>>(g, q.B, q.C, q.bt, q.ct));
   if (g.nchunks > 1) {
-    fwd_summary<NS, UNI><<<dim3(gx, g.nchunks - 1), block, 0, s>>>(g, q);
+    MKO_TIMED("selscan_fwd_summary", s, fwd_summary<NS, UNI><<<dim3(gx, g.nchunks - 1), block, 0, s>>>(g, q));
   }
-  chain<false><<<blocks_for(g.rows * g.dstate), 256, 0, s>>>(g, q.A, q.drive, q.sumd, q.states);
-  fwd_replay<NS, UNI><<<dim3(gx, g.nchunks), block, 0, s>>>(g, q);
+  MKO_TIMED("selscan_chain", s, chain<false><<<blocks_for(g.rows * g.dstate), 256, 0, s>>>(g, q.A, q.drive, q.sumd, q.states));
+  MKO_TIMED("selscan_fwd_replay", s, fwd_replay<NS, UNI><<<dim3(gx, g.nchunks), block, 0, s>>>(g, q));
   return mko_check_launch("selscan_fwd");
 }
 
@@ -820,21 +924,22 @@ static int launch_bwd(const Plan& pl, const Ptrs& q, const mko_selscan_params* p
   const dim3 block(g.wpg * kWave);
   const unsigned gx = static_cast<unsigned>((g.nwr + g.wpg - 1) / g.wpg);
   const int64_t bgl = g.batch * g.ngroups * g.length;
-  prep_time_major<NS><<<blocks_for(bgl), 256, 0, s>>>(g, q.B, q.C, q.bt, q.ct);
-  prep_state_major<<<blocks_for(bgl * NS), 256, 0, s>>>(g, NS, q.B, q.C, q.bn, q.cn);
+  MKO_TIMED("selscan_prep", s, prep_time_major<NS><<<blocks_for(bgl), 256, 0, s>>>(g, q.B, q.C, q.bt, q.ct);
+            prep_state_major<<<blocks_for(bgl * NS), 256, 0, s>>>(g, NS, q.B, q.C, q.bn, q.cn));
   if (g.nchunks > 1) {
-    bwd_summary<NS, UNI><<<dim3(gx, g.nchunks - 1), block, 0, s>>>(g, q);
+    MKO_TIMED("selscan_bwd_summary", s, bwd_summary<NS, UNI><<<dim3(gx, g.nchunks - 1), block, 0, s>>>(g, q));
   }
-  chain<true><<<blocks_for(g.rows * g.dstate), 256, 0, s>>>(g, q.A, q.drive, q.sumd, q.adj);
+  MKO_TIMED("selscan_chain", s, chain<true><<<blocks_for(g.rows * g.dstate), 256, 0, s>>>(g, q.A, q.drive, q.sumd, q.adj));
   if (!UNI) {
     const int64_t n = bgl * NS * 2;
-    zero_f32<<<blocks_for(n), 256, 0, s>>>(q.pbc, n);
+    MKO_TIMED("selscan_zero", s, zero_f32<<<blocks_for(n), 256, 0, s>>>(q.pbc, n));
   }
-  bwd_main<NS, UNI><<<dim3(gx, g.nchunks), block, 0, s>>>(g, q);
-  reduce_bc<NS><<<blocks_for(g.batch * g.ngroups * g.dstate * g.length), 256, 0, s>>>(
-      g, UNI ? g.ncb : 1, q.pbc, p->dB, p->dC);
-  reduce_params<<<blocks_for(g.dim * g.dstate), 256, 0, s>>>(g, NS, q.dap, q.ddp, q.dbp, p->dA, p->dD,
-                                                             p->ddelta_bias);
+  MKO_TIMED("selscan_bwd_main", s, bwd_main<NS, UNI><<<dim3(gx, g.nchunks), block, 0, s>>>(g, q));
+  MKO_TIMED("selscan_bwd_reduce", s,
+            reduce_bc<NS><<<blocks_for(g.batch * g.ngroups * g.dstate * g.length), 256, 0, s>>>(
+                g, UNI ? g.ncb : 1, q.pbc, p->dB, p->dC);
+            reduce_params<<<blocks_for(g.dim * g.dstate), 256, 0, s>>>(g, NS, q.dap, q.ddp, q.dbp, p->dA,
+                                                                       p->dD, p->ddelta_bias));
   return mko_check_launch("selscan_bwd");
 }
 

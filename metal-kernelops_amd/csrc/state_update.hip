@@ -401,14 +401,16 @@ namespace {
 
 template <typename TS>
 void launch_fwd_t(const Args& a, int vec, hipStream_t s, unsigned grid) {
-  if (vec == 4) fwd<TS, 4><<<grid, kThreads, 0, s>>>(a);
-  else fwd<TS, 1><<<grid, kThreads, 0, s>>>(a);
+  MKO_TIMED("state_update_fwd", s,
+            if (vec == 4) fwd<TS, 4><<<grid, kThreads, 0, s>>>(a);
+            else fwd<TS, 1><<<grid, kThreads, 0, s>>>(a));
 }
 
 template <typename TS>
 void launch_bwd_t(const Args& a, int vec, hipStream_t s, unsigned grid) {
-  if (vec == 4) bwd<TS, 4><<<grid, kThreads, 0, s>>>(a);
-  else bwd<TS, 1><<<grid, kThreads, 0, s>>>(a);
+  MKO_TIMED("state_update_bwd", s,
+            if (vec == 4) bwd<TS, 4><<<grid, kThreads, 0, s>>>(a);
+            else bwd<TS, 1><<<grid, kThreads, 0, s>>>(a));
 }
 
 Args base_args(const mko_state_update_params* p, const Geo& g) {
@@ -512,7 +514,8 @@ extern "C" int mko_state_update_bwd(const mko_state_update_params* p, void* stre
   const int64_t nred = g.batch * g.ngroups * g.dstate;
   int64_t total = nred > g.nheads * g.headdim ? nred : g.nheads * g.headdim;
   if (total < g.nheads) total = g.nheads;
-  reduce<<<static_cast<unsigned>((total + 255) / 256), 256, 0, s>>>(a, p->dB, p->dC, p->dA, p->dD,
-                                                                     p->ddt_bias);
+  MKO_TIMED("state_update_bwd_reduce", s,
+            reduce<<<static_cast<unsigned>((total + 255) / 256), 256, 0, s>>>(a, p->dB, p->dC, p->dA, p->dD,
+                                                                               p->ddt_bias));
   return mko_check_launch("state_update_bwd");
 }

@@ -71,6 +71,11 @@ _SIGNATURES = {
     "mko_selscan_bwd_workspace_size": ([ctypes.POINTER(SelscanParams)], ctypes.c_size_t),
     "mko_selscan_bwd": ([ctypes.POINTER(SelscanParams), _vp], ctypes.c_int),
     "mko_state_update_fwd": ([ctypes.POINTER(StateUpdateParams), _vp], ctypes.c_int),
+    "mko_profile_enable": ([ctypes.c_int], ctypes.c_int),
+    "mko_profile_reset": ([], None),
+    "mko_profile_count": ([], ctypes.c_int),
+    "mko_profile_entry": ([ctypes.c_int, ctypes.c_char_p, ctypes.c_size_t,
+                           ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64)], ctypes.c_int),
     "mko_state_update_bwd_workspace_size": ([ctypes.POINTER(StateUpdateParams)], ctypes.c_size_t),
     "mko_state_update_bwd": ([ctypes.POINTER(StateUpdateParams), _vp], ctypes.c_int),
 }
@@ -106,6 +111,28 @@ def lib():
                 raise RuntimeError(f"{struct.__name__} layout does not match libmko.so")
         _lib = handle
         return _lib
+
+
+def kernel_timing(enable):
+    """Turn the library's per-kernel HIP-event timing on or off; returns the old setting."""
+    return bool(lib().mko_profile_enable(1 if enable else 0))
+
+
+def kernel_timing_reset():
+    lib().mko_profile_reset()
+
+
+def kernel_times():
+    """``{kernel: (total_ms, launches)}`` since the last reset (synchronises on the events)."""
+    out = {}
+    handle = lib()
+    name = ctypes.create_string_buffer(128)
+    total = ctypes.c_double()
+    count = ctypes.c_int64()
+    for i in range(handle.mko_profile_count()):
+        if handle.mko_profile_entry(i, name, 128, ctypes.byref(total), ctypes.byref(count)) == 0:
+            out[name.value.decode()] = (total.value, count.value)
+    return out
 
 
 def exported_symbols():

@@ -88,13 +88,17 @@ def _selscan_bwd(dout: Tensor, u: Tensor, delta: Tensor, A: Tensor, B: Tensor, C
     dim = u.shape[1]
     f32 = dict(dtype=torch.float32, device=u.device)
     du, ddelta = torch.empty_like(u), torch.empty_like(delta)
-    dA = torch.zeros(A.shape, **f32)
-    dB, dC = torch.zeros_like(B), torch.zeros_like(C)
-    dD = torch.zeros(dim if D is not None else 0, **f32)
-    dz = torch.zeros_like(z) if z is not None else torch.empty(0, dtype=u.dtype, device=u.device)
-    dbias = torch.zeros(dim if delta_bias is not None else 0, **f32)
     if u.numel() == 0:
-        return du, ddelta, dA, dB, dC, dD, dz, dbias
+        return (du, ddelta, torch.zeros(A.shape, **f32), torch.zeros_like(B), torch.zeros_like(C),
+                torch.zeros(dim if D is not None else 0, **f32),
+                torch.zeros_like(z) if z is not None else u.new_empty(0),
+                torch.zeros(dim if delta_bias is not None else 0, **f32))
+    # every element of these is written by the kernels
+    dA = torch.empty(A.shape, **f32)
+    dB, dC = torch.empty_like(B), torch.empty_like(C)
+    dD = torch.empty(dim if D is not None else 0, **f32)
+    dz = torch.empty_like(z) if z is not None else u.new_empty(0)
+    dbias = torch.empty(dim if delta_bias is not None else 0, **f32)
     lib = nat.lib()
     p = _params(u, delta, A, B, C, D, z, delta_bias, softplus)
     p.states, p.dout = states.data_ptr(), dout.data_ptr()

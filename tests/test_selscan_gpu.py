@@ -108,8 +108,10 @@ def test_shapes_fp32(shape):
 @pytest.mark.parametrize("softplus", [True, False])
 def test_options(opts, softplus):
     inputs, dy = _random_problem(2, 128, 150, 16, 1, seed=7, **opts)
-    if not softplus:
+    if not softplus:  # raw steps must stay positive without the softplus
         inputs["dt"] = torch.rand(inputs["dt"].shape) * 0.3
+        if inputs["delta_bias"] is not None:
+            inputs["delta_bias"] = inputs["delta_bias"].abs() * 0.1
     _compare(inputs, dy, softplus, 1e-5, 1e-4)
 
 
@@ -162,7 +164,7 @@ def test_empty_inputs():
     for shape in ((2, 8, 0), (0, 8, 16)):
         b, d, length = shape
         u = torch.zeros(b, d, length, device=DEV, requires_grad=True)
-        A = -torch.ones(d, 4, device=DEV, requires_grad=True)
+        A = (-torch.ones(d, 4, device=DEV)).requires_grad_(True)
         B = torch.zeros(b, 2, 4, length, device=DEV, requires_grad=True)
         out = ss(u, torch.zeros_like(u), A, B, B.detach().clone(), D=torch.ones(d, device=DEV))
         assert out.shape == shape
@@ -175,6 +177,7 @@ def test_errors():
     ss = _selective_scan()
     inputs, _ = mamba1_c1()
     cpu = [inputs[k] for k in ("u", "dt", "A", "B", "C")]
+    cpu[1] = torch.nn.functional.softplus(cpu[1])  # the bare scan takes positive steps
     with pytest.raises(ValueError):
         ss(*cpu)
     gpu = [t.to(DEV) for t in cpu]
