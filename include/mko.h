@@ -46,6 +46,7 @@ const char* mko_last_error(void);
 /* sizeof() of the parameter blocks, so a binding can check its mirror of them. */
 size_t mko_sizeof_selscan_params(void);
 size_t mko_sizeof_state_update_params(void);
+size_t mko_sizeof_ssd_params(void);
 
 /* Kernel timing (observability).  While enabled, every kernel the library
  * launches is bracketed by HIP events on its launch stream; the per-kernel totals
@@ -169,6 +170,64 @@ int mko_state_update_fwd(const mko_state_update_params* p, void* stream);
  * gradient has one writer, so repeated runs are bit-identical. */
 size_t mko_state_update_bwd_workspace_size(const mko_state_update_params* p);
 int mko_state_update_bwd(const mko_state_update_params* p, void* stream);
+
+/* ======================================================================== */
+/* Mamba-2 SSD chunk scan                                                     */
+/* ======================================================================== */
+
+#define MKO_SSD_SOFTPLUS 1u  /* delta = softplus(dt + dt_bias) */
+#define MKO_SSD_D_PER_ROW 2u /* D is (nheads, headdim) instead of (nheads,) */
+
+typedef struct mko_ssd_params {
+  const void* x;              /* (batch, length, nheads, headdim)  x_dtype            */
+  const void* dt;             /* (batch, length, nheads)           dt_dtype, raw      */
+  const float* A;             /* (nheads,)                                            */
+  const void* B;              /* (batch, length, ngroups, dstate)  bc_dtype           */
+  const void* C;              /* (batch, length, ngroups, dstate)  bc_dtype           */
+  const float* D;             /* (nheads,) or (nheads, headdim), or NULL              */
+  const void* z;              /* (batch, length, nheads, headdim) x_dtype, or NULL    */
+  const float* dt_bias;       /* (nheads,) or NULL                                    */
+  const void* initial_states; /* (batch, nheads, headdim, dstate) x_dtype, or NULL    */
+  /* forward outputs */
+  void* y;                    /* (batch, length, nheads, headdim) x_dtype             */
+  void* final_state;          /* (batch, nheads, headdim, dstate) x_dtype             */
+  void* saved;                /* mko_ssd_saved_bytes(): written by the forward, read by
+                                 the backward (chunk states, step sums, C.B blocks)  */
+  /* backward inputs */
+  const void* dy;             /* (batch, length, nheads, headdim) x_dtype             */
+  const void* dfinal;         /* (batch, nheads, headdim, dstate) x_dtype, or NULL    */
+  /* backward outputs (dD/dz/ddt_bias/dinitial only with D/z/dt_bias/initial_states) */
+  void* dx;                   /* x_dtype                                              */
+  void* ddt;                  /* dt_dtype                                             */
+  float* dA;                  /* (nheads,)                                            */
+  void* dB;                   /* bc_dtype                                             */
+  void* dC;                   /* bc_dtype                                             */
+  float* dD;                  /* shape of D                                           */
+  void* dz;                   /* x_dtype                                              */
+  float* ddt_bias;            /* (nheads,)                                            */
+  void* dinitial;             /* x_dtype                                              */
+  void* workspace;
+  size_t workspace_bytes;
+  int64_t batch, length, nheads, headdim, ngroups, dstate;
+  int32_t x_dtype, dt_dtype, bc_dtype;
+  uint32_t flags;
+} mko_ssd_params;
+
+/* Size of the forward-to-backward save area (params.saved). */
+size_t mko_ssd_saved_bytes(const mko_ssd_params* p);
+
+/* Replaces mamba2_chunk_scan's composition and Metal forward
+ * (cv/mamba2_chunk.py:447-533, 568-614, 617-678): y and the final state of the SSD
+ * recurrence, computed in chunks with the intra-chunk, chunk-state and
+ * state-to-output contractions on the matrix cores.  The result does not depend
+ * on the caller's chunk_size; the kernels pick their own chunk (64 to 256). */
+size_t mko_ssd_fwd_workspace_size(const mko_ssd_params* p);
+int mko_ssd_fwd(const mko_ssd_params* p, void* stream);
+
+/* Replaces the torch autograd of that composition (the reference has no
+ * hand-written SSD backward): gradients of every differentiable input. */
+size_t mko_ssd_bwd_workspace_size(const mko_ssd_params* p);
+int mko_ssd_bwd(const mko_ssd_params* p, void* stream);
 
 #ifdef __cplusplus
 }

@@ -37,6 +37,8 @@ extern "C" size_t mko_sizeof_selscan_params(void) { return sizeof(mko_selscan_pa
 
 extern "C" size_t mko_sizeof_state_update_params(void) { return sizeof(mko_state_update_params); }
 
+extern "C" size_t mko_sizeof_ssd_params(void) { return sizeof(mko_ssd_params); }
+
 // ---------------------------------------------------------------- kernel timing
 //
 // Opt-in per-kernel timing with HIP events recorded on the launch stream around

@@ -1,0 +1,75 @@
+// 64x64 output tiles on CDNA4 matrix cores for a 256-thread workgroup.
+//
+// Each of the four wavefronts owns a 32x32 quadrant (wm = wave / 2 rows,
+// wn = wave % 2 columns) accumulated in 16 fp32 registers with the MFMA 32x32
+// output layout: register r of lane l holds row 8*(r/4) + 4*(l/32) + r%4 and
+// column l%32 of the quadrant.  Operands come from LDS, both stored K-contiguous:
+// A as [row][k], B transposed as [col][k], so a lane's operand slice is one
+// 16-byte read (bf16/f16) or one float (fp32).
+//
+// Operand types: bf16 and f16 use v_mfma_f32_32x32x16_{bf16,f16}; float uses
+// v_mfma_f32_32x32x2_f32, which keeps fp32 products (used for fp32 inputs).
+#pragma once
+
+#include "common.hpp"
+
+namespace mko {
+
+typedef __bf16 mfma_bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 mfma_f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// Leading dimension (elements) of a 64-wide K-contiguous LDS operand tile: padded so
+// the 16-byte reads of eight consecutive rows fall in distinct banks.
+template <typename TM>
+constexpr int tile_ld() { return sizeof(TM) == 2 ? 72 : 65; }
+
+template <typename TM>
+struct LdsTile {
+  static constexpr int ld = tile_ld<TM>();
+  static constexpr int elems = 64 * ld;
+};
+
+__device__ __forceinline__ void quadrant(int lane_wave, int& wm, int& wn) {
+  wm = lane_wave >> 1;
+  wn = lane_wave & 1;
+}
+
+// Row (within the 64x64 tile) of accumulator register r for this lane.
+__device__ __forceinline__ int acc_row(int wm, int lane, int r) {
+  return wm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+}
+__device__ __forceinline__ int acc_col(int wn, int lane) { return wn * 32 + (lane & 31); }
+
+// acc += A[wm*32 .. +32][0..k_len) * B[0..k_len)[wn*32 .. +32], with A and B^T in LDS.
+template <typename TM>
+__device__ __forceinline__ void mma_tile(f32x16& acc, const TM* A, const TM* Bt, int wm, int wn, int lane,
+                                         int k_len) {
+  constexpr int ld = tile_ld<TM>();
+  if constexpr (sizeof(TM) == 2) {
+    const TM* a = A + (wm * 32 + (lane & 31)) * ld + (lane >> 5) * 8;
+    const TM* b = Bt + (wn * 32 + (lane & 31)) * ld + (lane >> 5) * 8;
+    for (int k = 0; k < k_len; k += 16) {
+      const uint4 av = *reinterpret_cast<const uint4*>(a + k);
+      const uint4 bv = *reinterpret_cast<const uint4*>(b + k);
+      if constexpr (__is_same(TM, bf16)) {
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(mfma_bf16x8, av),
+                                                      __builtin_bit_cast(mfma_bf16x8, bv), acc, 0, 0, 0);
+      } else {
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(mfma_f16x8, av),
+                                                     __builtin_bit_cast(mfma_f16x8, bv), acc, 0, 0, 0);
+      }
+    }
+  } else {
+    const float* a = A + (wm * 32 + (lane & 31)) * ld + (lane >> 5);
+    const float* b = Bt + (wn * 32 + (lane & 31)) * ld + (lane >> 5);
+    for (int k = 0; k < k_len; k += 2) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[k], b[k], acc, 0, 0, 0);
+  }
+}
+
+__device__ __forceinline__ void zero(f32x16& acc) {
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+}
+
+}  // namespace mko

@@ -60,11 +60,33 @@ class StateUpdateParams(ctypes.Structure):
     ]
 
 
+class SsdParams(ctypes.Structure):
+    """Mirror of ``mko_ssd_params``."""
+
+    _fields_ = [
+        ("x", _vp), ("dt", _vp), ("A", _vp), ("B", _vp), ("C", _vp), ("D", _vp), ("z", _vp),
+        ("dt_bias", _vp), ("initial_states", _vp), ("y", _vp), ("final_state", _vp), ("saved", _vp),
+        ("dy", _vp), ("dfinal", _vp), ("dx", _vp), ("ddt", _vp), ("dA", _vp), ("dB", _vp),
+        ("dC", _vp), ("dD", _vp), ("dz", _vp), ("ddt_bias", _vp), ("dinitial", _vp),
+        ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
+        ("batch", ctypes.c_int64), ("length", ctypes.c_int64), ("nheads", ctypes.c_int64),
+        ("headdim", ctypes.c_int64), ("ngroups", ctypes.c_int64), ("dstate", ctypes.c_int64),
+        ("x_dtype", ctypes.c_int32), ("dt_dtype", ctypes.c_int32), ("bc_dtype", ctypes.c_int32),
+        ("flags", ctypes.c_uint32),
+    ]
+
+
 _SIGNATURES = {
     "mko_abi_version": ([], ctypes.c_int),
     "mko_last_error": ([], ctypes.c_char_p),
     "mko_sizeof_selscan_params": ([], ctypes.c_size_t),
     "mko_sizeof_state_update_params": ([], ctypes.c_size_t),
+    "mko_sizeof_ssd_params": ([], ctypes.c_size_t),
+    "mko_ssd_saved_bytes": ([ctypes.POINTER(SsdParams)], ctypes.c_size_t),
+    "mko_ssd_fwd_workspace_size": ([ctypes.POINTER(SsdParams)], ctypes.c_size_t),
+    "mko_ssd_fwd": ([ctypes.POINTER(SsdParams), _vp], ctypes.c_int),
+    "mko_ssd_bwd_workspace_size": ([ctypes.POINTER(SsdParams)], ctypes.c_size_t),
+    "mko_ssd_bwd": ([ctypes.POINTER(SsdParams), _vp], ctypes.c_int),
     "mko_selscan_num_checkpoints": ([ctypes.c_int64], ctypes.c_int64),
     "mko_selscan_fwd_workspace_size": ([ctypes.POINTER(SelscanParams)], ctypes.c_size_t),
     "mko_selscan_fwd": ([ctypes.POINTER(SelscanParams), _vp], ctypes.c_int),
@@ -106,7 +128,8 @@ def lib():
         if version != ABI_VERSION:
             raise RuntimeError(f"libmko.so ABI version {version}, this binding expects {ABI_VERSION}")
         for struct, fn in ((SelscanParams, handle.mko_sizeof_selscan_params),
-                           (StateUpdateParams, handle.mko_sizeof_state_update_params)):
+                           (StateUpdateParams, handle.mko_sizeof_state_update_params),
+                           (SsdParams, handle.mko_sizeof_ssd_params)):
             if ctypes.sizeof(struct) != fn():
                 raise RuntimeError(f"{struct.__name__} layout does not match libmko.so")
         _lib = handle

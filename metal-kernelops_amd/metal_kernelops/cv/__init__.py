@@ -7,10 +7,14 @@ RMSNorm, path scan, NSA selection, RoIAlign) are not part of this package.
 Importing it registers the ``mko::`` custom ops and launches nothing.
 """
 
+from .mamba2_chunk import last_path, mamba2_chunk_scan, mamba2_chunk_scan_reference
 from .mamba2_state import CHECKED_TORCH, mamba2_state_update, mamba2_state_update_reference
 
 __all__ = [
     "CHECKED_TORCH",
+    "last_path",
+    "mamba2_chunk_scan",
+    "mamba2_chunk_scan_reference",
     "mamba2_state_update",
     "mamba2_state_update_reference",
 ]
