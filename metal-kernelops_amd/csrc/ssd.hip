@@ -12,9 +12,6 @@
 // The backward mirrors these (see ssd_bwd.hip).  Operands of the products are
 // rounded to the input dtype (bf16/f16 products on the bf16/f16 matrix cores,
 // fp32 inputs on the fp32 ones); accumulation, decays and states are fp32.
-#include "common.hpp"
-#include "io.hpp"
-#include "mma.hpp"
 #include "ssd.hpp"
 
 namespace mko {
@@ -47,26 +44,6 @@ __global__ void __launch_bounds__(256) prep(Geo g, Ptrs p) {
     const int64_t o = ((b * g.nheads + h) * g.nc + c) * g.q + l;
     p.dl[o] = del;
     p.cs[o] = v;
-  }
-}
-
-// Stages a 64x64 operand tile from a row-major source (rows = tokens) into LDS,
-// row-major ([row][col]) or transposed ([col][row]); `val(row, col)` gives the
-// fp32 value (0 outside the problem).  256 threads, 16 elements each, the column
-// index fastest so global reads are contiguous along the source row.
-template <typename TM, bool TRANS, typename F>
-__device__ __forceinline__ void stage(TM* dst, F&& val) {
-  constexpr int ld = tile_ld<TM>();
-  const int tid = threadIdx.x;
-#pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    const int e = k * 256 + tid;
-    const int row = e >> 6, col = e & 63;
-    const float v = val(row, col);
-    if (TRANS)
-      dst[col * ld + row] = from_f32<TM>(v);
-    else
-      dst[row * ld + col] = from_f32<TM>(v);
   }
 }
 
@@ -106,68 +83,6 @@ __global__ void __launch_bounds__(256) cb_kernel(Geo g, Ptrs p) {
   for (int r = 0; r < 16; ++r) out[(64 * i + acc_row(wm, lane, r)) * g.q + 64 * j + acc_col(wn, lane)] = acc[r];
 }
 
-// out[p][n] = sum_l s1(l) X(l, p) Y(l, n) over the chunk, for one 64x64 (p, n) tile.
-//   FWD: X = x, s1 = step e^{T - cs}, Y = B  -> local chunk state
-//   BWD: X = dy * silu(z), s1 = e^{cs}, Y = C -> the chunk's contribution to the
-//        adjoint of its entering state
-template <typename TM, bool BWD>
-__global__ void __launch_bounds__(256) chunk_state(Geo g, Ptrs p, float* out) {
-  __shared__ TM sa[LdsTile<TM>::elems], sb[LdsTile<TM>::elems];
-  __shared__ float s1[64];
-  const int ntiles = static_cast<int>((g.dstate + 63) / 64);
-  const int pt = blockIdx.x / ntiles, nt = blockIdx.x % ntiles;
-  const int c = blockIdx.y;
-  const int64_t bh = blockIdx.z, b = bh / g.nheads, h = bh % g.nheads, gg = h / g.hpg;
-  const int lane = threadIdx.x & 63;
-  int wm, wn;
-  quadrant(threadIdx.x >> 6, wm, wn);
-  const int64_t so = (bh * g.nc + c) * g.q;
-  const float T = p.cs[so + g.q - 1];
-  f32x16 acc;
-  zero(acc);
-  for (int kb = 0; kb < g.qb; ++kb) {
-    const int64_t t0 = static_cast<int64_t>(c) * g.q + 64 * kb;
-    if (threadIdx.x < 64) {
-      const int64_t o = so + 64 * kb + threadIdx.x;
-      const bool ok = t0 + threadIdx.x < g.length;
-      s1[threadIdx.x] = !ok ? 0.0f : (BWD ? fast_exp(p.cs[o]) : p.dl[o] * fast_exp(T - p.cs[o]));
-    }
-    __syncthreads();
-    stage<TM, true>(sa, [&](int l, int pp) {  // A[p][l]
-      const int64_t t = t0 + l;
-      const int64_t pc = static_cast<int64_t>(pt) * 64 + pp;
-      if (t >= g.length || pc >= g.headdim) return 0.0f;
-      const int64_t xi = ((b * g.length + t) * g.nheads + h) * g.headdim + pc;
-      float v;
-      if (BWD) {
-        v = load_one(p.dy, g.x_dtype, xi);
-        if (p.z) {
-          const float zv = load_one(p.z, g.x_dtype, xi);
-          v *= zv * sigmoid(zv);
-        }
-      } else {
-        v = load_one(p.x, g.x_dtype, xi);
-      }
-      return s1[l] * v;
-    });
-    stage<TM, true>(sb, [&](int l, int n) {  // Bt[n][l]
-      const int64_t t = t0 + l;
-      const int64_t nn = static_cast<int64_t>(nt) * 64 + n;
-      if (t >= g.length || nn >= g.dstate) return 0.0f;
-      return load_one(BWD ? p.C : p.B, g.bc_dtype, ((b * g.length + t) * g.ngroups + gg) * g.dstate + nn);
-    });
-    __syncthreads();
-    mma_tile<TM>(acc, sa, sb, wm, wn, lane, 64);
-    __syncthreads();
-  }
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int64_t pp = static_cast<int64_t>(pt) * 64 + acc_row(wm, lane, r);
-    const int64_t nn = static_cast<int64_t>(nt) * 64 + acc_col(wn, lane);
-    if (pp < g.headdim && nn < g.dstate) out[((bh * g.nc + c) * g.headdim + pp) * g.dstate + nn] = acc[r];
-  }
-}
-
 // Entering state of every chunk (in place over the local states) and the final state.
 __global__ void __launch_bounds__(256) state_pass(Geo g, Ptrs p) {
   const int64_t pn = g.headdim * g.dstate;
@@ -190,55 +105,13 @@ __global__ void __launch_bounds__(256) chunk_scan(Geo g, Ptrs p) {
   __shared__ float csr[64], css[64], eo[64];
   const int i = blockIdx.x % g.qb, pt = blockIdx.x / g.qb;
   const int c = blockIdx.y;
-  const int64_t bh = blockIdx.z, b = bh / g.nheads, h = bh % g.nheads, gg = h / g.hpg;
+  const int64_t bh = blockIdx.z, b = bh / g.nheads, h = bh % g.nheads;
   const int lane = threadIdx.x & 63;
   int wm, wn;
   quadrant(threadIdx.x >> 6, wm, wn);
-  const int64_t so = (bh * g.nc + c) * g.q;
-  const int64_t tl0 = static_cast<int64_t>(c) * g.q + 64 * i;
-  const float* cbt = p.cb + ((b * g.nc + c) * g.ngroups + gg) * g.q * g.q;
-  if (threadIdx.x < 64) {
-    csr[threadIdx.x] = p.cs[so + 64 * i + threadIdx.x];
-    eo[threadIdx.x] = fast_exp(csr[threadIdx.x]);
-  }
   f32x16 acc;
-  zero(acc);
-  for (int j = 0; j <= i; ++j) {
-    const int64_t ts0 = static_cast<int64_t>(c) * g.q + 64 * j;
-    __syncthreads();
-    if (threadIdx.x < 64) css[threadIdx.x] = p.cs[so + 64 * j + threadIdx.x];
-    __syncthreads();
-    stage<TM, false>(sa, [&](int r, int s) {  // K[l][s]
-      if (64 * j + s > 64 * i + r) return 0.0f;
-      return cbt[(64 * i + r) * g.q + 64 * j + s] * fast_exp(csr[r] - css[s]);
-    });
-    stage<TM, true>(sb, [&](int s, int pp) {  // Bt[p][s] = step_s x_s[p]
-      const int64_t t = ts0 + s;
-      const int64_t pc = static_cast<int64_t>(pt) * 64 + pp;
-      if (t >= g.length || pc >= g.headdim) return 0.0f;
-      return p.dl[so + 64 * j + s] * load_one(p.x, g.x_dtype, ((b * g.length + t) * g.nheads + h) * g.headdim + pc);
-    });
-    __syncthreads();
-    mma_tile<TM>(acc, sa, sb, wm, wn, lane, 64);
-  }
-  const float* st = p.states + (bh * g.nc + c) * g.headdim * g.dstate;
-  for (int n0 = 0; n0 < g.dstate; n0 += 64) {
-    __syncthreads();
-    stage<TM, false>(sa, [&](int r, int k) {  // e^{cs_l} C_l[n]
-      const int64_t t = tl0 + r;
-      const int n = n0 + k;
-      if (t >= g.length || n >= g.dstate) return 0.0f;
-      return eo[r] * load_one(p.C, g.bc_dtype, ((b * g.length + t) * g.ngroups + gg) * g.dstate + n);
-    });
-    stage<TM, false>(sb, [&](int pp, int k) {  // Bt[p][n] = S_in[p][n]
-      const int64_t pc = static_cast<int64_t>(pt) * 64 + pp;
-      const int n = n0 + k;
-      if (pc >= g.headdim || n >= g.dstate) return 0.0f;
-      return st[pc * g.dstate + n];
-    });
-    __syncthreads();
-    mma_tile<TM>(acc, sa, sb, wm, wn, lane, 64);
-  }
+  chunk_out<TM>(g, p, acc, sa, sb, csr, css, eo, i, pt, c, bh);
+  const int64_t tl0 = static_cast<int64_t>(c) * g.q + 64 * i;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int64_t t = tl0 + acc_row(wm, lane, r);
@@ -279,7 +152,10 @@ int make_geo(const mko_ssd_params* prm, Geo* g) {
       return MKO_EINVAL;
     }
   }
-  g->qb = g->length >= 1024 ? 4 : (g->length >= 256 ? 2 : 1);
+  // Longer chunks give the matrix cores deeper products; fp32 inputs keep 64-token
+  // chunks, where the in-chunk decay exponents (differences of cumulative sums) stay
+  // small and the gradient with respect to them keeps fp32 accuracy.
+  g->qb = prm->x_dtype == MKO_F32 ? 1 : (g->length >= 1024 ? 4 : (g->length >= 256 ? 2 : 1));
   g->q = 64 * g->qb;
   g->nc = static_cast<int>((g->length + g->q - 1) / g->q);
   g->hpg = static_cast<int>(g->nheads / g->ngroups);
@@ -331,6 +207,11 @@ Ptrs base_ptrs(const mko_ssd_params* prm) {
   q.ddt = prm->ddt;
   q.dz = prm->dz;
   q.dinit = prm->dinitial;
+  q.dA = prm->dA;
+  q.dB = prm->dB;
+  q.dC = prm->dC;
+  q.dD = prm->dD;
+  q.dbias = prm->ddt_bias;
   return q;
 }
 
@@ -369,11 +250,12 @@ extern "C" int mko_ssd_fwd(const mko_ssd_params* prm, void* stream) {
   Geo g;
   int st = make_geo(prm, &g);
   if (st != MKO_OK) return st;
-  if (!prm->x || !prm->dt || !prm->A || !prm->B || !prm->C || !prm->y || !prm->final_state || !prm->saved) {
+  if (g.batch == 0) return MKO_OK;
+  if (!prm->A || !prm->final_state ||
+      (g.length > 0 && (!prm->x || !prm->dt || !prm->B || !prm->C || !prm->y || !prm->saved))) {
     mko_set_error("ssd_fwd: x, dt, A, B, C, y, final_state and saved are required");
     return MKO_EINVAL;
   }
-  if (g.batch == 0) return MKO_OK;
   Ptrs q = base_ptrs(prm);
   bind_saved(g, prm->saved, &q);
   hipStream_t s = static_cast<hipStream_t>(stream);

@@ -120,3 +120,177 @@ def test_config4_shape_batch_slice():
     assert max_rel(y[:1], y_ref) <= 2e-2
     assert max_rel(s[:1], s_ref) <= 2e-2
     assert torch.isfinite(y).all() and torch.isfinite(s).all()
+
+
+# ---------------------------------------------------------------- backward
+
+# Gradient norm-relative tolerances against the float64 oracle run on the same (rounded)
+# inputs: 1e-4 for fp32 (the reference's gradient bar); half precision rounds the
+# matrix-core operands, so 1e-2 (fp16) and 3e-2 (bf16).
+GRAD_TOL = {torch.float32: 1e-4, torch.float16: 1e-2, torch.bfloat16: 3e-2}
+ACTS = ("x", "B", "C", "z", "initial_states")
+NAMES = ("x", "dt", "A", "B", "C")
+
+
+def _leaves(tensors, device, dtype=None):
+    out = {}
+    for k, v in tensors.items():
+        t = v.detach().to(device)
+        if dtype is not None and k in ACTS:
+            t = t.to(dtype)
+        out[k] = t.requires_grad_(True)
+    return out
+
+
+def _run_grad(fn, leaves, dy, dfinal, softplus, double=False):
+    kw = {k: v for k, v in leaves.items() if k not in NAMES}
+    y, s = fn(*(leaves[k] for k in NAMES), **kw, dt_softplus=softplus)
+    loss = (y.double() * dy).sum() if dy is not None else 0
+    if dfinal is not None:
+        loss = loss + (s.double() * dfinal).sum()
+    loss.backward()
+    return {k: v.grad for k, v in leaves.items()}
+
+
+def _oracle_grads(inputs, dy, dfinal, softplus, dtype=torch.float64):
+    """float64 oracle gradients on the inputs rounded to the kernel's activation dtype."""
+    leaves = _leaves({k: (v.to(dtype) if k in ACTS else v).double() for k, v in inputs.items()}, "cpu")
+    return _run_grad(oracle.mamba2_chunk_scan_recurrence, leaves, dy, dfinal, softplus)
+
+
+def _gpu_grads(inputs, dy, dfinal, softplus, dtype):
+    leaves = _leaves(inputs, DEV, dtype)
+    api = lambda x, dt, A, B, C, **kw: _api()(x, dt, A, B, C, 64, **kw)
+    return _run_grad(api, leaves, None if dy is None else dy.to(DEV), None if dfinal is None else dfinal.to(DEV),
+                     softplus)
+
+
+def _inputs(shape, seed, options=("D", "z", "dt_bias", "initial_states"), d_row=False):
+    batch, length, nheads, headdim, ngroups, dstate = shape
+    x, dt, A, B, C = _problem(*shape, seed=seed)
+    inputs = dict(x=x, dt=dt, A=A, B=B, C=C)
+    opt = _options(batch, length, nheads, headdim, dstate, seed=seed + 10)
+    if d_row:
+        opt["D"] = torch.randn(nheads, headdim, generator=torch.Generator().manual_seed(seed + 20))
+    inputs.update({k: opt[k] for k in options})
+    g = torch.Generator().manual_seed(seed + 30)
+    dy = torch.randn(batch, length, nheads, headdim, generator=g, dtype=torch.float64)
+    dfinal = torch.randn(batch, nheads, headdim, dstate, generator=g, dtype=torch.float64)
+    return inputs, dy, dfinal
+
+
+def _compare(got, ref, tol, what):
+    for k, r in ref.items():
+        gk = got[k]
+        if r is None:  # the loss does not depend on this input
+            assert gk is None or torch.count_nonzero(gk) == 0, f"{what}: nonzero gradient for {k}"
+            continue
+        assert gk is not None, f"{what}: no gradient for {k}"
+        assert gk.shape == r.shape, f"{what}: {k} shape {tuple(gk.shape)} vs {tuple(r.shape)}"
+        assert torch.isfinite(gk).all(), f"{what}: {k} not finite"
+        err = norm_rel(gk, r)
+        assert err <= tol, f"{what}: d{k} norm-relative error {err:.3e} > {tol}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16], ids=str)
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_backward_option_matrix(shape, dtype):
+    inputs, dy, dfinal = _inputs(shape, seed=sum(shape) + 3)
+    ref = _oracle_grads(inputs, dy, dfinal, True, dtype)
+    got = _gpu_grads(inputs, dy, dfinal, True, dtype)
+    _compare(got, ref, GRAD_TOL[dtype], f"{shape} {dtype}")
+
+
+def test_reference_gradient_case():
+    """The reference's own gradient check (benchmarks/verify_mamba2_chunk.py:269-290):
+    (2, 21, 4, 4, 2, 5), chunk 8, every option, loss sum(y^2) + sum(state^2), fp32
+    gradients against float64 autograd of the recurrence, max-relative error 1e-5."""
+    shape = (2, 21, 4, 4, 2, 5)
+    x, dt, A, B, C = _problem(*shape, seed=13)
+    opt = _options(2, 21, 4, 4, 5, seed=14)
+
+    def grads(device, dtype, fn):
+        leaves = [t.to(device, dtype).requires_grad_(True) for t in (x, dt, A, B, C)]
+        kw = {k: v.to(device, dtype).requires_grad_(True) for k, v in opt.items()}
+        y, s = fn(*leaves, D=kw["D"], z=kw["z"], dt_bias=kw["dt_bias"], dt_softplus=True,
+                  initial_states=kw["initial_states"])
+        loss = (y * y).sum() + (s * s).sum()
+        return torch.autograd.grad(loss, (*leaves, kw["D"], kw["z"], kw["dt_bias"], kw["initial_states"]))
+
+    fast = grads(DEV, torch.float32, lambda *a, **k: _api()(*a[:5], 8, **k))
+    slow = grads("cpu", torch.float64, oracle.mamba2_chunk_scan_recurrence)
+    for name, got, ref in zip(("x", "dt", "A", "B", "C", "D", "z", "dt_bias", "init"), fast, slow):
+        assert max_rel(got, ref) <= 1e-5, f"grad {name}: {max_rel(got, ref):.3e}"
+
+
+@pytest.mark.parametrize("case", [
+    dict(options=()),
+    dict(options=("D",), d_row=True),
+    dict(options=("z",)),
+    dict(options=("dt_bias",), softplus=False),
+    dict(options=("initial_states",), dfinal=False),
+    dict(options=("D", "z"), dy=False),
+    dict(options=("D", "z", "dt_bias", "initial_states"), d_row=True, softplus=False),
+], ids=lambda c: "-".join(c["options"]) + ("-row" if c.get("d_row") else "") +
+       ("-nosp" if c.get("softplus") is False else "") + ("-nodfin" if c.get("dfinal") is False else "") +
+       ("-nody" if c.get("dy") is False else ""))
+def test_backward_each_option(case):
+    shape = (2, 150, 4, 5, 2, 3)
+    inputs, dy, dfinal = _inputs(shape, seed=5, options=case["options"], d_row=case.get("d_row", False))
+    if not case.get("softplus", True):
+        inputs["dt"] = inputs["dt"].abs() * 0.2 + 0.3
+    dy = dy if case.get("dy", True) else None
+    dfinal = dfinal if case.get("dfinal", True) else None
+    ref = _oracle_grads(inputs, dy, dfinal, case.get("softplus", True))
+    got = _gpu_grads(inputs, dy, dfinal, case.get("softplus", True), torch.float32)
+    _compare(got, ref, 1e-4, str(case))
+
+
+def test_backward_deterministic_and_graph_free_outputs():
+    shape = (2, 300, 8, 64, 2, 64)
+    inputs, dy, dfinal = _inputs(shape, seed=9)
+    a = _gpu_grads(inputs, dy, dfinal, True, torch.bfloat16)
+    b = _gpu_grads(inputs, dy, dfinal, True, torch.bfloat16)
+    for k in a:
+        assert torch.equal(a[k], b[k]), k
+
+
+def test_backward_empty_sequence():
+    inputs, dy, dfinal = _inputs((2, 0, 4, 6, 2, 5), seed=1)
+    got = _gpu_grads(inputs, dy, dfinal, True, torch.float32)
+    assert torch.equal(got["initial_states"].cpu(), dfinal.float())
+    for k in ("A", "D", "dt_bias"):
+        assert torch.count_nonzero(got[k]) == 0, k
+    assert got["x"].shape == (2, 0, 4, 6)
+
+
+def test_config4_backward_prefix():
+    """Config 4 geometry (b4 L4096 H64 P64 N128, bf16) with dy zero after 384 tokens and
+    no final-state gradient: by causality the exact gradients of the first 384 tokens
+    (and of A, D, dt_bias) are those of the 384-token problem, which the oracle runs,
+    and every per-token gradient after the prefix is zero."""
+    batch, length, nheads, headdim, ngroups, dstate = 4, 4096, 64, 64, 1, 128
+    cut = 384
+    p = ssd_problem(batch, length, nheads, headdim, ngroups, dstate, seed=4, act=torch.bfloat16, init=False)
+    p.pop("initial_states")
+    g = torch.Generator().manual_seed(44)
+    dy = torch.zeros(batch, length, nheads, headdim, dtype=torch.float64)
+    dy[:1, :cut] = torch.randn(1, cut, nheads, headdim, generator=g, dtype=torch.float64)
+    leaves = {k: v.detach().to(DEV).requires_grad_(True) for k, v in p.items()}
+    kw = {k: leaves[k] for k in ("D", "z", "dt_bias")}
+    y, _ = _api()(leaves["x"], leaves["dt"], leaves["A"], leaves["B"], leaves["C"], 256, **kw, dt_softplus=True)
+    (y.double() * dy.to(DEV)).sum().backward()
+    got = {k: v.grad for k, v in leaves.items()}
+    pre = {k: (v[:1, :cut] if k in ("x", "dt", "B", "C", "z") else v).detach().double().requires_grad_(True)
+           for k, v in p.items()}
+    yr, _ = oracle.mamba2_chunk_scan_composition(
+        pre["x"], pre["dt"], pre["A"], pre["B"], pre["C"], chunk_size=128, D=pre["D"], z=pre["z"],
+        dt_bias=pre["dt_bias"], dt_softplus=True)
+    (yr * dy[:1, :cut]).sum().backward()
+    for k, v in pre.items():
+        gk = got[k]
+        if k in ("x", "dt", "B", "C", "z"):
+            assert torch.count_nonzero(gk[:, cut:]) == 0 and torch.count_nonzero(gk[1:]) == 0, k
+            gk = gk[:1, :cut]
+        err = norm_rel(gk, v.grad)
+        assert err <= 3e-2, f"d{k} {err:.3e}"
