@@ -218,6 +218,113 @@ def decode_cpu_baseline(steps=4):
                       f"{per * 1e3:.1f} ms per step"}
 
 
+# --------------------------------------------------------------------- Mamba-2 SSD
+
+
+def ssd_flops(batch, length, nheads, headdim, ngroups, dstate, q):
+    """Algorithmic FLOPs per kernel, causal count: each contraction once, lower triangles only.
+
+    Per token and head: P(Q+1) for the masked scores . X product, 2NP for the chunk
+    state and 2NP for C . state; per token and group N(Q+1) for C . B^T.  The backward
+    does two gradient contractions per forward one.  The backward's recompute of the
+    chunk output (ssd_gate) is not algorithmic work and is reported apart.
+    """
+    tok = batch * length
+    P, N, H, G = headdim, dstate, nheads, ngroups
+    tri_x = tok * H * P * (q + 1)
+    state = tok * H * 2 * N * P
+    cb = tok * G * N * (q + 1)
+    return {
+        "ssd_cb": cb, "ssd_chunk_state": state, "ssd_chunk_scan": tri_x + state,
+        "ssd_chunk_state_bwd": state, "ssd_du": tri_x + state, "ssd_dcb": tri_x,
+        "ssd_dbc_state": 2 * state, "ssd_dbc_final": 2 * cb,
+    }, {"ssd_gate": tri_x + state}
+
+
+def ssd_bytes(batch, length, nheads, headdim, ngroups, dstate, act=2):
+    """Algorithmic bytes (fwd, bwd): each input read once, each output written once."""
+    e = batch * length * nheads * headdim
+    bc = batch * length * ngroups * dstate
+    dtb = batch * length * nheads * 4
+    st = batch * nheads * headdim * dstate * act
+    fwd = 3 * e * act + dtb + 2 * bc * act + st                  # x, z in, y out; dt; B, C; final
+    bwd = 5 * e * act + 2 * dtb + 4 * bc * act + st              # x, z, dy in; dx, dz out; dt, ddt; B, C, dB, dC; d_final
+    return fwd, bwd
+
+
+def ssd_case(steps, warmup, batch=4, length=4096, nheads=64, headdim=64, ngroups=1, dstate=128, chunk=256):
+    from cases import ssd_problem
+    from metal_kernelops.cv import mamba2_chunk_scan
+    dev = torch.device("cuda")
+    p = ssd_problem(batch, length, nheads, headdim, ngroups, dstate, seed=0, act=torch.bfloat16, init=False)
+    leaves = {k: v.to(dev).requires_grad_(True) for k, v in p.items() if v is not None}
+    g = torch.Generator().manual_seed(1)
+    dy = torch.randn(batch, length, nheads, headdim, generator=g).bfloat16().to(dev)
+    dfinal = torch.randn(batch, nheads, headdim, dstate, generator=g).bfloat16().to(dev)
+    order = list(leaves.values())
+    names = ("x", "dt", "A", "B", "C")
+
+    def step():
+        y, s = mamba2_chunk_scan(*(leaves[k] for k in names), chunk, D=leaves["D"], z=leaves["z"],
+                                 dt_bias=leaves["dt_bias"], dt_softplus=True)
+        torch.autograd.grad((y, s), order, (dy, dfinal))
+
+    ms, wall, kernels = timed(step, steps, warmup)
+    flops, recompute = ssd_flops(batch, length, nheads, headdim, ngroups, dstate, chunk)
+    total = sum(flops.values())
+    fwd_b, bwd_b = ssd_bytes(batch, length, nheads, headdim, ngroups, dstate)
+    per = {k: v[0] / max(v[1], 1) for k, v in kernels.items()}
+    mfma = {}
+    for k, f in {**flops, **recompute}.items():
+        if k in per:
+            tf = f / (per[k] * 1e-3) / 1e12
+            mfma[k] = {"ms": round(per[k], 4), "gflop": round(f / 1e9, 2), "tflops": round(tf, 1),
+                       "frac": round(tf / BF16_PEAK_TFLOPS, 4), "recompute": k in recompute}
+    name = max((k for k in per if k in flops), key=lambda k: per[k])
+    achieved = flops[name] / (per[name] * 1e-3) / 1e12
+    roof = {"bound": "mfma", "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
+            "traffic": load_traffic(f"{name}@{batch}x{length}x{nheads}x{headdim}x{dstate}"),
+            "kernel": name, "algorithmic_gflop": round(flops[name] / 1e9, 2)}
+    del leaves, dy, dfinal
+    torch.cuda.empty_cache()
+    tflops = total / (ms * 1e-3) / 1e12
+    return {"ms_per_step": ms, "wall_ms_per_step": wall, "tokens_per_s": batch * length / (ms * 1e-3),
+            "gflop_per_step": total / 1e9, "tflops": tflops, "mfma_frac": tflops / BF16_PEAK_TFLOPS,
+            "gbs": (fwd_b + bwd_b) / (ms * 1e-3) / 1e9, "bytes_per_step": fwd_b + bwd_b,
+            "roofline": roof, "kernels": mfma,
+            "kernels_ms": {k: round(v, 4) for k, v in sorted(per.items())}}
+
+
+def ssd_cpu_baseline(batch=4, length=4096):
+    """The reference's CPU composition (oracle restatement) at the c4 shape."""
+    import oracle
+    from cases import ssd_problem
+    torch.set_num_threads(os.cpu_count() or 1)
+    p = ssd_problem(batch, length, 64, 64, 1, 128, seed=0, act=torch.bfloat16, init=False)
+    leaves = {k: v.requires_grad_(True) for k, v in p.items() if v is not None}
+    dy = torch.randn(batch, length, 64, 64, generator=torch.Generator().manual_seed(1)).bfloat16()
+
+    def run():
+        y, _ = oracle.mamba2_chunk_scan_composition(
+            leaves["x"], leaves["dt"], leaves["A"], leaves["B"], leaves["C"], chunk_size=256, D=leaves["D"],
+            z=leaves["z"], dt_bias=leaves["dt_bias"], dt_softplus=True)
+        torch.autograd.grad(y, list(leaves.values()), dy)
+
+    run()
+    best = None
+    for _ in range(2):
+        t0 = time.perf_counter()
+        run()
+        dt = time.perf_counter() - t0
+        best = dt if best is None else min(best, dt)
+    return {"value": round(batch * length / best, 1), "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"SSD fwd+bwd, batch {batch} x seqlen {length} at the c4 head shape (H64 P64 N128, chunk 256), "
+                      f"bf16 chunked composition with autograd (oracle/ssm.py), best of 2 after 1 warm-up: "
+                      f"{best:.2f} s"}
+
+
 # --------------------------------------------------------------------- main
 
 
@@ -227,7 +334,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-cpu", action="store_true", help="skip the CPU baseline legs")
-    ap.add_argument("--only", choices=["mamba1", "decode", "all"], default="all")
+    ap.add_argument("--only", choices=["mamba1", "ssd", "decode", "all"], default="all",
+                    help="one workload (mamba1 = the config-3 headline alone) or all of them")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -238,10 +346,29 @@ def main():
         sys.exit(1)
     torch.backends.cuda.matmul.allow_tf32 = False
 
-    log("mamba1 config 3 (4x5120x4096) fwd+bwd")
-    head = mamba1_case(4, 5120, 4096, args.steps, args.warmup)
-    log(f"  {head['ms_per_step']:.3f} ms/step, {head['gbs']:.1f} GB/s; kernels {head['kernels_ms']}")
     also = {}
+    want = (lambda w: args.only in (w, "all"))
+    if want("ssd"):
+        log("mamba2 SSD config 4 (4x4096, H64 P64 N128, chunk 256) fwd+bwd")
+        ssd = ssd_case(args.steps, args.warmup)
+        also["mamba2_ssd_chunk_scan_fwd_bwd"] = {
+            "value": round(ssd["tokens_per_s"], 1), "unit": "tokens/s",
+            "ms_per_step": round(ssd["ms_per_step"], 4),
+            "gflop_per_step": round(ssd["gflop_per_step"], 2), "tflops": round(ssd["tflops"], 1),
+            "mfma_frac_whole_step": round(ssd["mfma_frac"], 4),
+            "hbm_gbs_whole_step": round(ssd["gbs"], 1),
+            "hbm_frac_whole_step": round(ssd["gbs"] / HBM_PEAK_GBS, 4),
+            "config": {"batch": 4, "seqlen": 4096, "nheads": 64, "headdim": 64, "dstate": 128, "ngroups": 1,
+                       "chunk_size": 256, "io_dtype": "bf16", "dt_dtype": "f32"},
+            "roofline": ssd["roofline"], "kernels": ssd["kernels"], "kernels_ms": ssd["kernels_ms"]}
+        log(f"  {ssd['ms_per_step']:.3f} ms/step, {ssd['tokens_per_s'] / 1e6:.2f} M tokens/s, "
+            f"{ssd['tflops']:.1f} TFLOP/s ({100 * ssd['mfma_frac']:.1f}% MFMA), {ssd['gbs']:.0f} GB/s; "
+            f"kernels {ssd['kernels_ms']}")
+    head = None
+    if want("mamba1"):
+        log("mamba1 config 3 (4x5120x4096) fwd+bwd")
+        head = mamba1_case(4, 5120, 4096, args.steps, args.warmup)
+        log(f"  {head['ms_per_step']:.3f} ms/step, {head['gbs']:.1f} GB/s; kernels {head['kernels_ms']}")
     if args.only == "all":
         log("mamba1 config 2 (8x1536x2048) fwd+bwd")
         c2 = mamba1_case(8, 1536, 2048, args.steps, args.warmup)
@@ -250,6 +377,7 @@ def main():
             "config": {"batch": 8, "dim": 1536, "seqlen": 2048, "dstate": 16, "ngroups": 1},
             "roofline": c2["roofline"], "kernels_ms": c2["kernels_ms"]}
         log(f"  {c2['ms_per_step']:.3f} ms/step, {c2['gbs']:.1f} GB/s")
+    if want("decode"):
         log("mamba2 decode config 5 (256x80x64x128), 1024 in-place steps")
         dec = decode_case()
         also["mamba2_decode_state_rmw"] = {
@@ -259,6 +387,9 @@ def main():
                        "state_dtype": "f32", "io_dtype": "bf16"},
             "roofline": dec["roofline"], "kernels_ms": dec["kernels_ms"]}
         log(f"  {dec['ms_per_step'] * 1e3:.1f} us/step, {dec['state_rmw_gbs']:.1f} GB/s state RMW")
+    if head is None:  # a single non-headline workload: print its own record
+        print(json.dumps(also), flush=True)
+        return
     cpu = None
     if not args.skip_cpu:
         log("cpu baseline (mamba1 sample)")
@@ -266,6 +397,8 @@ def main():
         log(f"  {cpu['sample']}")
         if "mamba2_decode_state_rmw" in also:
             also["mamba2_decode_state_rmw"]["cpu_baseline"] = decode_cpu_baseline()
+        if "mamba2_ssd_chunk_scan_fwd_bwd" in also:
+            also["mamba2_ssd_chunk_scan_fwd_bwd"]["cpu_baseline"] = ssd_cpu_baseline()
     line = {
         "metric": METRIC,
         "value": round(head["gbs"], 1),

@@ -572,7 +572,7 @@ void launch_bwd_t(const Geo& g, const BwdPlan& pl, const Ptrs& q, hipStream_t s)
   const unsigned bh = static_cast<unsigned>(g.batch * g.nheads);
   const unsigned ncg = static_cast<unsigned>(g.nc * g.ngroups);
   MKO_TIMED("ssd_gate", s, gate<TM><<<dim3(g.qb * pl.npt, g.nc, bh), 256, 0, s>>>(g, pl, q));
-  MKO_TIMED("ssd_chunk_state", s,
+  MKO_TIMED("ssd_chunk_state_bwd", s,
             chunk_state<TM, true><<<dim3(pl.npt * pl.nnt, g.nc, bh), 256, 0, s>>>(g, q, q.dstates));
   MKO_TIMED("ssd_state_rev", s, state_rev<<<dim3(pl.nblk, bh), 256, 0, s>>>(g, pl, q));
   MKO_TIMED("ssd_du", s, du_kernel<TM><<<dim3(g.qb * pl.npt, g.nc, bh), 256, 0, s>>>(g, pl, q));
@@ -620,7 +620,7 @@ extern "C" int mko_ssd_bwd(const mko_ssd_params* prm, void* stream) {
   const BwdLayout lay = bwd_layout(g, pl, prm->z != nullptr);
   if (prm->workspace_bytes < lay.total || (lay.total && !prm->workspace)) {
     mko_set_error("ssd_bwd: workspace of %zu bytes needed, %zu given", lay.total, prm->workspace_bytes);
-    return MKO_EINVAL;
+    return MKO_EWORKSPACE;
   }
   Ptrs q = base_ptrs(prm);
   bind_saved(g, prm->saved, &q);

@@ -174,6 +174,7 @@ def _setup(ctx, inputs, output):
     x, dt, A, B, C, D, z, dt_bias, init, softplus = inputs
     ctx.save_for_backward(x, dt, A, B, C, D, z, dt_bias, init, output[2])
     ctx.softplus = softplus
+    ctx.set_materialize_grads(False)  # no zero-filled gradient for the save area
 
 
 def _backward(ctx, dy, dfinal, _dsaved):
