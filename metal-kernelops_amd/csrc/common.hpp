@@ -32,15 +32,9 @@ template <>
 __device__ __forceinline__ _Float16 from_f32<_Float16>(float v) { return static_cast<_Float16>(v); }
 template <>
 __device__ __forceinline__ bf16 from_f32<bf16>(float v) {
-  // Round to nearest even; NaN stays a quiet NaN.
-  uint32_t u = __float_as_uint(v);
+  // Round to nearest even (v_cvt_pk_bf16_f32); NaN stays NaN.
   bf16 r;
-  if ((u & 0x7fffffffu) > 0x7f800000u) {
-    r.bits = static_cast<uint16_t>((u >> 16) | 0x40u);
-  } else {
-    u += 0x7fffu + ((u >> 16) & 1u);
-    r.bits = static_cast<uint16_t>(u >> 16);
-  }
+  r.bits = __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
   return r;
 }
 

@@ -20,9 +20,10 @@ typedef _Float16 mfma_f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 // Leading dimension (elements) of a 64-wide K-contiguous LDS operand tile: padded so
-// the 16-byte reads of eight consecutive rows fall in distinct banks.
+// the 16-byte (16-bit types) or 4-byte (fp32) operand reads of consecutive rows fall in
+// distinct banks, and even so that row pairs can be written as one word.
 template <typename TM>
-constexpr int tile_ld() { return sizeof(TM) == 2 ? 72 : 65; }
+constexpr int tile_ld() { return sizeof(TM) == 2 ? 72 : 66; }
 
 template <typename TM>
 struct LdsTile {

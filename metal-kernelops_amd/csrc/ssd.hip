@@ -49,7 +49,8 @@ __global__ void __launch_bounds__(256) prep(Geo g, Ptrs p) {
 
 template <typename TM>
 __global__ void __launch_bounds__(256) cb_kernel(Geo g, Ptrs p) {
-  __shared__ TM sa[LdsTile<TM>::elems], sb[LdsTile<TM>::elems];
+  constexpr int TE = LdsTile<TM>::elems;
+  __shared__ __align__(16) TM sbuf[2][2 * TE];
   // lower-triangular tile (i, j), j <= i
   const int idx = blockIdx.x;
   int i = 0;
@@ -60,71 +61,111 @@ __global__ void __launch_bounds__(256) cb_kernel(Geo g, Ptrs p) {
   const int lane = threadIdx.x & 63;
   int wm, wn;
   quadrant(threadIdx.x >> 6, wm, wn);
-  const int64_t tc0 = static_cast<int64_t>(c) * g.q + 64 * i, tb0 = static_cast<int64_t>(c) * g.q + 64 * j;
+  const int r0 = blk_r0(), c0 = blk_c0();
+  const int64_t tc = static_cast<int64_t>(c) * g.q;
+  const TM* Cm = static_cast<const TM*>(p.C);
+  const TM* Bm = static_cast<const TM*>(p.B);
+  V8<TM> ra[2], rb[2];
+  auto fetch = [&](int k) {
+    load_bc2(g, Cm, b, tc + 64 * i, gg, 64 * k, ra);
+    load_bc2(g, Bm, b, tc + 64 * j, gg, 64 * k, rb);
+  };
   f32x16 acc;
   zero(acc);
-  for (int n0 = 0; n0 < g.dstate; n0 += 64) {
-    stage<TM, false>(sa, [&](int r, int k) {
-      const int64_t t = tc0 + r;
-      const int n = n0 + k;
-      return (t < g.length && n < g.dstate) ? load_one(p.C, g.bc_dtype, ((b * g.length + t) * g.ngroups + gg) * g.dstate + n) : 0.0f;
-    });
-    stage<TM, false>(sb, [&](int s, int k) {
-      const int64_t t = tb0 + s;
-      const int n = n0 + k;
-      return (t < g.length && n < g.dstate) ? load_one(p.B, g.bc_dtype, ((b * g.length + t) * g.ngroups + gg) * g.dstate + n) : 0.0f;
-    });
+  fetch(0);
+  for (int k = 0; k < g.nnt; ++k) {
+    TM* buf = sbuf[k & 1];
+    float a[8], bb[8];
+    v8_f32(ra[0], a);
+    v8_f32(ra[1], bb);
+    put2x8<TM, false>(buf, r0, c0, a, bb);  // A[l][n] = C_l[n]
+    v8_f32(rb[0], a);
+    v8_f32(rb[1], bb);
+    put2x8<TM, false>(buf + TE, r0, c0, a, bb);  // Bt[s][n] = B_s[n]
     __syncthreads();
-    mma_tile<TM>(acc, sa, sb, wm, wn, lane, 64);
-    __syncthreads();
+    if (k + 1 < g.nnt) fetch(k + 1);
+    mma_tile<TM>(acc, buf, buf + TE, wm, wn, lane, 64);
   }
   float* out = p.cb + ((b * g.nc + c) * g.ngroups + gg) * g.q * g.q;
 #pragma unroll
   for (int r = 0; r < 16; ++r) out[(64 * i + acc_row(wm, lane, r)) * g.q + 64 * j + acc_col(wn, lane)] = acc[r];
 }
 
-// Entering state of every chunk (in place over the local states) and the final state.
+// Entering state of every chunk (in place over the local states) and the final
+// state, 8 consecutive state elements per thread, sequential over the chunks.
+template <typename TM>
 __global__ void __launch_bounds__(256) state_pass(Geo g, Ptrs p) {
   const int64_t pn = g.headdim * g.dstate;
-  const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (e >= pn) return;
+  const int64_t e0 = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 8;
+  if (e0 >= pn) return;
+  const int n = static_cast<int>(pn - e0 < 8 ? pn - e0 : 8);
   const int64_t bh = blockIdx.y;
-  float s = p.init ? load_one(p.init, g.x_dtype, bh * pn + e) : 0.0f;
-  for (int c = 0; c < g.nc; ++c) {
-    const int64_t o = (bh * g.nc + c) * pn + e;
-    const float loc = p.states[o];
-    p.states[o] = s;
-    s = fmaf(fast_exp(p.cs[(bh * g.nc + c) * g.q + g.q - 1]), s, loc);
+  TM* st = static_cast<TM*>(p.states);
+  float s[8];
+  if (p.init) {
+    V8<TM> v;
+    v8_load(v, static_cast<const TM*>(p.init) + bh * pn + e0, n, g.vec);
+    v8_f32(v, s);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) s[k] = 0.0f;
   }
-  store_one(p.final_state, g.x_dtype, bh * pn + e, s);
+  for (int c = 0; c < g.nc; ++c) {
+    TM* o = st + (bh * g.nc + c) * pn + e0;
+    V8<TM> v;
+    v8_load(v, o, n, g.vec);
+    float loc[8];
+    v8_f32(v, loc);
+    v8_store(o, n, g.vec, s);
+    const float eT = fast_exp(p.cs[(bh * g.nc + c) * g.q + g.q - 1]);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) s[k] = fmaf(eT, s[k], loc[k]);
+  }
+  v8_store(static_cast<TM*>(p.final_state) + bh * pn + e0, n, g.vec, s);
 }
 
 template <typename TM>
 __global__ void __launch_bounds__(256) chunk_scan(Geo g, Ptrs p) {
-  __shared__ TM sa[LdsTile<TM>::elems], sb[LdsTile<TM>::elems];
-  __shared__ float csr[64], css[64], eo[64];
+  constexpr int TE = LdsTile<TM>::elems;
+  __shared__ __align__(16) TM sbuf[2][2 * TE];
+  __shared__ float csc[256], dlc[256];
   const int i = blockIdx.x % g.qb, pt = blockIdx.x / g.qb;
   const int c = blockIdx.y;
   const int64_t bh = blockIdx.z, b = bh / g.nheads, h = bh % g.nheads;
   const int lane = threadIdx.x & 63;
   int wm, wn;
   quadrant(threadIdx.x >> 6, wm, wn);
+  const int r0 = blk_r0(), c0 = blk_c0();
+  load_chunk_cs(g, p, bh, c, csc, dlc);
+  __syncthreads();
   f32x16 acc;
-  chunk_out<TM>(g, p, acc, sa, sb, csr, css, eo, i, pt, c, bh);
-  const int64_t tl0 = static_cast<int64_t>(c) * g.q + 64 * i;
+  chunk_out<TM>(g, p, acc, sbuf, csc, dlc, i, pt, c, bh);
+  // epilogue through LDS: each thread owns rows r0, r0+1 and 8 consecutive d_head columns
+  float* red = reinterpret_cast<float*>(&sbuf[0][0]);
+  acc_to_lds(red, acc, wm, wn, lane);
+  __syncthreads();
+  float v[2][8];
+  lds_block(red, r0, c0, v[0], v[1]);
+  const int64_t tl0 = static_cast<int64_t>(c) * g.q + 64 * i, pc = static_cast<int64_t>(pt) * 64 + c0;
+  V8<TM> xv[2], zv[2];
+  load_x2(g, static_cast<const TM*>(p.x), b, tl0, h, pt * 64, xv);
+  if (p.z) load_x2(g, static_cast<const TM*>(p.z), b, tl0, h, pt * 64, zv);
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int64_t t = tl0 + acc_row(wm, lane, r);
-    const int64_t pc = static_cast<int64_t>(pt) * 64 + acc_col(wn, lane);
-    if (t >= g.length || pc >= g.headdim) continue;
-    const int64_t xi = ((b * g.length + t) * g.nheads + h) * g.headdim + pc;
-    float v = acc[r];
-    if (p.D) v = fmaf(g.d_per_row ? p.D[h * g.headdim + pc] : p.D[h], load_one(p.x, g.x_dtype, xi), v);
-    if (p.z) {
-      const float zv = load_one(p.z, g.x_dtype, xi);
-      v *= zv * sigmoid(zv);
+  for (int rr = 0; rr < 2; ++rr) {
+    const int64_t t = tl0 + r0 + rr;
+    const int n = t < g.length ? static_cast<int>(g.headdim - pc) : 0;
+    if (n <= 0) continue;
+    float xf[8], zf[8];
+    v8_f32(xv[rr], xf);
+    if (p.z) v8_f32(zv[rr], zf);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      float y = v[rr][k];
+      if (p.D && k < n) y = fmaf(g.d_per_row ? p.D[h * g.headdim + pc + k] : p.D[h], xf[k], y);
+      if (p.z) y *= zf[k] * sigmoid(zf[k]);
+      v[rr][k] = y;
     }
-    store_one(p.y, g.x_dtype, xi, v);
+    v8_store(static_cast<TM*>(p.y) + xidx(g, b, t, h, pc), n, g.vec, v[rr]);
   }
 }
 
@@ -152,6 +193,10 @@ int make_geo(const mko_ssd_params* prm, Geo* g) {
       return MKO_EINVAL;
     }
   }
+  if (prm->bc_dtype != prm->x_dtype) {
+    mko_set_error("ssd: B and C must have the dtype of x");
+    return MKO_EINVAL;
+  }
   // Longer chunks give the matrix cores deeper products; fp32 inputs keep 64-token
   // chunks, where the in-chunk decay exponents (differences of cumulative sums) stay
   // small and the gradient with respect to them keeps fp32 accuracy.
@@ -159,9 +204,18 @@ int make_geo(const mko_ssd_params* prm, Geo* g) {
   g->q = 64 * g->qb;
   g->nc = static_cast<int>((g->length + g->q - 1) / g->q);
   g->hpg = static_cast<int>(g->nheads / g->ngroups);
+  g->npt = static_cast<int>((g->headdim + 63) / 64);
+  g->nnt = static_cast<int>((g->dstate + 63) / 64);
+  g->nnp = (g->nnt + 1) / 2;
   g->x_dtype = prm->x_dtype;
   g->dt_dtype = prm->dt_dtype;
-  g->bc_dtype = prm->bc_dtype;
+  // 16-byte vectors of 8 elements: whole runs of d_head and d_state, aligned bases
+  bool vec = g->headdim % 8 == 0 && g->dstate % 8 == 0;
+  const void* ptrs[] = {prm->x,  prm->z,      prm->B,  prm->C,  prm->initial_states, prm->y,
+                        prm->final_state, prm->saved, prm->dy, prm->dfinal, prm->dx, prm->dz,
+                        prm->dB, prm->dC, prm->dinitial, prm->workspace};
+  for (const void* q : ptrs) vec = vec && (reinterpret_cast<uintptr_t>(q) % 16 == 0);
+  g->vec = vec ? 1 : 0;
   g->softplus = (prm->flags & MKO_SSD_SOFTPLUS) ? 1 : 0;
   g->d_per_row = (prm->flags & MKO_SSD_D_PER_ROW) ? 1 : 0;
   return MKO_OK;
@@ -171,7 +225,7 @@ SavedLayout saved_layout(const Geo& g) {
   SavedLayout l{};
   const size_t bh = static_cast<size_t>(g.batch * g.nheads);
   size_t o = 0;
-  l.states = o; o = align256(o + bh * g.nc * g.headdim * g.dstate * 4);
+  l.states = o; o = align256(o + bh * g.nc * g.headdim * g.dstate * dtype_size(g.x_dtype));
   l.dl = o; o = align256(o + bh * g.nc * g.q * 4);
   l.cs = o; o = align256(o + bh * g.nc * g.q * 4);
   l.cb = o; o = align256(o + static_cast<size_t>(g.batch) * g.nc * g.ngroups * g.q * g.q * 4);
@@ -182,7 +236,7 @@ SavedLayout saved_layout(const Geo& g) {
 void bind_saved(const Geo& g, void* saved, Ptrs* q) {
   const SavedLayout l = saved_layout(g);
   char* s = static_cast<char*>(saved);
-  q->states = reinterpret_cast<float*>(s + l.states);
+  q->states = s + l.states;
   q->dl = reinterpret_cast<float*>(s + l.dl);
   q->cs = reinterpret_cast<float*>(s + l.cs);
   q->cb = reinterpret_cast<float*>(s + l.cb);
@@ -218,14 +272,15 @@ Ptrs base_ptrs(const mko_ssd_params* prm) {
 template <typename TM>
 static void launch_fwd_t(const Geo& g, const Ptrs& q, hipStream_t s) {
   const unsigned bh = static_cast<unsigned>(g.batch * g.nheads);
-  const unsigned pt = static_cast<unsigned>((g.headdim + 63) / 64), nt = static_cast<unsigned>((g.dstate + 63) / 64);
   MKO_TIMED("ssd_prep", s, prep<<<dim3(g.nc, g.nheads, g.batch), 256, 0, s>>>(g, q));
   MKO_TIMED("ssd_cb", s,
             cb_kernel<TM><<<dim3(g.qb * (g.qb + 1) / 2, g.nc * g.ngroups, g.batch), 256, 0, s>>>(g, q));
-  MKO_TIMED("ssd_chunk_state", s, chunk_state<TM, false><<<dim3(pt * nt, g.nc, bh), 256, 0, s>>>(g, q, q.states));
+  MKO_TIMED("ssd_chunk_state", s,
+            chunk_state<TM, false><<<dim3(g.npt * g.nnp, g.nc, bh), 256, 0, s>>>(g, q, q.states));
   MKO_TIMED("ssd_state_pass", s,
-            state_pass<<<dim3(static_cast<unsigned>((g.headdim * g.dstate + 255) / 256), bh), 256, 0, s>>>(g, q));
-  MKO_TIMED("ssd_chunk_scan", s, chunk_scan<TM><<<dim3(g.qb * pt, g.nc, bh), 256, 0, s>>>(g, q));
+            state_pass<TM><<<dim3(static_cast<unsigned>((g.headdim * g.dstate + 2047) / 2048), bh), 256, 0, s>>>(
+                g, q));
+  MKO_TIMED("ssd_chunk_scan", s, chunk_scan<TM><<<dim3(g.qb * g.npt, g.nc, bh), 256, 0, s>>>(g, q));
 }
 
 }  // namespace ssd
@@ -261,9 +316,11 @@ extern "C" int mko_ssd_fwd(const mko_ssd_params* prm, void* stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (g.length == 0) {
     // no tokens: the final state is the initial state (or zero)
-    MKO_TIMED("ssd_state_pass", s,
-              state_pass<<<dim3(static_cast<unsigned>((g.headdim * g.dstate + 255) / 256),
-                                static_cast<unsigned>(g.batch * g.nheads)), 256, 0, s>>>(g, q));
+    const dim3 grid(static_cast<unsigned>((g.headdim * g.dstate + 2047) / 2048),
+                    static_cast<unsigned>(g.batch * g.nheads));
+    if (g.x_dtype == MKO_F32) MKO_TIMED("ssd_state_pass", s, state_pass<float><<<grid, 256, 0, s>>>(g, q));
+    else if (g.x_dtype == MKO_BF16) MKO_TIMED("ssd_state_pass", s, state_pass<bf16><<<grid, 256, 0, s>>>(g, q));
+    else MKO_TIMED("ssd_state_pass", s, state_pass<_Float16><<<grid, 256, 0, s>>>(g, q));
     return mko_check_launch("ssd_fwd");
   }
   if (g.x_dtype == MKO_F32) launch_fwd_t<float>(g, q, s);

@@ -1,10 +1,16 @@
-// Shared declarations and device helpers of the SSD chunk-scan kernels
+// Shared declarations and device code of the SSD chunk-scan kernels
 // (ssd.hip: forward, ssd_bwd.hip: backward).
+//
+// All activation-like tensors (x, z, dy, B, C, initial/final states and their
+// gradients) share one storage type TM, the operand type of the matrix cores
+// (float32, float16 or bfloat16); dt may differ.  Chunk states are stored in TM
+// too: they are matrix-core operands and the reference rounds them the same way.
 #pragma once
 
 #include "common.hpp"
 #include "io.hpp"
 #include "mma.hpp"
+#include "tile.hpp"
 
 namespace mko {
 namespace ssd {
@@ -15,16 +21,18 @@ struct Geo {
   int q;    // chunk length, 64 * qb
   int nc;   // number of chunks
   int hpg;  // heads per group
-  int x_dtype, dt_dtype, bc_dtype;
+  int npt;  // 64-wide d_head tiles
+  int nnt;  // 64-wide d_state tiles
+  int nnp;  // pairs of d_state tiles (a workgroup covers up to 128 states)
+  int x_dtype, dt_dtype;
   int softplus, d_per_row;
+  int vec;  // 16-byte vector access of 8-element runs is valid (P, N multiples of 8, aligned)
 };
 
 // Backward work split (ssd_bwd.hip).
 struct BwdPlan {
-  int npt;     // 64-wide d_head tiles
-  int nnt;     // 64-wide d_state tiles
-  int nblk;    // 256-element blocks of a (d_head x d_state) state
-  int npairs;  // lower (l-tile, s-tile) pairs of a chunk
+  int nblk;       // 2048-element blocks of a (d_head x d_state) state
+  int npairs;     // lower (l-tile, s-tile) pairs of a chunk
   int hb1, hpb1;  // head blocks (and heads per block) of the C.B^T adjoint
   int hb2, hpb2;  // head blocks (and heads per block) of the state terms of dB/dC
 };
@@ -53,19 +61,19 @@ struct Ptrs {
   float* dD;
   float* dbias;
   // forward save area
-  float* states;  // (b, H, nc, P, N) state entering each chunk
-  float* dl;      // (b, H, nc, q) step sizes (0 past the end)
-  float* cs;      // (b, H, nc, q) cumulative step * A inside the chunk
-  float* cb;      // (b, nc, G, q, q) C . B^T, lower tiles
+  void* states;  // (b, H, nc, P, N) TM: state entering each chunk
+  float* dl;     // (b, H, nc, q) step sizes (0 past the end)
+  float* cs;     // (b, H, nc, q) cumulative step * A inside the chunk
+  float* cb;     // (b, nc, G, q, q) C . B^T, lower tiles
   // backward workspace
-  const void* gy;  // (b, L, H, P) x dtype: dy * silu(z) (dy itself without z)
+  const void* gy;  // (b, L, H, P) TM: dy * silu(z) (dy itself without z)
   void* gyw;       // writable alias of gy when it is materialised
-  float* dstates;  // (b, H, nc, P, N) local state adjoints, then the adjoint of the state leaving each chunk
+  void* dstates;   // (b, H, nc, P, N) TM: local state adjoints, then G, the adjoint of the state leaving each chunk
   float* dT;       // (b, H, nc, nblk) partial e^T <G, S_in> per state block
   float* ya;       // (b, H, nc, npt, q) partial gy . (y - D x) per d_head tile
-  float* dsx;      // (b, H, nc, npt, q) partial x . du per d_head tile
-  float* ut;       // (b, H, nc, npt, q) partial u . du per d_head tile (u as the matrix cores see it)
-  float* tau;      // (b, H, nc, npt, q) partial u . du_state per d_head tile
+  float* dsx;      // (b, H, nc, npt, q) partial x . du
+  float* ut;       // (b, H, nc, npt, q) partial u . du (u as the matrix cores see it)
+  float* tau;      // (b, H, nc, npt, q) partial u . du_state
   float* pdD;      // (b, nc, qb, H, P) dD partials per 64-token tile
   float* dcb;      // (b, nc, G, hb1, q, q) head-block partials of the C.B^T adjoint
   float* pbc;      // (b, L, G, hb2, 2, N) head-block partials of the state terms of dB (0) and dC (1)
@@ -86,139 +94,234 @@ Ptrs base_ptrs(const mko_ssd_params* prm);
 
 // ------------------------------------------------------------ device helpers
 
-// Stages a 64x64 operand tile into LDS, row-major ([row][col]) or transposed
-// ([col][row]); `val(row, col)` gives the fp32 value (0 outside the problem).
-// 256 threads, 16 elements each, the column index fastest so global reads are
-// contiguous along the source row.
-template <typename TM, bool TRANS, typename F>
-__device__ __forceinline__ void stage(TM* dst, F&& val) {
-  constexpr int ld = tile_ld<TM>();
-  const int tid = threadIdx.x;
-#pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    const int e = k * 256 + tid;
-    const int row = e >> 6, col = e & 63;
-    const float v = val(row, col);
-    if (TRANS)
-      dst[col * ld + row] = from_f32<TM>(v);
-    else
-      dst[row * ld + col] = from_f32<TM>(v);
-  }
+__device__ __forceinline__ int64_t xidx(const Geo& g, int64_t b, int64_t t, int64_t h, int64_t pc) {
+  return ((b * g.length + t) * g.nheads + h) * g.headdim + pc;
+}
+__device__ __forceinline__ int64_t bcidx(const Geo& g, int64_t b, int64_t t, int64_t gg, int64_t n) {
+  return ((b * g.length + t) * g.ngroups + gg) * g.dstate + n;
 }
 
 // Writes an accumulator tile (value v[r] at (acc_row, acc_col)) to a 64x65 fp32 LDS tile.
-__device__ __forceinline__ void acc_to_lds(float* red, const float* v, int wm, int wn, int lane) {
+template <typename V>
+__device__ __forceinline__ void acc_to_lds(float* red, const V& v, int wm, int wn, int lane) {
 #pragma unroll
   for (int r = 0; r < 16; ++r) red[acc_row(wm, lane, r) * 65 + acc_col(wn, lane)] = v[r];
 }
 
-// out[p][n] = sum_l s1(l) X(l, p) Y(l, n) over the chunk, for one 64x64 (p, n) tile.
+// Loads the thread's 2x8 block of a token-major (b, L, H, P) tensor: rows = tokens
+// t0 + r0, t0 + r0 + 1 of head h, columns = d_head pc0 + c0 .. +8.
+template <typename TM>
+__device__ __forceinline__ void load_x2(const Geo& g, const TM* src, int64_t b, int64_t t0, int64_t h, int64_t pc0,
+                                        V8<TM> (&v)[2]) {
+  const int r0 = blk_r0(), c0 = blk_c0();
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr) {
+    const int64_t t = t0 + r0 + rr;
+    const int64_t pc = pc0 + c0;
+    const int n = (t < g.length) ? static_cast<int>(g.headdim - pc) : 0;
+    if (n > 0)
+      v8_load(v[rr], src + xidx(g, b, t, h, pc), n, g.vec);
+    else
+      v8_zero(v[rr]);
+  }
+}
+
+// Same for a (b, L, G, N) tensor (B or C): d_state columns nn0 + c0 .. +8.
+template <typename TM>
+__device__ __forceinline__ void load_bc2(const Geo& g, const TM* src, int64_t b, int64_t t0, int64_t gg, int64_t nn0,
+                                         V8<TM> (&v)[2]) {
+  const int r0 = blk_r0(), c0 = blk_c0();
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr) {
+    const int64_t t = t0 + r0 + rr;
+    const int64_t nn = nn0 + c0;
+    const int n = (t < g.length) ? static_cast<int>(g.dstate - nn) : 0;
+    if (n > 0)
+      v8_load(v[rr], src + bcidx(g, b, t, gg, nn), n, g.vec);
+    else
+      v8_zero(v[rr]);
+  }
+}
+
+// Same for a (P, N) state matrix: rows = d_head pc0 + r0 (+1), columns nn0 + c0 .. +8.
+template <typename TM>
+__device__ __forceinline__ void load_st2(const Geo& g, const TM* st, int64_t pc0, int64_t nn0, V8<TM> (&v)[2]) {
+  const int r0 = blk_r0(), c0 = blk_c0();
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr) {
+    const int64_t pc = pc0 + r0 + rr;
+    const int64_t nn = nn0 + c0;
+    const int n = (pc < g.headdim) ? static_cast<int>(g.dstate - nn) : 0;
+    if (n > 0)
+      v8_load(v[rr], st + pc * g.dstate + nn, n, g.vec);
+    else
+      v8_zero(v[rr]);
+  }
+}
+
+// Loads 8 fp32 of a row of cb (always in bounds, 32-byte aligned).
+__device__ __forceinline__ void load_f8(const float* p, float (&f)[8]) {
+  const float4 a = reinterpret_cast<const float4*>(p)[0];
+  const float4 b = reinterpret_cast<const float4*>(p)[1];
+  f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+  f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+}
+
+template <typename TM>
+__device__ __forceinline__ void scale8(const V8<TM>& v, float s, float (&f)[8]) {
+  v8_f32(v, f);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) f[k] *= s;
+}
+
+// out[p][n] = sum_l s1(l) X(l, p) Y(l, n) over the chunk, for one 64-row d_head tile
+// and two 64-column d_state tiles, stored in TM.
 //   FWD: X = x, s1 = step e^{T - cs}, Y = B  -> local chunk state
 //   BWD: X = gy, s1 = e^{cs}, Y = C          -> the chunk's own contribution to the
 //        adjoint of its entering state
+// Both operands are token-major in HBM and the contraction runs over tokens, so both
+// are staged transposed.  Double-buffered: the loads of the next 64 tokens are in
+// flight during the products of the current ones.
 template <typename TM, bool BWD>
-__global__ void __launch_bounds__(256) chunk_state(Geo g, Ptrs p, float* out) {
-  __shared__ TM sa[LdsTile<TM>::elems], sb[LdsTile<TM>::elems];
-  __shared__ float s1[64];
-  const int ntiles = static_cast<int>((g.dstate + 63) / 64);
-  const int pt = blockIdx.x / ntiles, nt = blockIdx.x % ntiles;
+__global__ void __launch_bounds__(256) chunk_state(Geo g, Ptrs p, void* out_) {
+  constexpr int TE = LdsTile<TM>::elems;
+  __shared__ __align__(16) TM sbuf[2][3 * TE];
+  __shared__ float s1[256];
+  const int pt = blockIdx.x / g.nnp, np = blockIdx.x % g.nnp;
   const int c = blockIdx.y;
   const int64_t bh = blockIdx.z, b = bh / g.nheads, h = bh % g.nheads, gg = h / g.hpg;
   const int lane = threadIdx.x & 63;
   int wm, wn;
   quadrant(threadIdx.x >> 6, wm, wn);
+  const int r0 = blk_r0(), c0 = blk_c0();
   const int64_t so = (bh * g.nc + c) * g.q;
   const float T = p.cs[so + g.q - 1];
-  f32x16 acc;
-  zero(acc);
-  for (int kb = 0; kb < g.qb; ++kb) {
+  for (int l = threadIdx.x; l < g.q; l += 256) {
+    const bool ok = static_cast<int64_t>(c) * g.q + l < g.length;
+    s1[l] = !ok ? 0.0f : (BWD ? fast_exp(p.cs[so + l]) : p.dl[so + l] * fast_exp(T - p.cs[so + l]));
+  }
+  const TM* X = static_cast<const TM*>(BWD ? p.gy : p.x);
+  const TM* Y = static_cast<const TM*>(BWD ? p.C : p.B);
+  const int64_t pc0 = static_cast<int64_t>(pt) * 64, nn0 = static_cast<int64_t>(np) * 128;
+  V8<TM> rx[2], ry0[2], ry1[2];
+  auto fetch = [&](int kb) {
     const int64_t t0 = static_cast<int64_t>(c) * g.q + 64 * kb;
-    if (threadIdx.x < 64) {
-      const int64_t o = so + 64 * kb + threadIdx.x;
-      const bool ok = t0 + threadIdx.x < g.length;
-      s1[threadIdx.x] = !ok ? 0.0f : (BWD ? fast_exp(p.cs[o]) : p.dl[o] * fast_exp(T - p.cs[o]));
+    load_x2(g, X, b, t0, h, pc0, rx);
+    load_bc2(g, Y, b, t0, gg, nn0, ry0);
+    load_bc2(g, Y, b, t0, gg, nn0 + 64, ry1);
+  };
+  f32x16 acc0, acc1;
+  zero(acc0);
+  zero(acc1);
+  fetch(0);
+  __syncthreads();  // s1
+  for (int kb = 0; kb < g.qb; ++kb) {
+    TM* buf = sbuf[kb & 1];
+    {
+      float a[8], bb[8];
+      scale8(rx[0], s1[64 * kb + r0], a);
+      scale8(rx[1], s1[64 * kb + r0 + 1], bb);
+      put2x8<TM, true>(buf, r0, c0, a, bb);  // A[p][l]
+      v8_f32(ry0[0], a);
+      v8_f32(ry0[1], bb);
+      put2x8<TM, true>(buf + TE, r0, c0, a, bb);  // Bt[n][l]
+      v8_f32(ry1[0], a);
+      v8_f32(ry1[1], bb);
+      put2x8<TM, true>(buf + 2 * TE, r0, c0, a, bb);
     }
     __syncthreads();
-    stage<TM, true>(sa, [&](int l, int pp) {  // A[p][l]
-      const int64_t t = t0 + l;
-      const int64_t pc = static_cast<int64_t>(pt) * 64 + pp;
-      if (t >= g.length || pc >= g.headdim) return 0.0f;
-      const int64_t xi = ((b * g.length + t) * g.nheads + h) * g.headdim + pc;
-      return s1[l] * load_one(BWD ? p.gy : p.x, g.x_dtype, xi);
-    });
-    stage<TM, true>(sb, [&](int l, int n) {  // Bt[n][l]
-      const int64_t t = t0 + l;
-      const int64_t nn = static_cast<int64_t>(nt) * 64 + n;
-      if (t >= g.length || nn >= g.dstate) return 0.0f;
-      return load_one(BWD ? p.C : p.B, g.bc_dtype, ((b * g.length + t) * g.ngroups + gg) * g.dstate + nn);
-    });
-    __syncthreads();
-    mma_tile<TM>(acc, sa, sb, wm, wn, lane, 64);
-    __syncthreads();
+    if (kb + 1 < g.qb) fetch(kb + 1);
+    mma_tile<TM>(acc0, buf, buf + TE, wm, wn, lane, 64);
+    mma_tile<TM>(acc1, buf, buf + 2 * TE, wm, wn, lane, 64);
   }
+  TM* out = static_cast<TM*>(out_) + (bh * g.nc + c) * g.headdim * g.dstate;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
-    const int64_t pp = static_cast<int64_t>(pt) * 64 + acc_row(wm, lane, r);
-    const int64_t nn = static_cast<int64_t>(nt) * 64 + acc_col(wn, lane);
-    if (pp < g.headdim && nn < g.dstate) out[((bh * g.nc + c) * g.headdim + pp) * g.dstate + nn] = acc[r];
+    const int64_t pp = pc0 + acc_row(wm, lane, r);
+    const int64_t nn = nn0 + acc_col(wn, lane);
+    if (pp < g.headdim) {
+      if (nn < g.dstate) out[pp * g.dstate + nn] = from_f32<TM>(acc0[r]);
+      if (nn + 64 < g.dstate) out[pp * g.dstate + nn + 64] = from_f32<TM>(acc1[r]);
+    }
   }
 }
 
 // Chunk output before the skip and the gate, for the 64-token tile i and d_head
 // tile pt of head (bh) in chunk c:
 //   acc[l][p] = sum_{s<=l} e^{cs_l - cs_s} CB[l][s] step_s x_s[p] + e^{cs_l} sum_n C_l[n] S_in[p][n]
-// csr/eo receive cs and e^{cs} of the tile's rows.  Leaves the workgroup synchronised
-// only on the LDS operand tiles; the caller owns the epilogue.
+// Stages 0..i are the intra-chunk tiles, then one stage per d_state tile.  csc/dlc
+// hold the chunk's cs and step (filled by the caller, visible before the call).
+// Ends with a barrier, so the caller may reuse sbuf.
 template <typename TM>
-__device__ __forceinline__ void chunk_out(const Geo& g, const Ptrs& p, f32x16& acc, TM* sa, TM* sb, float* csr,
-                                          float* css, float* eo, int i, int pt, int c, int64_t bh) {
+__device__ __forceinline__ void chunk_out(const Geo& g, const Ptrs& p, f32x16& acc, TM (*sbuf)[2 * LdsTile<TM>::elems],
+                                          const float* csc, const float* dlc, int i, int pt, int c, int64_t bh) {
+  constexpr int TE = LdsTile<TM>::elems;
   const int64_t b = bh / g.nheads, h = bh % g.nheads, gg = h / g.hpg;
   const int lane = threadIdx.x & 63;
   int wm, wn;
   quadrant(threadIdx.x >> 6, wm, wn);
-  const int64_t so = (bh * g.nc + c) * g.q;
-  const int64_t tl0 = static_cast<int64_t>(c) * g.q + 64 * i;
+  const int r0 = blk_r0(), c0 = blk_c0();
+  const int64_t tc = static_cast<int64_t>(c) * g.q;
+  const int64_t pc0 = static_cast<int64_t>(pt) * 64;
   const float* cbt = p.cb + ((b * g.nc + c) * g.ngroups + gg) * g.q * g.q;
-  if (threadIdx.x < 64) {
-    csr[threadIdx.x] = p.cs[so + 64 * i + threadIdx.x];
-    eo[threadIdx.x] = fast_exp(csr[threadIdx.x]);
-  }
+  const TM* X = static_cast<const TM*>(p.x);
+  const TM* Cm = static_cast<const TM*>(p.C);
+  const TM* S = static_cast<const TM*>(p.states) + (bh * g.nc + c) * g.headdim * g.dstate;
+  const int nstage = i + 1 + g.nnt;
+  float kf[2][8];  // cb rows (intra stages)
+  V8<TM> ra[2], rb[2];
+  auto fetch = [&](int k) {
+    if (k <= i) {
+      const int j = k;
+      load_f8(cbt + (64 * i + r0) * g.q + 64 * j + c0, kf[0]);
+      load_f8(cbt + (64 * i + r0 + 1) * g.q + 64 * j + c0, kf[1]);
+      load_x2(g, X, b, tc + 64 * j, h, pc0, rb);  // u rows s
+    } else {
+      const int64_t nn0 = static_cast<int64_t>(k - i - 1) * 64;
+      load_bc2(g, Cm, b, tc + 64 * i, gg, nn0, ra);  // C rows l
+      load_st2(g, S, pc0, nn0, rb);                  // S rows p
+    }
+  };
   zero(acc);
-  for (int j = 0; j <= i; ++j) {
-    const int64_t ts0 = static_cast<int64_t>(c) * g.q + 64 * j;
+  fetch(0);
+  for (int k = 0; k < nstage; ++k) {
+    TM* buf = sbuf[k & 1];
+    float a[8], bb[8];
+    if (k <= i) {
+      const int j = k;
+      const float cl0 = csc[64 * i + r0], cl1 = csc[64 * i + r0 + 1];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int s = 64 * j + c0 + e;
+        const float css = csc[s];
+        a[e] = (s <= 64 * i + r0) ? kf[0][e] * fast_exp(cl0 - css) : 0.0f;
+        bb[e] = (s <= 64 * i + r0 + 1) ? kf[1][e] * fast_exp(cl1 - css) : 0.0f;
+      }
+      put2x8<TM, false>(buf, r0, c0, a, bb);  // A[l][s] = K
+      scale8(rb[0], dlc[64 * j + r0], a);
+      scale8(rb[1], dlc[64 * j + r0 + 1], bb);
+      put2x8<TM, true>(buf + TE, r0, c0, a, bb);  // Bt[p][s] = step_s x_s[p]
+    } else {
+      scale8(ra[0], fast_exp(csc[64 * i + r0]), a);
+      scale8(ra[1], fast_exp(csc[64 * i + r0 + 1]), bb);
+      put2x8<TM, false>(buf, r0, c0, a, bb);  // A[l][n] = e^{cs_l} C_l[n]
+      v8_f32(rb[0], a);
+      v8_f32(rb[1], bb);
+      put2x8<TM, false>(buf + TE, r0, c0, a, bb);  // Bt[p][n] = S_in[p][n]
+    }
     __syncthreads();
-    if (threadIdx.x < 64) css[threadIdx.x] = p.cs[so + 64 * j + threadIdx.x];
-    __syncthreads();
-    stage<TM, false>(sa, [&](int r, int s) {  // K[l][s]
-      if (64 * j + s > 64 * i + r) return 0.0f;
-      return cbt[(64 * i + r) * g.q + 64 * j + s] * fast_exp(csr[r] - css[s]);
-    });
-    stage<TM, true>(sb, [&](int s, int pp) {  // Bt[p][s] = step_s x_s[p]
-      const int64_t t = ts0 + s;
-      const int64_t pc = static_cast<int64_t>(pt) * 64 + pp;
-      if (t >= g.length || pc >= g.headdim) return 0.0f;
-      return p.dl[so + 64 * j + s] * load_one(p.x, g.x_dtype, ((b * g.length + t) * g.nheads + h) * g.headdim + pc);
-    });
-    __syncthreads();
-    mma_tile<TM>(acc, sa, sb, wm, wn, lane, 64);
+    if (k + 1 < nstage) fetch(k + 1);
+    mma_tile<TM>(acc, buf, buf + TE, wm, wn, lane, 64);
   }
-  const float* st = p.states + (bh * g.nc + c) * g.headdim * g.dstate;
-  for (int n0 = 0; n0 < g.dstate; n0 += 64) {
-    __syncthreads();
-    stage<TM, false>(sa, [&](int r, int k) {  // e^{cs_l} C_l[n]
-      const int64_t t = tl0 + r;
-      const int n = n0 + k;
-      if (t >= g.length || n >= g.dstate) return 0.0f;
-      return eo[r] * load_one(p.C, g.bc_dtype, ((b * g.length + t) * g.ngroups + gg) * g.dstate + n);
-    });
-    stage<TM, false>(sb, [&](int pp, int k) {  // Bt[p][n] = S_in[p][n]
-      const int64_t pc = static_cast<int64_t>(pt) * 64 + pp;
-      const int n = n0 + k;
-      if (pc >= g.headdim || n >= g.dstate) return 0.0f;
-      return st[pc * g.dstate + n];
-    });
-    __syncthreads();
-    mma_tile<TM>(acc, sa, sb, wm, wn, lane, 64);
+  __syncthreads();
+}
+
+// Loads cs and step of a whole chunk into LDS (q <= 256 values each).
+__device__ __forceinline__ void load_chunk_cs(const Geo& g, const Ptrs& p, int64_t bh, int c, float* csc, float* dlc) {
+  const int64_t so = (bh * g.nc + c) * g.q;
+  for (int l = threadIdx.x; l < g.q; l += 256) {
+    csc[l] = p.cs[so + l];
+    dlc[l] = p.dl[so + l];
   }
 }
 

@@ -45,214 +45,280 @@ __device__ __forceinline__ float block_sum(float v, float* wsum) {
   return (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
 }
 
-__device__ __forceinline__ int64_t xidx(const Geo& g, int64_t b, int64_t t, int64_t h, int64_t pc) {
-  return ((b * g.length + t) * g.nheads + h) * g.headdim + pc;
-}
-__device__ __forceinline__ int64_t bcidx(const Geo& g, int64_t b, int64_t t, int64_t gg, int64_t n) {
-  return ((b * g.length + t) * g.ngroups + gg) * g.dstate + n;
-}
-
 template <typename TM>
 __global__ void __launch_bounds__(256) gate(Geo g, BwdPlan pl, Ptrs p) {
-  __shared__ TM sa[LdsTile<TM>::elems], sb[LdsTile<TM>::elems];
-  __shared__ float csr[64], css[64], eo[64];
-  __shared__ float red[64 * 65];
+  constexpr int TE = LdsTile<TM>::elems;
+  __shared__ __align__(16) TM sbuf[2][2 * TE];
+  __shared__ float csc[256], dlc[256];
+  __shared__ float colred[4][64];
   const int i = blockIdx.x % g.qb, pt = blockIdx.x / g.qb;
   const int c = blockIdx.y;
   const int64_t bh = blockIdx.z, b = bh / g.nheads, h = bh % g.nheads;
-  const int lane = threadIdx.x & 63;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int wm, wn;
-  quadrant(threadIdx.x >> 6, wm, wn);
-  f32x16 acc;
-  chunk_out<TM>(g, p, acc, sa, sb, csr, css, eo, i, pt, c, bh);
-  const int64_t tl0 = static_cast<int64_t>(c) * g.q + 64 * i;
-  float va[16], vd[16];
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int64_t t = tl0 + acc_row(wm, lane, r);
-    const int64_t pc = static_cast<int64_t>(pt) * 64 + acc_col(wn, lane);
-    va[r] = vd[r] = 0.0f;
-    if (t >= g.length || pc >= g.headdim) continue;
-    const int64_t xi = xidx(g, b, t, h, pc);
-    const float xv = load_one(p.x, g.x_dtype, xi);
-    const float dyv = load_one(p.dy, g.x_dtype, xi);
-    const float yt = acc[r];
-    float gyv = dyv;
-    if (p.z) {
-      const float zv = load_one(p.z, g.x_dtype, xi);
-      const float sg = sigmoid(zv);
-      gyv = to_f32(from_f32<TM>(dyv * zv * sg));  // as stored for the other kernels
-      float ypre = yt;
-      if (p.D) ypre = fmaf(g.d_per_row ? p.D[h * g.headdim + pc] : p.D[h], xv, ypre);
-      store_one(p.dz, g.x_dtype, xi, dyv * ypre * sg * fmaf(zv, 1.0f - sg, 1.0f));
-      store_one(p.gyw, g.x_dtype, xi, gyv);
-    }
-    va[r] = gyv * yt;
-    vd[r] = gyv * xv;
-  }
-  acc_to_lds(red, va, wm, wn, lane);
+  quadrant(wave, wm, wn);
+  const int r0 = blk_r0(), c0 = blk_c0();
+  load_chunk_cs(g, p, bh, c, csc, dlc);
   __syncthreads();
-  if (threadIdx.x < 64) {
-    float s = 0.0f;
-    for (int k = 0; k < 64; ++k) s += red[threadIdx.x * 65 + k];
-    p.ya[((bh * g.nc + c) * pl.npt + pt) * g.q + 64 * i + threadIdx.x] = s;
+  f32x16 acc;
+  chunk_out<TM>(g, p, acc, sbuf, csc, dlc, i, pt, c, bh);
+  float* red = reinterpret_cast<float*>(&sbuf[0][0]);
+  acc_to_lds(red, acc, wm, wn, lane);
+  __syncthreads();
+  float yt[2][8];
+  lds_block(red, r0, c0, yt[0], yt[1]);
+  const int64_t tl0 = static_cast<int64_t>(c) * g.q + 64 * i, pc = static_cast<int64_t>(pt) * 64 + c0;
+  V8<TM> xv[2], dyv[2], zv[2];
+  load_x2(g, static_cast<const TM*>(p.x), b, tl0, h, pt * 64, xv);
+  load_x2(g, static_cast<const TM*>(p.dy), b, tl0, h, pt * 64, dyv);
+  if (p.z) load_x2(g, static_cast<const TM*>(p.z), b, tl0, h, pt * 64, zv);
+  float dd[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) dd[k] = 0.0f;
+  const int64_t po = ((bh * g.nc + c) * g.npt + pt) * g.q + 64 * i;
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr) {
+    const int64_t t = tl0 + r0 + rr;
+    const int n = t < g.length ? static_cast<int>(g.headdim - pc) : 0;
+    float xf[8], gyf[8];
+    v8_f32(xv[rr], xf);
+    v8_f32(dyv[rr], gyf);
+    if (p.z) {
+      float zf[8], dzf[8];
+      v8_f32(zv[rr], zf);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float sg = sigmoid(zf[k]);
+        float ypre = yt[rr][k];
+        if (p.D && k < n) ypre = fmaf(g.d_per_row ? p.D[h * g.headdim + pc + k] : p.D[h], xf[k], ypre);
+        dzf[k] = gyf[k] * ypre * sg * fmaf(zf[k], 1.0f - sg, 1.0f);
+        gyf[k] = to_f32(from_f32<TM>(gyf[k] * zf[k] * sg));  // as stored for the other kernels
+      }
+      if (n > 0) {
+        const int64_t xi = xidx(g, b, t, h, pc);
+        v8_store(static_cast<TM*>(p.dz) + xi, n, g.vec, dzf);
+        v8_store(static_cast<TM*>(p.gyw) + xi, n, g.vec, gyf);
+      }
+    }
+    float ya = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      ya = fmaf(gyf[k], yt[rr][k], ya);
+      dd[k] = fmaf(gyf[k], xf[k], dd[k]);
+    }
+    ya = row8_sum(ya);
+    if ((threadIdx.x & 7) == 0) p.ya[po + r0 + rr] = ya;
   }
   if (p.D) {
+    // column sums over the 64 rows: lanes sharing tid%8 (xor 8, 16, 32), then the 4 wavefronts
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      float v = dd[k];
+      v += __shfl_xor(v, 8);
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      dd[k] = v;
+    }
+    if (lane < 8) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) colred[wave][c0 + k] = dd[k];
+    }
     __syncthreads();
-    acc_to_lds(red, vd, wm, wn, lane);
-    __syncthreads();
-    const int64_t pc = static_cast<int64_t>(pt) * 64 + threadIdx.x;
-    if (threadIdx.x < 64 && pc < g.headdim) {
-      float s = 0.0f;
-      for (int k = 0; k < 64; ++k) s += red[k * 65 + threadIdx.x];
-      p.pdD[(((b * g.nc + c) * g.qb + i) * g.nheads + h) * g.headdim + pc] = s;
+    if (threadIdx.x < 64 && pt * 64 + threadIdx.x < g.headdim) {
+      const int col = threadIdx.x;
+      const float sum = (colred[0][col] + colred[1][col]) + (colred[2][col] + colred[3][col]);
+      p.pdD[(((b * g.nc + c) * g.qb + i) * g.nheads + h) * g.headdim + pt * 64 + col] = sum;
     }
   }
 }
 
-// Backwards over the chunks, one thread per state element: G (the adjoint of the
+// Backwards over the chunks, 8 state elements per thread: G (the adjoint of the
 // state leaving each chunk) over the local adjoints in dstates, e^T <G, S_in> per
-// state block, and the adjoint of the initial state.
+// 2048-element state block, and the adjoint of the initial state.
+template <typename TM>
 __global__ void __launch_bounds__(256) state_rev(Geo g, BwdPlan pl, Ptrs p) {
   __shared__ float wsum[4];
   const int64_t pn = g.headdim * g.dstate;
   const int blk = blockIdx.x;
-  const int64_t e = static_cast<int64_t>(blk) * 256 + threadIdx.x;
-  const bool valid = e < pn;
+  const int64_t e0 = (static_cast<int64_t>(blk) * 256 + threadIdx.x) * 8;
+  const int n = e0 < pn ? static_cast<int>(pn - e0 < 8 ? pn - e0 : 8) : 0;
   const int64_t bh = blockIdx.y;
-  float gv = (valid && p.dfinal) ? load_one(p.dfinal, g.x_dtype, bh * pn + e) : 0.0f;
+  TM* ds = static_cast<TM*>(p.dstates);
+  const TM* st = static_cast<const TM*>(p.states);
+  float gv[8];
+  if (n > 0 && p.dfinal) {
+    V8<TM> v;
+    v8_load(v, static_cast<const TM*>(p.dfinal) + bh * pn + e0, n, g.vec);
+    v8_f32(v, gv);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) gv[k] = 0.0f;
+  }
   for (int c = g.nc - 1; c >= 0; --c) {
-    const int64_t o = (bh * g.nc + c) * pn + e;
+    const int64_t o = (bh * g.nc + c) * pn + e0;
     const float eT = fast_exp(p.cs[(bh * g.nc + c) * g.q + g.q - 1]);
-    const float dt = block_sum(valid ? gv * p.states[o] : 0.0f, wsum);
+    float part = 0.0f, loc[8];
+    if (n > 0) {
+      V8<TM> v;
+      v8_load(v, st + o, n, g.vec);
+      float sf[8];
+      v8_f32(v, sf);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) part = fmaf(gv[k], sf[k], part);
+      v8_load(v, ds + o, n, g.vec);
+      v8_f32(v, loc);
+      v8_store(ds + o, n, g.vec, gv);
+    }
+    const float dt = block_sum(part, wsum);
     if (threadIdx.x == 0) p.dT[(bh * g.nc + c) * pl.nblk + blk] = eT * dt;
-    if (valid) {
-      const float loc = p.dstates[o];
-      p.dstates[o] = gv;
-      gv = fmaf(eT, gv, loc);
+    if (n > 0) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) gv[k] = fmaf(eT, gv[k], loc[k]);
     }
   }
-  if (valid && p.dinit) store_one(p.dinit, g.x_dtype, bh * pn + e, gv);
+  if (n > 0 && p.dinit) v8_store(static_cast<TM*>(p.dinit) + bh * pn + e0, n, g.vec, gv);
 }
 
-// Row sums over the 64 columns of an accumulator-layout tile, through LDS; thread
-// t < 64 returns row t.  Brackets its LDS use with workgroup barriers.
-__device__ __forceinline__ float row_sums(float* red, const float* v, int wm, int wn, int lane) {
-  __syncthreads();
-  acc_to_lds(red, v, wm, wn, lane);
-  __syncthreads();
-  float s = 0.0f;
-  if (threadIdx.x < 64)
-    for (int k = 0; k < 64; ++k) s += red[threadIdx.x * 65 + k];
-  return s;
-}
-
+// du for the 64-token tile j and d_head tile pt of one (b, h, chunk):
+//   du[s][p] = e^{T - cs_s} sum_n B_s[n] G[p][n]  +  sum_{l >= s} K[l][s] gy_l[p]
+// The state part runs first and its u.du_state is taken before the intra part is added.
 template <typename TM>
 __global__ void __launch_bounds__(256) du_kernel(Geo g, BwdPlan pl, Ptrs p) {
-  __shared__ TM sa[LdsTile<TM>::elems], sb[LdsTile<TM>::elems];
-  __shared__ float csr[64], css[64], ws[64], dls[64];
-  __shared__ float red[64 * 65];
+  constexpr int TE = LdsTile<TM>::elems;
+  __shared__ __align__(16) TM sbuf[2][2 * TE];
+  __shared__ float csc[256], dlc[256];
   const int j = blockIdx.x % g.qb, pt = blockIdx.x / g.qb;
   const int c = blockIdx.y;
   const int64_t bh = blockIdx.z, b = bh / g.nheads, h = bh % g.nheads, gg = h / g.hpg;
   const int lane = threadIdx.x & 63;
   int wm, wn;
   quadrant(threadIdx.x >> 6, wm, wn);
-  const int64_t so = (bh * g.nc + c) * g.q;
-  const int64_t ts0 = static_cast<int64_t>(c) * g.q + 64 * j;
+  const int r0 = blk_r0(), c0 = blk_c0();
+  load_chunk_cs(g, p, bh, c, csc, dlc);
+  const int64_t tc = static_cast<int64_t>(c) * g.q, ts0 = tc + 64 * j;
+  const int64_t pc0 = static_cast<int64_t>(pt) * 64, pc = pc0 + c0;
   const float* cbt = p.cb + ((b * g.nc + c) * g.ngroups + gg) * g.q * g.q;
-  if (threadIdx.x < 64) {
-    const float T = p.cs[so + g.q - 1];
-    css[threadIdx.x] = p.cs[so + 64 * j + threadIdx.x];
-    ws[threadIdx.x] = fast_exp(T - css[threadIdx.x]);
-    dls[threadIdx.x] = p.dl[so + 64 * j + threadIdx.x];
-  }
-  // u_s[p] as the matrix cores see it (rounded like the forward's operand) and x_s[p]
-  float uv[16], xv[16];
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int64_t t = ts0 + acc_row(wm, lane, r);
-    const int64_t pc = static_cast<int64_t>(pt) * 64 + acc_col(wn, lane);
-    xv[r] = (t < g.length && pc < g.headdim) ? load_one(p.x, g.x_dtype, xidx(g, b, t, h, pc)) : 0.0f;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int r = 0; r < 16; ++r) uv[r] = to_f32(from_f32<TM>(dls[acc_row(wm, lane, r)] * xv[r]));
+  const TM* Bm = static_cast<const TM*>(p.B);
+  const TM* gy = static_cast<const TM*>(p.gy);
+  const TM* G = static_cast<const TM*>(p.dstates) + (bh * g.nc + c) * g.headdim * g.dstate;
+  const int nstate = g.nnt, nst = g.nnt + g.qb - j;
+  float kf[2][8];
+  V8<TM> ra[2], rb[2];
+  auto fetch = [&](int k) {
+    if (k < nstate) {
+      load_bc2(g, Bm, b, ts0, gg, 64 * k, ra);  // B rows s
+      load_st2(g, G, pc0, 64 * k, rb);          // G rows p
+    } else {
+      const int i = j + k - nstate;
+      load_f8(cbt + (64 * i + r0) * g.q + 64 * j + c0, kf[0]);      // cb rows l
+      load_f8(cbt + (64 * i + r0 + 1) * g.q + 64 * j + c0, kf[1]);
+      load_x2(g, gy, b, tc + 64 * i, h, pc0, rb);                   // gy rows l
+    }
+  };
+  // x and u of the thread's epilogue block (rows s = r0, r0+1 of tile j)
+  V8<TM> xv[2];
+  load_x2(g, static_cast<const TM*>(p.x), b, ts0, h, pc0, xv);
   f32x16 acc;
   zero(acc);
-  // state part: du_state[s][p] = e^{T - cs_s} sum_n B_s[n] G[p][n]
-  const float* gc = p.dstates + (bh * g.nc + c) * g.headdim * g.dstate;
-  for (int n0 = 0; n0 < g.dstate; n0 += 64) {
-    __syncthreads();
-    stage<TM, false>(sa, [&](int s, int k) {  // A[s][n] = e^{T - cs_s} B_s[n]
-      const int64_t t = ts0 + s;
-      const int n = n0 + k;
-      if (t >= g.length || n >= g.dstate) return 0.0f;
-      return ws[s] * load_one(p.B, g.bc_dtype, bcidx(g, b, t, gg, n));
-    });
-    stage<TM, false>(sb, [&](int pp, int k) {  // Bt[p][n] = G[p][n]
-      const int64_t pc = static_cast<int64_t>(pt) * 64 + pp;
-      const int n = n0 + k;
-      if (pc >= g.headdim || n >= g.dstate) return 0.0f;
-      return gc[pc * g.dstate + n];
-    });
-    __syncthreads();
-    mma_tile<TM>(acc, sa, sb, wm, wn, lane, 64);
-  }
-  const int64_t po = ((bh * g.nc + c) * pl.npt + pt) * g.q + 64 * j;
-  {
-    float v[16];
+  fetch(0);
+  __syncthreads();  // csc, dlc
+  const float T = csc[g.q - 1];
+  float xf[2][8], uf[2][8];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) v[r] = uv[r] * acc[r];
-    const float tau = row_sums(red, v, wm, wn, lane);
-    if (threadIdx.x < 64) p.tau[po + threadIdx.x] = tau;
-  }
-  // intra-chunk part: du[s][p] += sum_{l >= s} K[l][s] gy_l[p]
-  for (int i = j; i < g.qb; ++i) {
-    const int64_t tl0 = static_cast<int64_t>(c) * g.q + 64 * i;
-    __syncthreads();
-    if (threadIdx.x < 64) csr[threadIdx.x] = p.cs[so + 64 * i + threadIdx.x];
-    __syncthreads();
-    stage<TM, true>(sa, [&](int l, int s) {  // A[s][l] = K[l][s]
-      if (64 * j + s > 64 * i + l) return 0.0f;
-      return cbt[(64 * i + l) * g.q + 64 * j + s] * fast_exp(csr[l] - css[s]);
-    });
-    stage<TM, true>(sb, [&](int l, int pp) {  // Bt[p][l] = gy_l[p]
-      const int64_t t = tl0 + l;
-      const int64_t pc = static_cast<int64_t>(pt) * 64 + pp;
-      if (t >= g.length || pc >= g.headdim) return 0.0f;
-      return load_one(p.gy, g.x_dtype, xidx(g, b, t, h, pc));
-    });
-    __syncthreads();
-    mma_tile<TM>(acc, sa, sb, wm, wn, lane, 64);
-  }
-  float vx[16], vu[16];
+  for (int rr = 0; rr < 2; ++rr) {
+    v8_f32(xv[rr], xf[rr]);
+    const float d = dlc[64 * j + r0 + rr];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int s = acc_row(wm, lane, r);
-    const int64_t t = ts0 + s;
-    const int64_t pc = static_cast<int64_t>(pt) * 64 + acc_col(wn, lane);
-    const float du = acc[r];
-    vx[r] = xv[r] * du;
-    vu[r] = uv[r] * du;
-    if (t >= g.length || pc >= g.headdim) continue;
-    const int64_t xi = xidx(g, b, t, h, pc);
-    float dxv = dls[s] * du;
-    if (p.D) dxv = fmaf(g.d_per_row ? p.D[h * g.headdim + pc] : p.D[h], load_one(p.gy, g.x_dtype, xi), dxv);
-    store_one(p.dx, g.x_dtype, xi, dxv);
+    for (int k = 0; k < 8; ++k) uf[rr][k] = to_f32(from_f32<TM>(d * xf[rr][k]));
   }
-  const float sx = row_sums(red, vx, wm, wn, lane);
-  if (threadIdx.x < 64) p.dsx[po + threadIdx.x] = sx;
-  const float su = row_sums(red, vu, wm, wn, lane);
-  if (threadIdx.x < 64) p.ut[po + threadIdx.x] = su;
+  float* red = reinterpret_cast<float*>(&sbuf[0][0]);
+  const int64_t po = ((bh * g.nc + c) * g.npt + pt) * g.q + 64 * j;
+  for (int k = 0; k < nst; ++k) {
+    TM* buf = sbuf[k & 1];
+    float a[8], bb[8];
+    if (k < nstate) {
+      scale8(ra[0], fast_exp(T - csc[64 * j + r0]), a);
+      scale8(ra[1], fast_exp(T - csc[64 * j + r0 + 1]), bb);
+      put2x8<TM, false>(buf, r0, c0, a, bb);  // A[s][n] = e^{T - cs_s} B_s[n]
+      v8_f32(rb[0], a);
+      v8_f32(rb[1], bb);
+      put2x8<TM, false>(buf + TE, r0, c0, a, bb);  // Bt[p][n] = G[p][n]
+    } else {
+      const int i = j + k - nstate;
+      const float cl0 = csc[64 * i + r0], cl1 = csc[64 * i + r0 + 1];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int s = 64 * j + c0 + e;
+        const float css = csc[s];
+        a[e] = (s <= 64 * i + r0) ? kf[0][e] * fast_exp(cl0 - css) : 0.0f;
+        bb[e] = (s <= 64 * i + r0 + 1) ? kf[1][e] * fast_exp(cl1 - css) : 0.0f;
+      }
+      put2x8<TM, true>(buf, r0, c0, a, bb);  // A[s][l] = K[l][s]
+      v8_f32(rb[0], a);
+      v8_f32(rb[1], bb);
+      put2x8<TM, true>(buf + TE, r0, c0, a, bb);  // Bt[p][l] = gy_l[p]
+    }
+    __syncthreads();
+    if (k + 1 < nst) fetch(k + 1);
+    mma_tile<TM>(acc, buf, buf + TE, wm, wn, lane, 64);
+    if (k == nstate - 1) {
+      // tau_s = u_s . du_state_s
+      __syncthreads();
+      acc_to_lds(red, acc, wm, wn, lane);
+      __syncthreads();
+      float v[2][8];
+      lds_block(red, r0, c0, v[0], v[1]);
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) {
+        float tau = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) tau = fmaf(uf[rr][e], v[rr][e], tau);
+        tau = row8_sum(tau);
+        if ((threadIdx.x & 7) == 0) p.tau[po + r0 + rr] = tau;
+      }
+      __syncthreads();
+    }
+  }
+  __syncthreads();
+  acc_to_lds(red, acc, wm, wn, lane);
+  __syncthreads();
+  float du[2][8];
+  lds_block(red, r0, c0, du[0], du[1]);
+  V8<TM> gv[2];
+  load_x2(g, gy, b, ts0, h, pc0, gv);
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr) {
+    const int64_t t = ts0 + r0 + rr;
+    const int n = t < g.length ? static_cast<int>(g.headdim - pc) : 0;
+    float gf[8], dxf[8];
+    v8_f32(gv[rr], gf);
+    const float d = dlc[64 * j + r0 + rr];
+    float sx = 0.0f, su = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float v = d * du[rr][e];
+      if (p.D && e < n) v = fmaf(g.d_per_row ? p.D[h * g.headdim + pc + e] : p.D[h], gf[e], v);
+      dxf[e] = v;
+      sx = fmaf(xf[rr][e], du[rr][e], sx);
+      su = fmaf(uf[rr][e], du[rr][e], su);
+    }
+    if (n > 0) v8_store(static_cast<TM*>(p.dx) + xidx(g, b, t, h, pc), n, g.vec, dxf);
+    sx = row8_sum(sx);
+    su = row8_sum(su);
+    if ((threadIdx.x & 7) == 0) {
+      p.dsx[po + r0 + rr] = sx;
+      p.ut[po + r0 + rr] = su;
+    }
+  }
 }
 
 // Adjoint of C.B^T for one lower tile (i, j) of a chunk, summed over a block of the
 // group's heads: sum_h (gy_i u_j^T) o e^{cs_l - cs_s}.
 template <typename TM>
 __global__ void __launch_bounds__(256) dcb_kernel(Geo g, BwdPlan pl, Ptrs p) {
-  __shared__ TM sa[LdsTile<TM>::elems], sb[LdsTile<TM>::elems];
-  __shared__ float csr[64], css[64], dls[64];
+  constexpr int TE = LdsTile<TM>::elems;
+  __shared__ __align__(16) TM sbuf[2][2 * TE];
+  __shared__ float csr[2][64], css[2][64];
   const int pair = blockIdx.x / pl.hb1, hb = blockIdx.x % pl.hb1;
   int i = 0;
   while ((i + 1) * (i + 2) / 2 <= pair) ++i;
@@ -262,42 +328,57 @@ __global__ void __launch_bounds__(256) dcb_kernel(Geo g, BwdPlan pl, Ptrs p) {
   const int lane = threadIdx.x & 63;
   int wm, wn;
   quadrant(threadIdx.x >> 6, wm, wn);
-  const int64_t tl0 = static_cast<int64_t>(c) * g.q + 64 * i, ts0 = static_cast<int64_t>(c) * g.q + 64 * j;
+  const int r0 = blk_r0(), c0 = blk_c0();
+  const int64_t tc = static_cast<int64_t>(c) * g.q;
   const int64_t h0 = gg * g.hpg + static_cast<int64_t>(hb) * pl.hpb1;
-  const int64_t hend = (gg + 1) * g.hpg, h1 = h0 + pl.hpb1 < hend ? h0 + pl.hpb1 : hend;
-  f32x16 dacc;
-  zero(dacc);
-  for (int64_t h = h0; h < h1; ++h) {
+  const int64_t hend = (gg + 1) * g.hpg;
+  const int nh = static_cast<int>((h0 + pl.hpb1 < hend ? h0 + pl.hpb1 : hend) - h0);
+  const int nst = nh * g.npt;
+  const TM* gy = static_cast<const TM*>(p.gy);
+  const TM* X = static_cast<const TM*>(p.x);
+  V8<TM> ra[2], rb[2];
+  float dls[2], cr = 0.0f, cc = 0.0f;
+  auto fetch = [&](int k) {
+    const int hh = k / g.npt, pt = k % g.npt;
+    const int64_t h = h0 + hh;
     const int64_t so = ((b * g.nheads + h) * g.nc + c) * g.q;
+    load_x2(g, gy, b, tc + 64 * i, h, pt * 64, ra);  // gy rows l
+    load_x2(g, X, b, tc + 64 * j, h, pt * 64, rb);   // x rows s
+    dls[0] = p.dl[so + 64 * j + r0];
+    dls[1] = p.dl[so + 64 * j + r0 + 1];
+    if (pt == 0 && threadIdx.x < 64) {
+      cr = p.cs[so + 64 * i + threadIdx.x];
+      cc = p.cs[so + 64 * j + threadIdx.x];
+    }
+  };
+  f32x16 dacc, w;
+  zero(dacc);
+  zero(w);
+  if (nst > 0) fetch(0);
+  for (int k = 0; k < nst; ++k) {
+    const int hh = k / g.npt, pt = k % g.npt;
+    TM* buf = sbuf[k & 1];
+    float a[8], bb[8];
+    v8_f32(ra[0], a);
+    v8_f32(ra[1], bb);
+    put2x8<TM, false>(buf, r0, c0, a, bb);  // A[l][p] = gy_l[p]
+    scale8(rb[0], dls[0], a);
+    scale8(rb[1], dls[1], bb);
+    put2x8<TM, false>(buf + TE, r0, c0, a, bb);  // Bt[s][p] = step_s x_s[p]
+    if (pt == 0 && threadIdx.x < 64) {
+      csr[hh & 1][threadIdx.x] = cr;
+      css[hh & 1][threadIdx.x] = cc;
+    }
     __syncthreads();
-    if (threadIdx.x < 64) {
-      csr[threadIdx.x] = p.cs[so + 64 * i + threadIdx.x];
-      css[threadIdx.x] = p.cs[so + 64 * j + threadIdx.x];
-      dls[threadIdx.x] = p.dl[so + 64 * j + threadIdx.x];
-    }
-    f32x16 w;
-    zero(w);
-    for (int pt = 0; pt < pl.npt; ++pt) {
-      __syncthreads();
-      stage<TM, false>(sa, [&](int l, int pp) {  // A[l][p] = gy_l[p]
-        const int64_t t = tl0 + l;
-        const int64_t pc = static_cast<int64_t>(pt) * 64 + pp;
-        if (t >= g.length || pc >= g.headdim) return 0.0f;
-        return load_one(p.gy, g.x_dtype, xidx(g, b, t, h, pc));
-      });
-      stage<TM, false>(sb, [&](int s, int pp) {  // Bt[s][p] = step_s x_s[p]
-        const int64_t t = ts0 + s;
-        const int64_t pc = static_cast<int64_t>(pt) * 64 + pp;
-        if (t >= g.length || pc >= g.headdim) return 0.0f;
-        return dls[s] * load_one(p.x, g.x_dtype, xidx(g, b, t, h, pc));
-      });
-      __syncthreads();
-      mma_tile<TM>(w, sa, sb, wm, wn, lane, 64);
-    }
+    if (k + 1 < nst) fetch(k + 1);
+    mma_tile<TM>(w, buf, buf + TE, wm, wn, lane, 64);
+    if (pt == g.npt - 1) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int l = acc_row(wm, lane, r), s = acc_col(wn, lane);
-      if (i != j || s <= l) dacc[r] = fmaf(w[r], fast_exp(csr[l] - css[s]), dacc[r]);
+      for (int r = 0; r < 16; ++r) {
+        const int l = acc_row(wm, lane, r), s = acc_col(wn, lane);
+        if (i != j || s <= l) dacc[r] = fmaf(w[r], fast_exp(csr[hh & 1][l] - css[hh & 1][s]), dacc[r]);
+      }
+      zero(w);
     }
   }
   float* out = p.dcb + (((b * g.nc + c) * g.ngroups + gg) * pl.hb1 + hb) * g.q * g.q;
@@ -307,132 +388,175 @@ __global__ void __launch_bounds__(256) dcb_kernel(Geo g, BwdPlan pl, Ptrs p) {
 }
 
 // State terms of dB (which 0: sum_h e^{T - cs_s} step_s x_s G) and dC (which 1:
-// sum_h e^{cs_l} gy_l S_in) for one 64-token tile and one d_state tile, over a
+// sum_h e^{cs_l} gy_l S_in) for one 64-token tile and two d_state tiles, over a
 // block of the group's heads.
 template <typename TM>
 __global__ void __launch_bounds__(256) dbc_state(Geo g, BwdPlan pl, Ptrs p) {
-  __shared__ TM sa[LdsTile<TM>::elems], sb[LdsTile<TM>::elems];
-  __shared__ float sc[64];
+  constexpr int TE = LdsTile<TM>::elems;
+  __shared__ __align__(16) TM sbuf[2][3 * TE];
   int idx = blockIdx.x;
   const int hb = idx % pl.hb2;
   idx /= pl.hb2;
   const int which = idx % 2;
   idx /= 2;
-  const int nt = idx % pl.nnt, tt = idx / pl.nnt;
+  const int np = idx % g.nnp, tt = idx / g.nnp;
   const int c = blockIdx.y / g.ngroups;
   const int64_t gg = blockIdx.y % g.ngroups, b = blockIdx.z;
   const int lane = threadIdx.x & 63;
   int wm, wn;
   quadrant(threadIdx.x >> 6, wm, wn);
+  const int r0 = blk_r0(), c0 = blk_c0();
   const int64_t tl0 = static_cast<int64_t>(c) * g.q + 64 * tt;
+  const int64_t nn0 = static_cast<int64_t>(np) * 128;
   const int64_t h0 = gg * g.hpg + static_cast<int64_t>(hb) * pl.hpb2;
-  const int64_t hend = (gg + 1) * g.hpg, h1 = h0 + pl.hpb2 < hend ? h0 + pl.hpb2 : hend;
-  f32x16 acc;
-  zero(acc);
-  for (int64_t h = h0; h < h1; ++h) {
-    const int64_t bh = b * g.nheads + h;
+  const int64_t hend = (gg + 1) * g.hpg;
+  const int nh = static_cast<int>((h0 + pl.hpb2 < hend ? h0 + pl.hpb2 : hend) - h0);
+  const int nst = nh * g.npt;
+  const TM* src = static_cast<const TM*>(which ? p.gy : p.x);
+  const TM* stm = static_cast<const TM*>(which ? p.states : p.dstates);
+  V8<TM> ra[2], rb0[2], rb1[2];
+  float sc[2];
+  auto fetch = [&](int k) {
+    const int hh = k / g.npt, pt = k % g.npt;
+    const int64_t h = h0 + hh, bh = b * g.nheads + h;
     const int64_t so = (bh * g.nc + c) * g.q;
+    load_x2(g, src, b, tl0, h, pt * 64, ra);  // rows l
+    const TM* st = stm + (bh * g.nc + c) * g.headdim * g.dstate;
+    load_st2(g, st, pt * 64, nn0, rb0);        // rows p
+    load_st2(g, st, pt * 64, nn0 + 64, rb1);
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      const int l = 64 * tt + r0 + rr;
+      const float cl = p.cs[so + l];
+      sc[rr] = which ? fast_exp(cl) : p.dl[so + l] * fast_exp(p.cs[so + g.q - 1] - cl);
+    }
+  };
+  f32x16 acc0, acc1;
+  zero(acc0);
+  zero(acc1);
+  if (nst > 0) fetch(0);
+  for (int k = 0; k < nst; ++k) {
+    TM* buf = sbuf[k & 1];
+    float a[8], bb[8];
+    scale8(ra[0], sc[0], a);
+    scale8(ra[1], sc[1], bb);
+    put2x8<TM, false>(buf, r0, c0, a, bb);  // A[l][p]
+    v8_f32(rb0[0], a);
+    v8_f32(rb0[1], bb);
+    put2x8<TM, true>(buf + TE, r0, c0, a, bb);  // Bt[n][p] = S[p][n]
+    v8_f32(rb1[0], a);
+    v8_f32(rb1[1], bb);
+    put2x8<TM, true>(buf + 2 * TE, r0, c0, a, bb);
     __syncthreads();
-    if (threadIdx.x < 64) {
-      const float cl = p.cs[so + 64 * tt + threadIdx.x];
-      sc[threadIdx.x] = which ? fast_exp(cl) : p.dl[so + 64 * tt + threadIdx.x] * fast_exp(p.cs[so + g.q - 1] - cl);
-    }
-    const void* src = which ? p.gy : p.x;
-    const float* st = (which ? p.states : p.dstates) + (bh * g.nc + c) * g.headdim * g.dstate;
-    for (int pt = 0; pt < pl.npt; ++pt) {
-      __syncthreads();
-      stage<TM, false>(sa, [&](int l, int pp) {  // A[l][p]
-        const int64_t t = tl0 + l;
-        const int64_t pc = static_cast<int64_t>(pt) * 64 + pp;
-        if (t >= g.length || pc >= g.headdim) return 0.0f;
-        return sc[l] * load_one(src, g.x_dtype, xidx(g, b, t, h, pc));
-      });
-      stage<TM, true>(sb, [&](int pp, int n) {  // Bt[n][p] = S[p][n]
-        const int64_t pc = static_cast<int64_t>(pt) * 64 + pp;
-        const int64_t nn = static_cast<int64_t>(nt) * 64 + n;
-        if (pc >= g.headdim || nn >= g.dstate) return 0.0f;
-        return st[pc * g.dstate + nn];
-      });
-      __syncthreads();
-      mma_tile<TM>(acc, sa, sb, wm, wn, lane, 64);
-    }
+    if (k + 1 < nst) fetch(k + 1);
+    mma_tile<TM>(acc0, buf, buf + TE, wm, wn, lane, 64);
+    mma_tile<TM>(acc1, buf, buf + 2 * TE, wm, wn, lane, 64);
   }
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int64_t t = tl0 + acc_row(wm, lane, r);
-    const int64_t nn = static_cast<int64_t>(nt) * 64 + acc_col(wn, lane);
-    if (t >= g.length || nn >= g.dstate) continue;
-    p.pbc[((((b * g.length + t) * g.ngroups + gg) * pl.hb2 + hb) * 2 + which) * g.dstate + nn] = acc[r];
+    const int64_t nn = nn0 + acc_col(wn, lane);
+    if (t >= g.length) continue;
+    float* out = p.pbc + ((((b * g.length + t) * g.ngroups + gg) * pl.hb2 + hb) * 2 + which) * g.dstate;
+    if (nn < g.dstate) out[nn] = acc0[r];
+    if (nn + 64 < g.dstate) out[nn + 64] = acc1[r];
   }
 }
 
-// dC = dCB B (which 1) and dB = dCB^T C (which 0) for one 64-token tile and one
-// d_state tile, plus the head-block partials of the state terms.
+// dC = dCB B (which 1) and dB = dCB^T C (which 0) for one 64-token tile and two
+// d_state tiles, plus the head-block partials of the state terms.
 template <typename TM>
 __global__ void __launch_bounds__(256) dbc_final(Geo g, BwdPlan pl, Ptrs p) {
-  __shared__ TM sa[LdsTile<TM>::elems], sb[LdsTile<TM>::elems];
+  constexpr int TE = LdsTile<TM>::elems;
+  __shared__ __align__(16) TM sbuf[2][3 * TE];
   int idx = blockIdx.x;
   const int which = idx % 2;
   idx /= 2;
-  const int nt = idx % pl.nnt, tt = idx / pl.nnt;
+  const int np = idx % g.nnp, tt = idx / g.nnp;
   const int c = blockIdx.y / g.ngroups;
   const int64_t gg = blockIdx.y % g.ngroups, b = blockIdx.z;
   const int lane = threadIdx.x & 63;
   int wm, wn;
   quadrant(threadIdx.x >> 6, wm, wn);
+  const int r0 = blk_r0(), c0 = blk_c0();
+  const int64_t tc = static_cast<int64_t>(c) * g.q;
+  const int64_t nn0 = static_cast<int64_t>(np) * 128;
   const int64_t qq = static_cast<int64_t>(g.q) * g.q;
   const float* dcb = p.dcb + ((b * g.nc + c) * g.ngroups + gg) * pl.hb1 * qq;
-  auto dcb_at = [&](int l, int s) {  // sum over head blocks of dCB[l][s]
-    float v = 0.0f;
-    for (int k = 0; k < pl.hb1; ++k) v += dcb[k * qq + static_cast<int64_t>(l) * g.q + s];
-    return v;
-  };
-  const int64_t nn0 = static_cast<int64_t>(nt) * 64;
-  f32x16 acc;
-  zero(acc);
-  if (which) {
-    for (int j = 0; j <= tt; ++j) {
-      const int64_t ts0 = static_cast<int64_t>(c) * g.q + 64 * j;
-      __syncthreads();
-      stage<TM, false>(sa, [&](int l, int s) {  // A[l][s] = dCB[l][s]
-        if (64 * j + s > 64 * tt + l) return 0.0f;
-        return dcb_at(64 * tt + l, 64 * j + s);
-      });
-      stage<TM, true>(sb, [&](int s, int n) {  // Bt[n][s] = B_s[n]
-        const int64_t t = ts0 + s;
-        if (t >= g.length || nn0 + n >= g.dstate) return 0.0f;
-        return load_one(p.B, g.bc_dtype, bcidx(g, b, t, gg, nn0 + n));
-      });
-      __syncthreads();
-      mma_tile<TM>(acc, sa, sb, wm, wn, lane, 64);
-    }
-  } else {
-    for (int i = tt; i < g.qb; ++i) {
-      const int64_t tl0 = static_cast<int64_t>(c) * g.q + 64 * i;
-      __syncthreads();
-      stage<TM, true>(sa, [&](int l, int s) {  // A[s][l] = dCB[l][s]
-        if (64 * tt + s > 64 * i + l) return 0.0f;
-        return dcb_at(64 * i + l, 64 * tt + s);
-      });
-      stage<TM, true>(sb, [&](int l, int n) {  // Bt[n][l] = C_l[n]
-        const int64_t t = tl0 + l;
-        if (t >= g.length || nn0 + n >= g.dstate) return 0.0f;
-        return load_one(p.C, g.bc_dtype, bcidx(g, b, t, gg, nn0 + n));
-      });
-      __syncthreads();
-      mma_tile<TM>(acc, sa, sb, wm, wn, lane, 64);
-    }
-  }
-  const int64_t t0 = static_cast<int64_t>(c) * g.q + 64 * tt;
+  const TM* Om = static_cast<const TM*>(which ? p.B : p.C);  // the other operand
+  float kf[2][8];
+  V8<TM> rb0[2], rb1[2];
+  const int nst = which ? tt + 1 : g.qb - tt;
+  auto fetch = [&](int k) {
+    // which 1: rows l of tile tt, columns s of tile j = k;  which 0: rows l of tile i = tt + k, columns s of tile tt
+    const int lt = which ? tt : tt + k, st = which ? k : tt;
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int64_t t = t0 + acc_row(wm, lane, r);
-    const int64_t nn = nn0 + acc_col(wn, lane);
-    if (t >= g.length || nn >= g.dstate) continue;
-    float v = acc[r];
-    const float* part = p.pbc + (((b * g.length + t) * g.ngroups + gg) * pl.hb2 * 2 + which) * g.dstate + nn;
-    for (int k = 0; k < pl.hb2; ++k) v += part[static_cast<int64_t>(k) * 2 * g.dstate];
-    store_one(which ? p.dC : p.dB, g.bc_dtype, bcidx(g, b, t, gg, nn), v);
+    for (int rr = 0; rr < 2; ++rr) {
+      const float* row = dcb + static_cast<int64_t>(64 * lt + r0 + rr) * g.q + 64 * st + c0;
+      load_f8(row, kf[rr]);
+      for (int hb = 1; hb < pl.hb1; ++hb) {
+        float f[8];
+        load_f8(row + hb * qq, f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) kf[rr][e] += f[e];
+      }
+    }
+    const int64_t ot0 = tc + 64 * (which ? st : lt);  // token rows of the other operand
+    load_bc2(g, Om, b, ot0, gg, nn0, rb0);
+    load_bc2(g, Om, b, ot0, gg, nn0 + 64, rb1);
+  };
+  f32x16 acc0, acc1;
+  zero(acc0);
+  zero(acc1);
+  fetch(0);
+  for (int k = 0; k < nst; ++k) {
+    TM* buf = sbuf[k & 1];
+    float a[8], bb[8];
+    if (which)
+      put2x8<TM, false>(buf, r0, c0, kf[0], kf[1]);  // A[l][s] = dCB[l][s]
+    else
+      put2x8<TM, true>(buf, r0, c0, kf[0], kf[1]);   // A[s][l] = dCB[l][s]
+    v8_f32(rb0[0], a);
+    v8_f32(rb0[1], bb);
+    put2x8<TM, true>(buf + TE, r0, c0, a, bb);  // Bt[n][token] of B (which 1) or C (which 0)
+    v8_f32(rb1[0], a);
+    v8_f32(rb1[1], bb);
+    put2x8<TM, true>(buf + 2 * TE, r0, c0, a, bb);
+    __syncthreads();
+    if (k + 1 < nst) fetch(k + 1);
+    mma_tile<TM>(acc0, buf, buf + TE, wm, wn, lane, 64);
+    mma_tile<TM>(acc1, buf, buf + 2 * TE, wm, wn, lane, 64);
+  }
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(&sbuf[0][0]);
+  TM* out = static_cast<TM*>(which ? p.dC : p.dB);
+  const int64_t t0 = tc + 64 * tt;
+  for (int half = 0; half < 2; ++half) {
+    if (half) __syncthreads();
+    acc_to_lds(red, half ? acc1 : acc0, wm, wn, lane);
+    __syncthreads();
+    float v[2][8];
+    lds_block(red, r0, c0, v[0], v[1]);
+    const int64_t nn = nn0 + 64 * half + c0;
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      const int64_t t = t0 + r0 + rr;
+      const int n = t < g.length ? static_cast<int>(g.dstate - nn) : 0;
+      if (n <= 0) continue;
+      const float* part = p.pbc + (((b * g.length + t) * g.ngroups + gg) * pl.hb2 * 2 + which) * g.dstate + nn;
+      for (int hb = 0; hb < pl.hb2; ++hb) {
+        float f[8];
+        if (g.vec && n >= 8) {
+          load_f8(part + static_cast<int64_t>(hb) * 2 * g.dstate, f);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) f[e] = e < n ? part[static_cast<int64_t>(hb) * 2 * g.dstate + e] : 0.0f;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[rr][e] += f[e];
+      }
+      v8_store(out + bcidx(g, b, t, gg, nn), n, g.vec, v[rr]);
+    }
   }
 }
 
@@ -448,8 +572,8 @@ __global__ void __launch_bounds__(256) finish(Geo g, BwdPlan pl, Ptrs p) {
   const int64_t so = (bh * g.nc + c) * g.q;
   float dcs = 0.0f, dsxv = 0.0f, del = 0.0f, tau = 0.0f;
   if (active) {
-    for (int pt = 0; pt < pl.npt; ++pt) {
-      const int64_t o = ((bh * g.nc + c) * pl.npt + pt) * g.q + l;
+    for (int pt = 0; pt < g.npt; ++pt) {
+      const int64_t o = ((bh * g.nc + c) * g.npt + pt) * g.q + l;
       dcs += p.ya[o] - p.ut[o];
       dsxv += p.dsx[o];
       tau += p.tau[o];
@@ -530,16 +654,14 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 BwdPlan make_plan(const Geo& g) {
   BwdPlan pl{};
-  pl.npt = static_cast<int>(cdiv(g.headdim, 64));
-  pl.nnt = static_cast<int>(cdiv(g.dstate, 64));
-  pl.nblk = static_cast<int>(cdiv(g.headdim * g.dstate, 256));
+  pl.nblk = static_cast<int>(cdiv(g.headdim * g.dstate, 2048));
   pl.npairs = g.qb * (g.qb + 1) / 2;
   // Split the head sums so each launch has about 2048 workgroups.
   const int64_t base1 = std::max<int64_t>(1, g.batch * g.nc * g.ngroups * pl.npairs);
   pl.hb1 = static_cast<int>(std::min<int64_t>(g.hpg, std::max<int64_t>(1, cdiv(2048, base1))));
   pl.hpb1 = static_cast<int>(cdiv(g.hpg, pl.hb1));
   pl.hb1 = static_cast<int>(cdiv(g.hpg, pl.hpb1));
-  const int64_t base2 = std::max<int64_t>(1, g.batch * g.nc * g.ngroups * g.qb * pl.nnt * 2);
+  const int64_t base2 = std::max<int64_t>(1, g.batch * g.nc * g.ngroups * g.qb * g.nnp * 2);
   pl.hb2 = static_cast<int>(std::min<int64_t>(g.hpg, std::max<int64_t>(1, cdiv(2048, base2))));
   pl.hpb2 = static_cast<int>(cdiv(g.hpg, pl.hb2));
   pl.hb2 = static_cast<int>(cdiv(g.hpg, pl.hpb2));
@@ -551,13 +673,14 @@ BwdLayout bwd_layout(const Geo& g, const BwdPlan& pl, bool has_z) {
   const size_t bh = static_cast<size_t>(g.batch * g.nheads);
   const size_t chunks = bh * g.nc;
   size_t o = 0;
-  l.gy = o; o = align256(o + (has_z ? static_cast<size_t>(g.batch * g.length * g.nheads * g.headdim) * dtype_size(g.x_dtype) : 0));
-  l.dstates = o; o = align256(o + chunks * g.headdim * g.dstate * 4);
+  const size_t es = dtype_size(g.x_dtype);
+  l.gy = o; o = align256(o + (has_z ? static_cast<size_t>(g.batch * g.length * g.nheads * g.headdim) * es : 0));
+  l.dstates = o; o = align256(o + chunks * g.headdim * g.dstate * es);
   l.dT = o; o = align256(o + chunks * pl.nblk * 4);
-  l.ya = o; o = align256(o + chunks * pl.npt * g.q * 4);
-  l.dsx = o; o = align256(o + chunks * pl.npt * g.q * 4);
-  l.ut = o; o = align256(o + chunks * pl.npt * g.q * 4);
-  l.tau = o; o = align256(o + chunks * pl.npt * g.q * 4);
+  l.ya = o; o = align256(o + chunks * g.npt * g.q * 4);
+  l.dsx = o; o = align256(o + chunks * g.npt * g.q * 4);
+  l.ut = o; o = align256(o + chunks * g.npt * g.q * 4);
+  l.tau = o; o = align256(o + chunks * g.npt * g.q * 4);
   l.pdD = o; o = align256(o + chunks * g.qb * g.headdim * 4);
   l.dcb = o; o = align256(o + static_cast<size_t>(g.batch) * g.nc * g.ngroups * pl.hb1 * g.q * g.q * 4);
   l.pbc = o; o = align256(o + static_cast<size_t>(g.batch * g.length * g.ngroups) * pl.hb2 * 2 * g.dstate * 4);
@@ -571,18 +694,18 @@ template <typename TM>
 void launch_bwd_t(const Geo& g, const BwdPlan& pl, const Ptrs& q, hipStream_t s) {
   const unsigned bh = static_cast<unsigned>(g.batch * g.nheads);
   const unsigned ncg = static_cast<unsigned>(g.nc * g.ngroups);
-  MKO_TIMED("ssd_gate", s, gate<TM><<<dim3(g.qb * pl.npt, g.nc, bh), 256, 0, s>>>(g, pl, q));
+  MKO_TIMED("ssd_gate", s, gate<TM><<<dim3(g.qb * g.npt, g.nc, bh), 256, 0, s>>>(g, pl, q));
   MKO_TIMED("ssd_chunk_state_bwd", s,
-            chunk_state<TM, true><<<dim3(pl.npt * pl.nnt, g.nc, bh), 256, 0, s>>>(g, q, q.dstates));
-  MKO_TIMED("ssd_state_rev", s, state_rev<<<dim3(pl.nblk, bh), 256, 0, s>>>(g, pl, q));
-  MKO_TIMED("ssd_du", s, du_kernel<TM><<<dim3(g.qb * pl.npt, g.nc, bh), 256, 0, s>>>(g, pl, q));
+            chunk_state<TM, true><<<dim3(g.npt * g.nnp, g.nc, bh), 256, 0, s>>>(g, q, q.dstates));
+  MKO_TIMED("ssd_state_rev", s, state_rev<TM><<<dim3(pl.nblk, bh), 256, 0, s>>>(g, pl, q));
+  MKO_TIMED("ssd_du", s, du_kernel<TM><<<dim3(g.qb * g.npt, g.nc, bh), 256, 0, s>>>(g, pl, q));
   MKO_TIMED("ssd_dcb", s,
             dcb_kernel<TM><<<dim3(pl.npairs * pl.hb1, ncg, static_cast<unsigned>(g.batch)), 256, 0, s>>>(g, pl, q));
   MKO_TIMED("ssd_dbc_state", s,
-            dbc_state<TM><<<dim3(g.qb * pl.nnt * 2 * pl.hb2, ncg, static_cast<unsigned>(g.batch)), 256, 0, s>>>(
+            dbc_state<TM><<<dim3(g.qb * g.nnp * 2 * pl.hb2, ncg, static_cast<unsigned>(g.batch)), 256, 0, s>>>(
                 g, pl, q));
   MKO_TIMED("ssd_dbc_final", s,
-            dbc_final<TM><<<dim3(g.qb * pl.nnt * 2, ncg, static_cast<unsigned>(g.batch)), 256, 0, s>>>(g, pl, q));
+            dbc_final<TM><<<dim3(g.qb * g.nnp * 2, ncg, static_cast<unsigned>(g.batch)), 256, 0, s>>>(g, pl, q));
   MKO_TIMED("ssd_finish", s,
             finish<<<dim3(g.nc, static_cast<unsigned>(g.nheads), static_cast<unsigned>(g.batch)), 256, 0, s>>>(g, pl, q));
   MKO_TIMED("ssd_reduce", s, reduce_params<<<dim3(static_cast<unsigned>(g.nheads)), 256, 0, s>>>(g, pl, q));
@@ -627,7 +750,7 @@ extern "C" int mko_ssd_bwd(const mko_ssd_params* prm, void* stream) {
   char* ws = static_cast<char*>(prm->workspace);
   q.gyw = prm->z ? ws + lay.gy : nullptr;
   q.gy = prm->z ? static_cast<const void*>(ws + lay.gy) : prm->dy;
-  q.dstates = reinterpret_cast<float*>(ws + lay.dstates);
+  q.dstates = ws + lay.dstates;
   q.dT = reinterpret_cast<float*>(ws + lay.dT);
   q.ya = reinterpret_cast<float*>(ws + lay.ya);
   q.dsx = reinterpret_cast<float*>(ws + lay.dsx);
@@ -645,9 +768,12 @@ extern "C" int mko_ssd_bwd(const mko_ssd_params* prm, void* stream) {
     else launch_bwd_t<_Float16>(g, pl, q, s);
   } else {
     // no tokens: dinitial = dfinal (zero without it); the parameter gradients are zero
-    if (g.batch > 0 && q.dinit)
-      MKO_TIMED("ssd_state_rev", s,
-                state_rev<<<dim3(pl.nblk, static_cast<unsigned>(g.batch * g.nheads)), 256, 0, s>>>(g, pl, q));
+    if (g.batch > 0 && q.dinit) {
+      const dim3 grid(pl.nblk, static_cast<unsigned>(g.batch * g.nheads));
+      if (g.x_dtype == MKO_F32) MKO_TIMED("ssd_state_rev", s, state_rev<float><<<grid, 256, 0, s>>>(g, pl, q));
+      else if (g.x_dtype == MKO_BF16) MKO_TIMED("ssd_state_rev", s, state_rev<bf16><<<grid, 256, 0, s>>>(g, pl, q));
+      else MKO_TIMED("ssd_state_rev", s, state_rev<_Float16><<<grid, 256, 0, s>>>(g, pl, q));
+    }
     MKO_TIMED("ssd_reduce", s, reduce_params<<<dim3(static_cast<unsigned>(g.nheads)), 256, 0, s>>>(g, pl, q));
   }
   return mko_check_launch("ssd_bwd");

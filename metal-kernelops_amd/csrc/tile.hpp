@@ -1,0 +1,162 @@
+// Staging of 64x64 operand tiles from HBM into LDS for the mma.hpp tile products.
+//
+// A thread of the 256-thread workgroup owns a 2-row x 8-column block of a tile:
+// rows r0 = 2*(tid/8) and r0+1, columns c0 = 8*(tid%8) .. c0+7.  Eight lanes cover a
+// 64-element row, so a wavefront's loads are whole 128-byte lines of 16-bit data.
+// A block is loaded as raw 16-byte vectors (V8), converted to fp32 in registers,
+// transformed (scaled, decayed, masked), then rounded to the operand type and
+// written to LDS either as is ([row][col]) or transposed ([col][row], one word per
+// row pair) -- the transposed form turns token-major HBM data into the
+// K-contiguous layout the matrix cores read when the contraction runs over tokens.
+#pragma once
+
+#include "mma.hpp"
+
+namespace mko {
+
+__device__ __forceinline__ int blk_r0() { return 2 * static_cast<int>(threadIdx.x >> 3); }
+__device__ __forceinline__ int blk_c0() { return 8 * static_cast<int>(threadIdx.x & 7); }
+
+// Eight consecutive elements of T, raw.
+template <typename T>
+struct V8 {
+  static constexpr int kWords = static_cast<int>(sizeof(T)) * 2;
+  uint32_t w[kWords];
+};
+
+template <typename T>
+__device__ __forceinline__ void v8_zero(V8<T>& v) {
+#pragma unroll
+  for (int i = 0; i < V8<T>::kWords; ++i) v.w[i] = 0u;
+}
+
+// Loads elements p[0 .. min(n, 8)) (zero beyond): 16-byte vectors when `vec` and the
+// run is whole (p is then 16-byte aligned), element by element otherwise.
+template <typename T>
+__device__ __forceinline__ void v8_load(V8<T>& v, const T* p, int n, bool vec) {
+  constexpr int W = V8<T>::kWords;
+  if (vec && n >= 8) {
+    const uint4* q = reinterpret_cast<const uint4*>(p);
+#pragma unroll
+    for (int i = 0; i < W / 4; ++i) {
+      const uint4 t = q[i];
+      v.w[4 * i + 0] = t.x;
+      v.w[4 * i + 1] = t.y;
+      v.w[4 * i + 2] = t.z;
+      v.w[4 * i + 3] = t.w;
+    }
+  } else {
+    v8_zero(v);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if (e < n) {
+        if constexpr (sizeof(T) == 4)
+          v.w[e] = __builtin_bit_cast(uint32_t, p[e]);
+        else
+          v.w[e >> 1] |= static_cast<uint32_t>(__builtin_bit_cast(uint16_t, p[e])) << (16 * (e & 1));
+      }
+    }
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void v8_f32(const V8<T>& v, float (&f)[8]) {
+  if constexpr (sizeof(T) == 4) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = __uint_as_float(v.w[e]);
+  } else if constexpr (__is_same(T, bf16)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = __uint_as_float(v.w[i] << 16);
+      f[2 * i + 1] = __uint_as_float(v.w[i] & 0xffff0000u);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(v.w[i] & 0xffffu)));
+      f[2 * i + 1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(v.w[i] >> 16)));
+    }
+  }
+}
+
+// Two values rounded to a 16-bit type, packed low-first into one word.
+template <typename TM>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  if constexpr (__is_same(TM, bf16)) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    const bf16x2_t t = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+    return __builtin_bit_cast(uint32_t, t);
+  } else {
+    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+    const f16x2_t t = {static_cast<_Float16>(a), static_cast<_Float16>(b)};
+    return __builtin_bit_cast(uint32_t, t);
+  }
+}
+
+// Stores 8 fp32 values as T at p (16-byte aligned when `vec`), or the first n of them.
+template <typename T>
+__device__ __forceinline__ void v8_store(T* p, int n, bool vec, const float (&f)[8]) {
+  if (vec && n >= 8) {
+    if constexpr (sizeof(T) == 4) {
+      uint4* q = reinterpret_cast<uint4*>(p);
+      q[0] = make_uint4(__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]), __float_as_uint(f[3]));
+      q[1] = make_uint4(__float_as_uint(f[4]), __float_as_uint(f[5]), __float_as_uint(f[6]), __float_as_uint(f[7]));
+    } else {
+      *reinterpret_cast<uint4*>(p) = make_uint4(pack2<T>(f[0], f[1]), pack2<T>(f[2], f[3]), pack2<T>(f[4], f[5]),
+                                                pack2<T>(f[6], f[7]));
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (e < n) p[e] = from_f32<T>(f[e]);
+  }
+}
+
+// Writes the thread's block (row r0 = a, row r0+1 = b, columns c0..c0+7) into an LDS
+// operand tile, as is or transposed.
+template <typename TM, bool TRANS>
+__device__ __forceinline__ void put2x8(TM* dst, int r0, int c0, const float (&a)[8], const float (&b)[8]) {
+  constexpr int ld = tile_ld<TM>();
+  if constexpr (sizeof(TM) == 2) {
+    if constexpr (!TRANS) {
+      *reinterpret_cast<uint4*>(dst + r0 * ld + c0) =
+          make_uint4(pack2<TM>(a[0], a[1]), pack2<TM>(a[2], a[3]), pack2<TM>(a[4], a[5]), pack2<TM>(a[6], a[7]));
+      *reinterpret_cast<uint4*>(dst + (r0 + 1) * ld + c0) =
+          make_uint4(pack2<TM>(b[0], b[1]), pack2<TM>(b[2], b[3]), pack2<TM>(b[4], b[5]), pack2<TM>(b[6], b[7]));
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) *reinterpret_cast<uint32_t*>(dst + (c0 + k) * ld + r0) = pack2<TM>(a[k], b[k]);
+    }
+  } else {
+    if constexpr (!TRANS) {
+#pragma unroll
+      for (int k = 0; k < 8; k += 2) {
+        *reinterpret_cast<float2*>(dst + r0 * ld + c0 + k) = make_float2(a[k], a[k + 1]);
+        *reinterpret_cast<float2*>(dst + (r0 + 1) * ld + c0 + k) = make_float2(b[k], b[k + 1]);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) *reinterpret_cast<float2*>(dst + (c0 + k) * ld + r0) = make_float2(a[k], b[k]);
+    }
+  }
+}
+
+// Reads the thread's block back from a 64x65 fp32 LDS tile written in the accumulator
+// layout (acc_to_lds): a = row r0, b = row r0+1.
+__device__ __forceinline__ void lds_block(const float* red, int r0, int c0, float (&a)[8], float (&b)[8]) {
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    a[k] = red[r0 * 65 + c0 + k];
+    b[k] = red[(r0 + 1) * 65 + c0 + k];
+  }
+}
+
+// Sum over the 8 lanes that share a row pair (tid%8 varies): every one of them gets it.
+__device__ __forceinline__ float row8_sum(float v) {
+  v += __shfl_xor(v, 1);
+  v += __shfl_xor(v, 2);
+  v += __shfl_xor(v, 4);
+  return v;
+}
+
+}  // namespace mko

@@ -223,9 +223,9 @@ def mamba2_chunk_scan(x, dt, A, B, C, chunk_size=64, D=None, z=None, dt_bias=Non
     batch, length, nheads, headdim, ngroups, dstate, initial_states = _check(
         x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size)
     x, dt = x.contiguous(), dt.contiguous()
-    if B.dtype != C.dtype:
-        B, C = B.float(), C.float()
-    B, C = B.contiguous(), C.contiguous()
+    # B and C take x's dtype: every contraction runs with x.dtype operands (as the
+    # reference's composition does); autograd casts their gradients back.
+    B, C = B.to(x.dtype).contiguous(), C.to(x.dtype).contiguous()
     if z is not None:
         z = (z if z.dtype == x.dtype else z.to(x.dtype)).contiguous()
     if initial_states is not None:
