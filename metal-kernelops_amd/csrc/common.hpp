@@ -112,6 +112,27 @@ class ProfScope {
     __VA_ARGS__;                            \
   } while (0)
 
+// Coordinates of a 3-D problem launched as a 1-D grid of nx * ny * nz workgroups.
+// The dispatcher deals consecutive workgroups round-robin to the 8 XCDs of the
+// chip, each with its own L2; the workgroup index is permuted so that
+// consecutive logical indices (x fastest) run on one XCD and share its L2.
+struct WgId {
+  int x, y;
+  int64_t z;
+};
+constexpr int kXcds = 8;
+__device__ __forceinline__ WgId wg_id(int nx, int ny) {
+  const int64_t total = gridDim.x, w = blockIdx.x;
+  const int64_t per = total / kXcds;
+  const int64_t lid = (w < per * kXcds) ? (w % kXcds) * per + w / kXcds : w;
+  WgId r;
+  r.x = static_cast<int>(lid % nx);
+  const int64_t rest = lid / nx;
+  r.y = static_cast<int>(rest % ny);
+  r.z = rest / ny;
+  return r;
+}
+
 // Error reporting for the C ABI (defined in abi.hip).
 void mko_set_error(const char* fmt, ...);
 int mko_check_launch(const char* what);

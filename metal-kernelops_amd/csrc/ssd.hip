@@ -47,17 +47,18 @@ __global__ void __launch_bounds__(256) prep(Geo g, Ptrs p) {
   }
 }
 
-template <typename TM>
+template <typename TM, bool VEC>
 __global__ void __launch_bounds__(256) cb_kernel(Geo g, Ptrs p) {
   constexpr int TE = LdsTile<TM>::elems;
   __shared__ __align__(16) TM sbuf[2][2 * TE];
   // lower-triangular tile (i, j), j <= i
-  const int idx = blockIdx.x;
+  const WgId id = wg_id(g.qb * (g.qb + 1) / 2, g.nc * g.ngroups);
+  const int idx = id.x;
   int i = 0;
   while ((i + 1) * (i + 2) / 2 <= idx) ++i;
   const int j = idx - i * (i + 1) / 2;
-  const int c = blockIdx.y / g.ngroups;
-  const int64_t gg = blockIdx.y % g.ngroups, b = blockIdx.z;
+  const int c = id.y / g.ngroups;
+  const int64_t gg = id.y % g.ngroups, b = id.z;
   const int lane = threadIdx.x & 63;
   int wm, wn;
   quadrant(threadIdx.x >> 6, wm, wn);
@@ -65,30 +66,27 @@ __global__ void __launch_bounds__(256) cb_kernel(Geo g, Ptrs p) {
   const int64_t tc = static_cast<int64_t>(c) * g.q;
   const TM* Cm = static_cast<const TM*>(p.C);
   const TM* Bm = static_cast<const TM*>(p.B);
-  V8<TM> ra[2], rb[2];
-  auto fetch = [&](int k) {
-    load_bc2(g, Cm, b, tc + 64 * i, gg, 64 * k, ra);
-    load_bc2(g, Bm, b, tc + 64 * j, gg, 64 * k, rb);
+  struct Regs {
+    V8<TM> c[2], b[2];
+  };
+  auto fetch = [&](int k, Regs& r) {
+    load_bw<TM, VEC>(g, Cm, b, tc + 64 * i, gg, 64 * k, r.c);
+    load_bw<TM, VEC>(g, Bm, b, tc + 64 * j, gg, 64 * k, r.b);
+  };
+  auto put = [&](int k, Regs& r) {
+    TM* buf = sbuf[k & 1];
+    put_raw<TM, false>(buf, r0, c0, r.c[0], r.c[1]);       // A[l][n] = C_l[n]
+    put_raw<TM, false>(buf + TE, r0, c0, r.b[0], r.b[1]);  // Bt[s][n] = B_s[n]
   };
   f32x16 acc;
   zero(acc);
-  fetch(0);
-  for (int k = 0; k < g.nnt; ++k) {
-    TM* buf = sbuf[k & 1];
-    float a[8], bb[8];
-    v8_f32(ra[0], a);
-    v8_f32(ra[1], bb);
-    put2x8<TM, false>(buf, r0, c0, a, bb);  // A[l][n] = C_l[n]
-    v8_f32(rb[0], a);
-    v8_f32(rb[1], bb);
-    put2x8<TM, false>(buf + TE, r0, c0, a, bb);  // Bt[s][n] = B_s[n]
-    __syncthreads();
-    if (k + 1 < g.nnt) fetch(k + 1);
-    mma_tile<TM>(acc, buf, buf + TE, wm, wn, lane, 64);
-  }
-  float* out = p.cb + ((b * g.nc + c) * g.ngroups + gg) * g.q * g.q;
+  Regs ra, rb;
+  pipeline2(g.nnt, ra, rb, fetch, put,
+            [&](int k) { mma_tile<TM>(acc, sbuf[k & 1], sbuf[k & 1] + TE, wm, wn, lane, 64); });
+  TM* out = static_cast<TM*>(p.cb) + ((b * g.nc + c) * g.ngroups + gg) * g.q * g.q;
 #pragma unroll
-  for (int r = 0; r < 16; ++r) out[(64 * i + acc_row(wm, lane, r)) * g.q + 64 * j + acc_col(wn, lane)] = acc[r];
+  for (int r = 0; r < 16; ++r)
+    out[(64 * i + acc_row(wm, lane, r)) * g.q + 64 * j + acc_col(wn, lane)] = from_f32<TM>(acc[r]);
 }
 
 // Entering state of every chunk (in place over the local states) and the final
@@ -124,49 +122,51 @@ __global__ void __launch_bounds__(256) state_pass(Geo g, Ptrs p) {
   v8_store(static_cast<TM*>(p.final_state) + bh * pn + e0, n, g.vec, s);
 }
 
-template <typename TM>
+template <typename TM, bool VEC>
 __global__ void __launch_bounds__(256) chunk_scan(Geo g, Ptrs p) {
   constexpr int TE = LdsTile<TM>::elems;
   __shared__ __align__(16) TM sbuf[2][2 * TE];
-  __shared__ float csc[256], dlc[256];
-  const int i = blockIdx.x % g.qb, pt = blockIdx.x / g.qb;
-  const int c = blockIdx.y;
-  const int64_t bh = blockIdx.z, b = bh / g.nheads, h = bh % g.nheads;
+  __shared__ __align__(16) float csc[256], dlc[256];
+  const WgId id = wg_id(g.qb * g.npt, g.nc);
+  const int i = id.x % g.qb, pt = id.x / g.qb;
+  const int c = id.y;
+  const int64_t bh = id.z, b = bh / g.nheads, h = bh % g.nheads;
   const int lane = threadIdx.x & 63;
   int wm, wn;
   quadrant(threadIdx.x >> 6, wm, wn);
   const int r0 = blk_r0(), c0 = blk_c0();
+  const int64_t tl0 = static_cast<int64_t>(c) * g.q + 64 * i, pc0 = static_cast<int64_t>(pt) * 64;
+  // epilogue inputs, in flight during the products
+  V8<TM> xv[2], zv[2];
+  load_xw<TM, VEC>(g, static_cast<const TM*>(p.x), b, tl0, h, pc0, xv);
+  if (p.z) load_xw<TM, VEC>(g, static_cast<const TM*>(p.z), b, tl0, h, pc0, zv);
+  float dv[8];
+  load_d8(g, p, h, pc0 + c0, dv);
   load_chunk_cs(g, p, bh, c, csc, dlc);
   __syncthreads();
   f32x16 acc;
-  chunk_out<TM>(g, p, acc, sbuf, csc, dlc, i, pt, c, bh);
+  chunk_out<TM, VEC>(g, p, acc, sbuf, csc, dlc, i, pt, c, bh);
   // epilogue through LDS: each thread owns rows r0, r0+1 and 8 consecutive d_head columns
   float* red = reinterpret_cast<float*>(&sbuf[0][0]);
   acc_to_lds(red, acc, wm, wn, lane);
   __syncthreads();
   float v[2][8];
   lds_block(red, r0, c0, v[0], v[1]);
-  const int64_t tl0 = static_cast<int64_t>(c) * g.q + 64 * i, pc = static_cast<int64_t>(pt) * 64 + c0;
-  V8<TM> xv[2], zv[2];
-  load_x2(g, static_cast<const TM*>(p.x), b, tl0, h, pt * 64, xv);
-  if (p.z) load_x2(g, static_cast<const TM*>(p.z), b, tl0, h, pt * 64, zv);
+  const int64_t pc = pc0 + c0;
 #pragma unroll
   for (int rr = 0; rr < 2; ++rr) {
-    const int64_t t = tl0 + r0 + rr;
-    const int n = t < g.length ? static_cast<int>(g.headdim - pc) : 0;
-    if (n <= 0) continue;
     float xf[8], zf[8];
     v8_f32(xv[rr], xf);
     if (p.z) v8_f32(zv[rr], zf);
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       float y = v[rr][k];
-      if (p.D && k < n) y = fmaf(g.d_per_row ? p.D[h * g.headdim + pc + k] : p.D[h], xf[k], y);
+      y = fmaf(dv[k], xf[k], y);
       if (p.z) y *= zf[k] * sigmoid(zf[k]);
       v[rr][k] = y;
     }
-    v8_store(static_cast<TM*>(p.y) + xidx(g, b, t, h, pc), n, g.vec, v[rr]);
   }
+  store_xw<TM, VEC>(g, static_cast<TM*>(p.y), b, tl0, h, pc0, v[0], v[1]);
 }
 
 // ---------------------------------------------------------------- host
@@ -207,6 +207,10 @@ int make_geo(const mko_ssd_params* prm, Geo* g) {
   g->npt = static_cast<int>((g->headdim + 63) / 64);
   g->nnt = static_cast<int>((g->dstate + 63) / 64);
   g->nnp = (g->nnt + 1) / 2;
+  if (g->nheads * g->headdim >= (int64_t(1) << 24) || g->ngroups * g->dstate >= (int64_t(1) << 24)) {
+    mko_set_error("ssd: nheads * headdim and ngroups * dstate must be below 2^24");
+    return MKO_EUNSUPPORTED;
+  }
   g->x_dtype = prm->x_dtype;
   g->dt_dtype = prm->dt_dtype;
   // 16-byte vectors of 8 elements: whole runs of d_head and d_state, aligned bases
@@ -228,7 +232,7 @@ SavedLayout saved_layout(const Geo& g) {
   l.states = o; o = align256(o + bh * g.nc * g.headdim * g.dstate * dtype_size(g.x_dtype));
   l.dl = o; o = align256(o + bh * g.nc * g.q * 4);
   l.cs = o; o = align256(o + bh * g.nc * g.q * 4);
-  l.cb = o; o = align256(o + static_cast<size_t>(g.batch) * g.nc * g.ngroups * g.q * g.q * 4);
+  l.cb = o; o = align256(o + static_cast<size_t>(g.batch) * g.nc * g.ngroups * g.q * g.q * dtype_size(g.x_dtype));
   l.total = o;
   return l;
 }
@@ -239,7 +243,7 @@ void bind_saved(const Geo& g, void* saved, Ptrs* q) {
   q->states = s + l.states;
   q->dl = reinterpret_cast<float*>(s + l.dl);
   q->cs = reinterpret_cast<float*>(s + l.cs);
-  q->cb = reinterpret_cast<float*>(s + l.cb);
+  q->cb = s + l.cb;
 }
 
 Ptrs base_ptrs(const mko_ssd_params* prm) {
@@ -269,18 +273,24 @@ Ptrs base_ptrs(const mko_ssd_params* prm) {
   return q;
 }
 
-template <typename TM>
+template <typename TM, bool VEC>
 static void launch_fwd_t(const Geo& g, const Ptrs& q, hipStream_t s) {
   const unsigned bh = static_cast<unsigned>(g.batch * g.nheads);
   MKO_TIMED("ssd_prep", s, prep<<<dim3(g.nc, g.nheads, g.batch), 256, 0, s>>>(g, q));
   MKO_TIMED("ssd_cb", s,
-            cb_kernel<TM><<<dim3(g.qb * (g.qb + 1) / 2, g.nc * g.ngroups, g.batch), 256, 0, s>>>(g, q));
+            cb_kernel<TM, VEC><<<dim3(g.qb * (g.qb + 1) / 2 * g.nc * g.ngroups * g.batch), 256, 0, s>>>(g, q));
   MKO_TIMED("ssd_chunk_state", s,
-            chunk_state<TM, false><<<dim3(g.npt * g.nnp, g.nc, bh), 256, 0, s>>>(g, q, q.states));
+            chunk_state<TM, VEC, false><<<dim3(g.npt * g.nnp * g.nc * bh), 256, 0, s>>>(g, q, q.states));
   MKO_TIMED("ssd_state_pass", s,
             state_pass<TM><<<dim3(static_cast<unsigned>((g.headdim * g.dstate + 2047) / 2048), bh), 256, 0, s>>>(
                 g, q));
-  MKO_TIMED("ssd_chunk_scan", s, chunk_scan<TM><<<dim3(g.qb * g.npt, g.nc, bh), 256, 0, s>>>(g, q));
+  MKO_TIMED("ssd_chunk_scan", s, chunk_scan<TM, VEC><<<dim3(g.qb * g.npt * g.nc * bh), 256, 0, s>>>(g, q));
+}
+
+template <typename TM>
+static void launch_fwd_t(const Geo& g, const Ptrs& q, hipStream_t s) {
+  if (g.vec) launch_fwd_t<TM, true>(g, q, s);
+  else launch_fwd_t<TM, false>(g, q, s);
 }
 
 }  // namespace ssd

@@ -64,7 +64,7 @@ struct Ptrs {
   void* states;  // (b, H, nc, P, N) TM: state entering each chunk
   float* dl;     // (b, H, nc, q) step sizes (0 past the end)
   float* cs;     // (b, H, nc, q) cumulative step * A inside the chunk
-  float* cb;     // (b, nc, G, q, q) C . B^T, lower tiles
+  void* cb;      // (b, nc, G, q, q) TM: C . B^T, lower tiles
   // backward workspace
   const void* gy;  // (b, L, H, P) TM: dy * silu(z) (dy itself without z)
   void* gyw;       // writable alias of gy when it is materialised
@@ -100,6 +100,7 @@ __device__ __forceinline__ int64_t xidx(const Geo& g, int64_t b, int64_t t, int6
 __device__ __forceinline__ int64_t bcidx(const Geo& g, int64_t b, int64_t t, int64_t gg, int64_t n) {
   return ((b * g.length + t) * g.ngroups + gg) * g.dstate + n;
 }
+__device__ __forceinline__ int clamp64(int64_t v) { return v >= 64 ? 64 : (v < 0 ? 0 : static_cast<int>(v)); }
 
 // Writes an accumulator tile (value v[r] at (acc_row, acc_col)) to a 64x65 fp32 LDS tile.
 template <typename V>
@@ -108,58 +109,42 @@ __device__ __forceinline__ void acc_to_lds(float* red, const V& v, int wm, int w
   for (int r = 0; r < 16; ++r) red[acc_row(wm, lane, r) * 65 + acc_col(wn, lane)] = v[r];
 }
 
-// Loads the thread's 2x8 block of a token-major (b, L, H, P) tensor: rows = tokens
-// t0 + r0, t0 + r0 + 1 of head h, columns = d_head pc0 + c0 .. +8.
-template <typename TM>
-__device__ __forceinline__ void load_x2(const Geo& g, const TM* src, int64_t b, int64_t t0, int64_t h, int64_t pc0,
+// 64x64 windows of the problem's tensors; the base is uniform, each lane adds a
+// 32-bit offset (load_win / store_win).
+//   x-like (b, L, H, P): rows = tokens t0 .., columns = d_head pc0 ..
+template <typename TM, bool VEC>
+__device__ __forceinline__ void load_xw(const Geo& g, const TM* src, int64_t b, int64_t t0, int64_t h, int64_t pc0,
                                         V8<TM> (&v)[2]) {
-  const int r0 = blk_r0(), c0 = blk_c0();
-#pragma unroll
-  for (int rr = 0; rr < 2; ++rr) {
-    const int64_t t = t0 + r0 + rr;
-    const int64_t pc = pc0 + c0;
-    const int n = (t < g.length) ? static_cast<int>(g.headdim - pc) : 0;
-    if (n > 0)
-      v8_load(v[rr], src + xidx(g, b, t, h, pc), n, g.vec);
-    else
-      v8_zero(v[rr]);
-  }
+  load_win<TM, VEC>(src + xidx(g, b, t0, h, pc0), static_cast<int>(g.nheads * g.headdim), clamp64(g.length - t0),
+                    static_cast<int>(g.headdim - pc0), v, src);
+}
+template <typename TM, bool VEC>
+__device__ __forceinline__ void store_xw(const Geo& g, TM* dst, int64_t b, int64_t t0, int64_t h, int64_t pc0,
+                                         const float (&a)[8], const float (&bb)[8]) {
+  store_win<TM, VEC>(dst + xidx(g, b, t0, h, pc0), static_cast<int>(g.nheads * g.headdim), clamp64(g.length - t0),
+                     static_cast<int>(g.headdim - pc0), a, bb);
+}
+//   B/C-like (b, L, G, N): rows = tokens t0 .., columns = d_state nn0 ..
+template <typename TM, bool VEC>
+__device__ __forceinline__ void load_bw(const Geo& g, const TM* src, int64_t b, int64_t t0, int64_t gg, int64_t nn0,
+                                        V8<TM> (&v)[2]) {
+  load_win<TM, VEC>(src + bcidx(g, b, t0, gg, nn0), static_cast<int>(g.ngroups * g.dstate), clamp64(g.length - t0),
+                    static_cast<int>(g.dstate - nn0), v, src);
+}
+template <typename TM, bool VEC>
+__device__ __forceinline__ void store_bw(const Geo& g, TM* dst, int64_t b, int64_t t0, int64_t gg, int64_t nn0,
+                                         const float (&a)[8], const float (&bb)[8]) {
+  store_win<TM, VEC>(dst + bcidx(g, b, t0, gg, nn0), static_cast<int>(g.ngroups * g.dstate), clamp64(g.length - t0),
+                     static_cast<int>(g.dstate - nn0), a, bb);
+}
+//   a (P, N) state matrix: rows = d_head pc0 .., columns = d_state nn0 ..
+template <typename TM, bool VEC>
+__device__ __forceinline__ void load_sw(const Geo& g, const TM* st, int64_t pc0, int64_t nn0, V8<TM> (&v)[2]) {
+  load_win<TM, VEC>(st + pc0 * g.dstate + nn0, static_cast<int>(g.dstate), clamp64(g.headdim - pc0),
+                    static_cast<int>(g.dstate - nn0), v, st);
 }
 
-// Same for a (b, L, G, N) tensor (B or C): d_state columns nn0 + c0 .. +8.
-template <typename TM>
-__device__ __forceinline__ void load_bc2(const Geo& g, const TM* src, int64_t b, int64_t t0, int64_t gg, int64_t nn0,
-                                         V8<TM> (&v)[2]) {
-  const int r0 = blk_r0(), c0 = blk_c0();
-#pragma unroll
-  for (int rr = 0; rr < 2; ++rr) {
-    const int64_t t = t0 + r0 + rr;
-    const int64_t nn = nn0 + c0;
-    const int n = (t < g.length) ? static_cast<int>(g.dstate - nn) : 0;
-    if (n > 0)
-      v8_load(v[rr], src + bcidx(g, b, t, gg, nn), n, g.vec);
-    else
-      v8_zero(v[rr]);
-  }
-}
-
-// Same for a (P, N) state matrix: rows = d_head pc0 + r0 (+1), columns nn0 + c0 .. +8.
-template <typename TM>
-__device__ __forceinline__ void load_st2(const Geo& g, const TM* st, int64_t pc0, int64_t nn0, V8<TM> (&v)[2]) {
-  const int r0 = blk_r0(), c0 = blk_c0();
-#pragma unroll
-  for (int rr = 0; rr < 2; ++rr) {
-    const int64_t pc = pc0 + r0 + rr;
-    const int64_t nn = nn0 + c0;
-    const int n = (pc < g.headdim) ? static_cast<int>(g.dstate - nn) : 0;
-    if (n > 0)
-      v8_load(v[rr], st + pc * g.dstate + nn, n, g.vec);
-    else
-      v8_zero(v[rr]);
-  }
-}
-
-// Loads 8 fp32 of a row of cb (always in bounds, 32-byte aligned).
+// 8 fp32 at p (32-byte aligned).
 __device__ __forceinline__ void load_f8(const float* p, float (&f)[8]) {
   const float4 a = reinterpret_cast<const float4*>(p)[0];
   const float4 b = reinterpret_cast<const float4*>(p)[1];
@@ -182,14 +167,15 @@ __device__ __forceinline__ void scale8(const V8<TM>& v, float s, float (&f)[8]) 
 // Both operands are token-major in HBM and the contraction runs over tokens, so both
 // are staged transposed.  Double-buffered: the loads of the next 64 tokens are in
 // flight during the products of the current ones.
-template <typename TM, bool BWD>
+template <typename TM, bool VEC, bool BWD>
 __global__ void __launch_bounds__(256) chunk_state(Geo g, Ptrs p, void* out_) {
   constexpr int TE = LdsTile<TM>::elems;
   __shared__ __align__(16) TM sbuf[2][3 * TE];
   __shared__ float s1[256];
-  const int pt = blockIdx.x / g.nnp, np = blockIdx.x % g.nnp;
-  const int c = blockIdx.y;
-  const int64_t bh = blockIdx.z, b = bh / g.nheads, h = bh % g.nheads, gg = h / g.hpg;
+  const WgId id = wg_id(g.npt * g.nnp, g.nc);
+  const int pt = id.x / g.nnp, np = id.x % g.nnp;
+  const int c = id.y;
+  const int64_t bh = id.z, b = bh / g.nheads, h = bh % g.nheads, gg = h / g.hpg;
   const int lane = threadIdx.x & 63;
   int wm, wn;
   quadrant(threadIdx.x >> 6, wm, wn);
@@ -203,37 +189,34 @@ __global__ void __launch_bounds__(256) chunk_state(Geo g, Ptrs p, void* out_) {
   const TM* X = static_cast<const TM*>(BWD ? p.gy : p.x);
   const TM* Y = static_cast<const TM*>(BWD ? p.C : p.B);
   const int64_t pc0 = static_cast<int64_t>(pt) * 64, nn0 = static_cast<int64_t>(np) * 128;
-  V8<TM> rx[2], ry0[2], ry1[2];
-  auto fetch = [&](int kb) {
+  struct Regs {
+    V8<TM> x[2], y0[2], y1[2];
+  };
+  auto fetch = [&](int kb, Regs& r) {
     const int64_t t0 = static_cast<int64_t>(c) * g.q + 64 * kb;
-    load_x2(g, X, b, t0, h, pc0, rx);
-    load_bc2(g, Y, b, t0, gg, nn0, ry0);
-    load_bc2(g, Y, b, t0, gg, nn0 + 64, ry1);
+    load_xw<TM, VEC>(g, X, b, t0, h, pc0, r.x);
+    load_bw<TM, VEC>(g, Y, b, t0, gg, nn0, r.y0);
+    load_bw<TM, VEC>(g, Y, b, t0, gg, nn0 + 64, r.y1);
+  };
+  auto put = [&](int kb, Regs& r) {
+    TM* buf = sbuf[kb & 1];
+    float a[8], bb[8];
+    scale8(r.x[0], s1[64 * kb + r0], a);
+    scale8(r.x[1], s1[64 * kb + r0 + 1], bb);
+    put2x8<TM, true>(buf, r0, c0, a, bb);                     // A[p][l]
+    put_raw<TM, true>(buf + TE, r0, c0, r.y0[0], r.y0[1]);      // Bt[n][l]
+    put_raw<TM, true>(buf + 2 * TE, r0, c0, r.y1[0], r.y1[1]);
   };
   f32x16 acc0, acc1;
   zero(acc0);
   zero(acc1);
-  fetch(0);
   __syncthreads();  // s1
-  for (int kb = 0; kb < g.qb; ++kb) {
+  Regs ra, rb;
+  pipeline2(g.qb, ra, rb, fetch, put, [&](int kb) {
     TM* buf = sbuf[kb & 1];
-    {
-      float a[8], bb[8];
-      scale8(rx[0], s1[64 * kb + r0], a);
-      scale8(rx[1], s1[64 * kb + r0 + 1], bb);
-      put2x8<TM, true>(buf, r0, c0, a, bb);  // A[p][l]
-      v8_f32(ry0[0], a);
-      v8_f32(ry0[1], bb);
-      put2x8<TM, true>(buf + TE, r0, c0, a, bb);  // Bt[n][l]
-      v8_f32(ry1[0], a);
-      v8_f32(ry1[1], bb);
-      put2x8<TM, true>(buf + 2 * TE, r0, c0, a, bb);
-    }
-    __syncthreads();
-    if (kb + 1 < g.qb) fetch(kb + 1);
     mma_tile<TM>(acc0, buf, buf + TE, wm, wn, lane, 64);
     mma_tile<TM>(acc1, buf, buf + 2 * TE, wm, wn, lane, 64);
-  }
+  });
   TM* out = static_cast<TM*>(out_) + (bh * g.nc + c) * g.headdim * g.dstate;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
@@ -252,7 +235,7 @@ __global__ void __launch_bounds__(256) chunk_state(Geo g, Ptrs p, void* out_) {
 // Stages 0..i are the intra-chunk tiles, then one stage per d_state tile.  csc/dlc
 // hold the chunk's cs and step (filled by the caller, visible before the call).
 // Ends with a barrier, so the caller may reuse sbuf.
-template <typename TM>
+template <typename TM, bool VEC>
 __device__ __forceinline__ void chunk_out(const Geo& g, const Ptrs& p, f32x16& acc, TM (*sbuf)[2 * LdsTile<TM>::elems],
                                           const float* csc, const float* dlc, int i, int pt, int c, int64_t bh) {
   constexpr int TE = LdsTile<TM>::elems;
@@ -263,63 +246,84 @@ __device__ __forceinline__ void chunk_out(const Geo& g, const Ptrs& p, f32x16& a
   const int r0 = blk_r0(), c0 = blk_c0();
   const int64_t tc = static_cast<int64_t>(c) * g.q;
   const int64_t pc0 = static_cast<int64_t>(pt) * 64;
-  const float* cbt = p.cb + ((b * g.nc + c) * g.ngroups + gg) * g.q * g.q;
+  const TM* cbt = static_cast<const TM*>(p.cb) + ((b * g.nc + c) * g.ngroups + gg) * g.q * g.q;
   const TM* X = static_cast<const TM*>(p.x);
   const TM* Cm = static_cast<const TM*>(p.C);
   const TM* S = static_cast<const TM*>(p.states) + (bh * g.nc + c) * g.headdim * g.dstate;
-  const int nstage = i + 1 + g.nnt;
-  float kf[2][8];  // cb rows (intra stages)
-  V8<TM> ra[2], rb[2];
-  auto fetch = [&](int k) {
-    if (k <= i) {
-      const int j = k;
-      load_f8(cbt + (64 * i + r0) * g.q + 64 * j + c0, kf[0]);
-      load_f8(cbt + (64 * i + r0 + 1) * g.q + 64 * j + c0, kf[1]);
-      load_x2(g, X, b, tc + 64 * j, h, pc0, rb);  // u rows s
+  const float cl0 = csc[64 * i + r0], cl1 = csc[64 * i + r0 + 1];
+  const float e0 = fast_exp(cl0), e1 = fast_exp(cl1);
+  // Stages 0 .. nnt-1: state part, A = e^{cs_l} C_l[n], Bt = S_in[p][n];
+  // stages nnt .. nnt+i: intra-chunk tiles j, A = K[l][s], Bt = step_s x_s[p].
+  // Both kinds load two rows of two 64-wide windows, so the loads in flight are the
+  // same on every path.
+  struct Regs {
+    V8<TM> a[2], b[2];
+  };
+  auto fetch = [&](int k, Regs& r) {
+    if (k < g.nnt) {
+      load_bw<TM, VEC>(g, Cm, b, tc + 64 * i, gg, 64 * k, r.a);  // C rows l
+      load_sw<TM, VEC>(g, S, pc0, 64 * k, r.b);                  // S rows p
     } else {
-      const int64_t nn0 = static_cast<int64_t>(k - i - 1) * 64;
-      load_bc2(g, Cm, b, tc + 64 * i, gg, nn0, ra);  // C rows l
-      load_st2(g, S, pc0, nn0, rb);                  // S rows p
+      const int j = k - g.nnt;
+      load_win<TM, true>(cbt + (64 * i) * g.q + 64 * j, g.q, 64, 64, r.a, cbt);  // cb rows l
+      load_xw<TM, VEC>(g, X, b, tc + 64 * j, h, pc0, r.b);                      // x rows s
+    }
+  };
+  auto put = [&](int k, Regs& r) {
+    TM* buf = sbuf[k & 1];
+    float a[8], bb[8];
+    if (k < g.nnt) {
+      scale8(r.a[0], e0, a);
+      scale8(r.a[1], e1, bb);
+      put2x8<TM, false>(buf, r0, c0, a, bb);                  // A[l][n] = e^{cs_l} C_l[n]
+      put_raw<TM, false>(buf + TE, r0, c0, r.b[0], r.b[1]);  // Bt[p][n] = S_in[p][n]
+    } else {
+      const int j = k - g.nnt;
+      const float4 cs_a = *reinterpret_cast<const float4*>(csc + 64 * j + c0);
+      const float4 cs_b = *reinterpret_cast<const float4*>(csc + 64 * j + c0 + 4);
+      const float css[8] = {cs_a.x, cs_a.y, cs_a.z, cs_a.w, cs_b.x, cs_b.y, cs_b.z, cs_b.w};
+      v8_f32(r.a[0], a);
+      v8_f32(r.a[1], bb);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        a[e] *= fast_exp(cl0 - css[e]);
+        bb[e] *= fast_exp(cl1 - css[e]);
+      }
+      if (j == i) {  // causal mask on the diagonal tile
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          if (c0 + e > r0) a[e] = 0.0f;
+          if (c0 + e > r0 + 1) bb[e] = 0.0f;
+        }
+      }
+      put2x8<TM, false>(buf, r0, c0, a, bb);  // A[l][s] = K
+      scale8(r.b[0], dlc[64 * j + r0], a);
+      scale8(r.b[1], dlc[64 * j + r0 + 1], bb);
+      put2x8<TM, true>(buf + TE, r0, c0, a, bb);  // Bt[p][s] = step_s x_s[p]
     }
   };
   zero(acc);
-  fetch(0);
-  for (int k = 0; k < nstage; ++k) {
-    TM* buf = sbuf[k & 1];
-    float a[8], bb[8];
-    if (k <= i) {
-      const int j = k;
-      const float cl0 = csc[64 * i + r0], cl1 = csc[64 * i + r0 + 1];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int s = 64 * j + c0 + e;
-        const float css = csc[s];
-        a[e] = (s <= 64 * i + r0) ? kf[0][e] * fast_exp(cl0 - css) : 0.0f;
-        bb[e] = (s <= 64 * i + r0 + 1) ? kf[1][e] * fast_exp(cl1 - css) : 0.0f;
-      }
-      put2x8<TM, false>(buf, r0, c0, a, bb);  // A[l][s] = K
-      scale8(rb[0], dlc[64 * j + r0], a);
-      scale8(rb[1], dlc[64 * j + r0 + 1], bb);
-      put2x8<TM, true>(buf + TE, r0, c0, a, bb);  // Bt[p][s] = step_s x_s[p]
-    } else {
-      scale8(ra[0], fast_exp(csc[64 * i + r0]), a);
-      scale8(ra[1], fast_exp(csc[64 * i + r0 + 1]), bb);
-      put2x8<TM, false>(buf, r0, c0, a, bb);  // A[l][n] = e^{cs_l} C_l[n]
-      v8_f32(rb[0], a);
-      v8_f32(rb[1], bb);
-      put2x8<TM, false>(buf + TE, r0, c0, a, bb);  // Bt[p][n] = S_in[p][n]
-    }
-    __syncthreads();
-    if (k + 1 < nstage) fetch(k + 1);
-    mma_tile<TM>(acc, buf, buf + TE, wm, wn, lane, 64);
-  }
+  Regs ra, rb;
+  pipeline2(g.nnt + i + 1, ra, rb, fetch, put,
+            [&](int k) { mma_tile<TM>(acc, sbuf[k & 1], sbuf[k & 1] + TE, wm, wn, lane, 64); });
   __syncthreads();
+}
+
+// The skip weights D of the thread's 8 d_head columns (zero without D).
+__device__ __forceinline__ void load_d8(const Geo& g, const Ptrs& p, int64_t h, int64_t pc, float (&d)[8]) {
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    float v = 0.0f;
+    if (p.D) v = g.d_per_row ? (pc + k < g.headdim ? p.D[h * g.headdim + pc + k] : 0.0f) : p.D[h];
+    d[k] = v;
+  }
 }
 
 // Loads cs and step of a whole chunk into LDS (q <= 256 values each).
 __device__ __forceinline__ void load_chunk_cs(const Geo& g, const Ptrs& p, int64_t bh, int c, float* csc, float* dlc) {
   const int64_t so = (bh * g.nc + c) * g.q;
-  for (int l = threadIdx.x; l < g.q; l += 256) {
+  const int l = threadIdx.x;  // q <= 256
+  if (l < g.q) {
     csc[l] = p.cs[so + l];
     dlc[l] = p.dl[so + l];
   }

@@ -45,59 +45,57 @@ __device__ __forceinline__ float block_sum(float v, float* wsum) {
   return (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
 }
 
-template <typename TM>
+template <typename TM, bool VEC>
 __global__ void __launch_bounds__(256) gate(Geo g, BwdPlan pl, Ptrs p) {
   constexpr int TE = LdsTile<TM>::elems;
   __shared__ __align__(16) TM sbuf[2][2 * TE];
-  __shared__ float csc[256], dlc[256];
+  __shared__ __align__(16) float csc[256], dlc[256];
   __shared__ float colred[4][64];
-  const int i = blockIdx.x % g.qb, pt = blockIdx.x / g.qb;
-  const int c = blockIdx.y;
-  const int64_t bh = blockIdx.z, b = bh / g.nheads, h = bh % g.nheads;
+  const WgId id = wg_id(g.qb * g.npt, g.nc);
+  const int i = id.x % g.qb, pt = id.x / g.qb;
+  const int c = id.y;
+  const int64_t bh = id.z, b = bh / g.nheads, h = bh % g.nheads;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int wm, wn;
   quadrant(wave, wm, wn);
   const int r0 = blk_r0(), c0 = blk_c0();
+  const int64_t tl0 = static_cast<int64_t>(c) * g.q + 64 * i, pc0 = static_cast<int64_t>(pt) * 64, pc = pc0 + c0;
+  // epilogue inputs, in flight during the products
+  V8<TM> xv[2], dyv[2], zv[2];
+  load_xw<TM, VEC>(g, static_cast<const TM*>(p.x), b, tl0, h, pc0, xv);
+  load_xw<TM, VEC>(g, static_cast<const TM*>(p.dy), b, tl0, h, pc0, dyv);
+  if (p.z) load_xw<TM, VEC>(g, static_cast<const TM*>(p.z), b, tl0, h, pc0, zv);
+  float dv[8];
+  load_d8(g, p, h, pc, dv);
   load_chunk_cs(g, p, bh, c, csc, dlc);
   __syncthreads();
   f32x16 acc;
-  chunk_out<TM>(g, p, acc, sbuf, csc, dlc, i, pt, c, bh);
+  chunk_out<TM, VEC>(g, p, acc, sbuf, csc, dlc, i, pt, c, bh);
   float* red = reinterpret_cast<float*>(&sbuf[0][0]);
   acc_to_lds(red, acc, wm, wn, lane);
   __syncthreads();
   float yt[2][8];
   lds_block(red, r0, c0, yt[0], yt[1]);
-  const int64_t tl0 = static_cast<int64_t>(c) * g.q + 64 * i, pc = static_cast<int64_t>(pt) * 64 + c0;
-  V8<TM> xv[2], dyv[2], zv[2];
-  load_x2(g, static_cast<const TM*>(p.x), b, tl0, h, pt * 64, xv);
-  load_x2(g, static_cast<const TM*>(p.dy), b, tl0, h, pt * 64, dyv);
-  if (p.z) load_x2(g, static_cast<const TM*>(p.z), b, tl0, h, pt * 64, zv);
-  float dd[8];
+  float dd[8], gyo[2][8], dzo[2][8];
 #pragma unroll
   for (int k = 0; k < 8; ++k) dd[k] = 0.0f;
   const int64_t po = ((bh * g.nc + c) * g.npt + pt) * g.q + 64 * i;
 #pragma unroll
   for (int rr = 0; rr < 2; ++rr) {
-    const int64_t t = tl0 + r0 + rr;
-    const int n = t < g.length ? static_cast<int>(g.headdim - pc) : 0;
     float xf[8], gyf[8];
     v8_f32(xv[rr], xf);
     v8_f32(dyv[rr], gyf);
     if (p.z) {
-      float zf[8], dzf[8];
+      float zf[8];
       v8_f32(zv[rr], zf);
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         const float sg = sigmoid(zf[k]);
         float ypre = yt[rr][k];
-        if (p.D && k < n) ypre = fmaf(g.d_per_row ? p.D[h * g.headdim + pc + k] : p.D[h], xf[k], ypre);
-        dzf[k] = gyf[k] * ypre * sg * fmaf(zf[k], 1.0f - sg, 1.0f);
+        ypre = fmaf(dv[k], xf[k], ypre);
+        dzo[rr][k] = gyf[k] * ypre * sg * fmaf(zf[k], 1.0f - sg, 1.0f);
         gyf[k] = to_f32(from_f32<TM>(gyf[k] * zf[k] * sg));  // as stored for the other kernels
-      }
-      if (n > 0) {
-        const int64_t xi = xidx(g, b, t, h, pc);
-        v8_store(static_cast<TM*>(p.dz) + xi, n, g.vec, dzf);
-        v8_store(static_cast<TM*>(p.gyw) + xi, n, g.vec, gyf);
+        gyo[rr][k] = gyf[k];
       }
     }
     float ya = 0.0f;
@@ -108,6 +106,10 @@ __global__ void __launch_bounds__(256) gate(Geo g, BwdPlan pl, Ptrs p) {
     }
     ya = row8_sum(ya);
     if ((threadIdx.x & 7) == 0) p.ya[po + r0 + rr] = ya;
+  }
+  if (p.z) {
+    store_xw<TM, VEC>(g, static_cast<TM*>(p.dz), b, tl0, h, pc0, dzo[0], dzo[1]);
+    store_xw<TM, VEC>(g, static_cast<TM*>(p.gyw), b, tl0, h, pc0, gyo[0], gyo[1]);
   }
   if (p.D) {
     // column sums over the 64 rows: lanes sharing tid%8 (xor 8, 16, 32), then the 4 wavefronts
@@ -124,10 +126,10 @@ __global__ void __launch_bounds__(256) gate(Geo g, BwdPlan pl, Ptrs p) {
       for (int k = 0; k < 8; ++k) colred[wave][c0 + k] = dd[k];
     }
     __syncthreads();
-    if (threadIdx.x < 64 && pt * 64 + threadIdx.x < g.headdim) {
+    if (threadIdx.x < 64 && pc0 + threadIdx.x < g.headdim) {
       const int col = threadIdx.x;
       const float sum = (colred[0][col] + colred[1][col]) + (colred[2][col] + colred[3][col]);
-      p.pdD[(((b * g.nc + c) * g.qb + i) * g.nheads + h) * g.headdim + pt * 64 + col] = sum;
+      p.pdD[(((b * g.nc + c) * g.qb + i) * g.nheads + h) * g.headdim + pc0 + col] = sum;
     }
   }
 }
@@ -182,14 +184,15 @@ __global__ void __launch_bounds__(256) state_rev(Geo g, BwdPlan pl, Ptrs p) {
 // du for the 64-token tile j and d_head tile pt of one (b, h, chunk):
 //   du[s][p] = e^{T - cs_s} sum_n B_s[n] G[p][n]  +  sum_{l >= s} K[l][s] gy_l[p]
 // The state part runs first and its u.du_state is taken before the intra part is added.
-template <typename TM>
+template <typename TM, bool VEC>
 __global__ void __launch_bounds__(256) du_kernel(Geo g, BwdPlan pl, Ptrs p) {
   constexpr int TE = LdsTile<TM>::elems;
   __shared__ __align__(16) TM sbuf[2][2 * TE];
-  __shared__ float csc[256], dlc[256];
-  const int j = blockIdx.x % g.qb, pt = blockIdx.x / g.qb;
-  const int c = blockIdx.y;
-  const int64_t bh = blockIdx.z, b = bh / g.nheads, h = bh % g.nheads, gg = h / g.hpg;
+  __shared__ __align__(16) float csc[256], dlc[256];
+  const WgId id = wg_id(g.qb * g.npt, g.nc);
+  const int j = id.x % g.qb, pt = id.x / g.qb;
+  const int c = id.y;
+  const int64_t bh = id.z, b = bh / g.nheads, h = bh % g.nheads, gg = h / g.hpg;
   const int lane = threadIdx.x & 63;
   int wm, wn;
   quadrant(threadIdx.x >> 6, wm, wn);
@@ -197,30 +200,18 @@ __global__ void __launch_bounds__(256) du_kernel(Geo g, BwdPlan pl, Ptrs p) {
   load_chunk_cs(g, p, bh, c, csc, dlc);
   const int64_t tc = static_cast<int64_t>(c) * g.q, ts0 = tc + 64 * j;
   const int64_t pc0 = static_cast<int64_t>(pt) * 64, pc = pc0 + c0;
-  const float* cbt = p.cb + ((b * g.nc + c) * g.ngroups + gg) * g.q * g.q;
+  const TM* cbt = static_cast<const TM*>(p.cb) + ((b * g.nc + c) * g.ngroups + gg) * g.q * g.q;
   const TM* Bm = static_cast<const TM*>(p.B);
   const TM* gy = static_cast<const TM*>(p.gy);
   const TM* G = static_cast<const TM*>(p.dstates) + (bh * g.nc + c) * g.headdim * g.dstate;
-  const int nstate = g.nnt, nst = g.nnt + g.qb - j;
-  float kf[2][8];
-  V8<TM> ra[2], rb[2];
-  auto fetch = [&](int k) {
-    if (k < nstate) {
-      load_bc2(g, Bm, b, ts0, gg, 64 * k, ra);  // B rows s
-      load_st2(g, G, pc0, 64 * k, rb);          // G rows p
-    } else {
-      const int i = j + k - nstate;
-      load_f8(cbt + (64 * i + r0) * g.q + 64 * j + c0, kf[0]);      // cb rows l
-      load_f8(cbt + (64 * i + r0 + 1) * g.q + 64 * j + c0, kf[1]);
-      load_x2(g, gy, b, tc + 64 * i, h, pc0, rb);                   // gy rows l
-    }
-  };
-  // x and u of the thread's epilogue block (rows s = r0, r0+1 of tile j)
-  V8<TM> xv[2];
-  load_x2(g, static_cast<const TM*>(p.x), b, ts0, h, pc0, xv);
+  // x and gy of the thread's epilogue block (rows s = r0, r0+1 of tile j)
+  V8<TM> xv[2], gv[2];
+  load_xw<TM, VEC>(g, static_cast<const TM*>(p.x), b, ts0, h, pc0, xv);
+  load_xw<TM, VEC>(g, gy, b, ts0, h, pc0, gv);
+  float dv[8];
+  load_d8(g, p, h, pc, dv);
   f32x16 acc;
   zero(acc);
-  fetch(0);
   __syncthreads();  // csc, dlc
   const float T = csc[g.q - 1];
   float xf[2][8], uf[2][8];
@@ -233,36 +224,61 @@ __global__ void __launch_bounds__(256) du_kernel(Geo g, BwdPlan pl, Ptrs p) {
   }
   float* red = reinterpret_cast<float*>(&sbuf[0][0]);
   const int64_t po = ((bh * g.nc + c) * g.npt + pt) * g.q + 64 * j;
-  for (int k = 0; k < nst; ++k) {
+  // Stages 0 .. nnt-1: state part, A = e^{T - cs_s} B_s[n], Bt = G[p][n]; then
+  // tau_s = u_s . du_state_s; stages nnt .. : intra-chunk tiles i >= j,
+  // A = K[l][s] (transposed), Bt = gy_l[p] (transposed).  Both kinds load two rows
+  // of two 64-wide windows.
+  struct Regs {
+    V8<TM> a[2], b[2];
+  };
+  auto fetch = [&](int k, Regs& r) {
+    if (k < g.nnt) {
+      load_bw<TM, VEC>(g, Bm, b, ts0, gg, 64 * k, r.a);  // B rows s
+      load_sw<TM, VEC>(g, G, pc0, 64 * k, r.b);          // G rows p
+    } else {
+      const int i = j + k - g.nnt;
+      load_win<TM, true>(cbt + (64 * i) * g.q + 64 * j, g.q, 64, 64, r.a, cbt);  // cb rows l
+      load_xw<TM, VEC>(g, gy, b, tc + 64 * i, h, pc0, r.b);                     // gy rows l
+    }
+  };
+  const float w0 = fast_exp(T - csc[64 * j + r0]), w1 = fast_exp(T - csc[64 * j + r0 + 1]);
+  const float4 cs_a = *reinterpret_cast<const float4*>(csc + 64 * j + c0);
+  const float4 cs_b = *reinterpret_cast<const float4*>(csc + 64 * j + c0 + 4);
+  const float css[8] = {cs_a.x, cs_a.y, cs_a.z, cs_a.w, cs_b.x, cs_b.y, cs_b.z, cs_b.w};
+  auto put = [&](int k, Regs& r) {
     TM* buf = sbuf[k & 1];
     float a[8], bb[8];
-    if (k < nstate) {
-      scale8(ra[0], fast_exp(T - csc[64 * j + r0]), a);
-      scale8(ra[1], fast_exp(T - csc[64 * j + r0 + 1]), bb);
-      put2x8<TM, false>(buf, r0, c0, a, bb);  // A[s][n] = e^{T - cs_s} B_s[n]
-      v8_f32(rb[0], a);
-      v8_f32(rb[1], bb);
-      put2x8<TM, false>(buf + TE, r0, c0, a, bb);  // Bt[p][n] = G[p][n]
+    if (k < g.nnt) {
+      scale8(r.a[0], w0, a);
+      scale8(r.a[1], w1, bb);
+      put2x8<TM, false>(buf, r0, c0, a, bb);                  // A[s][n] = e^{T - cs_s} B_s[n]
+      put_raw<TM, false>(buf + TE, r0, c0, r.b[0], r.b[1]);  // Bt[p][n] = G[p][n]
     } else {
-      const int i = j + k - nstate;
+      const int i = j + k - g.nnt;
       const float cl0 = csc[64 * i + r0], cl1 = csc[64 * i + r0 + 1];
+      v8_f32(r.a[0], a);
+      v8_f32(r.a[1], bb);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int s = 64 * j + c0 + e;
-        const float css = csc[s];
-        a[e] = (s <= 64 * i + r0) ? kf[0][e] * fast_exp(cl0 - css) : 0.0f;
-        bb[e] = (s <= 64 * i + r0 + 1) ? kf[1][e] * fast_exp(cl1 - css) : 0.0f;
+        a[e] *= fast_exp(cl0 - css[e]);
+        bb[e] *= fast_exp(cl1 - css[e]);
       }
-      put2x8<TM, true>(buf, r0, c0, a, bb);  // A[s][l] = K[l][s]
-      v8_f32(rb[0], a);
-      v8_f32(rb[1], bb);
-      put2x8<TM, true>(buf + TE, r0, c0, a, bb);  // Bt[p][l] = gy_l[p]
+      if (i == j) {  // causal mask on the diagonal tile
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          if (c0 + e > r0) a[e] = 0.0f;
+          if (c0 + e > r0 + 1) bb[e] = 0.0f;
+        }
+      }
+      put2x8<TM, true>(buf, r0, c0, a, bb);                  // A[s][l] = K[l][s]
+      put_raw<TM, true>(buf + TE, r0, c0, r.b[0], r.b[1]);  // Bt[p][l] = gy_l[p]
     }
-    __syncthreads();
-    if (k + 1 < nst) fetch(k + 1);
-    mma_tile<TM>(acc, buf, buf + TE, wm, wn, lane, 64);
-    if (k == nstate - 1) {
-      // tau_s = u_s . du_state_s
+  };
+  Regs ra, rb;
+  pipeline2(g.nnt + g.qb - j, ra, rb, fetch, put, [&](int k) {
+    mma_tile<TM>(acc, sbuf[k & 1], sbuf[k & 1] + TE, wm, wn, lane, 64);
+    if (k == g.nnt - 1) {
+      // tau_s = u_s . du_state_s (red aliases sbuf[0]; barriers on both sides)
       __syncthreads();
       acc_to_lds(red, acc, wm, wn, lane);
       __syncthreads();
@@ -278,31 +294,26 @@ __global__ void __launch_bounds__(256) du_kernel(Geo g, BwdPlan pl, Ptrs p) {
       }
       __syncthreads();
     }
-  }
+  });
   __syncthreads();
   acc_to_lds(red, acc, wm, wn, lane);
   __syncthreads();
-  float du[2][8];
+  float du[2][8], dxo[2][8];
   lds_block(red, r0, c0, du[0], du[1]);
-  V8<TM> gv[2];
-  load_x2(g, gy, b, ts0, h, pc0, gv);
 #pragma unroll
   for (int rr = 0; rr < 2; ++rr) {
-    const int64_t t = ts0 + r0 + rr;
-    const int n = t < g.length ? static_cast<int>(g.headdim - pc) : 0;
-    float gf[8], dxf[8];
+    float gf[8];
     v8_f32(gv[rr], gf);
     const float d = dlc[64 * j + r0 + rr];
     float sx = 0.0f, su = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       float v = d * du[rr][e];
-      if (p.D && e < n) v = fmaf(g.d_per_row ? p.D[h * g.headdim + pc + e] : p.D[h], gf[e], v);
-      dxf[e] = v;
+      v = fmaf(dv[e], gf[e], v);
+      dxo[rr][e] = v;
       sx = fmaf(xf[rr][e], du[rr][e], sx);
       su = fmaf(uf[rr][e], du[rr][e], su);
     }
-    if (n > 0) v8_store(static_cast<TM*>(p.dx) + xidx(g, b, t, h, pc), n, g.vec, dxf);
     sx = row8_sum(sx);
     su = row8_sum(su);
     if ((threadIdx.x & 7) == 0) {
@@ -310,21 +321,23 @@ __global__ void __launch_bounds__(256) du_kernel(Geo g, BwdPlan pl, Ptrs p) {
       p.ut[po + r0 + rr] = su;
     }
   }
+  store_xw<TM, VEC>(g, static_cast<TM*>(p.dx), b, ts0, h, pc0, dxo[0], dxo[1]);
 }
 
 // Adjoint of C.B^T for one lower tile (i, j) of a chunk, summed over a block of the
 // group's heads: sum_h (gy_i u_j^T) o e^{cs_l - cs_s}.
-template <typename TM>
+template <typename TM, bool VEC>
 __global__ void __launch_bounds__(256) dcb_kernel(Geo g, BwdPlan pl, Ptrs p) {
   constexpr int TE = LdsTile<TM>::elems;
   __shared__ __align__(16) TM sbuf[2][2 * TE];
   __shared__ float csr[2][64], css[2][64];
-  const int pair = blockIdx.x / pl.hb1, hb = blockIdx.x % pl.hb1;
+  const WgId id = wg_id(pl.npairs * pl.hb1, g.nc * g.ngroups);
+  const int pair = id.x / pl.hb1, hb = id.x % pl.hb1;
   int i = 0;
   while ((i + 1) * (i + 2) / 2 <= pair) ++i;
   const int j = pair - i * (i + 1) / 2;
-  const int c = blockIdx.y / g.ngroups;
-  const int64_t gg = blockIdx.y % g.ngroups, b = blockIdx.z;
+  const int c = id.y / g.ngroups;
+  const int64_t gg = id.y % g.ngroups, b = id.z;
   const int lane = threadIdx.x & 63;
   int wm, wn;
   quadrant(threadIdx.x >> 6, wm, wn);
@@ -336,51 +349,51 @@ __global__ void __launch_bounds__(256) dcb_kernel(Geo g, BwdPlan pl, Ptrs p) {
   const int nst = nh * g.npt;
   const TM* gy = static_cast<const TM*>(p.gy);
   const TM* X = static_cast<const TM*>(p.x);
-  V8<TM> ra[2], rb[2];
-  float dls[2], cr = 0.0f, cc = 0.0f;
-  auto fetch = [&](int k) {
+  struct Regs {
+    V8<TM> gm[2], xm[2];
+    float dls[2], cr, cc;
+  };
+  auto fetch = [&](int k, Regs& r) {
     const int hh = k / g.npt, pt = k % g.npt;
     const int64_t h = h0 + hh;
     const int64_t so = ((b * g.nheads + h) * g.nc + c) * g.q;
-    load_x2(g, gy, b, tc + 64 * i, h, pt * 64, ra);  // gy rows l
-    load_x2(g, X, b, tc + 64 * j, h, pt * 64, rb);   // x rows s
-    dls[0] = p.dl[so + 64 * j + r0];
-    dls[1] = p.dl[so + 64 * j + r0 + 1];
+    load_xw<TM, VEC>(g, gy, b, tc + 64 * i, h, pt * 64, r.gm);  // gy rows l
+    load_xw<TM, VEC>(g, X, b, tc + 64 * j, h, pt * 64, r.xm);   // x rows s
+    r.dls[0] = p.dl[so + 64 * j + r0];
+    r.dls[1] = p.dl[so + 64 * j + r0 + 1];
+    r.cr = p.cs[so + 64 * i + lane];
+    r.cc = p.cs[so + 64 * j + lane];
+  };
+  auto put = [&](int k, Regs& r) {
+    const int hh = k / g.npt, pt = k % g.npt;
+    TM* buf = sbuf[k & 1];
+    float a[8], bb[8];
+    put_raw<TM, false>(buf, r0, c0, r.gm[0], r.gm[1]);  // A[l][p] = gy_l[p]
+    scale8(r.xm[0], r.dls[0], a);
+    scale8(r.xm[1], r.dls[1], bb);
+    put2x8<TM, false>(buf + TE, r0, c0, a, bb);  // Bt[s][p] = step_s x_s[p]
     if (pt == 0 && threadIdx.x < 64) {
-      cr = p.cs[so + 64 * i + threadIdx.x];
-      cc = p.cs[so + 64 * j + threadIdx.x];
+      csr[hh & 1][threadIdx.x] = r.cr;
+      css[hh & 1][threadIdx.x] = r.cc;
     }
   };
   f32x16 dacc, w;
   zero(dacc);
   zero(w);
-  if (nst > 0) fetch(0);
-  for (int k = 0; k < nst; ++k) {
+  Regs ra, rb;
+  pipeline2(nst, ra, rb, fetch, put, [&](int k) {
     const int hh = k / g.npt, pt = k % g.npt;
-    TM* buf = sbuf[k & 1];
-    float a[8], bb[8];
-    v8_f32(ra[0], a);
-    v8_f32(ra[1], bb);
-    put2x8<TM, false>(buf, r0, c0, a, bb);  // A[l][p] = gy_l[p]
-    scale8(rb[0], dls[0], a);
-    scale8(rb[1], dls[1], bb);
-    put2x8<TM, false>(buf + TE, r0, c0, a, bb);  // Bt[s][p] = step_s x_s[p]
-    if (pt == 0 && threadIdx.x < 64) {
-      csr[hh & 1][threadIdx.x] = cr;
-      css[hh & 1][threadIdx.x] = cc;
-    }
-    __syncthreads();
-    if (k + 1 < nst) fetch(k + 1);
-    mma_tile<TM>(w, buf, buf + TE, wm, wn, lane, 64);
+    mma_tile<TM>(w, sbuf[k & 1], sbuf[k & 1] + TE, wm, wn, lane, 64);
     if (pt == g.npt - 1) {
+      const float cs_s = css[hh & 1][acc_col(wn, lane)];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int l = acc_row(wm, lane, r), s = acc_col(wn, lane);
-        if (i != j || s <= l) dacc[r] = fmaf(w[r], fast_exp(csr[hh & 1][l] - css[hh & 1][s]), dacc[r]);
+        if (i != j || s <= l) dacc[r] = fmaf(w[r], fast_exp(csr[hh & 1][l] - cs_s), dacc[r]);
       }
       zero(w);
     }
-  }
+  });
   float* out = p.dcb + (((b * g.nc + c) * g.ngroups + gg) * pl.hb1 + hb) * g.q * g.q;
 #pragma unroll
   for (int r = 0; r < 16; ++r)
@@ -390,18 +403,19 @@ __global__ void __launch_bounds__(256) dcb_kernel(Geo g, BwdPlan pl, Ptrs p) {
 // State terms of dB (which 0: sum_h e^{T - cs_s} step_s x_s G) and dC (which 1:
 // sum_h e^{cs_l} gy_l S_in) for one 64-token tile and two d_state tiles, over a
 // block of the group's heads.
-template <typename TM>
+template <typename TM, bool VEC>
 __global__ void __launch_bounds__(256) dbc_state(Geo g, BwdPlan pl, Ptrs p) {
   constexpr int TE = LdsTile<TM>::elems;
   __shared__ __align__(16) TM sbuf[2][3 * TE];
-  int idx = blockIdx.x;
+  const WgId id = wg_id(g.qb * g.nnp * 2 * pl.hb2, g.nc * g.ngroups);
+  int idx = id.x;
   const int hb = idx % pl.hb2;
   idx /= pl.hb2;
   const int which = idx % 2;
   idx /= 2;
   const int np = idx % g.nnp, tt = idx / g.nnp;
-  const int c = blockIdx.y / g.ngroups;
-  const int64_t gg = blockIdx.y % g.ngroups, b = blockIdx.z;
+  const int c = id.y / g.ngroups;
+  const int64_t gg = id.y % g.ngroups, b = id.z;
   const int lane = threadIdx.x & 63;
   int wm, wn;
   quadrant(threadIdx.x >> 6, wm, wn);
@@ -414,44 +428,45 @@ __global__ void __launch_bounds__(256) dbc_state(Geo g, BwdPlan pl, Ptrs p) {
   const int nst = nh * g.npt;
   const TM* src = static_cast<const TM*>(which ? p.gy : p.x);
   const TM* stm = static_cast<const TM*>(which ? p.states : p.dstates);
-  V8<TM> ra[2], rb0[2], rb1[2];
-  float sc[2];
-  auto fetch = [&](int k) {
+  struct Regs {
+    V8<TM> src[2], s0[2], s1[2];
+    float cl[2], dl[2], T;
+  };
+  auto fetch = [&](int k, Regs& r) {
     const int hh = k / g.npt, pt = k % g.npt;
     const int64_t h = h0 + hh, bh = b * g.nheads + h;
     const int64_t so = (bh * g.nc + c) * g.q;
-    load_x2(g, src, b, tl0, h, pt * 64, ra);  // rows l
+    load_xw<TM, VEC>(g, src, b, tl0, h, pt * 64, r.src);  // rows l
     const TM* st = stm + (bh * g.nc + c) * g.headdim * g.dstate;
-    load_st2(g, st, pt * 64, nn0, rb0);        // rows p
-    load_st2(g, st, pt * 64, nn0 + 64, rb1);
+    load_sw<TM, VEC>(g, st, pt * 64, nn0, r.s0);  // rows p
+    load_sw<TM, VEC>(g, st, pt * 64, nn0 + 64, r.s1);
 #pragma unroll
     for (int rr = 0; rr < 2; ++rr) {
-      const int l = 64 * tt + r0 + rr;
-      const float cl = p.cs[so + l];
-      sc[rr] = which ? fast_exp(cl) : p.dl[so + l] * fast_exp(p.cs[so + g.q - 1] - cl);
+      r.cl[rr] = p.cs[so + 64 * tt + r0 + rr];
+      r.dl[rr] = p.dl[so + 64 * tt + r0 + rr];
     }
+    r.T = p.cs[so + g.q - 1];
+  };
+  auto put = [&](int k, Regs& r) {
+    TM* buf = sbuf[k & 1];
+    float a[8], bb[8];
+    const float sc0 = which ? fast_exp(r.cl[0]) : r.dl[0] * fast_exp(r.T - r.cl[0]);
+    const float sc1 = which ? fast_exp(r.cl[1]) : r.dl[1] * fast_exp(r.T - r.cl[1]);
+    scale8(r.src[0], sc0, a);
+    scale8(r.src[1], sc1, bb);
+    put2x8<TM, false>(buf, r0, c0, a, bb);                    // A[l][p]
+    put_raw<TM, true>(buf + TE, r0, c0, r.s0[0], r.s0[1]);      // Bt[n][p] = S[p][n]
+    put_raw<TM, true>(buf + 2 * TE, r0, c0, r.s1[0], r.s1[1]);
   };
   f32x16 acc0, acc1;
   zero(acc0);
   zero(acc1);
-  if (nst > 0) fetch(0);
-  for (int k = 0; k < nst; ++k) {
+  Regs ra, rb;
+  pipeline2(nst, ra, rb, fetch, put, [&](int k) {
     TM* buf = sbuf[k & 1];
-    float a[8], bb[8];
-    scale8(ra[0], sc[0], a);
-    scale8(ra[1], sc[1], bb);
-    put2x8<TM, false>(buf, r0, c0, a, bb);  // A[l][p]
-    v8_f32(rb0[0], a);
-    v8_f32(rb0[1], bb);
-    put2x8<TM, true>(buf + TE, r0, c0, a, bb);  // Bt[n][p] = S[p][n]
-    v8_f32(rb1[0], a);
-    v8_f32(rb1[1], bb);
-    put2x8<TM, true>(buf + 2 * TE, r0, c0, a, bb);
-    __syncthreads();
-    if (k + 1 < nst) fetch(k + 1);
     mma_tile<TM>(acc0, buf, buf + TE, wm, wn, lane, 64);
     mma_tile<TM>(acc1, buf, buf + 2 * TE, wm, wn, lane, 64);
-  }
+  });
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int64_t t = tl0 + acc_row(wm, lane, r);
@@ -465,16 +480,17 @@ __global__ void __launch_bounds__(256) dbc_state(Geo g, BwdPlan pl, Ptrs p) {
 
 // dC = dCB B (which 1) and dB = dCB^T C (which 0) for one 64-token tile and two
 // d_state tiles, plus the head-block partials of the state terms.
-template <typename TM>
+template <typename TM, bool VEC>
 __global__ void __launch_bounds__(256) dbc_final(Geo g, BwdPlan pl, Ptrs p) {
   constexpr int TE = LdsTile<TM>::elems;
   __shared__ __align__(16) TM sbuf[2][3 * TE];
-  int idx = blockIdx.x;
+  const WgId id = wg_id(g.qb * g.nnp * 2, g.nc * g.ngroups);
+  int idx = id.x;
   const int which = idx % 2;
   idx /= 2;
   const int np = idx % g.nnp, tt = idx / g.nnp;
-  const int c = blockIdx.y / g.ngroups;
-  const int64_t gg = blockIdx.y % g.ngroups, b = blockIdx.z;
+  const int c = id.y / g.ngroups;
+  const int64_t gg = id.y % g.ngroups, b = id.z;
   const int lane = threadIdx.x & 63;
   int wm, wn;
   quadrant(threadIdx.x >> 6, wm, wn);
@@ -484,49 +500,47 @@ __global__ void __launch_bounds__(256) dbc_final(Geo g, BwdPlan pl, Ptrs p) {
   const int64_t qq = static_cast<int64_t>(g.q) * g.q;
   const float* dcb = p.dcb + ((b * g.nc + c) * g.ngroups + gg) * pl.hb1 * qq;
   const TM* Om = static_cast<const TM*>(which ? p.B : p.C);  // the other operand
-  float kf[2][8];
-  V8<TM> rb0[2], rb1[2];
   const int nst = which ? tt + 1 : g.qb - tt;
-  auto fetch = [&](int k) {
-    // which 1: rows l of tile tt, columns s of tile j = k;  which 0: rows l of tile i = tt + k, columns s of tile tt
+  struct Regs {
+    float kf[2][8];
+    V8<TM> o0[2], o1[2];
+  };
+  auto fetch = [&](int k, Regs& r) {
+    // which 1: rows l of tile tt, columns s of tile k;  which 0: rows l of tile tt + k, columns s of tile tt
     const int lt = which ? tt : tt + k, st = which ? k : tt;
 #pragma unroll
     for (int rr = 0; rr < 2; ++rr) {
-      const float* row = dcb + static_cast<int64_t>(64 * lt + r0 + rr) * g.q + 64 * st + c0;
-      load_f8(row, kf[rr]);
+      const float* row = dcb + (64 * lt + r0 + rr) * g.q + 64 * st + c0;
+      load_f8(row, r.kf[rr]);
       for (int hb = 1; hb < pl.hb1; ++hb) {
         float f[8];
         load_f8(row + hb * qq, f);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) kf[rr][e] += f[e];
+        for (int e = 0; e < 8; ++e) r.kf[rr][e] += f[e];
       }
     }
     const int64_t ot0 = tc + 64 * (which ? st : lt);  // token rows of the other operand
-    load_bc2(g, Om, b, ot0, gg, nn0, rb0);
-    load_bc2(g, Om, b, ot0, gg, nn0 + 64, rb1);
+    load_bw<TM, VEC>(g, Om, b, ot0, gg, nn0, r.o0);
+    load_bw<TM, VEC>(g, Om, b, ot0, gg, nn0 + 64, r.o1);
+  };
+  auto put = [&](int k, Regs& r) {
+    TM* buf = sbuf[k & 1];
+    if (which)
+      put2x8<TM, false>(buf, r0, c0, r.kf[0], r.kf[1]);  // A[l][s] = dCB[l][s]
+    else
+      put2x8<TM, true>(buf, r0, c0, r.kf[0], r.kf[1]);   // A[s][l] = dCB[l][s]
+    put_raw<TM, true>(buf + TE, r0, c0, r.o0[0], r.o0[1]);  // Bt[n][token] of B (which 1) or C (which 0)
+    put_raw<TM, true>(buf + 2 * TE, r0, c0, r.o1[0], r.o1[1]);
   };
   f32x16 acc0, acc1;
   zero(acc0);
   zero(acc1);
-  fetch(0);
-  for (int k = 0; k < nst; ++k) {
+  Regs ra, rb;
+  pipeline2(nst, ra, rb, fetch, put, [&](int k) {
     TM* buf = sbuf[k & 1];
-    float a[8], bb[8];
-    if (which)
-      put2x8<TM, false>(buf, r0, c0, kf[0], kf[1]);  // A[l][s] = dCB[l][s]
-    else
-      put2x8<TM, true>(buf, r0, c0, kf[0], kf[1]);   // A[s][l] = dCB[l][s]
-    v8_f32(rb0[0], a);
-    v8_f32(rb0[1], bb);
-    put2x8<TM, true>(buf + TE, r0, c0, a, bb);  // Bt[n][token] of B (which 1) or C (which 0)
-    v8_f32(rb1[0], a);
-    v8_f32(rb1[1], bb);
-    put2x8<TM, true>(buf + 2 * TE, r0, c0, a, bb);
-    __syncthreads();
-    if (k + 1 < nst) fetch(k + 1);
     mma_tile<TM>(acc0, buf, buf + TE, wm, wn, lane, 64);
     mma_tile<TM>(acc1, buf, buf + 2 * TE, wm, wn, lane, 64);
-  }
+  });
   __syncthreads();
   float* red = reinterpret_cast<float*>(&sbuf[0][0]);
   TM* out = static_cast<TM*>(which ? p.dC : p.dB);
@@ -546,7 +560,7 @@ __global__ void __launch_bounds__(256) dbc_final(Geo g, BwdPlan pl, Ptrs p) {
       const float* part = p.pbc + (((b * g.length + t) * g.ngroups + gg) * pl.hb2 * 2 + which) * g.dstate + nn;
       for (int hb = 0; hb < pl.hb2; ++hb) {
         float f[8];
-        if (g.vec && n >= 8) {
+        if (VEC) {
           load_f8(part + static_cast<int64_t>(hb) * 2 * g.dstate, f);
         } else {
 #pragma unroll
@@ -555,8 +569,8 @@ __global__ void __launch_bounds__(256) dbc_final(Geo g, BwdPlan pl, Ptrs p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[rr][e] += f[e];
       }
-      v8_store(out + bcidx(g, b, t, gg, nn), n, g.vec, v[rr]);
     }
+    store_bw<TM, VEC>(g, out, b, t0, gg, nn0 + 64 * half, v[0], v[1]);
   }
 }
 
@@ -634,19 +648,40 @@ __global__ void __launch_bounds__(256) reduce_params(Geo g, BwdPlan pl, Ptrs p) 
     if (p.dbias) p.dbias[h] = sb;
   }
   if (!p.dD) return;
-  const int64_t nrow = nbc * g.qb;  // (b, chunk, tile) partial rows
-  if (g.d_per_row) {
-    for (int64_t pc = tid; pc < g.headdim; pc += 256) {
-      float s = 0.0f;
-      for (int64_t k = 0; k < nrow; ++k) s += p.pdD[(k * g.nheads + h) * g.headdim + pc];
-      p.dD[h * g.headdim + pc] = s;
+  // dD: (b, chunk, tile) partial rows; 64 columns x 4 row groups per pass
+  __shared__ float part[4][64];
+  const int64_t nrow = nbc * g.qb;
+  const int col = tid & 63, grp = tid >> 6;
+  float hsum = 0.0f;
+  for (int pt = 0; pt < g.npt; ++pt) {
+    const int64_t pc = static_cast<int64_t>(pt) * 64 + col;
+    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+    if (pc < g.headdim) {
+      const float* q = p.pdD + h * g.headdim + pc;
+      const int64_t stride = g.nheads * g.headdim;
+      int64_t k = grp;
+      for (; k + 12 < nrow; k += 16) {
+        s0 += q[k * stride];
+        s1 += q[(k + 4) * stride];
+        s2 += q[(k + 8) * stride];
+        s3 += q[(k + 12) * stride];
+      }
+      for (; k < nrow; k += 4) s0 += q[k * stride];
     }
-  } else {
-    float s = 0.0f;
-    for (int64_t pc = tid; pc < g.headdim; pc += 256)
-      for (int64_t k = 0; k < nrow; ++k) s += p.pdD[(k * g.nheads + h) * g.headdim + pc];
-    s = block_sum(s, wsum);
-    if (tid == 0) p.dD[h] = s;
+    __syncthreads();
+    part[grp][col] = (s0 + s1) + (s2 + s3);
+    __syncthreads();
+    if (tid < 64 && pc < g.headdim) {
+      const float tot = (part[0][col] + part[1][col]) + (part[2][col] + part[3][col]);
+      if (g.d_per_row)
+        p.dD[h * g.headdim + pc] = tot;
+      else
+        hsum += tot;
+    }
+  }
+  if (!g.d_per_row) {
+    hsum = block_sum(hsum, wsum);
+    if (tid == 0) p.dD[h] = hsum;
   }
 }
 
@@ -690,25 +725,29 @@ BwdLayout bwd_layout(const Geo& g, const BwdPlan& pl, bool has_z) {
   return l;
 }
 
-template <typename TM>
+template <typename TM, bool VEC>
 void launch_bwd_t(const Geo& g, const BwdPlan& pl, const Ptrs& q, hipStream_t s) {
   const unsigned bh = static_cast<unsigned>(g.batch * g.nheads);
   const unsigned ncg = static_cast<unsigned>(g.nc * g.ngroups);
-  MKO_TIMED("ssd_gate", s, gate<TM><<<dim3(g.qb * g.npt, g.nc, bh), 256, 0, s>>>(g, pl, q));
+  const unsigned nb = static_cast<unsigned>(g.batch);
+  MKO_TIMED("ssd_gate", s, gate<TM, VEC><<<dim3(g.qb * g.npt * g.nc * bh), 256, 0, s>>>(g, pl, q));
   MKO_TIMED("ssd_chunk_state_bwd", s,
-            chunk_state<TM, true><<<dim3(g.npt * g.nnp, g.nc, bh), 256, 0, s>>>(g, q, q.dstates));
+            chunk_state<TM, VEC, true><<<dim3(g.npt * g.nnp * g.nc * bh), 256, 0, s>>>(g, q, q.dstates));
   MKO_TIMED("ssd_state_rev", s, state_rev<TM><<<dim3(pl.nblk, bh), 256, 0, s>>>(g, pl, q));
-  MKO_TIMED("ssd_du", s, du_kernel<TM><<<dim3(g.qb * g.npt, g.nc, bh), 256, 0, s>>>(g, pl, q));
-  MKO_TIMED("ssd_dcb", s,
-            dcb_kernel<TM><<<dim3(pl.npairs * pl.hb1, ncg, static_cast<unsigned>(g.batch)), 256, 0, s>>>(g, pl, q));
+  MKO_TIMED("ssd_du", s, du_kernel<TM, VEC><<<dim3(g.qb * g.npt * g.nc * bh), 256, 0, s>>>(g, pl, q));
+  MKO_TIMED("ssd_dcb", s, dcb_kernel<TM, VEC><<<dim3(pl.npairs * pl.hb1 * ncg * nb), 256, 0, s>>>(g, pl, q));
   MKO_TIMED("ssd_dbc_state", s,
-            dbc_state<TM><<<dim3(g.qb * g.nnp * 2 * pl.hb2, ncg, static_cast<unsigned>(g.batch)), 256, 0, s>>>(
-                g, pl, q));
-  MKO_TIMED("ssd_dbc_final", s,
-            dbc_final<TM><<<dim3(g.qb * g.nnp * 2, ncg, static_cast<unsigned>(g.batch)), 256, 0, s>>>(g, pl, q));
+            dbc_state<TM, VEC><<<dim3(g.qb * g.nnp * 2 * pl.hb2 * ncg * nb), 256, 0, s>>>(g, pl, q));
+  MKO_TIMED("ssd_dbc_final", s, dbc_final<TM, VEC><<<dim3(g.qb * g.nnp * 2 * ncg * nb), 256, 0, s>>>(g, pl, q));
   MKO_TIMED("ssd_finish", s,
-            finish<<<dim3(g.nc, static_cast<unsigned>(g.nheads), static_cast<unsigned>(g.batch)), 256, 0, s>>>(g, pl, q));
+            finish<<<dim3(g.nc, static_cast<unsigned>(g.nheads), nb), 256, 0, s>>>(g, pl, q));
   MKO_TIMED("ssd_reduce", s, reduce_params<<<dim3(static_cast<unsigned>(g.nheads)), 256, 0, s>>>(g, pl, q));
+}
+
+template <typename TM>
+void launch_bwd_t(const Geo& g, const BwdPlan& pl, const Ptrs& q, hipStream_t s) {
+  if (g.vec) launch_bwd_t<TM, true>(g, pl, q, s);
+  else launch_bwd_t<TM, false>(g, pl, q, s);
 }
 
 }  // namespace

@@ -18,16 +18,21 @@ __device__ __forceinline__ int blk_r0() { return 2 * static_cast<int>(threadIdx.
 __device__ __forceinline__ int blk_c0() { return 8 * static_cast<int>(threadIdx.x & 7); }
 
 // Eight consecutive elements of T, raw.
+// `mask` is all ones when the row lies inside its window and zero otherwise; every
+// consumer applies it, so a load can be issued unconditionally and its result masked
+// only when it is used (after the wait it needs anyway).
 template <typename T>
 struct V8 {
   static constexpr int kWords = static_cast<int>(sizeof(T)) * 2;
   uint32_t w[kWords];
+  uint32_t mask;
 };
 
 template <typename T>
 __device__ __forceinline__ void v8_zero(V8<T>& v) {
 #pragma unroll
   for (int i = 0; i < V8<T>::kWords; ++i) v.w[i] = 0u;
+  v.mask = 0u;
 }
 
 // Loads elements p[0 .. min(n, 8)) (zero beyond): 16-byte vectors when `vec` and the
@@ -35,6 +40,7 @@ __device__ __forceinline__ void v8_zero(V8<T>& v) {
 template <typename T>
 __device__ __forceinline__ void v8_load(V8<T>& v, const T* p, int n, bool vec) {
   constexpr int W = V8<T>::kWords;
+  v.mask = ~0u;
   if (vec && n >= 8) {
     const uint4* q = reinterpret_cast<const uint4*>(p);
 #pragma unroll
@@ -46,7 +52,8 @@ __device__ __forceinline__ void v8_load(V8<T>& v, const T* p, int n, bool vec) {
       v.w[4 * i + 3] = t.w;
     }
   } else {
-    v8_zero(v);
+#pragma unroll
+    for (int i = 0; i < W; ++i) v.w[i] = 0u;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       if (e < n) {
@@ -63,18 +70,20 @@ template <typename T>
 __device__ __forceinline__ void v8_f32(const V8<T>& v, float (&f)[8]) {
   if constexpr (sizeof(T) == 4) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) f[e] = __uint_as_float(v.w[e]);
+    for (int e = 0; e < 8; ++e) f[e] = __uint_as_float(v.w[e] & v.mask);
   } else if constexpr (__is_same(T, bf16)) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      f[2 * i] = __uint_as_float(v.w[i] << 16);
-      f[2 * i + 1] = __uint_as_float(v.w[i] & 0xffff0000u);
+      const uint32_t w = v.w[i] & v.mask;
+      f[2 * i] = __uint_as_float(w << 16);
+      f[2 * i + 1] = __uint_as_float(w & 0xffff0000u);
     }
   } else {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      f[2 * i] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(v.w[i] & 0xffffu)));
-      f[2 * i + 1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(v.w[i] >> 16)));
+      const uint32_t w = v.w[i] & v.mask;
+      f[2 * i] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w & 0xffffu)));
+      f[2 * i + 1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w >> 16)));
     }
   }
 }
@@ -138,6 +147,119 @@ __device__ __forceinline__ void put2x8(TM* dst, int r0, int c0, const float (&a)
 #pragma unroll
       for (int k = 0; k < 8; ++k) *reinterpret_cast<float2*>(dst + (c0 + k) * ld + r0) = make_float2(a[k], b[k]);
     }
+  }
+}
+
+// Loads the thread's 2x8 block of a 64x64 window of a row-major view: window element
+// (r, c) is base[r * ld + c] (base and ld uniform, r * ld < 2^31); rows >= nrows and
+// columns >= ncols read as zero.  VEC: whole 8-element runs, 16-byte aligned, and the
+// loads are unconditional (a lane outside the window reads `safe`, any valid aligned
+// address, and discards it), so the number of loads in flight is static and the
+// compiler can wait for exactly the ones it needs.
+template <typename T, bool VEC>
+__device__ __forceinline__ void load_win(const T* base, int ld, int nrows, int ncols, V8<T> (&v)[2],
+                                         const T* safe) {
+  const int r0 = blk_r0(), c0 = blk_c0();
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr) {
+    const int r = r0 + rr;
+    if constexpr (VEC) {
+      const bool ok = r < nrows && c0 < ncols;
+      const T* p = ok ? base + (r * ld + c0) : safe;
+      const uint4* q = reinterpret_cast<const uint4*>(p);
+#pragma unroll
+      for (int i = 0; i < V8<T>::kWords / 4; ++i) {
+        const uint4 t = q[i];
+        v[rr].w[4 * i + 0] = t.x;
+        v[rr].w[4 * i + 1] = t.y;
+        v[rr].w[4 * i + 2] = t.z;
+        v[rr].w[4 * i + 3] = t.w;
+      }
+      v[rr].mask = ok ? ~0u : 0u;
+    } else {
+      const int n = r < nrows ? ncols - c0 : 0;
+      if (n > 0)
+        v8_load(v[rr], base + (r * ld + c0), n, false);
+      else
+        v8_zero(v[rr]);
+    }
+  }
+}
+
+// Stores the thread's block (rows r0, r0+1 of a 64x64 window at base with row stride
+// ld) as T, inside nrows x ncols.
+template <typename T, bool VEC>
+__device__ __forceinline__ void store_win(T* base, int ld, int nrows, int ncols, const float (&a)[8],
+                                          const float (&b)[8]) {
+  const int r0 = blk_r0(), c0 = blk_c0();
+  const int n = ncols - c0;
+  if (r0 < nrows && n > 0) v8_store(base + (r0 * ld + c0), n, VEC, a);
+  if (r0 + 1 < nrows && n > 0) v8_store(base + ((r0 + 1) * ld + c0), n, VEC, b);
+}
+
+// Writes the thread's raw block (rows a, b) into an LDS operand tile without conversion.
+template <typename TM, bool TRANS>
+__device__ __forceinline__ void put_raw(TM* dst, int r0, int c0, const V8<TM>& a, const V8<TM>& b) {
+  constexpr int ld = tile_ld<TM>();
+  constexpr int W = V8<TM>::kWords;
+  uint32_t aw[W], bw[W];
+#pragma unroll
+  for (int i = 0; i < W; ++i) {
+    aw[i] = a.w[i] & a.mask;
+    bw[i] = b.w[i] & b.mask;
+  }
+  if constexpr (sizeof(TM) == 2) {
+    if constexpr (!TRANS) {
+      *reinterpret_cast<uint4*>(dst + r0 * ld + c0) = make_uint4(aw[0], aw[1], aw[2], aw[3]);
+      *reinterpret_cast<uint4*>(dst + (r0 + 1) * ld + c0) = make_uint4(bw[0], bw[1], bw[2], bw[3]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        // column 2i: low halves of a and b; column 2i+1: high halves
+        *reinterpret_cast<uint32_t*>(dst + (c0 + 2 * i) * ld + r0) = __builtin_amdgcn_perm(bw[i], aw[i], 0x05040100u);
+        *reinterpret_cast<uint32_t*>(dst + (c0 + 2 * i + 1) * ld + r0) = __builtin_amdgcn_perm(bw[i], aw[i], 0x07060302u);
+      }
+    }
+  } else {
+    if constexpr (!TRANS) {
+#pragma unroll
+      for (int k = 0; k < 8; k += 2) {
+        *reinterpret_cast<uint2*>(dst + r0 * ld + c0 + k) = make_uint2(aw[k], aw[k + 1]);
+        *reinterpret_cast<uint2*>(dst + (r0 + 1) * ld + c0 + k) = make_uint2(bw[k], bw[k + 1]);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) *reinterpret_cast<uint2*>(dst + (c0 + k) * ld + r0) = make_uint2(aw[k], bw[k]);
+    }
+  }
+}
+
+// Runs n >= 1 stages of a tile product with two register sets of prefetched operands
+// (the loads of stage k+2 are issued while stage k is multiplied) and a double-buffered
+// LDS tile (one barrier per stage).  fetch(k, regs) issues the loads of stage k,
+// put(k, regs) writes them to LDS buffer k & 1, mma(k) multiplies from that buffer.
+// Prefetches are unconditional (past the end they repeat the last stage's loads), so
+// the loads in flight at each put are the same on every path.
+template <class Regs, class Fetch, class Put, class Mma>
+__device__ __forceinline__ void pipeline2(int n, Regs& ra, Regs& rb, Fetch&& fetch, Put&& put, Mma&& mma) {
+  const int last = n - 1;
+  fetch(0, ra);
+  fetch(1 < last ? 1 : last, rb);
+  int k = 0;
+  for (; k + 1 < n; k += 2) {
+    put(k, ra);
+    __syncthreads();
+    fetch(k + 2 < last ? k + 2 : last, ra);
+    mma(k);
+    put(k + 1, rb);
+    __syncthreads();
+    fetch(k + 3 < last ? k + 3 : last, rb);
+    mma(k + 1);
+  }
+  if (k < n) {
+    put(k, ra);
+    __syncthreads();
+    mma(k);
   }
 }
 
