@@ -482,11 +482,12 @@ __global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
   float* dap = p.dap + static_cast<int64_t>(c) * NS * R;
   float* qx = p.qx + static_cast<int64_t>(c) * 3 * NS * R;
 
-  if (li.active) {
-    for (int n = 0; n < N; ++n) {
-      hcs[n * R + li.row] = p.adj[(li.row * g.nchunks + c) * N + n];
-      dap[n * R + li.row] = 0.0f;
-    }
+  // adjoint carried between quarters and the dA sums, one per state, in registers
+  float hcr[NS], dar[NS];
+#pragma unroll
+  for (int n = 0; n < NS; ++n) {
+    hcr[n] = n < N ? p.adj[(li.row * g.nchunks + c) * N + n] : 0.0f;
+    dar[n] = 0.0f;
   }
 
   int64_t cb = 0;
@@ -563,20 +564,15 @@ __global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
       // per-lane carries, state-major: element (n, row) at n * R + row
       const float* xin_p = q == 0 ? srow : qx + ((q - 1) * NS) * R + li.row;
       const int xin_stride = q == 0 ? 1 : static_cast<int>(R);
-      float* hc_p = hcs + li.row;
-      float* da_p = dap + li.row;
       const float* bn_p = p.bn + (li.bg * NS) * g.length + qs;
       const float* cn_p = p.cn + (li.bg * NS) * g.length + qs;
-      const int rstride = static_cast<int>(R);
       float xin_n = xin_p[0];
-      float hc_n = hc_p[0];
-      for (int n = 0; n < N; ++n) {
+#pragma unroll
+      for (int n = 0; n < NS; ++n) {
+        if (n >= N) break;
         const bool more = n + 1 < N;
-        float xin_x = 0.0f, hc_x = 0.0f;
-        if (more) {
-          xin_x = xin_p[(n + 1) * xin_stride];
-          hc_x = hc_p[(n + 1) * rstride];
-        }
+        float xin_x = 0.0f;
+        if (more) xin_x = xin_p[(n + 1) * xin_stride];
         float bv[HS], cv[HS];
         if (UNI) {
 #pragma unroll
@@ -598,7 +594,7 @@ __global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
           x = fmaf(ah[i], x, du[i] * bv[i]);
           xh[i] = x;
         }
-        float hc = hc_n;
+        float hc = hcr[n];
         float dan = 0.0f;
 #pragma unroll
         for (int i = HS - 1; i >= 0; --i) {
@@ -613,10 +609,8 @@ __global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
           trans[lane * kTransPitch + HS + i] = gy[i] * xh[i];
           hc = ah[i] * h;
         }
-        if (li.active) {
-          hc_p[n * rstride] = hc;
-          da_p[n * rstride] += dan;
-        }
+        hcr[n] = hc;
+        dar[n] += dan;
         wave_lds_sync();
         if (UNI) {
           // lane l sums column (l mod 32) over one half of the 64 rows; the
@@ -635,10 +629,7 @@ __global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
           }
         }
         wave_lds_sync();
-        if (more) {
-          xin_n = xin_x;
-          hc_n = hc_x;
-        }
+        if (more) xin_n = xin_x;
       }
       // ---- per-step gradients of the quarter
       {
@@ -695,6 +686,9 @@ __global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
     }
   }
   if (li.active) {
+#pragma unroll
+    for (int n = 0; n < NS; ++n)
+      if (n < N) dap[n * R + li.row] = dar[n];
     p.ddp[static_cast<int64_t>(c) * g.rows + li.row] = dD_acc;
     p.dbp[static_cast<int64_t>(c) * g.rows + li.row] = db_acc;
   }
