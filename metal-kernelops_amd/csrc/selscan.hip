@@ -20,6 +20,8 @@
 // Per-step inputs of the state-inner loops (one lane, all states, one step at a
 // time) are staged through LDS so the step loop is a real loop and B_t/C_t are
 // fetched one step at a time.
+#include <type_traits>
+
 #include "common.hpp"
 #include "io.hpp"
 
@@ -249,7 +251,93 @@ __device__ __forceinline__ float load_steps(const Geo& g, const Ptrs& p, int64_t
   return sd;
 }
 
-template <int NS, bool UNI>
+// The element type of u / z / dout / du / dz.  Dyn: read from Geo at run time (any
+// length, any alignment, any delta dtype); float / _Float16 / bf16: the typed path
+// (delta float32, whole 16-step blocks, 16-byte aligned rows), whose loads keep the
+// raw words in registers until they are used, so a block's inputs can be requested
+// while the previous block is computed.
+struct Dyn {};
+
+template <class T>
+struct RawRun {  // HS consecutive elements of a row, raw
+  static constexpr int W = HS * static_cast<int>(sizeof(T)) / 4;
+  uint32_t w[W];
+  __device__ __forceinline__ void load(const Geo&, const void* base, int, int64_t off, int) {
+    const uint4* q = reinterpret_cast<const uint4*>(static_cast<const T*>(base) + off);
+#pragma unroll
+    for (int i = 0; i < W / 4; ++i) {
+      const uint4 t = q[i];
+      w[4 * i] = t.x;
+      w[4 * i + 1] = t.y;
+      w[4 * i + 2] = t.z;
+      w[4 * i + 3] = t.w;
+    }
+  }
+  __device__ __forceinline__ void get(float (&f)[HS]) const {
+    if constexpr (sizeof(T) == 4) {
+#pragma unroll
+      for (int i = 0; i < HS; ++i) f[i] = __uint_as_float(w[i]);
+    } else if constexpr (__is_same(T, bf16)) {
+#pragma unroll
+      for (int i = 0; i < W; ++i) {
+        f[2 * i] = __uint_as_float(w[i] << 16);
+        f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < W; ++i) {
+        f[2 * i] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w[i] & 0xffffu)));
+        f[2 * i + 1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w[i] >> 16)));
+      }
+    }
+  }
+};
+
+template <>
+struct RawRun<Dyn> {
+  float f[HS];
+  __device__ __forceinline__ void load(const Geo& g, const void* base, int dtype, int64_t off, int nv) {
+    load_run<HS>(base, dtype, off, nv, g.vec, f);
+  }
+  __device__ __forceinline__ void get(float (&o)[HS]) const {
+#pragma unroll
+    for (int i = 0; i < HS; ++i) o[i] = f[i];
+  }
+};
+
+// delta's type in each path
+template <class TU>
+using DeltaT = typename std::conditional<__is_same(TU, Dyn), Dyn, float>::type;
+
+template <class TU>
+__device__ __forceinline__ void store_u(const Geo& g, void* base, int64_t off, int nv, const float (&v)[HS]) {
+  if constexpr (__is_same(TU, Dyn))
+    store_run<HS>(base, g.u_dtype, off, nv, g.vec, v);
+  else
+    store_run_t<TU, HS>(static_cast<TU*>(base) + off, HS, true, v);
+}
+template <class TU>
+__device__ __forceinline__ void store_d(const Geo& g, void* base, int64_t off, int nv, const float (&v)[HS]) {
+  if constexpr (__is_same(TU, Dyn))
+    store_run<HS>(base, g.d_dtype, off, nv, g.vec, v);
+  else
+    store_run_t<float, HS>(static_cast<float*>(base) + off, HS, true, v);
+}
+
+// Step sizes and du = step * u of one block from raw runs; returns the sum of steps.
+__device__ __forceinline__ float steps_from(const Geo& g, const float (&raw)[HS], const float (&uu)[HS], int nv,
+                                            float bias, float (&del)[HS], float (&du)[HS]) {
+  float sd = 0.0f;
+#pragma unroll
+  for (int i = 0; i < HS; ++i) {
+    del[i] = i < nv ? step_of(g, raw[i], bias) : 0.0f;
+    du[i] = del[i] * uu[i];
+    sd += del[i];
+  }
+  return sd;
+}
+
+template <int NS, bool UNI, class TU>
 __global__ void __launch_bounds__(256) fwd_summary(Geo g, Ptrs p) {
   const LaneInfo li = lane_info(g, UNI);
   const int N = static_cast<int>(g.dstate);
@@ -265,10 +353,20 @@ __global__ void __launch_bounds__(256) fwd_summary(Geo g, Ptrs p) {
   for (int n = 0; n < NS; ++n) x[n] = 0.0f;
   float sd = 0.0f;
   const int64_t rbase = li.row * g.length;
+  const int t_last = t_begin + ((t_end - t_begin - 1) / HS) * HS;
+  RawRun<DeltaT<TU>> rd;
+  RawRun<TU> ru;
+  rd.load(g, p.delta, g.d_dtype, rbase + t_begin, min(HS, t_end - t_begin));
+  ru.load(g, p.u, g.u_dtype, rbase + t_begin, min(HS, t_end - t_begin));
   for (int t0 = t_begin; t0 < t_end; t0 += HS) {
     const int nv = min(HS, t_end - t0);
-    float del[HS], du[HS];
-    sd += load_steps(g, p, rbase + t0, nv, bias, del, du);
+    float raw[HS], uu[HS], del[HS], du[HS];
+    rd.get(raw);
+    ru.get(uu);
+    const int tn = t0 + HS < t_last ? t0 + HS : t_last;  // next block (the last one repeats)
+    rd.load(g, p.delta, g.d_dtype, rbase + tn, min(HS, t_end - tn));
+    ru.load(g, p.u, g.u_dtype, rbase + tn, min(HS, t_end - tn));
+    sd += steps_from(g, raw, uu, nv, bias, del, du);
     forward_block<NS, UNI, false>(p.bt, nullptr, li.bg * g.length, t0, nv, del, du, A2, x, unused);
   }
   if (li.active) {
@@ -309,7 +407,7 @@ __global__ void __launch_bounds__(256) chain(Geo g, const float* __restrict__ A,
   }
 }
 
-template <int NS, bool UNI>
+template <int NS, bool UNI, class TU>
 __global__ void __launch_bounds__(256) fwd_replay(Geo g, Ptrs p) {
   const LaneInfo li = lane_info(g, UNI);
   const int N = static_cast<int>(g.dstate);
@@ -327,6 +425,13 @@ __global__ void __launch_bounds__(256) fwd_replay(Geo g, Ptrs p) {
 #pragma unroll
   for (int n = 0; n < NS; ++n) x[n] = n < N ? srow[(t_begin / CK) * N + n] : 0.0f;
   const int64_t rbase = li.row * g.length;
+  const int t_last = t_begin + ((t_end - t_begin - 1) / HS) * HS;
+  RawRun<DeltaT<TU>> rd;
+  RawRun<TU> ru, rz;
+  const void* zsrc = has_z ? p.z : p.u;  // without z the third run repeats u (unused)
+  rd.load(g, p.delta, g.d_dtype, rbase + t_begin, min(HS, t_end - t_begin));
+  ru.load(g, p.u, g.u_dtype, rbase + t_begin, min(HS, t_end - t_begin));
+  rz.load(g, zsrc, g.u_dtype, rbase + t_begin, min(HS, t_end - t_begin));
   for (int t0 = t_begin; t0 < t_end; t0 += HS) {
     if (t0 != t_begin && (t0 % CK) == 0 && li.active) {
 #pragma unroll
@@ -334,26 +439,29 @@ __global__ void __launch_bounds__(256) fwd_replay(Geo g, Ptrs p) {
         if (n < N) srow[(t0 / CK) * N + n] = x[n];
     }
     const int nv = min(HS, t_end - t0);
-    float del[HS], du[HS], y[HS];
-    load_steps(g, p, rbase + t0, nv, bias, del, du);
+    float raw[HS], uu[HS], zz[HS], del[HS], du[HS], y[HS];
+    rd.get(raw);
+    ru.get(uu);
+    rz.get(zz);
+    const int tn = t0 + HS < t_last ? t0 + HS : t_last;  // next block (the last one repeats)
+    rd.load(g, p.delta, g.d_dtype, rbase + tn, min(HS, t_end - tn));
+    ru.load(g, p.u, g.u_dtype, rbase + tn, min(HS, t_end - tn));
+    rz.load(g, zsrc, g.u_dtype, rbase + tn, min(HS, t_end - tn));
+    steps_from(g, raw, uu, nv, bias, del, du);
     forward_block<NS, UNI, true>(p.bt, p.ct, li.bg * g.length, t0, nv, del, du, A2, x, y);
-    float uu[HS];
-    load_run<HS>(p.u, g.u_dtype, rbase + t0, nv, g.vec, uu);
 #pragma unroll
     for (int i = 0; i < HS; ++i) y[i] = fmaf(Dd, uu[i], y[i]);
     if (has_z) {
-      float zz[HS];
-      load_run<HS>(p.z, g.u_dtype, rbase + t0, nv, g.vec, zz);
 #pragma unroll
       for (int i = 0; i < HS; ++i) y[i] *= zz[i] * sigmoid(zz[i]);
     }
-    if (li.active) store_run<HS>(p.out, g.u_dtype, rbase + t0, nv, g.vec, y);
+    if (li.active) store_u<TU>(g, p.out, rbase + t0, nv, y);
   }
 }
 
 // ---------------------------------------------------------------- backward
 
-template <int NS, bool UNI>
+template <int NS, bool UNI, class TU>
 __global__ void __launch_bounds__(256) bwd_summary(Geo g, Ptrs p) {
   const LaneInfo li = lane_info(g, UNI);
   const int N = static_cast<int>(g.dstate);
@@ -372,15 +480,29 @@ __global__ void __launch_bounds__(256) bwd_summary(Geo g, Ptrs p) {
   const int64_t rbase = li.row * g.length;
   const int64_t row0 = li.bg * g.length;
   const int nblk = (t_end - t_begin + HS - 1) / HS;
+  const void* zsrc = has_z ? p.z : p.dout;  // without z the third run repeats dout (unused)
+  RawRun<DeltaT<TU>> rd;
+  RawRun<TU> rg, rz;
+  {
+    const int t0 = t_begin + (nblk - 1) * HS, nv = min(HS, t_end - t0);
+    rd.load(g, p.delta, g.d_dtype, rbase + t0, nv);
+    rg.load(g, p.dout, g.u_dtype, rbase + t0, nv);
+    rz.load(g, zsrc, g.u_dtype, rbase + t0, nv);
+  }
   for (int blk = nblk - 1; blk >= 0; --blk) {
     const int t0 = t_begin + blk * HS;
     const int nv = min(HS, t_end - t0);
-    float del[HS], gy[HS];
-    load_run<HS>(p.delta, g.d_dtype, rbase + t0, nv, g.vec, del);
-    load_run<HS>(p.dout, g.u_dtype, rbase + t0, nv, g.vec, gy);
+    float del[HS], gy[HS], zz[HS];
+    rd.get(del);
+    rg.get(gy);
+    rz.get(zz);
+    {
+      const int tp = t_begin + (blk > 0 ? blk - 1 : 0) * HS, np = min(HS, t_end - tp);  // previous block
+      rd.load(g, p.delta, g.d_dtype, rbase + tp, np);
+      rg.load(g, p.dout, g.u_dtype, rbase + tp, np);
+      rz.load(g, zsrc, g.u_dtype, rbase + tp, np);
+    }
     if (has_z) {
-      float zz[HS];
-      load_run<HS>(p.z, g.u_dtype, rbase + t0, nv, g.vec, zz);
 #pragma unroll
       for (int i = 0; i < HS; ++i) gy[i] *= zz[i] * sigmoid(zz[i]);
     }
@@ -897,7 +1019,7 @@ static inline unsigned blocks_for(int64_t n, int per = 256) {
   return static_cast<unsigned>((n + per - 1) / per);
 }
 
-template <int NS, bool UNI>
+template <int NS, bool UNI, class TU>
 static int launch_fwd(const Plan& pl, const Ptrs& q, hipStream_t s) {
   const Geo& g = pl.g;
   const dim3 block(g.wpg * kWave);
@@ -905,14 +1027,14 @@ static int launch_fwd(const Plan& pl, const Ptrs& q, hipStream_t s) {
   const int64_t bgl = g.batch * g.ngroups * g.length;
   MKO_TIMED("selscan_prep", s, prep_time_major<NS><<<blocks_for(bgl), 256, 0, s>>>(g, q.B, q.C, q.bt, q.ct));
   if (g.nchunks > 1) {
-    MKO_TIMED("selscan_fwd_summary", s, fwd_summary<NS, UNI><<<dim3(gx, g.nchunks - 1), block, 0, s>>>(g, q));
+    MKO_TIMED("selscan_fwd_summary", s, fwd_summary<NS, UNI, TU><<<dim3(gx, g.nchunks - 1), block, 0, s>>>(g, q));
   }
   MKO_TIMED("selscan_chain", s, chain<false><<<blocks_for(g.rows * g.dstate), 256, 0, s>>>(g, q.A, q.drive, q.sumd, q.states));
-  MKO_TIMED("selscan_fwd_replay", s, fwd_replay<NS, UNI><<<dim3(gx, g.nchunks), block, 0, s>>>(g, q));
+  MKO_TIMED("selscan_fwd_replay", s, fwd_replay<NS, UNI, TU><<<dim3(gx, g.nchunks), block, 0, s>>>(g, q));
   return mko_check_launch("selscan_fwd");
 }
 
-template <int NS, bool UNI>
+template <int NS, bool UNI, class TU>
 static int launch_bwd(const Plan& pl, const Ptrs& q, const mko_selscan_params* p, hipStream_t s) {
   const Geo& g = pl.g;
   const dim3 block(g.wpg * kWave);
@@ -921,7 +1043,7 @@ static int launch_bwd(const Plan& pl, const Ptrs& q, const mko_selscan_params* p
   MKO_TIMED("selscan_prep", s, prep_time_major<NS><<<blocks_for(bgl), 256, 0, s>>>(g, q.B, q.C, q.bt, q.ct);
             prep_state_major<<<blocks_for(bgl * NS), 256, 0, s>>>(g, NS, q.B, q.C, q.bn, q.cn));
   if (g.nchunks > 1) {
-    MKO_TIMED("selscan_bwd_summary", s, bwd_summary<NS, UNI><<<dim3(gx, g.nchunks - 1), block, 0, s>>>(g, q));
+    MKO_TIMED("selscan_bwd_summary", s, bwd_summary<NS, UNI, TU><<<dim3(gx, g.nchunks - 1), block, 0, s>>>(g, q));
   }
   MKO_TIMED("selscan_chain", s, chain<true><<<blocks_for(g.rows * g.dstate), 256, 0, s>>>(g, q.A, q.drive, q.sumd, q.adj));
   if (!UNI) {
@@ -935,6 +1057,17 @@ static int launch_bwd(const Plan& pl, const Ptrs& q, const mko_selscan_params* p
             reduce_params<<<blocks_for(g.dim * g.dstate), 256, 0, s>>>(g, NS, q.dap, q.ddp, q.dbp, p->dA,
                                                                        p->dD, p->ddelta_bias));
   return mko_check_launch("selscan_bwd");
+}
+
+// Typed path when delta is float32, every 16-step block is whole and rows are aligned.
+template <class F>
+static int dispatch_types(const Plan& pl, int u_dtype, int d_dtype, F&& f) {
+  const Geo& g = pl.g;
+  const bool typed = d_dtype == MKO_F32 && g.vec && g.length % HS == 0;
+  if (typed && u_dtype == MKO_BF16) return f(bf16{});
+  if (typed && u_dtype == MKO_F16) return f(_Float16{});
+  if (typed && u_dtype == MKO_F32) return f(float{});
+  return f(Dyn{});
 }
 
 }  // namespace ss
@@ -976,8 +1109,11 @@ extern "C" int mko_selscan_fwd(const mko_selscan_params* p, void* stream) {
                                       {p->out, p->u_dtype}}) ? 1 : 0;
   Ptrs q = make_ptrs(p, pl);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (pl.ns == 16) return pl.uni ? launch_fwd<16, true>(pl, q, s) : launch_fwd<16, false>(pl, q, s);
-  return pl.uni ? launch_fwd<32, true>(pl, q, s) : launch_fwd<32, false>(pl, q, s);
+  return dispatch_types(pl, p->u_dtype, p->delta_dtype, [&](auto tag) {
+    using TU = decltype(tag);
+    if (pl.ns == 16) return pl.uni ? launch_fwd<16, true, TU>(pl, q, s) : launch_fwd<16, false, TU>(pl, q, s);
+    return pl.uni ? launch_fwd<32, true, TU>(pl, q, s) : launch_fwd<32, false, TU>(pl, q, s);
+  });
 }
 
 extern "C" int mko_selscan_bwd(const mko_selscan_params* p, void* stream) {
@@ -1002,6 +1138,9 @@ extern "C" int mko_selscan_bwd(const mko_selscan_params* p, void* stream) {
                                       {p->dz, p->u_dtype}}) ? 1 : 0;
   Ptrs q = make_ptrs(p, pl);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (pl.ns == 16) return pl.uni ? launch_bwd<16, true>(pl, q, p, s) : launch_bwd<16, false>(pl, q, p, s);
-  return pl.uni ? launch_bwd<32, true>(pl, q, p, s) : launch_bwd<32, false>(pl, q, p, s);
+  return dispatch_types(pl, p->u_dtype, p->delta_dtype, [&](auto tag) {
+    using TU = decltype(tag);
+    if (pl.ns == 16) return pl.uni ? launch_bwd<16, true, TU>(pl, q, p, s) : launch_bwd<16, false, TU>(pl, q, p, s);
+    return pl.uni ? launch_bwd<32, true, TU>(pl, q, p, s) : launch_bwd<32, false, TU>(pl, q, p, s);
+  });
 }

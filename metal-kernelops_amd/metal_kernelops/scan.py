@@ -183,8 +183,8 @@ def _check_shapes(u, dt, A, B, C, D, z, delta_bias):
 def _run(u, dt, A, B, C, D, z, delta_bias, softplus):
     _require_gpu(u)
     _check_shapes(u, dt, A, B, C, D, z, delta_bias)
-    if dt.dtype not in (torch.float32, u.dtype):
-        dt = dt.float()
+    if dt.dtype != torch.float32:
+        dt = dt.float()  # the kernels take float32 step sizes (autograd casts ddelta back)
     if B.dtype != C.dtype:
         B, C = B.float(), C.float()
     if z is not None and z.dtype != u.dtype:
