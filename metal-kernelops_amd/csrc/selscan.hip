@@ -816,50 +816,82 @@ __global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
   }
 }
 
-// dB/dC (bg, N, L) = sum over channel blocks of the partials.
+// dB/dC (bg, N, L) = sum over channel blocks of the partials (bg, ncb, L, NS, 2).
+// A workgroup covers 256/NS steps x NS states: it reads the partials contiguously
+// (state fastest) and writes through an LDS transpose so the stores run along L.
 template <int NS>
 __global__ void __launch_bounds__(256) reduce_bc(Geo g, int ncb, const float* __restrict__ pbc,
                                                  void* dB, void* dC) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int64_t total = g.batch * g.ngroups * g.dstate * g.length;
-  if (i >= total) return;
-  const int64_t t = i % g.length;
-  const int64_t n = (i / g.length) % g.dstate;
-  const int64_t bg = i / (g.length * g.dstate);
-  float sb = 0.0f, sc = 0.0f;
-  for (int cbk = 0; cbk < ncb; ++cbk) {
-    const float* q = pbc + (((bg * ncb + cbk) * g.length + t) * NS + n) * 2;
-    sb += q[0];
-    sc += q[1];
+  constexpr int TT = 256 / NS;
+  __shared__ float sb[NS][TT + 1], sc[NS][TT + 1];
+  const int64_t nt = (g.length + TT - 1) / TT;
+  const int64_t bg = blockIdx.x / nt;
+  const int64_t t0 = (blockIdx.x % nt) * TT;
+  const int tid = threadIdx.x;
+  {
+    const int tl = tid / NS, n = tid % NS;
+    const int64_t t = t0 + tl;
+    float vb = 0.0f, vc = 0.0f;
+    if (t < g.length) {
+      for (int cbk = 0; cbk < ncb; ++cbk) {
+        const float2 q = *reinterpret_cast<const float2*>(pbc + (((bg * ncb + cbk) * g.length + t) * NS + n) * 2);
+        vb += q.x;
+        vc += q.y;
+      }
+    }
+    sb[n][tl] = vb;
+    sc[n][tl] = vc;
   }
-  if (dB) store_one(dB, g.bc_dtype, i, sb);
-  if (dC) store_one(dC, g.bc_dtype, i, sc);
+  __syncthreads();
+  const int n = tid / TT, tl = tid % TT;
+  const int64_t t = t0 + tl;
+  if (n < g.dstate && t < g.length) {
+    const int64_t o = (bg * g.dstate + n) * g.length + t;
+    if (dB) store_one(dB, g.bc_dtype, o, sb[n][tl]);
+    if (dC) store_one(dC, g.bc_dtype, o, sc[n][tl]);
+  }
 }
 
 // dA (dim, N) = sum over (chunk, batch) of partials; dD, ddelta_bias likewise.
+// A workgroup covers 64 channels of one output row (a state n, or the dD / dbias
+// row when n == N): 4 groups of 64 threads split the (chunk, batch) partials, read
+// channel-fastest, and are added in a fixed order.
 __global__ void __launch_bounds__(256) reduce_params(Geo g, int ns, const float* __restrict__ dap,
                                                      const float* __restrict__ ddp,
                                                      const float* __restrict__ dbp, float* dA,
                                                      float* dD, float* dbias) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  __shared__ float part[2][4][64];
   const int N = static_cast<int>(g.dstate);
-  if (i < g.dim * N) {
-    const int64_t d = i / N, n = i % N;
-    float s = 0.0f;
-    for (int c = 0; c < g.nchunks; ++c)
-      for (int64_t b = 0; b < g.batch; ++b)
-        s += dap[(static_cast<int64_t>(c) * ns + n) * g.rows + b * g.dim + d];
-    if (dA) dA[i] = s;
-  }
-  if (i < g.dim) {
-    float s1 = 0.0f, s2 = 0.0f;
-    for (int c = 0; c < g.nchunks; ++c)
-      for (int64_t b = 0; b < g.batch; ++b) {
-        s1 += ddp[static_cast<int64_t>(c) * g.rows + b * g.dim + i];
-        s2 += dbp[static_cast<int64_t>(c) * g.rows + b * g.dim + i];
+  const int64_t dblocks = (g.dim + 63) / 64;
+  const int n = static_cast<int>(blockIdx.x / dblocks);  // 0..N (N: the dD / dbias row)
+  const int64_t d = (blockIdx.x % dblocks) * 64 + (threadIdx.x & 63);
+  const int grp = threadIdx.x >> 6;
+  const int64_t npart = static_cast<int64_t>(g.nchunks) * g.batch;
+  float s0 = 0.0f, s1 = 0.0f;
+  if (d < g.dim) {
+    for (int64_t k = grp; k < npart; k += 4) {
+      const int64_t c = k / g.batch, b = k % g.batch;
+      if (n < N) {
+        s0 += dap[(c * ns + n) * g.rows + b * g.dim + d];
+      } else {
+        s0 += ddp[c * g.rows + b * g.dim + d];
+        s1 += dbp[c * g.rows + b * g.dim + d];
       }
-    if (dD) dD[i] = s1;
-    if (dbias) dbias[i] = s2;
+    }
+  }
+  part[0][grp][threadIdx.x & 63] = s0;
+  part[1][grp][threadIdx.x & 63] = s1;
+  __syncthreads();
+  if (threadIdx.x < 64 && d < g.dim) {
+    const int l = threadIdx.x;
+    const float t0 = (part[0][0][l] + part[0][1][l]) + (part[0][2][l] + part[0][3][l]);
+    const float t1 = (part[1][0][l] + part[1][1][l]) + (part[1][2][l] + part[1][3][l]);
+    if (n < N) {
+      if (dA) dA[d * N + n] = t0;
+    } else {
+      if (dD) dD[d] = t0;
+      if (dbias) dbias[d] = t1;
+    }
   }
 }
 
@@ -1052,10 +1084,10 @@ static int launch_bwd(const Plan& pl, const Ptrs& q, const mko_selscan_params* p
   }
   MKO_TIMED("selscan_bwd_main", s, bwd_main<NS, UNI><<<dim3(gx, g.nchunks), block, 0, s>>>(g, q));
   MKO_TIMED("selscan_bwd_reduce", s,
-            reduce_bc<NS><<<blocks_for(g.batch * g.ngroups * g.dstate * g.length), 256, 0, s>>>(
-                g, UNI ? g.ncb : 1, q.pbc, p->dB, p->dC);
-            reduce_params<<<blocks_for(g.dim * g.dstate), 256, 0, s>>>(g, NS, q.dap, q.ddp, q.dbp, p->dA,
-                                                                       p->dD, p->ddelta_bias));
+            reduce_bc<NS><<<static_cast<unsigned>(g.batch * g.ngroups * ((g.length + 256 / NS - 1) / (256 / NS))),
+                            256, 0, s>>>(g, UNI ? g.ncb : 1, q.pbc, p->dB, p->dC);
+            reduce_params<<<static_cast<unsigned>((g.dstate + 1) * ((g.dim + 63) / 64)), 256, 0, s>>>(
+                g, NS, q.dap, q.ddp, q.dbp, p->dA, p->dD, p->ddelta_bias));
   return mko_check_launch("selscan_bwd");
 }
 
