@@ -63,9 +63,9 @@ int mko_profile_entry(int index, char* name, size_t name_len, double* total_ms, 
 
 #define MKO_SS_SOFTPLUS 1u /* delta = softplus(delta + delta_bias) (threshold 20) */
 
-/* Steps between two saved scan states (the forward writes one state per 64
- * steps; the backward restarts its recompute from them). */
-#define MKO_SS_CHECKPOINT 64
+/* Steps between two saved scan states (the forward writes one state per 16
+ * steps; the backward restarts its recompute of each 16-step block from them). */
+#define MKO_SS_CHECKPOINT 16
 
 typedef struct mko_selscan_params {
   /* forward inputs (also read by the backward) */
@@ -79,9 +79,9 @@ typedef struct mko_selscan_params {
   const float* delta_bias;  /* (dim,) or NULL                                     */
   /* forward outputs */
   void* out;                /* (batch, dim, length) u_dtype                        */
-  float* states;            /* (batch, dim, mko_selscan_num_checkpoints(length), dstate):
-                               the state entering every 64-step block; written by the
-                               forward, read by the backward                        */
+  float* states;            /* (batch, mko_selscan_num_checkpoints(length), dstate, dim):
+                               the state entering every 16-step block, channel-fastest;
+                               written by the forward, read by the backward         */
   /* backward input */
   const void* dout;         /* (batch, dim, length) u_dtype                        */
   /* backward outputs (any may be NULL when that gradient is not wanted, except

@@ -110,6 +110,13 @@ __device__ __forceinline__ float step_of(const Geo& g, float raw, float bias) {
   return g.softplus ? softplus(v) : v;
 }
 
+// Saved scan states, (batch, checkpoint, state, dim): channel-fastest, so a
+// wavefront's 64 rows (consecutive channels) read or write 256 contiguous bytes.
+__device__ __forceinline__ int64_t ck_index(const Geo& g, int64_t row, int64_t k, int64_t n) {
+  const int64_t b = row / g.dim, d = row - b * g.dim;
+  return ((b * g.nck + k) * g.dstate + n) * g.dim + d;
+}
+
 // ---------------------------------------------------------------- layout prep
 
 // B, C (bg, N, L) any dtype -> time-major fp32 (bg, L, NS), states >= N zeroed.
@@ -395,7 +402,7 @@ __global__ void __launch_bounds__(256) chain(Geo g, const float* __restrict__ A,
     const int per = g.lc / CK;
     float x = 0.0f;
     for (int c = 0; c < k; ++c) {
-      out[(row * g.nck + static_cast<int64_t>(c) * per) * N + n] = x;
+      out[ck_index(g, row, static_cast<int64_t>(c) * per, n)] = x;
       if (c + 1 < k) x = fmaf(fast_exp2(a2 * sumd[row * k + c]), x, drive[(row * k + c) * N + n]);
     }
   } else {
@@ -407,7 +414,8 @@ __global__ void __launch_bounds__(256) chain(Geo g, const float* __restrict__ A,
   }
 }
 
-template <int NS, bool UNI, class TU>
+// FULL: dstate == NS (no padded states), so the saved-state stores need no guards.
+template <int NS, bool UNI, class TU, bool FULL>
 __global__ void __launch_bounds__(256) fwd_replay(Geo g, Ptrs p) {
   const LaneInfo li = lane_info(g, UNI);
   const int N = static_cast<int>(g.dstate);
@@ -420,10 +428,9 @@ __global__ void __launch_bounds__(256) fwd_replay(Geo g, Ptrs p) {
   const float bias = p.bias ? p.bias[li.d] : 0.0f;
   const float Dd = p.D ? p.D[li.d] : 0.0f;
   const bool has_z = p.z != nullptr;
-  float* srow = p.states + li.row * g.nck * N;
   float x[NS];
 #pragma unroll
-  for (int n = 0; n < NS; ++n) x[n] = n < N ? srow[(t_begin / CK) * N + n] : 0.0f;
+  for (int n = 0; n < NS; ++n) x[n] = n < N ? p.states[ck_index(g, li.row, t_begin / CK, n)] : 0.0f;
   const int64_t rbase = li.row * g.length;
   const int t_last = t_begin + ((t_end - t_begin - 1) / HS) * HS;
   RawRun<DeltaT<TU>> rd;
@@ -433,10 +440,17 @@ __global__ void __launch_bounds__(256) fwd_replay(Geo g, Ptrs p) {
   ru.load(g, p.u, g.u_dtype, rbase + t_begin, min(HS, t_end - t_begin));
   rz.load(g, zsrc, g.u_dtype, rbase + t_begin, min(HS, t_end - t_begin));
   for (int t0 = t_begin; t0 < t_end; t0 += HS) {
-    if (t0 != t_begin && (t0 % CK) == 0 && li.active) {
+    // the state entering this block (saved every block, CK == HS; at the chunk's
+    // first block it rewrites the value the chain stored).  Unconditional, so the
+    // loads in flight are the same on every path; lanes past the last row hold the
+    // clamped last row and store identical values.
+    static_assert(CK == HS, "one saved state per block");
+    {
+      float* sp = p.states + ck_index(g, li.row, t0 / CK, 0);
+      const int sd = static_cast<int>(g.dim);
 #pragma unroll
       for (int n = 0; n < NS; ++n)
-        if (n < N) srow[(t0 / CK) * N + n] = x[n];
+        if (FULL || n < N) sp[n * sd] = x[n];
     }
     const int nv = min(HS, t_end - t0);
     float raw[HS], uu[HS], zz[HS], del[HS], du[HS], y[HS];
@@ -575,7 +589,8 @@ __device__ __forceinline__ void load_state_rows(const float* __restrict__ bn, co
   }
 }
 
-template <int NS, bool UNI>
+// FULL: dstate == NS, so the per-state loop has no run-time guards.
+template <int NS, bool UNI, bool FULL>
 __global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
   __shared__ float lds[4 * MainLds<NS>::kWaveFloats + MainLds<NS>::kRows];
   const LaneInfo li = lane_info(g, UNI);
@@ -629,12 +644,14 @@ __global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
     const int tb = j * CK;
     const int te = min(tb + CK, t_end);
     const int nq = (te - tb + HS - 1) / HS;
-    const float* srow = p.states + (li.row * g.nck + j) * N;
+    // saved state entering block j, element n at srow[n * srow_stride]
+    const float* srow = p.states + ck_index(g, li.row, j, 0);
+    const int srow_stride = static_cast<int>(g.dim);
     // ---- states entering quarters 1..nq-1, state-inner sweep from the saved state
     if (nq > 1) {
       float x[NS];
 #pragma unroll
-      for (int n = 0; n < NS; ++n) x[n] = n < N ? srow[n] : 0.0f;
+      for (int n = 0; n < NS; ++n) x[n] = n < N ? srow[n * srow_stride] : 0.0f;
       for (int q = 0; q < nq - 1; ++q) {
         const int qs = tb + q * HS;
         float sdel[HS], sdu[HS], unused[HS];
@@ -685,14 +702,14 @@ __global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
       }
       // per-lane carries, state-major: element (n, row) at n * R + row
       const float* xin_p = q == 0 ? srow : qx + ((q - 1) * NS) * R + li.row;
-      const int xin_stride = q == 0 ? 1 : static_cast<int>(R);
+      const int xin_stride = q == 0 ? srow_stride : static_cast<int>(R);
       const float* bn_p = p.bn + (li.bg * NS) * g.length + qs;
       const float* cn_p = p.cn + (li.bg * NS) * g.length + qs;
       float xin_n = xin_p[0];
 #pragma unroll
       for (int n = 0; n < NS; ++n) {
-        if (n >= N) break;
-        const bool more = n + 1 < N;
+        if (!FULL && n >= N) break;
+        const bool more = n + 1 < (FULL ? NS : N);
         float xin_x = 0.0f;
         if (more) xin_x = xin_p[(n + 1) * xin_stride];
         float bv[HS], cv[HS];
@@ -999,7 +1016,7 @@ static int make_plan(const mko_selscan_params* p, Plan* pl) {
   pl->off_ddp = o; o = align_up(o + rk * 4);
   pl->off_dbp = o; o = align_up(o + rk * 4);
   pl->off_hcs = o; o = align_up(o + rk * ns * 4);
-  pl->off_qx = o; o = align_up(o + rk * 3 * ns * 4);
+  pl->off_qx = o; o = align_up(o + (CK > HS ? rk * 3 * ns * 4 : 0));  // quarter-entry states (only when saves are sparser than 16 steps)
   pl->bwd_bytes = o;
   return MKO_OK;
 }
@@ -1062,7 +1079,10 @@ static int launch_fwd(const Plan& pl, const Ptrs& q, hipStream_t s) {
     MKO_TIMED("selscan_fwd_summary", s, fwd_summary<NS, UNI, TU><<<dim3(gx, g.nchunks - 1), block, 0, s>>>(g, q));
   }
   MKO_TIMED("selscan_chain", s, chain<false><<<blocks_for(g.rows * g.dstate), 256, 0, s>>>(g, q.A, q.drive, q.sumd, q.states));
-  MKO_TIMED("selscan_fwd_replay", s, fwd_replay<NS, UNI, TU><<<dim3(gx, g.nchunks), block, 0, s>>>(g, q));
+  if (g.dstate == NS)
+    MKO_TIMED("selscan_fwd_replay", s, fwd_replay<NS, UNI, TU, true><<<dim3(gx, g.nchunks), block, 0, s>>>(g, q));
+  else
+    MKO_TIMED("selscan_fwd_replay", s, fwd_replay<NS, UNI, TU, false><<<dim3(gx, g.nchunks), block, 0, s>>>(g, q));
   return mko_check_launch("selscan_fwd");
 }
 
@@ -1082,7 +1102,10 @@ static int launch_bwd(const Plan& pl, const Ptrs& q, const mko_selscan_params* p
     const int64_t n = bgl * NS * 2;
     MKO_TIMED("selscan_zero", s, zero_f32<<<blocks_for(n), 256, 0, s>>>(q.pbc, n));
   }
-  MKO_TIMED("selscan_bwd_main", s, bwd_main<NS, UNI><<<dim3(gx, g.nchunks), block, 0, s>>>(g, q));
+  if (g.dstate == NS)
+    MKO_TIMED("selscan_bwd_main", s, bwd_main<NS, UNI, true><<<dim3(gx, g.nchunks), block, 0, s>>>(g, q));
+  else
+    MKO_TIMED("selscan_bwd_main", s, bwd_main<NS, UNI, false><<<dim3(gx, g.nchunks), block, 0, s>>>(g, q));
   MKO_TIMED("selscan_bwd_reduce", s,
             reduce_bc<NS><<<static_cast<unsigned>(g.batch * g.ngroups * ((g.length + 256 / NS - 1) / (256 / NS))),
                             256, 0, s>>>(g, UNI ? g.ncb : 1, q.pbc, p->dB, p->dC);

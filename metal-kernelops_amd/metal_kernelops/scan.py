@@ -50,8 +50,11 @@ def _params(u, delta, A, B, C, D, z, bias, softplus):
     return p
 
 
+_CHECKPOINT = 16  # MKO_SS_CHECKPOINT: steps between the scan states the forward saves
+
+
 def _num_checkpoints(length):
-    return (length + CHUNK - 1) // CHUNK
+    return (length + _CHECKPOINT - 1) // _CHECKPOINT
 
 
 @torch.library.custom_op("mko::selscan_fwd", mutates_args=(), device_types="cuda")
@@ -60,7 +63,7 @@ def _selscan_fwd(u: Tensor, delta: Tensor, A: Tensor, B: Tensor, C: Tensor, D: O
                  ) -> Tuple[Tensor, Tensor]:
     batch, dim, length = u.shape
     out = torch.empty_like(u)
-    states = torch.empty(batch, dim, _num_checkpoints(length), A.shape[1], dtype=torch.float32,
+    states = torch.empty(batch, _num_checkpoints(length), A.shape[1], dim, dtype=torch.float32,
                          device=u.device)
     if out.numel() == 0:
         return out, states
@@ -76,7 +79,7 @@ def _selscan_fwd(u: Tensor, delta: Tensor, A: Tensor, B: Tensor, C: Tensor, D: O
 @_selscan_fwd.register_fake
 def _(u, delta, A, B, C, D, z, delta_bias, softplus):
     batch, dim, length = u.shape
-    return torch.empty_like(u), u.new_empty(batch, dim, _num_checkpoints(length), A.shape[1],
+    return torch.empty_like(u), u.new_empty(batch, _num_checkpoints(length), A.shape[1], dim,
                                             dtype=torch.float32)
 
 

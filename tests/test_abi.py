@@ -52,7 +52,7 @@ def test_host_side_validation_without_gpu(native):
     assert lib.mko_selscan_fwd(ctypes.byref(p), None) == 3
     p.dstate = 16
     assert lib.mko_selscan_fwd_workspace_size(ctypes.byref(p)) > 0
-    assert lib.mko_selscan_num_checkpoints(130) == 3
+    assert lib.mko_selscan_num_checkpoints(130) == 9  # ceil(130 / MKO_SS_CHECKPOINT), 16-step saves
     p.workspace, p.workspace_bytes = None, 0
     for name in ("u", "delta", "A", "B", "C", "out", "states"):
         setattr(p, name, 16)  # never dereferenced: the workspace check fails first
