@@ -258,6 +258,60 @@ __device__ __forceinline__ float load_steps(const Geo& g, const Ptrs& p, int64_t
   return sd;
 }
 
+// One 16-step block of the time-major B (and C) rows of a wavefront's (batch, group),
+// staged through the wavefront's own LDS: each lane fetches HS*NS/64 floats per
+// matrix (coalesced) one block ahead, then writes them to the idle buffer.  The step
+// loop reads a step's row with broadcast LDS loads, whose waits are exact (unlike
+// scalar loads, which can only be waited for all together).
+template <int NS, bool WB, bool WC>
+struct WaveBC {
+  static constexpr int PER = HS * NS / kWave;
+  float rb[PER], rc[PER];
+  __device__ __forceinline__ void fetch(const float* __restrict__ bt, const float* __restrict__ ct, int64_t off) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      if (WB) rb[k] = bt[off + lane + k * kWave];
+      if (WC) rc[k] = ct[off + lane + k * kWave];
+    }
+  }
+  __device__ __forceinline__ void put(float* sb, float* sc) const {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      if (WB) sb[lane + k * kWave] = rb[k];
+      if (WC) sc[lane + k * kWave] = rc[k];
+    }
+  }
+};
+
+template <int NS>
+__device__ __forceinline__ void lds_row(const float* src, float (&v)[NS]) {
+#pragma unroll
+  for (int q = 0; q < NS / 4; ++q) {
+    const float4 w = reinterpret_cast<const float4*>(src)[q];
+    v[4 * q] = w.x;
+    v[4 * q + 1] = w.y;
+    v[4 * q + 2] = w.z;
+    v[4 * q + 3] = w.w;
+  }
+}
+
+// forward_block over a whole block with B/C rows from LDS (sb/sc: [HS][NS]).
+template <int NS, bool WITH_Y>
+__device__ __forceinline__ void forward_block_lds(const float* sb, const float* sc, const float (&del)[HS],
+                                                  const float (&du)[HS], const float (&A2)[NS], float (&x)[NS],
+                                                  float (&y)[HS]) {
+#pragma unroll
+  for (int i = 0; i < HS; ++i) {
+    float b[NS], c[NS];
+    lds_row<NS>(sb + i * NS, b);
+    if (WITH_Y) lds_row<NS>(sc + i * NS, c);
+    const float acc = advance<NS, WITH_Y>(A2, del[i], du[i], b, c, x);
+    if (WITH_Y) y[i] = acc;
+  }
+}
+
 // The element type of u / z / dout / du / dz.  Dyn: read from Geo at run time (any
 // length, any alignment, any delta dtype); float / _Float16 / bf16: the typed path
 // (delta float32, whole 16-step blocks, 16-byte aligned rows), whose loads keep the
@@ -365,6 +419,17 @@ __global__ void __launch_bounds__(256) fwd_summary(Geo g, Ptrs p) {
   RawRun<TU> ru;
   rd.load(g, p.delta, g.d_dtype, rbase + t_begin, min(HS, t_end - t_begin));
   ru.load(g, p.u, g.u_dtype, rbase + t_begin, min(HS, t_end - t_begin));
+  constexpr bool kLds = UNI && !__is_same(TU, Dyn);
+  __shared__ float sbc[kLds ? 4 * 2 * HS * NS : 1];  // per wavefront: two buffers of [HS][NS] B rows
+  float* wb = sbc + (kLds ? (threadIdx.x >> 6) * 2 * HS * NS : 0);
+  WaveBC<NS, true, false> st;
+  const int64_t brow = li.bg * g.length;
+  if constexpr (kLds) {
+    st.fetch(p.bt, nullptr, (brow + t_begin) * NS);
+    st.put(wb, nullptr);
+    wave_lds_sync();
+  }
+  int cur = 0;
   for (int t0 = t_begin; t0 < t_end; t0 += HS) {
     const int nv = min(HS, t_end - t0);
     float raw[HS], uu[HS], del[HS], du[HS];
@@ -374,7 +439,15 @@ __global__ void __launch_bounds__(256) fwd_summary(Geo g, Ptrs p) {
     rd.load(g, p.delta, g.d_dtype, rbase + tn, min(HS, t_end - tn));
     ru.load(g, p.u, g.u_dtype, rbase + tn, min(HS, t_end - tn));
     sd += steps_from(g, raw, uu, nv, bias, del, du);
-    forward_block<NS, UNI, false>(p.bt, nullptr, li.bg * g.length, t0, nv, del, du, A2, x, unused);
+    if constexpr (kLds) {
+      st.fetch(p.bt, nullptr, (brow + tn) * NS);
+      forward_block_lds<NS, false>(wb + cur * HS * NS, nullptr, del, du, A2, x, unused);
+      cur ^= 1;
+      st.put(wb + cur * HS * NS, nullptr);
+      wave_lds_sync();
+    } else {
+      forward_block<NS, UNI, false>(p.bt, nullptr, brow, t0, nv, del, du, A2, x, unused);
+    }
   }
   if (li.active) {
     const int64_t o = (li.row * g.nchunks + c) * N;
@@ -439,6 +512,18 @@ __global__ void __launch_bounds__(256) fwd_replay(Geo g, Ptrs p) {
   rd.load(g, p.delta, g.d_dtype, rbase + t_begin, min(HS, t_end - t_begin));
   ru.load(g, p.u, g.u_dtype, rbase + t_begin, min(HS, t_end - t_begin));
   rz.load(g, zsrc, g.u_dtype, rbase + t_begin, min(HS, t_end - t_begin));
+  constexpr bool kLds = UNI && !__is_same(TU, Dyn);
+  __shared__ float sbc[kLds ? 4 * 4 * HS * NS : 1];  // per wavefront: two buffers of B rows, two of C rows
+  float* wb = sbc + (kLds ? (threadIdx.x >> 6) * 4 * HS * NS : 0);
+  float* wc = wb + 2 * HS * NS;
+  WaveBC<NS, true, true> st;
+  const int64_t brow = li.bg * g.length;
+  if constexpr (kLds) {
+    st.fetch(p.bt, p.ct, (brow + t_begin) * NS);
+    st.put(wb, wc);
+    wave_lds_sync();
+  }
+  int cur = 0;
   for (int t0 = t_begin; t0 < t_end; t0 += HS) {
     // the state entering this block (saved every block, CK == HS; at the chunk's
     // first block it rewrites the value the chain stored).  Unconditional, so the
@@ -462,7 +547,15 @@ __global__ void __launch_bounds__(256) fwd_replay(Geo g, Ptrs p) {
     ru.load(g, p.u, g.u_dtype, rbase + tn, min(HS, t_end - tn));
     rz.load(g, zsrc, g.u_dtype, rbase + tn, min(HS, t_end - tn));
     steps_from(g, raw, uu, nv, bias, del, du);
-    forward_block<NS, UNI, true>(p.bt, p.ct, li.bg * g.length, t0, nv, del, du, A2, x, y);
+    if constexpr (kLds) {
+      st.fetch(p.bt, p.ct, (brow + tn) * NS);
+      forward_block_lds<NS, true>(wb + cur * HS * NS, wc + cur * HS * NS, del, du, A2, x, y);
+      cur ^= 1;
+      st.put(wb + cur * HS * NS, wc + cur * HS * NS);
+      wave_lds_sync();
+    } else {
+      forward_block<NS, UNI, true>(p.bt, p.ct, brow, t0, nv, del, du, A2, x, y);
+    }
 #pragma unroll
     for (int i = 0; i < HS; ++i) y[i] = fmaf(Dd, uu[i], y[i]);
     if (has_z) {
@@ -503,6 +596,16 @@ __global__ void __launch_bounds__(256) bwd_summary(Geo g, Ptrs p) {
     rg.load(g, p.dout, g.u_dtype, rbase + t0, nv);
     rz.load(g, zsrc, g.u_dtype, rbase + t0, nv);
   }
+  constexpr bool kLds = UNI && !__is_same(TU, Dyn);
+  __shared__ float sbc[kLds ? 4 * 2 * HS * NS : 1];  // per wavefront: two buffers of [HS][NS] C rows
+  float* wc = sbc + (kLds ? (threadIdx.x >> 6) * 2 * HS * NS : 0);
+  WaveBC<NS, false, true> st;
+  if constexpr (kLds) {
+    st.fetch(nullptr, p.ct, (row0 + t_begin + (nblk - 1) * HS) * NS);
+    st.put(nullptr, wc);
+    wave_lds_sync();
+  }
+  int cur = 0;
   for (int blk = nblk - 1; blk >= 0; --blk) {
     const int t0 = t_begin + blk * HS;
     const int nv = min(HS, t_end - t0);
@@ -524,6 +627,22 @@ __global__ void __launch_bounds__(256) bwd_summary(Geo g, Ptrs p) {
     for (int i = 0; i < HS; ++i) {
       del[i] = i < nv ? step_of(g, del[i], bias) : 0.0f;
       sd += del[i];
+    }
+    if constexpr (kLds) {
+      st.fetch(nullptr, p.ct, (row0 + t_begin + (blk > 0 ? blk - 1 : 0) * HS) * NS);
+      const float* sc = wc + cur * HS * NS;
+#pragma unroll
+      for (int i = HS - 1; i >= 0; --i) {
+        float cv[NS];
+        lds_row<NS>(sc + i * NS, cv);
+        const float d = del[i], gv = gy[i];
+#pragma unroll
+        for (int n = 0; n < NS; ++n) hc[n] = fast_exp2(A2[n] * d) * fmaf(gv, cv[n], hc[n]);
+      }
+      cur ^= 1;
+      st.put(nullptr, wc + cur * HS * NS);
+      wave_lds_sync();
+      continue;
     }
     StepBC<NS, UNI, false, true> e0, e1;
     e0.load(nullptr, p.ct, (row0 + t0 + nv - 1) * NS);
