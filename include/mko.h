@@ -177,6 +177,9 @@ int mko_state_update_bwd(const mko_state_update_params* p, void* stream);
 
 #define MKO_SSD_SOFTPLUS 1u  /* delta = softplus(dt + dt_bias) */
 #define MKO_SSD_D_PER_ROW 2u /* D is (nheads, headdim) instead of (nheads,) */
+#define MKO_SSD_SAVE_Y 4u    /* the forward also saves the chunk output before the skip and
+                                the gate (fp32), so the backward need not recompute it; the
+                                flag must be the same for the forward and its backward */
 
 typedef struct mko_ssd_params {
   const void* x;              /* (batch, length, nheads, headdim)  x_dtype            */

@@ -152,6 +152,7 @@ __global__ void __launch_bounds__(256) chunk_scan(Geo g, Ptrs p) {
   __syncthreads();
   float v[2][8];
   lds_block(red, r0, c0, v[0], v[1]);
+  if (p.yt) store_xw<float, VEC>(g, p.yt, b, tl0, h, pc0, v[0], v[1]);
   const int64_t pc = pc0 + c0;
 #pragma unroll
   for (int rr = 0; rr < 2; ++rr) {
@@ -222,6 +223,7 @@ int make_geo(const mko_ssd_params* prm, Geo* g) {
   g->vec = vec ? 1 : 0;
   g->softplus = (prm->flags & MKO_SSD_SOFTPLUS) ? 1 : 0;
   g->d_per_row = (prm->flags & MKO_SSD_D_PER_ROW) ? 1 : 0;
+  g->save_y = (prm->flags & MKO_SSD_SAVE_Y) ? 1 : 0;
   return MKO_OK;
 }
 
@@ -233,6 +235,7 @@ SavedLayout saved_layout(const Geo& g) {
   l.dl = o; o = align256(o + bh * g.nc * g.q * 4);
   l.cs = o; o = align256(o + bh * g.nc * g.q * 4);
   l.cb = o; o = align256(o + static_cast<size_t>(g.batch) * g.nc * g.ngroups * g.q * g.q * dtype_size(g.x_dtype));
+  l.yt = o; o = align256(o + (g.save_y ? static_cast<size_t>(g.batch * g.length * g.nheads * g.headdim) * 4 : 0));
   l.total = o;
   return l;
 }
@@ -244,6 +247,7 @@ void bind_saved(const Geo& g, void* saved, Ptrs* q) {
   q->dl = reinterpret_cast<float*>(s + l.dl);
   q->cs = reinterpret_cast<float*>(s + l.cs);
   q->cb = s + l.cb;
+  q->yt = g.save_y ? reinterpret_cast<float*>(s + l.yt) : nullptr;
 }
 
 Ptrs base_ptrs(const mko_ssd_params* prm) {

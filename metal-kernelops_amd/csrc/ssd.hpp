@@ -25,7 +25,7 @@ struct Geo {
   int nnt;  // 64-wide d_state tiles
   int nnp;  // pairs of d_state tiles (a workgroup covers up to 128 states)
   int x_dtype, dt_dtype;
-  int softplus, d_per_row;
+  int softplus, d_per_row, save_y;
   int vec;  // 16-byte vector access of 8-element runs is valid (P, N multiples of 8, aligned)
 };
 
@@ -65,6 +65,7 @@ struct Ptrs {
   float* dl;     // (b, H, nc, q) step sizes (0 past the end)
   float* cs;     // (b, H, nc, q) cumulative step * A inside the chunk
   void* cb;      // (b, nc, G, q, q) TM: C . B^T, lower tiles
+  float* yt;     // (b, L, H, P) chunk output before the skip and the gate (save_y), else null
   // backward workspace
   const void* gy;  // (b, L, H, P) TM: dy * silu(z) (dy itself without z)
   void* gyw;       // writable alias of gy when it is materialised
@@ -82,7 +83,7 @@ struct Ptrs {
 };
 
 struct SavedLayout {
-  size_t states, dl, cs, cb, total;
+  size_t states, dl, cs, cb, yt, total;
 };
 
 inline size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }

@@ -45,7 +45,8 @@ __device__ __forceinline__ float block_sum(float v, float* wsum) {
   return (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
 }
 
-template <typename TM, bool VEC>
+// SAVED: the forward saved the chunk output (p.yt); otherwise it is recomputed here.
+template <typename TM, bool VEC, bool SAVED>
 __global__ void __launch_bounds__(256) gate(Geo g, BwdPlan pl, Ptrs p) {
   constexpr int TE = LdsTile<TM>::elems;
   __shared__ __align__(16) TM sbuf[2][2 * TE];
@@ -67,15 +68,22 @@ __global__ void __launch_bounds__(256) gate(Geo g, BwdPlan pl, Ptrs p) {
   if (p.z) load_xw<TM, VEC>(g, static_cast<const TM*>(p.z), b, tl0, h, pc0, zv);
   float dv[8];
   load_d8(g, p, h, pc, dv);
-  load_chunk_cs(g, p, bh, c, csc, dlc);
-  __syncthreads();
-  f32x16 acc;
-  chunk_out<TM, VEC>(g, p, acc, sbuf, csc, dlc, i, pt, c, bh);
-  float* red = reinterpret_cast<float*>(&sbuf[0][0]);
-  acc_to_lds(red, acc, wm, wn, lane);
-  __syncthreads();
   float yt[2][8];
-  lds_block(red, r0, c0, yt[0], yt[1]);
+  if constexpr (SAVED) {
+    V8<float> yv[2];
+    load_xw<float, VEC>(g, p.yt, b, tl0, h, pc0, yv);
+    v8_f32(yv[0], yt[0]);
+    v8_f32(yv[1], yt[1]);
+  } else {
+    load_chunk_cs(g, p, bh, c, csc, dlc);
+    __syncthreads();
+    f32x16 acc;
+    chunk_out<TM, VEC>(g, p, acc, sbuf, csc, dlc, i, pt, c, bh);
+    float* red = reinterpret_cast<float*>(&sbuf[0][0]);
+    acc_to_lds(red, acc, wm, wn, lane);
+    __syncthreads();
+    lds_block(red, r0, c0, yt[0], yt[1]);
+  }
   float dd[8], gyo[2][8], dzo[2][8];
 #pragma unroll
   for (int k = 0; k < 8; ++k) dd[k] = 0.0f;
@@ -730,7 +738,10 @@ void launch_bwd_t(const Geo& g, const BwdPlan& pl, const Ptrs& q, hipStream_t s)
   const unsigned bh = static_cast<unsigned>(g.batch * g.nheads);
   const unsigned ncg = static_cast<unsigned>(g.nc * g.ngroups);
   const unsigned nb = static_cast<unsigned>(g.batch);
-  MKO_TIMED("ssd_gate", s, gate<TM, VEC><<<dim3(g.qb * g.npt * g.nc * bh), 256, 0, s>>>(g, pl, q));
+  if (q.yt)
+    MKO_TIMED("ssd_gate", s, gate<TM, VEC, true><<<dim3(g.qb * g.npt * g.nc * bh), 256, 0, s>>>(g, pl, q));
+  else
+    MKO_TIMED("ssd_gate", s, gate<TM, VEC, false><<<dim3(g.qb * g.npt * g.nc * bh), 256, 0, s>>>(g, pl, q));
   MKO_TIMED("ssd_chunk_state_bwd", s,
             chunk_state<TM, VEC, true><<<dim3(g.npt * g.nnp * g.nc * bh), 256, 0, s>>>(g, q, q.dstates));
   MKO_TIMED("ssd_state_rev", s, state_rev<TM><<<dim3(pl.nblk, bh), 256, 0, s>>>(g, pl, q));

@@ -40,7 +40,7 @@ from .. import _native as nat
 __all__ = ["mamba2_chunk_scan", "mamba2_chunk_scan_reference", "last_path"]
 
 _FLOATS = (torch.float32, torch.float16, torch.bfloat16)
-_SOFTPLUS, _D_PER_ROW = 1, 2
+_SOFTPLUS, _D_PER_ROW, _SAVE_Y = 1, 2, 4
 
 _path = "none"
 """Which path the last :func:`mamba2_chunk_scan` call took."""
@@ -98,7 +98,7 @@ def _check(x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size):
     return batch, length, nheads, headdim, ngroups, dstate, initial_states
 
 
-def _params(x, dt, A, B, C, D, z, dt_bias, init, softplus):
+def _params(x, dt, A, B, C, D, z, dt_bias, init, softplus, save_y=False):
     batch, length, nheads, headdim = x.shape
     p = nat.SsdParams()
     p.x, p.dt, p.A, p.B, p.C = (nat.ptr(t) for t in (x, dt, A, B, C))
@@ -106,19 +106,20 @@ def _params(x, dt, A, B, C, D, z, dt_bias, init, softplus):
     p.batch, p.length, p.nheads, p.headdim = batch, length, nheads, headdim
     p.ngroups, p.dstate = B.shape[2], B.shape[3]
     p.x_dtype, p.dt_dtype, p.bc_dtype = nat.code(x.dtype), nat.code(dt.dtype), nat.code(B.dtype)
-    p.flags = (_SOFTPLUS if softplus else 0) | (_D_PER_ROW if D is not None and D.dim() == 2 else 0)
+    p.flags = ((_SOFTPLUS if softplus else 0) | (_D_PER_ROW if D is not None and D.dim() == 2 else 0)
+               | (_SAVE_Y if save_y else 0))
     return p
 
 
 @torch.library.custom_op("mko::ssd_fwd", mutates_args=(), device_types="cuda")
 def _ssd_fwd(x: Tensor, dt: Tensor, A: Tensor, B: Tensor, C: Tensor, D: Optional[Tensor],
              z: Optional[Tensor], dt_bias: Optional[Tensor], initial_states: Optional[Tensor],
-             softplus: bool) -> Tuple[Tensor, Tensor, Tensor]:
+             softplus: bool, save_y: bool) -> Tuple[Tensor, Tensor, Tensor]:
     batch, length, nheads, headdim = x.shape
     y = torch.empty_like(x)
     final = torch.empty(batch, nheads, headdim, B.shape[3], dtype=x.dtype, device=x.device)
     lib = nat.lib()
-    p = _params(x, dt, A, B, C, D, z, dt_bias, initial_states, softplus)
+    p = _params(x, dt, A, B, C, D, z, dt_bias, initial_states, softplus, save_y)
     saved = nat.workspace(lib.mko_ssd_saved_bytes(ctypes.byref(p)), x.device)
     p.y, p.final_state, p.saved = y.data_ptr(), final.data_ptr(), saved.data_ptr()
     nat.check(lib.mko_ssd_fwd(ctypes.byref(p), nat.stream_of(x.device)), "mko_ssd_fwd")
@@ -126,7 +127,7 @@ def _ssd_fwd(x: Tensor, dt: Tensor, A: Tensor, B: Tensor, C: Tensor, D: Optional
 
 
 @_ssd_fwd.register_fake
-def _(x, dt, A, B, C, D, z, dt_bias, initial_states, softplus):
+def _(x, dt, A, B, C, D, z, dt_bias, initial_states, softplus, save_y):
     batch, length, nheads, headdim = x.shape
     return (torch.empty_like(x), x.new_empty(batch, nheads, headdim, B.shape[3]),
             x.new_empty(0, dtype=torch.uint8))
@@ -135,7 +136,7 @@ def _(x, dt, A, B, C, D, z, dt_bias, initial_states, softplus):
 @torch.library.custom_op("mko::ssd_bwd", mutates_args=(), device_types="cuda")
 def _ssd_bwd(dy: Tensor, dfinal: Optional[Tensor], x: Tensor, dt: Tensor, A: Tensor, B: Tensor,
              C: Tensor, D: Optional[Tensor], z: Optional[Tensor], dt_bias: Optional[Tensor],
-             initial_states: Optional[Tensor], softplus: bool, saved: Tensor
+             initial_states: Optional[Tensor], softplus: bool, save_y: bool, saved: Tensor
              ) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
     f32 = dict(dtype=torch.float32, device=x.device)
     dx, ddt = torch.empty_like(x), torch.empty_like(dt)
@@ -146,7 +147,7 @@ def _ssd_bwd(dy: Tensor, dfinal: Optional[Tensor], x: Tensor, dt: Tensor, A: Ten
     dbias = torch.empty(dt_bias.shape if dt_bias is not None else (0,), **f32)
     dinit = torch.empty_like(initial_states) if initial_states is not None else x.new_empty(0)
     lib = nat.lib()
-    p = _params(x, dt, A, B, C, D, z, dt_bias, initial_states, softplus)
+    p = _params(x, dt, A, B, C, D, z, dt_bias, initial_states, softplus, save_y)
     p.saved, p.dy, p.dfinal = saved.data_ptr(), dy.data_ptr(), nat.ptr(dfinal)
     p.dx, p.ddt, p.dA, p.dB, p.dC = (t.data_ptr() for t in (dx, ddt, dA, dB, dC))
     p.dD = dD.data_ptr() if D is not None else None
@@ -160,7 +161,7 @@ def _ssd_bwd(dy: Tensor, dfinal: Optional[Tensor], x: Tensor, dt: Tensor, A: Ten
 
 
 @_ssd_bwd.register_fake
-def _(dy, dfinal, x, dt, A, B, C, D, z, dt_bias, initial_states, softplus, saved):
+def _(dy, dfinal, x, dt, A, B, C, D, z, dt_bias, initial_states, softplus, save_y, saved):
     def f(shape):
         return x.new_empty(shape, dtype=torch.float32)
     return (torch.empty_like(x), torch.empty_like(dt), f(A.shape), torch.empty_like(B),
@@ -171,9 +172,10 @@ def _(dy, dfinal, x, dt, A, B, C, D, z, dt_bias, initial_states, softplus, saved
 
 
 def _setup(ctx, inputs, output):
-    x, dt, A, B, C, D, z, dt_bias, init, softplus = inputs
+    x, dt, A, B, C, D, z, dt_bias, init, softplus, save_y = inputs
     ctx.save_for_backward(x, dt, A, B, C, D, z, dt_bias, init, output[2])
     ctx.softplus = softplus
+    ctx.save_y = save_y
     ctx.set_materialize_grads(False)  # no zero-filled gradient for the save area
 
 
@@ -183,9 +185,9 @@ def _backward(ctx, dy, dfinal, _dsaved):
         dy = torch.zeros_like(x)
     dx, ddt, dA, dB, dC, dD, dz, dbias, dinit = torch.ops.mko.ssd_bwd(
         dy.contiguous(), None if dfinal is None else dfinal.contiguous(), x, dt, A, B, C, D, z, bias,
-        init, ctx.softplus, saved)
+        init, ctx.softplus, ctx.save_y, saved)
     return (dx, ddt, dA, dB, dC, dD if D is not None else None, dz if z is not None else None,
-            dbias if bias is not None else None, dinit if init is not None else None, None)
+            dbias if bias is not None else None, dinit if init is not None else None, None, None)
 
 
 torch.library.register_autograd("mko::ssd_fwd", _backward, setup_context=_setup)
@@ -232,8 +234,11 @@ def mamba2_chunk_scan(x, dt, A, B, C, chunk_size=64, D=None, z=None, dt_bias=Non
         initial_states = initial_states.to(x.dtype).contiguous()
     A, D, dt_bias = _f32(A), _f32(D), _f32(dt_bias)
     _path = "hip"
+    # The forward keeps its chunk output for the backward only when a gradient will be taken.
+    save_y = torch.is_grad_enabled() and any(
+        t is not None and t.requires_grad for t in (x, dt, A, B, C, D, z, dt_bias, initial_states))
     y, final, _ = torch.ops.mko.ssd_fwd(x, dt, A, B, C, D, z, dt_bias, initial_states,
-                                        bool(dt_softplus))
+                                        bool(dt_softplus), bool(save_y))
     return y, final
 
 
