@@ -9,6 +9,12 @@
 //
 // Operand types: bf16 and f16 use v_mfma_f32_32x32x16_{bf16,f16}; float uses
 // v_mfma_f32_32x32x2_f32, which keeps fp32 products (used for fp32 inputs).
+//
+// 16-bit tiles are XOR-swizzled in 8-element (16-byte) units: element (row, k) lives
+// at row * 72 + (k ^ (row & 0x38)).  Rows 8 apart are 288 words apart, the same bank
+// with 32 banks, so the transposed stores of a staging pass (eight lanes writing rows
+// 8m + j, m = 0..7, at one k) would all hit one bank; the swizzle spreads them over
+// eight 4-bank groups and leaves 16-byte runs whole and aligned for the operand reads.
 #pragma once
 
 #include "common.hpp"
@@ -31,6 +37,15 @@ struct LdsTile {
   static constexpr int elems = 64 * ld;
 };
 
+// Element offset of (row, k) in an LDS operand tile (k: the contiguous dimension).
+template <typename TM>
+__device__ __forceinline__ int lds_idx(int row, int k) {
+  if constexpr (sizeof(TM) == 2)
+    return row * tile_ld<TM>() + (k ^ (row & 0x38));
+  else
+    return row * tile_ld<TM>() + k;
+}
+
 __device__ __forceinline__ void quadrant(int lane_wave, int& wm, int& wn) {
   wm = lane_wave >> 1;
   wn = lane_wave & 1;
@@ -48,11 +63,10 @@ __device__ __forceinline__ void mma_tile(f32x16& acc, const TM* A, const TM* Bt,
                                          int k_len) {
   constexpr int ld = tile_ld<TM>();
   if constexpr (sizeof(TM) == 2) {
-    const TM* a = A + (wm * 32 + (lane & 31)) * ld + (lane >> 5) * 8;
-    const TM* b = Bt + (wn * 32 + (lane & 31)) * ld + (lane >> 5) * 8;
+    const int ra = wm * 32 + (lane & 31), rb = wn * 32 + (lane & 31), kh = (lane >> 5) * 8;
     for (int k = 0; k < k_len; k += 16) {
-      const uint4 av = *reinterpret_cast<const uint4*>(a + k);
-      const uint4 bv = *reinterpret_cast<const uint4*>(b + k);
+      const uint4 av = *reinterpret_cast<const uint4*>(A + lds_idx<TM>(ra, k + kh));
+      const uint4 bv = *reinterpret_cast<const uint4*>(Bt + lds_idx<TM>(rb, k + kh));
       if constexpr (__is_same(TM, bf16)) {
         acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(mfma_bf16x8, av),
                                                       __builtin_bit_cast(mfma_bf16x8, bv), acc, 0, 0, 0);

@@ -136,16 +136,16 @@ __global__ void __launch_bounds__(256) chunk_scan(Geo g, Ptrs p) {
   quadrant(threadIdx.x >> 6, wm, wn);
   const int r0 = blk_r0(), c0 = blk_c0();
   const int64_t tl0 = static_cast<int64_t>(c) * g.q + 64 * i, pc0 = static_cast<int64_t>(pt) * 64;
-  // epilogue inputs, in flight during the products
+  load_chunk_cs(g, p, bh, c, csc, dlc);
+  __syncthreads();
+  f32x16 acc;
+  chunk_out<TM, VEC>(g, p, acc, sbuf, csc, dlc, i, pt, c, bh);
+  // epilogue inputs, loaded while the accumulators go through LDS
   V8<TM> xv[2], zv[2];
   load_xw<TM, VEC>(g, static_cast<const TM*>(p.x), b, tl0, h, pc0, xv);
   if (p.z) load_xw<TM, VEC>(g, static_cast<const TM*>(p.z), b, tl0, h, pc0, zv);
   float dv[8];
   load_d8(g, p, h, pc0 + c0, dv);
-  load_chunk_cs(g, p, bh, c, csc, dlc);
-  __syncthreads();
-  f32x16 acc;
-  chunk_out<TM, VEC>(g, p, acc, sbuf, csc, dlc, i, pt, c, bh);
   // epilogue through LDS: each thread owns rows r0, r0+1 and 8 consecutive d_head columns
   float* red = reinterpret_cast<float*>(&sbuf[0][0]);
   acc_to_lds(red, acc, wm, wn, lane);

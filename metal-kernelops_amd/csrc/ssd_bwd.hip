@@ -189,16 +189,23 @@ __global__ void __launch_bounds__(256) state_rev(Geo g, BwdPlan pl, Ptrs p) {
   if (n > 0 && p.dinit) v8_store(static_cast<TM*>(p.dinit) + bh * pn + e0, n, g.vec, gv);
 }
 
-// du for the 64-token tile j and d_head tile pt of one (b, h, chunk):
+// du for the 64-token tiles ja = jx and jb = qb-1-jx (one tile when they coincide) and
+// d_head tile pt of one (b, h, chunk):
 //   du[s][p] = e^{T - cs_s} sum_n B_s[n] G[p][n]  +  sum_{l >= s} K[l][s] gy_l[p]
-// The state part runs first and its u.du_state is taken before the intra part is added.
+// Tile j takes nnt state stages, then qb - j intra stages, so a pair takes
+// 2 nnt + qb + 1 stages whichever jx it is; both tiles run through one pipeline.  The
+// state part of a tile runs first and its u.du_state is taken before the intra part
+// is added.  Between stages the LDS buffer the next stage will fill is free, so the
+// snapshots and epilogues go through it.
 template <typename TM, bool VEC>
-__global__ void __launch_bounds__(256) du_kernel(Geo g, BwdPlan pl, Ptrs p) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) du_kernel(Geo g, BwdPlan pl, Ptrs p) {
   constexpr int TE = LdsTile<TM>::elems;
   __shared__ __align__(16) TM sbuf[2][2 * TE];
   __shared__ __align__(16) float csc[256], dlc[256];
-  const WgId id = wg_id(g.qb * g.npt, g.nc);
-  const int j = id.x % g.qb, pt = id.x / g.qb;
+  const int nj = (g.qb + 1) / 2;
+  const WgId id = wg_id(nj * g.npt, g.nc);
+  const int jx = id.x % nj, pt = id.x / nj;
+  const int ja = jx, jb = g.qb - 1 - jx;
   const int c = id.y;
   const int64_t bh = id.z, b = bh / g.nheads, h = bh % g.nheads, gg = h / g.hpg;
   const int lane = threadIdx.x & 63;
@@ -206,64 +213,71 @@ __global__ void __launch_bounds__(256) du_kernel(Geo g, BwdPlan pl, Ptrs p) {
   quadrant(threadIdx.x >> 6, wm, wn);
   const int r0 = blk_r0(), c0 = blk_c0();
   load_chunk_cs(g, p, bh, c, csc, dlc);
-  const int64_t tc = static_cast<int64_t>(c) * g.q, ts0 = tc + 64 * j;
+  const int64_t tc = static_cast<int64_t>(c) * g.q;
   const int64_t pc0 = static_cast<int64_t>(pt) * 64, pc = pc0 + c0;
   const TM* cbt = static_cast<const TM*>(p.cb) + ((b * g.nc + c) * g.ngroups + gg) * g.q * g.q;
   const TM* Bm = static_cast<const TM*>(p.B);
   const TM* gy = static_cast<const TM*>(p.gy);
   const TM* G = static_cast<const TM*>(p.dstates) + (bh * g.nc + c) * g.headdim * g.dstate;
-  // x and gy of the thread's epilogue block (rows s = r0, r0+1 of tile j)
-  V8<TM> xv[2], gv[2];
-  load_xw<TM, VEC>(g, static_cast<const TM*>(p.x), b, ts0, h, pc0, xv);
-  load_xw<TM, VEC>(g, gy, b, ts0, h, pc0, gv);
-  float dv[8];
-  load_d8(g, p, h, pc, dv);
+  const int na = g.nnt + g.qb - ja;
+  const int n = na + (jb != ja ? g.nnt + g.qb - jb : 0);
+  // stage k -> tile j and its stage kk within the tile
+  auto tile_of = [&](int k, int& j, int& kk) {
+    j = k < na ? ja : jb;
+    kk = k < na ? k : k - na;
+  };
   f32x16 acc;
   zero(acc);
   __syncthreads();  // csc, dlc
   const float T = csc[g.q - 1];
-  float xf[2][8], uf[2][8];
-#pragma unroll
-  for (int rr = 0; rr < 2; ++rr) {
-    v8_f32(xv[rr], xf[rr]);
+  // x of the thread's block (rows s = r0, r0+1 of tile j) and u_s = R(dt_s x_s), the
+  // rounded input of the forward's products
+  auto load_x = [&](int j, V8<TM> (&xv)[2]) {
+    load_xw<TM, VEC>(g, static_cast<const TM*>(p.x), b, tc + 64 * j, h, pc0, xv);
+  };
+  auto u8 = [&](int j, const V8<TM> (&xv)[2], int rr, float (&xf)[8], float (&uf)[8]) {
+    v8_f32(xv[rr], xf);
     const float d = dlc[64 * j + r0 + rr];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) uf[rr][k] = to_f32(from_f32<TM>(d * xf[rr][k]));
-  }
-  float* red = reinterpret_cast<float*>(&sbuf[0][0]);
-  const int64_t po = ((bh * g.nc + c) * g.npt + pt) * g.q + 64 * j;
-  // Stages 0 .. nnt-1: state part, A = e^{T - cs_s} B_s[n], Bt = G[p][n]; then
-  // tau_s = u_s . du_state_s; stages nnt .. : intra-chunk tiles i >= j,
+    for (int k = 0; k < 8; ++k) uf[k] = to_f32(from_f32<TM>(d * xf[k]));
+  };
+  const int64_t po0 = ((bh * g.nc + c) * g.npt + pt) * g.q;
+  // Per tile: stages 0 .. nnt-1: state part, A = e^{T - cs_s} B_s[n], Bt = G[p][n];
+  // then tau_s = u_s . du_state_s; stages nnt .. : intra-chunk tiles i >= j,
   // A = K[l][s] (transposed), Bt = gy_l[p] (transposed).  Both kinds load two rows
   // of two 64-wide windows.
   struct Regs {
     V8<TM> a[2], b[2];
   };
   auto fetch = [&](int k, Regs& r) {
-    if (k < g.nnt) {
-      load_bw<TM, VEC>(g, Bm, b, ts0, gg, 64 * k, r.a);  // B rows s
-      load_sw<TM, VEC>(g, G, pc0, 64 * k, r.b);          // G rows p
+    int j, kk;
+    tile_of(k, j, kk);
+    if (kk < g.nnt) {
+      load_bw<TM, VEC>(g, Bm, b, tc + 64 * j, gg, 64 * kk, r.a);  // B rows s
+      load_sw<TM, VEC>(g, G, pc0, 64 * kk, r.b);                  // G rows p
     } else {
-      const int i = j + k - g.nnt;
+      const int i = j + kk - g.nnt;
       load_win<TM, true>(cbt + (64 * i) * g.q + 64 * j, g.q, 64, 64, r.a, cbt);  // cb rows l
       load_xw<TM, VEC>(g, gy, b, tc + 64 * i, h, pc0, r.b);                     // gy rows l
     }
   };
-  const float w0 = fast_exp(T - csc[64 * j + r0]), w1 = fast_exp(T - csc[64 * j + r0 + 1]);
-  const float4 cs_a = *reinterpret_cast<const float4*>(csc + 64 * j + c0);
-  const float4 cs_b = *reinterpret_cast<const float4*>(csc + 64 * j + c0 + 4);
-  const float css[8] = {cs_a.x, cs_a.y, cs_a.z, cs_a.w, cs_b.x, cs_b.y, cs_b.z, cs_b.w};
   auto put = [&](int k, Regs& r) {
+    int j, kk;
+    tile_of(k, j, kk);
     TM* buf = sbuf[k & 1];
     float a[8], bb[8];
-    if (k < g.nnt) {
+    if (kk < g.nnt) {
+      const float w0 = fast_exp(T - csc[64 * j + r0]), w1 = fast_exp(T - csc[64 * j + r0 + 1]);
       scale8(r.a[0], w0, a);
       scale8(r.a[1], w1, bb);
       put2x8<TM, false>(buf, r0, c0, a, bb);                  // A[s][n] = e^{T - cs_s} B_s[n]
       put_raw<TM, false>(buf + TE, r0, c0, r.b[0], r.b[1]);  // Bt[p][n] = G[p][n]
     } else {
-      const int i = j + k - g.nnt;
+      const int i = j + kk - g.nnt;
       const float cl0 = csc[64 * i + r0], cl1 = csc[64 * i + r0 + 1];
+      const float4 cs_a = *reinterpret_cast<const float4*>(csc + 64 * j + c0);
+      const float4 cs_b = *reinterpret_cast<const float4*>(csc + 64 * j + c0 + 4);
+      const float css[8] = {cs_a.x, cs_a.y, cs_a.z, cs_a.w, cs_b.x, cs_b.y, cs_b.z, cs_b.w};
       v8_f32(r.a[0], a);
       v8_f32(r.a[1], bb);
 #pragma unroll
@@ -282,60 +296,82 @@ __global__ void __launch_bounds__(256) du_kernel(Geo g, BwdPlan pl, Ptrs p) {
       put_raw<TM, true>(buf + TE, r0, c0, r.b[0], r.b[1]);  // Bt[p][l] = gy_l[p]
     }
   };
-  Regs ra, rb;
-  pipeline2(g.nnt + g.qb - j, ra, rb, fetch, put, [&](int k) {
-    mma_tile<TM>(acc, sbuf[k & 1], sbuf[k & 1] + TE, wm, wn, lane, 64);
-    if (k == g.nnt - 1) {
-      // tau_s = u_s . du_state_s (red aliases sbuf[0]; barriers on both sides)
-      __syncthreads();
-      acc_to_lds(red, acc, wm, wn, lane);
-      __syncthreads();
-      float v[2][8];
-      lds_block(red, r0, c0, v[0], v[1]);
+  // tau_s = u_s . du_state_s for tile j; red is the free buffer
+  auto tau_snapshot = [&](int j, float* red) {
+    V8<TM> xv[2];
+    load_x(j, xv);
+    acc_to_lds(red, acc, wm, wn, lane);
+    __syncthreads();
+    float v[2][8];
+    lds_block(red, r0, c0, v[0], v[1]);
 #pragma unroll
-      for (int rr = 0; rr < 2; ++rr) {
-        float tau = 0.0f;
+    for (int rr = 0; rr < 2; ++rr) {
+      float xf[8], uf[8];
+      u8(j, xv, rr, xf, uf);
+      float tau = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) tau = fmaf(uf[rr][e], v[rr][e], tau);
-        tau = row8_sum(tau);
-        if ((threadIdx.x & 7) == 0) p.tau[po + r0 + rr] = tau;
+      for (int e = 0; e < 8; ++e) tau = fmaf(uf[e], v[rr][e], tau);
+      tau = row8_sum(tau);
+      if ((threadIdx.x & 7) == 0) p.tau[po0 + 64 * j + r0 + rr] = tau;
+    }
+    __syncthreads();  // red is refilled by the next stage
+  };
+  // dx = dt du + D gy, and the row sums x.du and u.du of tile j; red is the free buffer
+  auto epilogue = [&](int j, float* red) {
+    V8<TM> gv[2], xv[2];
+    load_xw<TM, VEC>(g, gy, b, tc + 64 * j, h, pc0, gv);
+    load_x(j, xv);
+    float dv[8];
+    load_d8(g, p, h, pc, dv);
+    acc_to_lds(red, acc, wm, wn, lane);
+    __syncthreads();
+    float du[2][8], dxo[2][8];
+    lds_block(red, r0, c0, du[0], du[1]);
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      float gf[8], xf[8], uf[8];
+      v8_f32(gv[rr], gf);
+      u8(j, xv, rr, xf, uf);
+      const float d = dlc[64 * j + r0 + rr];
+      float sx = 0.0f, su = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float v = d * du[rr][e];
+        v = fmaf(dv[e], gf[e], v);
+        dxo[rr][e] = v;
+        sx = fmaf(xf[e], du[rr][e], sx);
+        su = fmaf(uf[e], du[rr][e], su);
       }
-      __syncthreads();
+      sx = row8_sum(sx);
+      su = row8_sum(su);
+      if ((threadIdx.x & 7) == 0) {
+        p.dsx[po0 + 64 * j + r0 + rr] = sx;
+        p.ut[po0 + 64 * j + r0 + rr] = su;
+      }
+    }
+    store_xw<TM, VEC>(g, static_cast<TM*>(p.dx), b, tc + 64 * j, h, pc0, dxo[0], dxo[1]);
+    __syncthreads();  // red is refilled by the next stage
+  };
+  Regs ra, rb;
+  pipeline2(n, ra, rb, fetch, put, [&](int k) {
+    mma_tile<TM>(acc, sbuf[k & 1], sbuf[k & 1] + TE, wm, wn, lane, 64);
+    int j, kk;
+    tile_of(k, j, kk);
+    // buffer (k+1)&1 was last read by stage k-1, which every wave finished before the
+    // barrier that published stage k
+    float* red = reinterpret_cast<float*>(&sbuf[(k + 1) & 1][0]);
+    if (kk == g.nnt - 1) tau_snapshot(j, red);
+    if (kk == g.nnt + g.qb - j - 1) {
+      epilogue(j, red);
+      zero(acc);
     }
   });
-  __syncthreads();
-  acc_to_lds(red, acc, wm, wn, lane);
-  __syncthreads();
-  float du[2][8], dxo[2][8];
-  lds_block(red, r0, c0, du[0], du[1]);
-#pragma unroll
-  for (int rr = 0; rr < 2; ++rr) {
-    float gf[8];
-    v8_f32(gv[rr], gf);
-    const float d = dlc[64 * j + r0 + rr];
-    float sx = 0.0f, su = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float v = d * du[rr][e];
-      v = fmaf(dv[e], gf[e], v);
-      dxo[rr][e] = v;
-      sx = fmaf(xf[rr][e], du[rr][e], sx);
-      su = fmaf(uf[rr][e], du[rr][e], su);
-    }
-    sx = row8_sum(sx);
-    su = row8_sum(su);
-    if ((threadIdx.x & 7) == 0) {
-      p.dsx[po + r0 + rr] = sx;
-      p.ut[po + r0 + rr] = su;
-    }
-  }
-  store_xw<TM, VEC>(g, static_cast<TM*>(p.dx), b, ts0, h, pc0, dxo[0], dxo[1]);
 }
 
 // Adjoint of C.B^T for one lower tile (i, j) of a chunk, summed over a block of the
 // group's heads: sum_h (gy_i u_j^T) o e^{cs_l - cs_s}.
 template <typename TM, bool VEC>
-__global__ void __launch_bounds__(256) dcb_kernel(Geo g, BwdPlan pl, Ptrs p) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) dcb_kernel(Geo g, BwdPlan pl, Ptrs p) {
   constexpr int TE = LdsTile<TM>::elems;
   __shared__ __align__(16) TM sbuf[2][2 * TE];
   __shared__ float csr[2][64], css[2][64];
@@ -745,7 +781,7 @@ void launch_bwd_t(const Geo& g, const BwdPlan& pl, const Ptrs& q, hipStream_t s)
   MKO_TIMED("ssd_chunk_state_bwd", s,
             chunk_state<TM, VEC, true><<<dim3(g.npt * g.nnp * g.nc * bh), 256, 0, s>>>(g, q, q.dstates));
   MKO_TIMED("ssd_state_rev", s, state_rev<TM><<<dim3(pl.nblk, bh), 256, 0, s>>>(g, pl, q));
-  MKO_TIMED("ssd_du", s, du_kernel<TM, VEC><<<dim3(g.qb * g.npt * g.nc * bh), 256, 0, s>>>(g, pl, q));
+  MKO_TIMED("ssd_du", s, du_kernel<TM, VEC><<<dim3((g.qb + 1) / 2 * g.npt * g.nc * bh), 256, 0, s>>>(g, pl, q));
   MKO_TIMED("ssd_dcb", s, dcb_kernel<TM, VEC><<<dim3(pl.npairs * pl.hb1 * ncg * nb), 256, 0, s>>>(g, pl, q));
   MKO_TIMED("ssd_dbc_state", s,
             dbc_state<TM, VEC><<<dim3(g.qb * g.nnp * 2 * pl.hb2 * ncg * nb), 256, 0, s>>>(g, pl, q));
