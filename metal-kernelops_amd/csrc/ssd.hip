@@ -126,7 +126,7 @@ template <typename TM, bool VEC>
 __global__ void __launch_bounds__(256) chunk_scan(Geo g, Ptrs p) {
   constexpr int TE = LdsTile<TM>::elems;
   __shared__ __align__(16) TM sbuf[2][2 * TE];
-  __shared__ __align__(16) float csc[256], dlc[256];
+  __shared__ __align__(16) float csc[256], dlc[256], ecol[256];
   const WgId id = wg_id(g.qb * g.npt, g.nc);
   const int i = id.x % g.qb, pt = id.x / g.qb;
   const int c = id.y;
@@ -136,10 +136,10 @@ __global__ void __launch_bounds__(256) chunk_scan(Geo g, Ptrs p) {
   quadrant(threadIdx.x >> 6, wm, wn);
   const int r0 = blk_r0(), c0 = blk_c0();
   const int64_t tl0 = static_cast<int64_t>(c) * g.q + 64 * i, pc0 = static_cast<int64_t>(pt) * 64;
-  load_chunk_cs(g, p, bh, c, csc, dlc);
+  load_chunk_cs(g, p, bh, c, csc, dlc, ecol);
   __syncthreads();
   f32x16 acc;
-  chunk_out<TM, VEC>(g, p, acc, sbuf, csc, dlc, i, pt, c, bh);
+  chunk_out<TM, VEC>(g, p, acc, sbuf, csc, dlc, ecol, i, pt, c, bh);
   // epilogue inputs, loaded while the accumulators go through LDS
   V8<TM> xv[2], zv[2];
   load_xw<TM, VEC>(g, static_cast<const TM*>(p.x), b, tl0, h, pc0, xv);

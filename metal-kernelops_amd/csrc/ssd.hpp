@@ -230,15 +230,70 @@ __global__ void __launch_bounds__(256) chunk_state(Geo g, Ptrs p, void* out_) {
   }
 }
 
+// Loads cs and step of a whole chunk into LDS (q <= 256 values each), and the column
+// decay factors ecol[s] = e^{cs_e - cs_s}, e = the last token of s's 64-token tile.
+__device__ __forceinline__ void load_chunk_cs(const Geo& g, const Ptrs& p, int64_t bh, int c, float* csc, float* dlc,
+                                              float* ecol) {
+  const int64_t so = (bh * g.nc + c) * g.q;
+  const int l = threadIdx.x;  // q <= 256
+  if (l < g.q) {
+    const float cs = p.cs[so + l];
+    csc[l] = cs;
+    dlc[l] = p.dl[so + l];
+    ecol[l] = fast_exp(p.cs[so + (l | 63)] - cs);
+  }
+}
+
+// The thread's block of K[l][s] = cb[l][s] e^{cs_l - cs_s} for rows l = 64i + r0, r0+1
+// (a, bb) and columns s = 64j + c0 .. +7, from the raw cb block (ra, rb); zero above
+// the diagonal of the diagonal tile.  Off the diagonal (i > j) the decay splits at the
+// last token e of tile j, e^{cs_l - cs_e} e^{cs_e - cs_s}: one exponential per row and
+// the column factors from ecol instead of one per element.  With a non-increasing cs
+// (A step <= 0) both factors are at most 1, and one underflows only where the whole
+// product does.  Every kernel that multiplies by K uses this routine, so the forward
+// and the backward round the same K.
+template <typename TM>
+__device__ __forceinline__ void k_block(const V8<TM>& ra, const V8<TM>& rb, const float* csc, const float* ecol, int i,
+                                        int j, int r0, int c0, float (&a)[8], float (&bb)[8]) {
+  const float cl0 = csc[64 * i + r0], cl1 = csc[64 * i + r0 + 1];
+  v8_f32(ra, a);
+  v8_f32(rb, bb);
+  if (i != j) {
+    const float ref = csc[64 * j + 63];
+    const float e0 = fast_exp(cl0 - ref), e1 = fast_exp(cl1 - ref);
+    const float4 ea = *reinterpret_cast<const float4*>(ecol + 64 * j + c0);
+    const float4 eb = *reinterpret_cast<const float4*>(ecol + 64 * j + c0 + 4);
+    const float ec[8] = {ea.x, ea.y, ea.z, ea.w, eb.x, eb.y, eb.z, eb.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      a[e] = (a[e] * ec[e]) * e0;
+      bb[e] = (bb[e] * ec[e]) * e1;
+    }
+  } else {
+    const float4 cs_a = *reinterpret_cast<const float4*>(csc + 64 * j + c0);
+    const float4 cs_b = *reinterpret_cast<const float4*>(csc + 64 * j + c0 + 4);
+    const float css[8] = {cs_a.x, cs_a.y, cs_a.z, cs_a.w, cs_b.x, cs_b.y, cs_b.z, cs_b.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      a[e] *= fast_exp(cl0 - css[e]);
+      bb[e] *= fast_exp(cl1 - css[e]);
+      if (c0 + e > r0) a[e] = 0.0f;
+      if (c0 + e > r0 + 1) bb[e] = 0.0f;
+    }
+  }
+}
+
 // Chunk output before the skip and the gate, for the 64-token tile i and d_head
 // tile pt of head (bh) in chunk c:
 //   acc[l][p] = sum_{s<=l} e^{cs_l - cs_s} CB[l][s] step_s x_s[p] + e^{cs_l} sum_n C_l[n] S_in[p][n]
-// Stages 0..i are the intra-chunk tiles, then one stage per d_state tile.  csc/dlc
-// hold the chunk's cs and step (filled by the caller, visible before the call).
+// Stages 0..i are the intra-chunk tiles, then one stage per d_state tile.  csc/dlc/ecol
+// hold the chunk's cs, step and column decay factors (load_chunk_cs, visible before the
+// call).
 // Ends with a barrier, so the caller may reuse sbuf.
 template <typename TM, bool VEC>
 __device__ __forceinline__ void chunk_out(const Geo& g, const Ptrs& p, f32x16& acc, TM (*sbuf)[2 * LdsTile<TM>::elems],
-                                          const float* csc, const float* dlc, int i, int pt, int c, int64_t bh) {
+                                          const float* csc, const float* dlc, const float* ecol, int i, int pt, int c,
+                                          int64_t bh) {
   constexpr int TE = LdsTile<TM>::elems;
   const int64_t b = bh / g.nheads, h = bh % g.nheads, gg = h / g.hpg;
   const int lane = threadIdx.x & 63;
@@ -280,23 +335,7 @@ __device__ __forceinline__ void chunk_out(const Geo& g, const Ptrs& p, f32x16& a
       put_raw<TM, false>(buf + TE, r0, c0, r.b[0], r.b[1]);  // Bt[p][n] = S_in[p][n]
     } else {
       const int j = k - g.nnt;
-      const float4 cs_a = *reinterpret_cast<const float4*>(csc + 64 * j + c0);
-      const float4 cs_b = *reinterpret_cast<const float4*>(csc + 64 * j + c0 + 4);
-      const float css[8] = {cs_a.x, cs_a.y, cs_a.z, cs_a.w, cs_b.x, cs_b.y, cs_b.z, cs_b.w};
-      v8_f32(r.a[0], a);
-      v8_f32(r.a[1], bb);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        a[e] *= fast_exp(cl0 - css[e]);
-        bb[e] *= fast_exp(cl1 - css[e]);
-      }
-      if (j == i) {  // causal mask on the diagonal tile
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          if (c0 + e > r0) a[e] = 0.0f;
-          if (c0 + e > r0 + 1) bb[e] = 0.0f;
-        }
-      }
+      k_block<TM>(r.a[0], r.a[1], csc, ecol, i, j, r0, c0, a, bb);
       put2x8<TM, false>(buf, r0, c0, a, bb);  // A[l][s] = K
       scale8(r.b[0], dlc[64 * j + r0], a);
       scale8(r.b[1], dlc[64 * j + r0 + 1], bb);
@@ -320,15 +359,6 @@ __device__ __forceinline__ void load_d8(const Geo& g, const Ptrs& p, int64_t h, 
   }
 }
 
-// Loads cs and step of a whole chunk into LDS (q <= 256 values each).
-__device__ __forceinline__ void load_chunk_cs(const Geo& g, const Ptrs& p, int64_t bh, int c, float* csc, float* dlc) {
-  const int64_t so = (bh * g.nc + c) * g.q;
-  const int l = threadIdx.x;  // q <= 256
-  if (l < g.q) {
-    csc[l] = p.cs[so + l];
-    dlc[l] = p.dl[so + l];
-  }
-}
 
 }  // namespace ssd
 }  // namespace mko

@@ -50,7 +50,7 @@ template <typename TM, bool VEC, bool SAVED>
 __global__ void __launch_bounds__(256) gate(Geo g, BwdPlan pl, Ptrs p) {
   constexpr int TE = LdsTile<TM>::elems;
   __shared__ __align__(16) TM sbuf[2][2 * TE];
-  __shared__ __align__(16) float csc[256], dlc[256];
+  __shared__ __align__(16) float csc[256], dlc[256], ecol[256];
   __shared__ float colred[4][64];
   const WgId id = wg_id(g.qb * g.npt, g.nc);
   const int i = id.x % g.qb, pt = id.x / g.qb;
@@ -75,10 +75,10 @@ __global__ void __launch_bounds__(256) gate(Geo g, BwdPlan pl, Ptrs p) {
     v8_f32(yv[0], yt[0]);
     v8_f32(yv[1], yt[1]);
   } else {
-    load_chunk_cs(g, p, bh, c, csc, dlc);
+    load_chunk_cs(g, p, bh, c, csc, dlc, ecol);
     __syncthreads();
     f32x16 acc;
-    chunk_out<TM, VEC>(g, p, acc, sbuf, csc, dlc, i, pt, c, bh);
+    chunk_out<TM, VEC>(g, p, acc, sbuf, csc, dlc, ecol, i, pt, c, bh);
     float* red = reinterpret_cast<float*>(&sbuf[0][0]);
     acc_to_lds(red, acc, wm, wn, lane);
     __syncthreads();
@@ -201,7 +201,7 @@ template <typename TM, bool VEC>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) du_kernel(Geo g, BwdPlan pl, Ptrs p) {
   constexpr int TE = LdsTile<TM>::elems;
   __shared__ __align__(16) TM sbuf[2][2 * TE];
-  __shared__ __align__(16) float csc[256], dlc[256];
+  __shared__ __align__(16) float csc[256], dlc[256], ecol[256], dcol[64];
   const int nj = (g.qb + 1) / 2;
   const WgId id = wg_id(nj * g.npt, g.nc);
   const int jx = id.x % nj, pt = id.x / nj;
@@ -212,9 +212,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) d
   int wm, wn;
   quadrant(threadIdx.x >> 6, wm, wn);
   const int r0 = blk_r0(), c0 = blk_c0();
-  load_chunk_cs(g, p, bh, c, csc, dlc);
+  load_chunk_cs(g, p, bh, c, csc, dlc, ecol);
   const int64_t tc = static_cast<int64_t>(c) * g.q;
-  const int64_t pc0 = static_cast<int64_t>(pt) * 64, pc = pc0 + c0;
+  const int64_t pc0 = static_cast<int64_t>(pt) * 64;
+  if (threadIdx.x < 64) {
+    const int64_t pp = pc0 + threadIdx.x;
+    dcol[threadIdx.x] = !p.D ? 0.0f : g.d_per_row ? (pp < g.headdim ? p.D[h * g.headdim + pp] : 0.0f) : p.D[h];
+  }
   const TM* cbt = static_cast<const TM*>(p.cb) + ((b * g.nc + c) * g.ngroups + gg) * g.q * g.q;
   const TM* Bm = static_cast<const TM*>(p.B);
   const TM* gy = static_cast<const TM*>(p.gy);
@@ -226,15 +230,16 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) d
     j = k < na ? ja : jb;
     kk = k < na ? k : k - na;
   };
+  // x of the tile in progress (for tau and the epilogue) and gy of its epilogue, issued
+  // stages ahead of their use so that waiting for them does not drain the prefetches
+  V8<TM> xv[2], gv[2];
+  load_xw<TM, VEC>(g, static_cast<const TM*>(p.x), b, tc + 64 * ja, h, pc0, xv);
   f32x16 acc;
   zero(acc);
-  __syncthreads();  // csc, dlc
+  __syncthreads();  // csc, dlc, ecol, dcol
   const float T = csc[g.q - 1];
   // x of the thread's block (rows s = r0, r0+1 of tile j) and u_s = R(dt_s x_s), the
   // rounded input of the forward's products
-  auto load_x = [&](int j, V8<TM> (&xv)[2]) {
-    load_xw<TM, VEC>(g, static_cast<const TM*>(p.x), b, tc + 64 * j, h, pc0, xv);
-  };
   auto u8 = [&](int j, const V8<TM> (&xv)[2], int rr, float (&xf)[8], float (&uf)[8]) {
     v8_f32(xv[rr], xf);
     const float d = dlc[64 * j + r0 + rr];
@@ -274,32 +279,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) d
       put_raw<TM, false>(buf + TE, r0, c0, r.b[0], r.b[1]);  // Bt[p][n] = G[p][n]
     } else {
       const int i = j + kk - g.nnt;
-      const float cl0 = csc[64 * i + r0], cl1 = csc[64 * i + r0 + 1];
-      const float4 cs_a = *reinterpret_cast<const float4*>(csc + 64 * j + c0);
-      const float4 cs_b = *reinterpret_cast<const float4*>(csc + 64 * j + c0 + 4);
-      const float css[8] = {cs_a.x, cs_a.y, cs_a.z, cs_a.w, cs_b.x, cs_b.y, cs_b.z, cs_b.w};
-      v8_f32(r.a[0], a);
-      v8_f32(r.a[1], bb);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        a[e] *= fast_exp(cl0 - css[e]);
-        bb[e] *= fast_exp(cl1 - css[e]);
-      }
-      if (i == j) {  // causal mask on the diagonal tile
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          if (c0 + e > r0) a[e] = 0.0f;
-          if (c0 + e > r0 + 1) bb[e] = 0.0f;
-        }
-      }
+      k_block<TM>(r.a[0], r.a[1], csc, ecol, i, j, r0, c0, a, bb);
       put2x8<TM, true>(buf, r0, c0, a, bb);                  // A[s][l] = K[l][s]
       put_raw<TM, true>(buf + TE, r0, c0, r.b[0], r.b[1]);  // Bt[p][l] = gy_l[p]
     }
   };
   // tau_s = u_s . du_state_s for tile j; red is the free buffer
   auto tau_snapshot = [&](int j, float* red) {
-    V8<TM> xv[2];
-    load_x(j, xv);
     acc_to_lds(red, acc, wm, wn, lane);
     __syncthreads();
     float v[2][8];
@@ -314,19 +300,18 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) d
       tau = row8_sum(tau);
       if ((threadIdx.x & 7) == 0) p.tau[po0 + 64 * j + r0 + rr] = tau;
     }
+    load_xw<TM, VEC>(g, gy, b, tc + 64 * j, h, pc0, gv);
     __syncthreads();  // red is refilled by the next stage
   };
   // dx = dt du + D gy, and the row sums x.du and u.du of tile j; red is the free buffer
   auto epilogue = [&](int j, float* red) {
-    V8<TM> gv[2], xv[2];
-    load_xw<TM, VEC>(g, gy, b, tc + 64 * j, h, pc0, gv);
-    load_x(j, xv);
-    float dv[8];
-    load_d8(g, p, h, pc, dv);
     acc_to_lds(red, acc, wm, wn, lane);
     __syncthreads();
     float du[2][8], dxo[2][8];
     lds_block(red, r0, c0, du[0], du[1]);
+    const float4 da = *reinterpret_cast<const float4*>(dcol + c0);
+    const float4 db = *reinterpret_cast<const float4*>(dcol + c0 + 4);
+    const float dv[8] = {da.x, da.y, da.z, da.w, db.x, db.y, db.z, db.w};
 #pragma unroll
     for (int rr = 0; rr < 2; ++rr) {
       float gf[8], xf[8], uf[8];
@@ -350,6 +335,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) d
       }
     }
     store_xw<TM, VEC>(g, static_cast<TM*>(p.dx), b, tc + 64 * j, h, pc0, dxo[0], dxo[1]);
+    if (j != jb) load_xw<TM, VEC>(g, static_cast<const TM*>(p.x), b, tc + 64 * jb, h, pc0, xv);
     __syncthreads();  // red is refilled by the next stage
   };
   Regs ra, rb;
@@ -421,23 +407,62 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) d
       css[hh & 1][threadIdx.x] = r.cc;
     }
   };
-  f32x16 dacc, w;
+  f32x16 dacc;
   zero(dacc);
-  zero(w);
-  Regs ra, rb;
-  pipeline2(nst, ra, rb, fetch, put, [&](int k) {
-    const int hh = k / g.npt, pt = k % g.npt;
-    mma_tile<TM>(w, sbuf[k & 1], sbuf[k & 1] + TE, wm, wn, lane, 64);
-    if (pt == g.npt - 1) {
-      const float cs_s = css[hh & 1][acc_col(wn, lane)];
+  if (i == j) {
+    // diagonal tile: per head, the product times e^{cs_l - cs_s} below the diagonal
+    f32x16 w;
+    zero(w);
+    Regs ra, rb;
+    pipeline2(nst, ra, rb, fetch, put, [&](int k) {
+      const int hh = k / g.npt, pt = k % g.npt;
+      mma_tile<TM>(w, sbuf[k & 1], sbuf[k & 1] + TE, wm, wn, lane, 64);
+      if (pt == g.npt - 1) {
+        const float cs_s = css[hh & 1][acc_col(wn, lane)];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int l = acc_row(wm, lane, r), s = acc_col(wn, lane);
-        if (i != j || s <= l) dacc[r] = fmaf(w[r], fast_exp(csr[hh & 1][l] - cs_s), dacc[r]);
+        for (int r = 0; r < 16; ++r) {
+          const int l = acc_row(wm, lane, r), s = acc_col(wn, lane);
+          if (s <= l) dacc[r] = fmaf(w[r], fast_exp(csr[hh & 1][l] - cs_s), dacc[r]);
+        }
+        zero(w);
       }
-      zero(w);
-    }
-  });
+    });
+  } else {
+    // i > j: e^{cs_l - cs_s} = e^{cs_l - cs_e} e^{cs_e - cs_s} (e = the last token of
+    // tile j, both factors at most 1 for a non-increasing cs) goes into the operands'
+    // rows, and the products of all heads accumulate in the matrix cores.
+    struct RegsO {
+      V8<TM> gm[2], xm[2];
+      float dls[2], ci[2], cj[2], ce;
+    };
+    auto fetch_o = [&](int k, RegsO& r) {
+      const int hh = k / g.npt, pt = k % g.npt;
+      const int64_t h = h0 + hh;
+      const int64_t so = ((b * g.nheads + h) * g.nc + c) * g.q;
+      load_xw<TM, VEC>(g, gy, b, tc + 64 * i, h, pt * 64, r.gm);  // gy rows l
+      load_xw<TM, VEC>(g, X, b, tc + 64 * j, h, pt * 64, r.xm);   // x rows s
+      r.dls[0] = p.dl[so + 64 * j + r0];
+      r.dls[1] = p.dl[so + 64 * j + r0 + 1];
+      r.ci[0] = p.cs[so + 64 * i + r0];
+      r.ci[1] = p.cs[so + 64 * i + r0 + 1];
+      r.cj[0] = p.cs[so + 64 * j + r0];
+      r.cj[1] = p.cs[so + 64 * j + r0 + 1];
+      r.ce = p.cs[so + 64 * j + 63];
+    };
+    auto put_o = [&](int k, RegsO& r) {
+      TM* buf = sbuf[k & 1];
+      float a[8], bb[8];
+      scale8(r.gm[0], fast_exp(r.ci[0] - r.ce), a);
+      scale8(r.gm[1], fast_exp(r.ci[1] - r.ce), bb);
+      put2x8<TM, false>(buf, r0, c0, a, bb);  // A[l][p] = e^{cs_l - cs_e} gy_l[p]
+      scale8(r.xm[0], r.dls[0] * fast_exp(r.ce - r.cj[0]), a);
+      scale8(r.xm[1], r.dls[1] * fast_exp(r.ce - r.cj[1]), bb);
+      put2x8<TM, false>(buf + TE, r0, c0, a, bb);  // Bt[s][p] = e^{cs_e - cs_s} step_s x_s[p]
+    };
+    RegsO ra, rb;
+    pipeline2(nst, ra, rb, fetch_o, put_o,
+              [&](int k) { mma_tile<TM>(dacc, sbuf[k & 1], sbuf[k & 1] + TE, wm, wn, lane, 64); });
+  }
   float* out = p.dcb + (((b * g.nc + c) * g.ngroups + gg) * pl.hb1 + hb) * g.q * g.q;
 #pragma unroll
   for (int r = 0; r < 16; ++r)

@@ -275,11 +275,20 @@ __device__ __forceinline__ void lds_block(const float* red, int r0, int c0, floa
   }
 }
 
-// Sum over the 8 lanes that share a row pair (tid%8 varies): every one of them gets it.
+// Lane exchange within rows of 16 lanes by a DPP control word (no LDS round trip).
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), kCtrl, 0xf, 0xf, false));
+}
+
+// Sum over the 8 lanes that share a row pair (tid%8 varies): every one of them gets it,
+// summed as ((v0+v1)+(v2+v3))+((v4+v5)+(v6+v7)).  DPP: quad_perm [1,0,3,2] and
+// [2,3,0,1] swap neighbours and pairs, row_half_mirror (lane 7-i of each 8) brings in
+// the other quad's sum.
 __device__ __forceinline__ float row8_sum(float v) {
-  v += __shfl_xor(v, 1);
-  v += __shfl_xor(v, 2);
-  v += __shfl_xor(v, 4);
+  v += dpp_f32<0xb1>(v);
+  v += dpp_f32<0x4e>(v);
+  v += dpp_f32<0x141>(v);
   return v;
 }
 
