@@ -126,7 +126,7 @@ template <typename TM, bool VEC>
 __global__ void __launch_bounds__(256) chunk_scan(Geo g, Ptrs p) {
   constexpr int TE = LdsTile<TM>::elems;
   __shared__ __align__(16) TM sbuf[2][2 * TE];
-  __shared__ __align__(16) float csc[256], dlc[256], ecol[256];
+  __shared__ __align__(16) float csc[256], dlc[256], ecol[256], dcol[64];
   const WgId id = wg_id(g.qb * g.npt, g.nc);
   const int i = id.x % g.qb, pt = id.x / g.qb;
   const int c = id.y;
@@ -137,37 +137,40 @@ __global__ void __launch_bounds__(256) chunk_scan(Geo g, Ptrs p) {
   const int r0 = blk_r0(), c0 = blk_c0();
   const int64_t tl0 = static_cast<int64_t>(c) * g.q + 64 * i, pc0 = static_cast<int64_t>(pt) * 64;
   load_chunk_cs(g, p, bh, c, csc, dlc, ecol);
+  if (threadIdx.x < 64) {
+    const int64_t pp = pc0 + threadIdx.x;
+    dcol[threadIdx.x] = !p.D ? 0.0f : g.d_per_row ? (pp < g.headdim ? p.D[h * g.headdim + pp] : 0.0f) : p.D[h];
+  }
   __syncthreads();
   f32x16 acc;
-  chunk_out<TM, VEC>(g, p, acc, sbuf, csc, dlc, ecol, i, pt, c, bh);
-  // epilogue inputs, loaded while the accumulators go through LDS
-  V8<TM> xv[2], zv[2];
-  load_xw<TM, VEC>(g, static_cast<const TM*>(p.x), b, tl0, h, pc0, xv);
-  if (p.z) load_xw<TM, VEC>(g, static_cast<const TM*>(p.z), b, tl0, h, pc0, zv);
-  float dv[8];
-  load_d8(g, p, h, pc0 + c0, dv);
-  // epilogue through LDS: each thread owns rows r0, r0+1 and 8 consecutive d_head columns
-  float* red = reinterpret_cast<float*>(&sbuf[0][0]);
-  acc_to_lds(red, acc, wm, wn, lane);
-  __syncthreads();
-  float v[2][8];
-  lds_block(red, r0, c0, v[0], v[1]);
-  if (p.yt) store_xw<float, VEC>(g, p.yt, b, tl0, h, pc0, v[0], v[1]);
-  const int64_t pc = pc0 + c0;
+  // epilogue through LDS: each thread owns rows r0, r0+1 and 8 consecutive d_head columns;
+  // x and z of the block come from the pipeline's last loads
+  chunk_out<TM, VEC, true>(g, p, acc, sbuf, csc, dlc, ecol, i, pt, c, bh,
+                           [&](const V8<TM> (&xv)[2], const V8<TM> (&zv)[2]) {
+    float* red = reinterpret_cast<float*>(&sbuf[0][0]);
+    acc_to_lds(red, acc, wm, wn, lane);
+    __syncthreads();
+    float v[2][8];
+    lds_block(red, r0, c0, v[0], v[1]);
+    const float4 da = *reinterpret_cast<const float4*>(dcol + c0);
+    const float4 db = *reinterpret_cast<const float4*>(dcol + c0 + 4);
+    const float dv[8] = {da.x, da.y, da.z, da.w, db.x, db.y, db.z, db.w};
+    if (p.yt) store_xw<float, VEC>(g, p.yt, b, tl0, h, pc0, v[0], v[1]);
 #pragma unroll
-  for (int rr = 0; rr < 2; ++rr) {
-    float xf[8], zf[8];
-    v8_f32(xv[rr], xf);
-    if (p.z) v8_f32(zv[rr], zf);
+    for (int rr = 0; rr < 2; ++rr) {
+      float xf[8], zf[8];
+      v8_f32(xv[rr], xf);
+      if (p.z) v8_f32(zv[rr], zf);
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      float y = v[rr][k];
-      y = fmaf(dv[k], xf[k], y);
-      if (p.z) y *= zf[k] * sigmoid(zf[k]);
-      v[rr][k] = y;
+      for (int k = 0; k < 8; ++k) {
+        float y = v[rr][k];
+        y = fmaf(dv[k], xf[k], y);
+        if (p.z) y *= zf[k] * sigmoid(zf[k]);
+        v[rr][k] = y;
+      }
     }
-  }
-  store_xw<TM, VEC>(g, static_cast<TM*>(p.y), b, tl0, h, pc0, v[0], v[1]);
+    store_xw<TM, VEC>(g, static_cast<TM*>(p.y), b, tl0, h, pc0, v[0], v[1]);
+  });
 }
 
 // ---------------------------------------------------------------- host

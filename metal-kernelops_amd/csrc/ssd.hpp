@@ -289,11 +289,17 @@ __device__ __forceinline__ void k_block(const V8<TM>& ra, const V8<TM>& rb, cons
 // Stages 0..i are the intra-chunk tiles, then one stage per d_state tile.  csc/dlc/ecol
 // hold the chunk's cs, step and column decay factors (load_chunk_cs, visible before the
 // call).
-// Ends with a barrier, so the caller may reuse sbuf.
-template <typename TM, bool VEC>
+// Ends with a barrier, so the caller may reuse sbuf.  With EPI the fetches past the last
+// stage load the epilogue's inputs instead, x rows l and z rows l (x again without z), so
+// that they arrive during the products, and epi(x, z) runs after that barrier.
+struct NoEpi {
+  template <class V>
+  __device__ void operator()(const V&, const V&) const {}
+};
+template <typename TM, bool VEC, bool EPI = false, class Epi = NoEpi>
 __device__ __forceinline__ void chunk_out(const Geo& g, const Ptrs& p, f32x16& acc, TM (*sbuf)[2 * LdsTile<TM>::elems],
                                           const float* csc, const float* dlc, const float* ecol, int i, int pt, int c,
-                                          int64_t bh) {
+                                          int64_t bh, Epi&& epi = NoEpi{}) {
   constexpr int TE = LdsTile<TM>::elems;
   const int64_t b = bh / g.nheads, h = bh % g.nheads, gg = h / g.hpg;
   const int lane = threadIdx.x & 63;
@@ -315,8 +321,12 @@ __device__ __forceinline__ void chunk_out(const Geo& g, const Ptrs& p, f32x16& a
   struct Regs {
     V8<TM> a[2], b[2];
   };
+  const int n = g.nnt + i + 1;
   auto fetch = [&](int k, Regs& r) {
-    if (k < g.nnt) {
+    if (EPI && k == n) {
+      load_xw<TM, VEC>(g, X, b, tc + 64 * i, h, pc0, r.a);                                   // x rows l
+      load_xw<TM, VEC>(g, p.z ? static_cast<const TM*>(p.z) : X, b, tc + 64 * i, h, pc0, r.b);  // z rows l
+    } else if (k < g.nnt) {
       load_bw<TM, VEC>(g, Cm, b, tc + 64 * i, gg, 64 * k, r.a);  // C rows l
       load_sw<TM, VEC>(g, S, pc0, 64 * k, r.b);                  // S rows p
     } else {
@@ -344,9 +354,16 @@ __device__ __forceinline__ void chunk_out(const Geo& g, const Ptrs& p, f32x16& a
   };
   zero(acc);
   Regs ra, rb;
-  pipeline2(g.nnt + i + 1, ra, rb, fetch, put,
-            [&](int k) { mma_tile<TM>(acc, sbuf[k & 1], sbuf[k & 1] + TE, wm, wn, lane, 64); });
-  __syncthreads();
+  auto mma = [&](int k) { mma_tile<TM>(acc, sbuf[k & 1], sbuf[k & 1] + TE, wm, wn, lane, 64); };
+  if constexpr (EPI) {
+    pipeline2e(n, ra, rb, fetch, put, mma, [&](const Regs& r) {
+      __syncthreads();
+      epi(r.a, r.b);
+    });
+  } else {
+    pipeline2(n, ra, rb, fetch, put, mma);
+    __syncthreads();
+  }
 }
 
 // The skip weights D of the thread's 8 d_head columns (zero without D).

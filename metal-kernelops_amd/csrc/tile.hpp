@@ -265,6 +265,35 @@ __device__ __forceinline__ void pipeline2(int n, Regs& ra, Regs& rb, Fetch&& fet
   }
 }
 
+// As pipeline2, but the fetches past the last stage load stage n -- the epilogue's
+// inputs -- instead of repeating stage n-1, and epi(regs) is called at the end with the
+// set that holds them (even n: both do; odd n: rb).  Two call sites instead of a select
+// keep both sets in registers.
+template <class Regs, class Fetch, class Put, class Mma, class Epi>
+__device__ __forceinline__ void pipeline2e(int n, Regs& ra, Regs& rb, Fetch&& fetch, Put&& put, Mma&& mma, Epi&& epi) {
+  fetch(0, ra);
+  fetch(1 < n ? 1 : n, rb);
+  int k = 0;
+  for (; k + 1 < n; k += 2) {
+    put(k, ra);
+    __syncthreads();
+    fetch(k + 2 < n ? k + 2 : n, ra);
+    mma(k);
+    put(k + 1, rb);
+    __syncthreads();
+    fetch(k + 3 < n ? k + 3 : n, rb);
+    mma(k + 1);
+  }
+  if (k < n) {
+    put(k, ra);
+    __syncthreads();
+    mma(k);
+    epi(rb);
+  } else {
+    epi(ra);
+  }
+}
+
 // Reads the thread's block back from a 64x65 fp32 LDS tile written in the accumulator
 // layout (acc_to_lds): a = row r0, b = row r0+1.
 __device__ __forceinline__ void lds_block(const float* red, int r0, int c0, float (&a)[8], float (&b)[8]) {
