@@ -15,7 +15,8 @@ bytes per launch over its average launch time, both measured live with HIP event
 recorded by libmko on the kernel's own stream.  ``cpu_baseline`` times the float64
 oracle's restatement (run in float32 with autograd) on a bounded sample on this
 host.  ``also`` carries the other workloads of the path (Mamba-1 130M layer,
-Mamba-2 decode, Mamba-2 SSD chunk scan when present) with their own rooflines.
+Mamba-2 decode, Mamba-2 SSD chunk scan, the four-path 2D scan) with their own
+rooflines.
 """
 
 from __future__ import annotations
@@ -325,6 +326,81 @@ def ssd_cpu_baseline(batch=4, length=4096):
                       f"{best:.2f} s"}
 
 
+# --------------------------------------------------------------------- ss2d
+
+SS2D_SHAPE = (1, 96, 1, 16, 56, 56)  # batch, channels, groups, states, height, width (b1_d96_56x56)
+
+
+def ss2d_bytes(batch, channels, groups, states, height, width):
+    """Algorithmic bytes (fwd, bwd) of one four-path scan step, float32 throughout."""
+    e = batch * channels * height * width
+    bc = batch * groups * states * height * width
+    return 4 * (3 * e + 2 * bc), 4 * (5 * e + 4 * bc)  # u, dt, out / u, dt, dy, du, ddt; B, C (+ dB, dC)
+
+
+def ss2d_inputs(shape, seed=101):
+    batch, channels, groups, states, height, width = shape
+    g = torch.Generator().manual_seed(seed)
+    dims = (batch, channels, height, width)
+    return {"u": torch.randn(dims, generator=g), "dt": torch.rand(dims, generator=g) * 0.2 + 0.05,
+            "A": -(torch.rand((channels, states), generator=g) + 0.1),
+            "B": torch.randn((batch, groups, states, height, width), generator=g),
+            "C": torch.randn((batch, groups, states, height, width), generator=g)}, torch.randn(dims, generator=g)
+
+
+def ss2d_case(steps, warmup, shape=SS2D_SHAPE):
+    from metal_kernelops.cv import ss2d_scan
+    inputs, dy = ss2d_inputs(shape)
+    dev = torch.device("cuda")
+    leaves = {k: v.to(dev).requires_grad_(True) for k, v in inputs.items()}
+    dy = dy.to(dev)
+    order = list(leaves.values())
+
+    def step():
+        out = ss2d_scan(**leaves)
+        torch.autograd.grad(out, order, dy)
+
+    ms, wall, kernels = timed(step, steps, warmup)
+    fwd_b, bwd_b = ss2d_bytes(*shape)
+    name, avg, count = dominant(kernels)
+    per_kernel = {"selscan_bwd_main": bwd_b, "selscan_fwd_replay": fwd_b}
+    roof = roofline(per_kernel.get(name, fwd_b + bwd_b), avg)
+    roof["kernel"] = name
+    roof["algorithmic_bytes"] = per_kernel.get(name, fwd_b + bwd_b)
+    del leaves, dy
+    torch.cuda.empty_cache()
+    return {"ms_per_step": ms, "wall_ms_per_step": wall, "gbs": (fwd_b + bwd_b) / (ms * 1e-3) / 1e9,
+            "bytes_per_step": fwd_b + bwd_b, "roofline": roof,
+            "kernels_ms": {k: round(v[0] / max(v[1], 1), 4) for k, v in sorted(kernels.items())}}
+
+
+def ss2d_cpu_baseline(shape=(1, 96, 1, 16, 28, 28)):
+    """The oracle's four-path restatement in float32 with autograd on the host cores.
+
+    A bounded sample: the GPU workload's channels and states on a 28 x 28 map (a
+    quarter of its steps), so one run stays near 6 s.
+    """
+    import oracle
+    torch.set_num_threads(os.cpu_count() or 1)
+    inputs, dy = ss2d_inputs(shape)
+    leaves = {k: v.requires_grad_(True) for k, v in inputs.items()}
+
+    def run():
+        out = oracle.ss2d_scan(**leaves, dtype=torch.float32)
+        torch.autograd.grad(out, list(leaves.values()), dy)
+
+    run()
+    t0 = time.perf_counter()
+    run()
+    best = time.perf_counter() - t0
+    fwd_b, bwd_b = ss2d_bytes(*shape)
+    return {"value": round((fwd_b + bwd_b) / best / 1e9, 6), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"ss2d fwd+bwd at {shape} (batch, channels, groups, states, H, W), float32 per-step "
+                      f"recurrence over the four paths with autograd (oracle/ssm.py), one run after 1 warm-up: "
+                      f"{best:.2f} s"}
+
+
 # --------------------------------------------------------------------- main
 
 
@@ -334,7 +410,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-cpu", action="store_true", help="skip the CPU baseline legs")
-    ap.add_argument("--only", choices=["mamba1", "ssd", "decode", "all"], default="all",
+    ap.add_argument("--only", choices=["mamba1", "ssd", "decode", "ss2d", "all"], default="all",
                     help="one workload (mamba1 = the config-3 headline alone) or all of them")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -387,6 +463,15 @@ def main():
                        "state_dtype": "f32", "io_dtype": "bf16"},
             "roofline": dec["roofline"], "kernels_ms": dec["kernels_ms"]}
         log(f"  {dec['ms_per_step'] * 1e3:.1f} us/step, {dec['state_rmw_gbs']:.1f} GB/s state RMW")
+    if want("ss2d"):
+        log(f"ss2d four-path scan {SS2D_SHAPE} (batch, channels, groups, states, H, W) fwd+bwd, float32")
+        s2 = ss2d_case(args.steps, args.warmup)
+        also["ss2d_four_path_scan_fwd_bwd"] = {
+            "value": round(s2["gbs"], 1), "unit": "GB/s", "ms_per_step": round(s2["ms_per_step"], 4),
+            "config": dict(zip(("batch", "channels", "groups", "states", "height", "width"), SS2D_SHAPE),
+                           dtype="f32"),
+            "roofline": s2["roofline"], "kernels_ms": s2["kernels_ms"]}
+        log(f"  {s2['ms_per_step']:.3f} ms/step, {s2['gbs']:.1f} GB/s; kernels {s2['kernels_ms']}")
     if head is None:  # a single non-headline workload: print its own record
         print(json.dumps(also), flush=True)
         return
@@ -399,6 +484,8 @@ def main():
             also["mamba2_decode_state_rmw"]["cpu_baseline"] = decode_cpu_baseline()
         if "mamba2_ssd_chunk_scan_fwd_bwd" in also:
             also["mamba2_ssd_chunk_scan_fwd_bwd"]["cpu_baseline"] = ssd_cpu_baseline()
+        if "ss2d_four_path_scan_fwd_bwd" in also:
+            also["ss2d_four_path_scan_fwd_bwd"]["cpu_baseline"] = ss2d_cpu_baseline()
     line = {
         "metric": METRIC,
         "value": round(head["gbs"], 1),

@@ -47,6 +47,7 @@ const char* mko_last_error(void);
 size_t mko_sizeof_selscan_params(void);
 size_t mko_sizeof_state_update_params(void);
 size_t mko_sizeof_ssd_params(void);
+size_t mko_sizeof_path_params(void);
 
 /* Kernel timing (observability).  While enabled, every kernel the library
  * launches is bracketed by HIP events on its launch stream; the per-kernel totals
@@ -231,6 +232,39 @@ int mko_ssd_fwd(const mko_ssd_params* p, void* stream);
  * hand-written SSD backward): gradients of every differentiable input. */
 size_t mko_ssd_bwd_workspace_size(const mko_ssd_params* p);
 int mko_ssd_bwd(const mko_ssd_params* p, void* stream);
+
+/* ======================================================================== */
+/* Four-path 2D scan layout (VMamba's ss2d, cv/path_scan.py)                  */
+/* ======================================================================== */
+
+/* A (batch, rows, height, width) map is read along four paths; path k visits pixel
+ * pos_k(i) at step i of L = height * width:
+ *   k = 0: i      k = 1: (i % height) * width + i / height (down each column)
+ *   k = 2: L-1-i  k = 3: pos_1(L-1-i)
+ * rows is the channel count of u/dt/dy, or groups * dstate of B/C.  The 2D scan is
+ * the Mamba-1 scan (mko_selscan_fwd/bwd) over the stacked layout, with dim and
+ * ngroups four times the map's. */
+typedef struct mko_path_params {
+  const void* src;
+  void* dst;
+  int64_t batch, rows, height, width;
+  int32_t dtype; /* of src and dst */
+  float scale;   /* multiplies every output */
+} mko_path_params;
+
+/* src (batch, rows, L) -> dst (batch, 4 * rows, L):
+ *   dst[b][k * rows + r][i] = scale * src[b][r][pos_k(i)].
+ * Replaces _stack_spatial / _stack_groups (cv/path_scan.py:165-188), with the state
+ * transpose of the Metal transpose_states kernel (:267-282) left to the scan's own
+ * layout pass. */
+int mko_path_stack(const mko_path_params* p, void* stream);
+
+/* src (batch, 4 * rows, L) in step order -> dst (batch, rows, L) per pixel:
+ *   dst[b][r][pix] = scale * ((s0 + s2) + (s1 + s3)), s_k = src[b][k * rows + r][step_k(pix)]
+ * with step_k the inverse of pos_k.  Replaces merge_paths (cv/path_scan.py:380-404),
+ * in its permuting form; the reference's forward merges per-pixel slices, this
+ * build's forward merges step-ordered ones like its backward. */
+int mko_path_merge(const mko_path_params* p, void* stream);
 
 #ifdef __cplusplus
 }

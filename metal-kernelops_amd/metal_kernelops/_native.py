@@ -76,12 +76,25 @@ class SsdParams(ctypes.Structure):
     ]
 
 
+class PathParams(ctypes.Structure):
+    """Mirror of ``mko_path_params``."""
+
+    _fields_ = [
+        ("src", _vp), ("dst", _vp),
+        ("batch", ctypes.c_int64), ("rows", ctypes.c_int64), ("height", ctypes.c_int64),
+        ("width", ctypes.c_int64), ("dtype", ctypes.c_int32), ("scale", ctypes.c_float),
+    ]
+
+
 _SIGNATURES = {
     "mko_abi_version": ([], ctypes.c_int),
     "mko_last_error": ([], ctypes.c_char_p),
     "mko_sizeof_selscan_params": ([], ctypes.c_size_t),
     "mko_sizeof_state_update_params": ([], ctypes.c_size_t),
     "mko_sizeof_ssd_params": ([], ctypes.c_size_t),
+    "mko_sizeof_path_params": ([], ctypes.c_size_t),
+    "mko_path_stack": ([ctypes.POINTER(PathParams), _vp], ctypes.c_int),
+    "mko_path_merge": ([ctypes.POINTER(PathParams), _vp], ctypes.c_int),
     "mko_ssd_saved_bytes": ([ctypes.POINTER(SsdParams)], ctypes.c_size_t),
     "mko_ssd_fwd_workspace_size": ([ctypes.POINTER(SsdParams)], ctypes.c_size_t),
     "mko_ssd_fwd": ([ctypes.POINTER(SsdParams), _vp], ctypes.c_int),
@@ -129,7 +142,8 @@ def lib():
             raise RuntimeError(f"libmko.so ABI version {version}, this binding expects {ABI_VERSION}")
         for struct, fn in ((SelscanParams, handle.mko_sizeof_selscan_params),
                            (StateUpdateParams, handle.mko_sizeof_state_update_params),
-                           (SsdParams, handle.mko_sizeof_ssd_params)):
+                           (SsdParams, handle.mko_sizeof_ssd_params),
+                           (PathParams, handle.mko_sizeof_path_params)):
             if ctypes.sizeof(struct) != fn():
                 raise RuntimeError(f"{struct.__name__} layout does not match libmko.so")
         _lib = handle

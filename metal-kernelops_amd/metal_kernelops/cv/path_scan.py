@@ -1,0 +1,262 @@
+"""Four-path 2D selective scan (VMamba's ``ss2d``) on MI355X.
+
+Public surface, as in dbydd/metal-kernelops ``cv/path_scan.py:94-639``:
+``ss2d_scan(u, dt, A, B, C, merge="sum")``, ``ss2d_scan_reference``,
+``path_orders``, ``MERGE_MODES``, ``MAX_STATES``.
+
+A ``(batch, channels, height, width)`` map is traversed along four paths (row-major,
+column-major, and their reverses; ``path_orders``), each path is the Mamba-1 scan
+``x_t = exp(dt_t A) x_{t-1} + dt_t B_t u_t``, ``y_t = <C_t, x_t>`` with zero initial
+state and no skip, gate or bias, and the four results are added at every pixel
+(``merge="mean"`` divides by four).
+
+How it runs: the four paths of every channel are one Mamba-1 problem with four times
+the channels and groups.  ``mko::path_stack`` (a HIP gather) writes u, dt, B and C in
+path-step order, ``mko::selscan_fwd`` scans the stacked rows with the same kernels as
+``selective_scan``, and ``mko::path_merge`` (a HIP gather) adds the four step-ordered
+slices back per pixel in the reference's ``(0 + 2) + (1 + 3)`` order.  The backward
+re-stacks the inputs and the output gradient, runs ``mko::selscan_bwd`` on the stacked
+problem, and folds du, ddt, dB and dC back with ``path_merge``; dA sums the four
+paths.  The reference stacks for its backward in the same way (``:477-543``) and
+walks the paths with a cursor in its forward; here both directions share the 1-D
+scan's kernels and their deterministic dB/dC reductions.
+
+Differences from the reference, all widenings: tensors live on the ROCm GPU (the
+reference runs on MPS only); u, B and C may also be float16 or bfloat16 (computed in
+float32, dt taken as float32), and gradients come back in each input's dtype.
+``states`` is limited to 32 as in the reference (``:97``), here by the scan kernels'
+register budget.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+from torch import Tensor
+
+from .. import _native as nat
+from ..scan import _require_gpu
+
+__all__ = ["MAX_STATES", "MERGE_MODES", "path_orders", "ss2d_scan", "ss2d_scan_reference"]
+
+MERGE_MODES = ("sum", "mean")
+"""How the four path outputs combine: elementwise sum, or their mean."""
+
+MAX_STATES = 32
+"""Largest state axis the scan kernels carry (``dstate <= 32``)."""
+
+_FLOATS = (torch.float32, torch.float16, torch.bfloat16)
+
+
+def _check_merge(merge):
+    if merge not in MERGE_MODES:
+        raise ValueError(f"merge must be one of {MERGE_MODES}, got {merge!r}")
+
+
+def _shape_contract(u, dt, A, B, C, where):
+    """Validate the shared shape contract (``cv/path_scan.py:116-150``); returns the sizes."""
+    if u.dim() != 4:
+        raise ValueError(f"{where}: u must be (batch, channels, height, width), got {tuple(u.shape)}")
+    batch, channels, height, width = u.shape
+    if dt.shape != u.shape:
+        raise ValueError(f"{where}: dt {tuple(dt.shape)} != u {tuple(u.shape)}")
+    if A.dim() != 2:
+        raise ValueError(f"{where}: A must be (channels, states), got {tuple(A.shape)}")
+    if A.shape[0] != channels:
+        raise ValueError(f"{where}: A has {A.shape[0]} rows for {channels} channels")
+    if B.dim() != 5:
+        raise ValueError(f"{where}: B must be (batch, groups, states, height, width), got {tuple(B.shape)}")
+    if C.shape != B.shape:
+        raise ValueError(f"{where}: C {tuple(C.shape)} != B {tuple(B.shape)}")
+    if B.shape[0] != batch:
+        raise ValueError(f"{where}: B batch {B.shape[0]} != u batch {batch}")
+    if B.shape[2] != A.shape[1]:
+        raise ValueError(f"{where}: B has {B.shape[2]} states, A has {A.shape[1]}")
+    if tuple(B.shape[3:]) != (height, width):
+        raise ValueError(f"{where}: B spatial {tuple(B.shape[3:])} != {(height, width)}")
+    groups = B.shape[1]
+    if channels and groups < 1:
+        raise ValueError(f"{where}: {channels} channels need at least one group")
+    if groups and channels % groups:
+        raise ValueError(f"{where}: {channels} channels do not divide into {groups} groups; "
+                         f"a channel would map to no group")
+    return batch, channels, groups, A.shape[1], height, width
+
+
+def path_orders(height, width, device=None):
+    """Spatial index order of each of the four scan paths, as a list of tensors.
+
+    Entry ``p[i]`` of path ``k`` is the flat ``h * width + w`` index of the pixel at
+    step ``i``; paths 2 and 3 are the reverses of paths 0 and 1 (``:153-162``).
+    """
+    row_major = torch.arange(height * width, device=device).reshape(height, width)
+    flat = row_major.reshape(-1)
+    column_major = row_major.transpose(0, 1).reshape(-1)
+    return [flat, column_major, flat.flip(0), column_major.flip(0)]
+
+
+def _zero_result(shape, tensors):
+    """A zero result that still carries the gradient graph of ``tensors`` (``:191-197``)."""
+    zero = tensors[0].sum() * 0
+    for tensor in tensors[1:]:
+        zero = zero + tensor.sum() * 0
+    return tensors[0].new_zeros(shape) + zero
+
+
+# --------------------------------------------------------------------------- layout ops
+
+
+def _path_call(fn, x, out, height, width, scale):
+    p = nat.PathParams()
+    p.src, p.dst = x.data_ptr(), out.data_ptr()
+    p.batch, p.height, p.width = x.shape[0], height, width
+    p.rows = out.shape[1] if fn == "mko_path_merge" else x.shape[1]
+    p.dtype, p.scale = nat.code(x.dtype), float(scale)
+    lib = nat.lib()
+    nat.check(getattr(lib, fn)(ctypes.byref(p), nat.stream_of(x.device)), fn)
+
+
+@torch.library.custom_op("mko::path_stack", mutates_args=(), device_types="cuda")
+def _path_stack(x: Tensor, height: int, width: int, scale: float) -> Tensor:
+    """(batch, rows, H*W) -> (batch, 4 rows, H*W): the four paths in step order."""
+    out = x.new_empty(x.shape[0], 4 * x.shape[1], x.shape[2])
+    if out.numel():
+        _path_call("mko_path_stack", x, out, height, width, scale)
+    return out
+
+
+@_path_stack.register_fake
+def _(x, height, width, scale):
+    return x.new_empty(x.shape[0], 4 * x.shape[1], x.shape[2])
+
+
+@torch.library.custom_op("mko::path_merge", mutates_args=(), device_types="cuda")
+def _path_merge(x: Tensor, height: int, width: int, scale: float) -> Tensor:
+    """(batch, 4 rows, H*W) in step order -> (batch, rows, H*W) per pixel."""
+    out = x.new_empty(x.shape[0], x.shape[1] // 4, x.shape[2])
+    if out.numel():
+        _path_call("mko_path_merge", x, out, height, width, scale)
+    return out
+
+
+@_path_merge.register_fake
+def _(x, height, width, scale):
+    return x.new_empty(x.shape[0], x.shape[1] // 4, x.shape[2])
+
+
+def _stacked(u, dt, A, B, C):
+    """The four-path problem as one Mamba-1 problem: (b, 4C, L), (4C, N), (b, 4G, N, L)."""
+    batch, channels, height, width = u.shape
+    groups, states = B.shape[1], A.shape[1]
+    length = height * width
+    stack = torch.ops.mko.path_stack
+    su = stack(u.reshape(batch, channels, length), height, width, 1.0)
+    sdt = stack(dt.reshape(batch, channels, length), height, width, 1.0)
+    sb = stack(B.reshape(batch, groups * states, length), height, width, 1.0)
+    sc = stack(C.reshape(batch, groups * states, length), height, width, 1.0)
+    shape = (batch, 4 * groups, states, length)
+    return su, sdt, A.repeat(4, 1).contiguous(), sb.view(shape), sc.view(shape)
+
+
+class _PathScan(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, u, dt, A, B, C, scale):
+        batch, channels, height, width = u.shape
+        su, sdt, sa, sb, sc = _stacked(u, dt, A, B, C)
+        ys, ck = torch.ops.mko.selscan_fwd(su, sdt, sa, sb, sc, None, None, None, False)
+        out = torch.ops.mko.path_merge(ys, height, width, scale)
+        ctx.scale = scale
+        ctx.save_for_backward(u, dt, A, B, C, ck)
+        return out.view(batch, channels, height, width)
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, dy):
+        u, dt, A, B, C, ck = ctx.saved_tensors
+        batch, channels, height, width = u.shape
+        groups, states = B.shape[1], A.shape[1]
+        length = height * width
+        su, sdt, sa, sb, sc = _stacked(u, dt, A, B, C)
+        sdy = torch.ops.mko.path_stack(dy.to(u.dtype).contiguous().reshape(batch, channels, length),
+                                       height, width, ctx.scale)
+        dus, ddts, das, dbs, dcs, _, _, _ = torch.ops.mko.selscan_bwd(
+            sdy, su, sdt, sa, sb, sc, None, None, None, False, ck)
+        merge = torch.ops.mko.path_merge
+        du = merge(dus, height, width, 1.0).view(batch, channels, height, width)
+        ddt = merge(ddts, height, width, 1.0).view(batch, channels, height, width)
+        rows = (batch, 4 * groups * states, length)
+        dB = merge(dbs.reshape(rows), height, width, 1.0).view(batch, groups, states, height, width)
+        dC = merge(dcs.reshape(rows), height, width, 1.0).view(batch, groups, states, height, width)
+        dA = das.view(4, channels, states).sum(0)
+        return du, ddt, dA, dB, dC, None
+
+
+def ss2d_scan(u, dt, A, B, C, merge="sum"):
+    """Four-path 2D selective scan on the ROCm GPU.
+
+    Args:
+        u, dt: (batch, channels, height, width)
+        A: (channels, states), negative; states <= 32
+        B, C: (batch, groups, states, height, width), groups dividing channels
+        merge: ``"sum"`` adds the four path outputs, ``"mean"`` divides by four.
+
+    Returns:
+        (batch, channels, height, width), contiguous, in u's dtype.  Strided inputs are
+        accepted (copied to their dense layout first), as in ``cv/path_scan.py:546-576``.
+    """
+    _check_merge(merge)
+    batch, channels, groups, states, height, width = _shape_contract(u, dt, A, B, C, "ss2d_scan")
+    for name, tensor in (("u", u), ("dt", dt), ("A", A), ("B", B), ("C", C)):
+        _require_gpu(tensor)
+        if tensor.dtype not in _FLOATS:
+            raise ValueError(f"ss2d_scan takes float32, float16 or bfloat16, {name} is {tensor.dtype}")
+        if tensor.device != u.device:
+            raise ValueError(f"ss2d_scan: {name} is on {tensor.device}, u is on {u.device}")
+    if states > MAX_STATES:
+        raise ValueError(f"ss2d_scan carries at most {MAX_STATES} states, got {states}")
+    if u.numel() == 0 or B.numel() == 0:
+        return _zero_result((batch, channels, height, width), (u, dt, A, B, C))
+    # the scan kernels take float32 step sizes and decays, and B and C of one dtype;
+    # autograd casts each gradient back to its input's dtype
+    dt = dt.float() if dt.dtype != torch.float32 else dt
+    A = A.float() if A.dtype != torch.float32 else A
+    if B.dtype != C.dtype:
+        B, C = B.float(), C.float()
+    u, dt, A, B, C = (t.contiguous() for t in (u, dt, A, B, C))
+    return _PathScan.apply(u, dt, A, B, C, 0.25 if merge == "mean" else 1.0)
+
+
+def ss2d_scan_reference(u, dt, A, B, C, merge="sum"):
+    """Pure-torch twin of :func:`ss2d_scan` on any device and dtype (``:608-639``).
+
+    Built from index lists rather than views: the four paths are gathered with
+    ``path_orders`` into one stacked problem of four times the channels and groups,
+    scanned step by step with :func:`metal_kernelops.reference.selective_scan`, and
+    each path is scattered back with its inverse order, so it also checks the GPU
+    path's permutations.
+    """
+    from ..reference import selective_scan as reference_scan
+
+    _check_merge(merge)
+    batch, channels, groups, states, height, width = _shape_contract(u, dt, A, B, C, "ss2d_scan_reference")
+    if u.numel() == 0 or B.numel() == 0:
+        return _zero_result((batch, channels, height, width), (u, dt, A, B, C))
+    length = height * width
+    orders = path_orders(height, width, u.device)
+
+    def stacked(x, rows):
+        flat = x.reshape(batch, rows, length)
+        return torch.cat([flat.index_select(-1, order) for order in orders], dim=1)
+
+    bc_shape = (batch, 4 * groups, states, length)
+    steps = reference_scan(stacked(u, channels), stacked(dt, channels), A.repeat(4, 1),
+                           stacked(B, groups * states).view(bc_shape),
+                           stacked(C, groups * states).view(bc_shape))
+    paths = steps.view(batch, 4, channels, length)
+    # path k stands on pixel orders[k][i] at step i; argsort inverts that map
+    back = [paths[:, k].index_select(-1, torch.argsort(order)) for k, order in enumerate(orders)]
+    total = (back[0] + back[2]) + (back[1] + back[3])
+    if merge == "mean":
+        total = total * 0.25
+    return total.reshape(batch, channels, height, width)

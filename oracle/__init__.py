@@ -19,5 +19,7 @@ from .ssm import (  # noqa: F401
     selective_scan,
     selective_scan_loop,
     softplus,
+    ss2d_path_orders,
+    ss2d_scan,
     ssd_minimal_discrete,
 )

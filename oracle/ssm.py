@@ -99,6 +99,48 @@ def selective_scan(u, dt, A, B, C, D=None, z=None, delta_bias=None,
     return y
 
 
+def ss2d_path_orders(height, width):
+    """The four traversal orders of an ``height x width`` map as Python lists.
+
+    Entry ``i`` of path ``k`` is the flat ``h * width + w`` pixel visited at step ``i``:
+    row-major, column-major (down each column, columns left to right), and the two
+    reversed (``cv/path_scan.py:9-22, 153-162``).
+    """
+    row = [h * width + w for h in range(height) for w in range(width)]
+    col = [h * width + w for w in range(width) for h in range(height)]
+    return [row, col, row[::-1], col[::-1]]
+
+
+def ss2d_scan(u, dt, A, B, C, merge="sum", dtype=F64):
+    """Four-path 2D selective scan (VMamba's ss2d), differentiable.
+
+    Restates ``cv/path_scan.py:579-639``: each path of :func:`ss2d_path_orders` is the
+    Mamba-1 recurrence (:func:`selective_scan`, zero state, no skip/gate/bias) over the
+    pixels in that order; the path outputs are written back at the pixels they were
+    computed for and added as ``(p0 + p2) + (p1 + p3)``, times 1/4 for ``"mean"``.
+
+    Shapes: ``u, dt`` (b, C, H, W); ``A`` (C, N); ``B, C`` (b, G, N, H, W).
+    """
+    batch, channels, height, width = u.shape
+    groups, states = B.shape[1], B.shape[2]
+    length = height * width
+    uf = u.to(dtype).reshape(batch, channels, length)
+    df = dt.to(dtype).reshape(batch, channels, length)
+    bf = B.to(dtype).reshape(batch, groups, states, length)
+    cf = C.to(dtype).reshape(batch, groups, states, length)
+    paths = []
+    for order in ss2d_path_orders(height, width):
+        idx = torch.tensor(order, dtype=torch.long)
+        yk = selective_scan(uf[..., idx], df[..., idx], A, bf[..., idx], cf[..., idx], dtype=dtype)
+        back = uf.new_zeros(batch, channels, length)
+        back[..., idx] = yk
+        paths.append(back)
+    total = (paths[0] + paths[2]) + (paths[1] + paths[3])
+    if merge == "mean":
+        total = total * 0.25
+    return total.reshape(batch, channels, height, width)
+
+
 # --------------------------------------------------------------------------- Mamba-2
 
 

@@ -40,6 +40,24 @@ def test_abi_version_and_struct_layouts(native):
     assert lib.mko_abi_version() == native.ABI_VERSION
     assert ctypes.sizeof(native.SelscanParams) == lib.mko_sizeof_selscan_params()
     assert ctypes.sizeof(native.StateUpdateParams) == lib.mko_sizeof_state_update_params()
+    assert ctypes.sizeof(native.SsdParams) == lib.mko_sizeof_ssd_params()
+    assert ctypes.sizeof(native.PathParams) == lib.mko_sizeof_path_params()
+
+
+def test_path_layout_validation_without_gpu(native):
+    lib = native.lib()
+    p = native.PathParams()
+    p.batch, p.rows, p.height, p.width, p.dtype, p.scale = 1, 4, -3, 5, 0, 1.0
+    assert lib.mko_path_stack(ctypes.byref(p), None) == 1
+    assert b"negative" in lib.mko_last_error()
+    p.height, p.dtype = 3, 7
+    assert lib.mko_path_merge(ctypes.byref(p), None) == 1
+    assert b"dtype" in lib.mko_last_error()
+    p.dtype = 0
+    assert lib.mko_path_stack(ctypes.byref(p), None) == 1  # null src/dst with elements
+    p.height = 0  # an empty map launches nothing and needs no pointers
+    assert lib.mko_path_stack(ctypes.byref(p), None) == 0
+    assert lib.mko_path_merge(ctypes.byref(p), None) == 0
 
 
 def test_host_side_validation_without_gpu(native):
