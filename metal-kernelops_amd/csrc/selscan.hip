@@ -712,10 +712,28 @@ __device__ __forceinline__ void load_state_rows(const float* __restrict__ bn, co
 template <int NS, bool UNI, bool FULL>
 __global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
   __shared__ float lds[4 * MainLds<NS>::kWaveFloats + MainLds<NS>::kRows];
+  // non-uniform mode: per wavefront, the first lane and the (batch, group) of each run
+  // of lanes that share a group (segment s covers lanes seg_first[s] .. seg_first[s+1])
+  __shared__ int seg_first[UNI ? 1 : 4][kWave + 1], seg_bg[UNI ? 1 : 4][kWave];
   const LaneInfo li = lane_info(g, UNI);
   const int N = static_cast<int>(g.dstate);
   const int lane = threadIdx.x & 63;
   const int wave = uniform(static_cast<int>(threadIdx.x >> 6));
+  int nseg = 0;
+  if constexpr (!UNI) {
+    const int bgi = static_cast<int>(li.bg);
+    const int prev = __shfl_up(bgi, 1);
+    const bool first = lane == 0 || prev != bgi;
+    const unsigned long long mask = __ballot(first);
+    nseg = __popcll(mask);
+    if (first) {
+      const int sidx = __popcll(mask & ((1ull << lane) - 1ull));
+      seg_first[wave][sidx] = lane;
+      seg_bg[wave][sidx] = bgi;
+    }
+    if (lane == 0) seg_first[wave][nseg] = kWave;
+    wave_lds_sync();
+  }
   float* trans = lds + wave * kWave * kTransPitch;                // [64][kTransPitch]
   float* acc_all = lds + 4 * kWave * kTransPitch;                 // [wave][NS][64]
   float* acc = acc_all + wave * NS * kWave;
@@ -879,11 +897,19 @@ __global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
 #pragma unroll 8
           for (int r = 0; r < 32; ++r) sum += trans[(r0 + r) * kTransPitch + col];
           acc[n * kWave + lane] = sum;
-        } else if (li.active) {
-          float* dst = p.pbc + (li.bg * g.length + qs) * NS * 2;
-          for (int i = 0; i < nv; ++i) {
-            atomicAdd(dst + (static_cast<int64_t>(i) * NS + n) * 2 + 0, trans[lane * kTransPitch + i]);
-            atomicAdd(dst + (static_cast<int64_t>(i) * NS + n) * 2 + 1, trans[lane * kTransPitch + HS + i]);
+        } else {
+          // One sum per (segment, column) over the segment's rows, then one atomic
+          // each: lanes of one group no longer add into the same address one by one.
+          // Inactive lanes hold zeros (act = 0) and sit in the last row's segment.
+          for (int w = lane; w < nseg * 2 * HS; w += kWave) {
+            const int sidx = w / (2 * HS), col = w % (2 * HS);
+            const int i = col % HS, k = col / HS;
+            if (i >= nv) continue;
+            float sum = 0.0f;
+            for (int r = seg_first[wave][sidx]; r < seg_first[wave][sidx + 1]; ++r)
+              sum += trans[r * kTransPitch + col];
+            const int64_t bgs = seg_bg[wave][sidx];
+            atomicAdd(p.pbc + ((bgs * g.length + qs + i) * NS + n) * 2 + k, sum);
           }
         }
         wave_lds_sync();
