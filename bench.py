@@ -410,8 +410,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-cpu", action="store_true", help="skip the CPU baseline legs")
-    ap.add_argument("--only", choices=["mamba1", "ssd", "decode", "ss2d", "all"], default="all",
-                    help="one workload (mamba1 = the config-3 headline alone) or all of them")
+    ap.add_argument("--only", choices=["mamba1", "ssd", "decode", "ss2d", "copy", "all"], default="all",
+                    help="one workload (mamba1 = the config-3 headline alone) or all of them; copy = "
+                         "a plain 1 GiB device copy, the calibration point of the PMC byte counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -422,6 +423,17 @@ def main():
         sys.exit(1)
     torch.backends.cuda.matmul.allow_tf32 = False
 
+    if args.only == "copy":
+        # A device-to-device copy of 1 GiB, three times: under rocprofv3 --pmc its
+        # FETCH_SIZE / WRITE_SIZE per dispatch calibrate the counters against a known
+        # 1 GiB read and 1 GiB write.
+        src = torch.empty(1 << 28, dtype=torch.float32, device="cuda").fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": src.numel() * 4, "copy_bytes_written": dst.numel() * 4}), flush=True)
+        return
     also = {}
     want = (lambda w: args.only in (w, "all"))
     if want("ssd"):
