@@ -68,6 +68,14 @@ __device__ __forceinline__ float sigmoid(float v) { return fast_rcp(1.0f + fast_
 // d softplus / dv with the same threshold: sigmoid(v), or 1 above 20.
 __device__ __forceinline__ float softplus_grad(float v) { return v > 20.0f ? 1.0f : sigmoid(v); }
 
+// The same derivative from the softplus value s = softplus(v): sigmoid(v) = 1 - e^{-s}
+// exactly (and s = v > 20 gives 1 - e^{-20} = 1 in float).  Below 1/8 a 4-term series
+// of 1 - e^{-s} avoids the cancellation (truncation s^4/120 relative).
+__device__ __forceinline__ float softplus_grad_from_value(float s) {
+  if (s < 0.125f) return s * (1.0f - s * (0.5f - s * (1.0f / 6.0f - s * (1.0f / 24.0f))));
+  return 1.0f - fast_exp(-s);
+}
+
 // Pointer into the constant address space: loads through it with a wave-uniform
 // address compile to scalar (SMEM) loads.
 typedef const float __attribute__((address_space(4)))* cfptr;

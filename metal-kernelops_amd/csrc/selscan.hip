@@ -1,8 +1,8 @@
 // Mamba-1 selective scan, forward and backward, for gfx950.
 //
 // Mapping: one lane per channel row (batch, d).  A wavefront holds 64 channels of
-// one (batch, group) whenever dim/ngroups is a multiple of 64, so B_t and C_t are
-// wave-uniform (scalar loads) and the dB/dC sums over channels are cross-lane
+// one (batch, group) whenever dim/ngroups is a multiple of 64 ("uniform" mode), so
+// B_t and C_t are wave-uniform and the dB/dC sums over channels are cross-lane
 // reductions.  Each lane walks time sequentially with its N states in registers.
 //
 // Time parallelism: the sequence is cut into `nchunks` coarse chunks of `lc`
@@ -11,11 +11,11 @@
 //      of its steps (its decay is exp(A * sum));
 //   2. chain: per (row, state), the exact entering state of every chunk;
 //   3. fwd_replay: replays every chunk from its entering state, writes
-//      out = (C.x + D u) * silu(z) and the state entering every 64-step block.
+//      out = (C.x + D u) * silu(z) and the state entering every 16-step block.
 // The backward mirrors it: bwd_summary (each chunk's adjoint from a zero exit),
-// a reverse chain, then bwd_main, which walks every chunk backwards in 16-step
-// quarters, recomputing the forward states of a quarter from the saved 64-step
-// state, and finally small reduction kernels for dB/dC, dA, dD and ddelta_bias.
+// a reverse chain, then bwd_main, which walks every chunk backwards one 16-step
+// block at a time, recomputing the block's forward states from the saved state,
+// and finally small reduction kernels for dB/dC, dA, dD and ddelta_bias.
 //
 // Per-step inputs of the state-inner loops (one lane, all states, one step at a
 // time) are staged through LDS so the step loop is a real loop and B_t/C_t are
@@ -71,8 +71,6 @@ struct Ptrs {
   float* adj;    // (rows, nchunks, N) adjoint entering each chunk from the right
   float* pbc;    // (batch*G, ncb, L, NS, 2) dB/dC partial sums
   float* dap;    // (nchunks, NS, rows) dA partials
-  float* hcs;    // (nchunks, NS, rows) adjoint carried between quarters
-  float* qx;     // (nchunks, 3, NS, rows) states entering quarters 1..3 of a 64-block
   float* ddp;    // (nchunks, rows) dD partials
   float* dbp;    // (nchunks, rows) ddelta_bias partials
 };
@@ -239,23 +237,6 @@ __device__ __forceinline__ void forward_block(const float* __restrict__ bt, cons
       if (WITH_Y) y[i + 1] = acc;
     }
   }
-}
-
-// Per-step inputs of one block: del = step size (0 past the end), du = del * u.
-// Returns the sum of the steps.
-__device__ __forceinline__ float load_steps(const Geo& g, const Ptrs& p, int64_t off, int nv, float bias,
-                                            float (&del)[HS], float (&du)[HS]) {
-  float uu[HS];
-  load_run<HS>(p.delta, g.d_dtype, off, nv, g.vec, del);
-  load_run<HS>(p.u, g.u_dtype, off, nv, g.vec, uu);
-  float sd = 0.0f;
-#pragma unroll
-  for (int i = 0; i < HS; ++i) {
-    del[i] = i < nv ? step_of(g, del[i], bias) : 0.0f;
-    du[i] = del[i] * uu[i];
-    sd += del[i];
-  }
-  return sd;
 }
 
 // One 16-step block of the time-major B (and C) rows of a wavefront's (batch, group),
@@ -674,7 +655,7 @@ __global__ void __launch_bounds__(256) bwd_summary(Geo g, Ptrs p) {
 }
 
 // bwd_main LDS (floats): per wavefront a transposition buffer [64][2*HS+1] and
-// its dB/dC half-column sums [NS][64]; per workgroup the quarter's B and C rows
+// its dB/dC half-column sums [NS][64]; per workgroup the block's B and C rows
 // [2][NS][HS] when the workgroup shares (batch, group).
 constexpr int kTransPitch = 2 * HS + 1;
 
@@ -684,7 +665,7 @@ struct MainLds {
   static constexpr int kRows = 2 * NS * HS;
 };
 
-// One state's B and C over the HS steps of a quarter (state-major rows).
+// One state's B and C over the HS steps of a block (state-major rows).
 template <bool UNI>
 __device__ __forceinline__ void load_state_rows(const float* __restrict__ bn, const float* __restrict__ cn,
                                                 int64_t off, float (&bv)[HS], float (&cv)[HS]) {
@@ -712,6 +693,9 @@ __device__ __forceinline__ void load_state_rows(const float* __restrict__ bn, co
 template <int NS, bool UNI, bool FULL>
 __global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
   __shared__ float lds[4 * MainLds<NS>::kWaveFloats + MainLds<NS>::kRows];
+  // per wavefront, the block's dz factor dy sigma(z) (1 + z (1 - sigma(z))) per step and
+  // lane, computed from the block's first loads so the gradients need no second read
+  __shared__ float dzs[4][HS * kWave];
   // non-uniform mode: per wavefront, the first lane and the (batch, group) of each run
   // of lanes that share a group (segment s covers lanes seg_first[s] .. seg_first[s+1])
   __shared__ int seg_first[UNI ? 1 : 4][kWave + 1], seg_bg[UNI ? 1 : 4][kWave];
@@ -750,13 +734,11 @@ __global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
   const float* arow = p.A + li.d * N;
   const float act = li.active ? 1.0f : 0.0f;
   const int64_t R = g.rows;
-  // Per-(chunk, state, row) carries in the workspace, state-major so a
-  // wavefront's 64 lanes touch 256 contiguous bytes.
-  float* hcs = p.hcs + static_cast<int64_t>(c) * NS * R;
+  // dA partials per (chunk, state, row), state-major so a wavefront's 64 lanes
+  // touch 256 contiguous bytes.
   float* dap = p.dap + static_cast<int64_t>(c) * NS * R;
-  float* qx = p.qx + static_cast<int64_t>(c) * 3 * NS * R;
 
-  // adjoint carried between quarters and the dA sums, one per state, in registers
+  // adjoint carried between blocks and the dA sums, one per state, in registers
   float hcr[NS], dar[NS];
 #pragma unroll
   for (int n = 0; n < NS; ++n) {
@@ -775,34 +757,17 @@ __global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
   float dD_acc = 0.0f, db_acc = 0.0f;
   const int64_t brow0 = li.bg * g.length;
 
+  static_assert(CK == HS, "one saved state per 16-step block");
   const int jb = t_begin / CK;
   const int je = (t_end + CK - 1) / CK;
+  // blocks in reverse, states one at a time
   for (int j = je - 1; j >= jb; --j) {
-    const int tb = j * CK;
-    const int te = min(tb + CK, t_end);
-    const int nq = (te - tb + HS - 1) / HS;
+    const int qs = j * CK;
     // saved state entering block j, element n at srow[n * srow_stride]
     const float* srow = p.states + ck_index(g, li.row, j, 0);
     const int srow_stride = static_cast<int>(g.dim);
-    // ---- states entering quarters 1..nq-1, state-inner sweep from the saved state
-    if (nq > 1) {
-      float x[NS];
-#pragma unroll
-      for (int n = 0; n < NS; ++n) x[n] = n < N ? srow[n * srow_stride] : 0.0f;
-      for (int q = 0; q < nq - 1; ++q) {
-        const int qs = tb + q * HS;
-        float sdel[HS], sdu[HS], unused[HS];
-        load_steps(g, p, rbase + qs, HS, bias, sdel, sdu);
-        forward_block<NS, UNI, false>(p.bt, nullptr, brow0, qs, HS, sdel, sdu, A2, x, unused);
-#pragma unroll
-        for (int n = 0; n < NS; ++n)
-          if (n < N) qx[(q * NS + n) * R + li.row] = x[n];
-      }
-    }
-    // ---- quarters in reverse, states one at a time
-    for (int q = nq - 1; q >= 0; --q) {
-      const int qs = tb + q * HS;
-      const int nv = min(HS, te - qs);
+    {
+      const int nv = min(HS, t_end - qs);
       float del[HS], du[HS], gy[HS];
       {
         float uu[HS];
@@ -813,7 +778,11 @@ __global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
           float zz[HS];
           load_run<HS>(p.z, g.u_dtype, rbase + qs, nv, g.vec, zz);
 #pragma unroll
-          for (int i = 0; i < HS; ++i) gy[i] *= zz[i] * sigmoid(zz[i]);
+          for (int i = 0; i < HS; ++i) {
+            const float sg = sigmoid(zz[i]);
+            dzs[wave][i * kWave + lane] = gy[i] * sg * (1.0f + zz[i] * (1.0f - sg));  // gy is dy here
+            gy[i] *= zz[i] * sg;
+          }
         }
 #pragma unroll
         for (int i = 0; i < HS; ++i) {
@@ -827,7 +796,7 @@ __global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
       for (int i = 0; i < HS; ++i) s1[i] = s2[i] = ya[i] = 0.0f;
 
       if (UNI) {
-        // The quarter's B/C rows, shared by the workgroup (the previous quarter's
+        // The block's B/C rows, shared by the workgroup (the previous block's
         // flush barrier orders this write after every read of the old rows).
         for (int e = threadIdx.x; e < NS * HS; e += blockDim.x) {
           const int n = e / HS, i = e % HS;
@@ -837,9 +806,8 @@ __global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
         }
         __syncthreads();
       }
-      // per-lane carries, state-major: element (n, row) at n * R + row
-      const float* xin_p = q == 0 ? srow : qx + ((q - 1) * NS) * R + li.row;
-      const int xin_stride = q == 0 ? srow_stride : static_cast<int>(R);
+      const float* xin_p = srow;
+      const int xin_stride = srow_stride;
       const float* bn_p = p.bn + (li.bg * NS) * g.length + qs;
       const float* cn_p = p.cn + (li.bg * NS) * g.length + qs;
       float xin_n = xin_p[0];
@@ -915,16 +883,15 @@ __global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
         wave_lds_sync();
         if (more) xin_n = xin_x;
       }
-      // ---- per-step gradients of the quarter
+      // ---- per-step gradients of the block
       {
-        float raw[HS], uu[HS], o1[HS], o2[HS];
-        load_run<HS>(p.delta, g.d_dtype, rbase + qs, nv, g.vec, raw);
+        float uu[HS], o1[HS], o2[HS];
         load_run<HS>(p.u, g.u_dtype, rbase + qs, nv, g.vec, uu);
 #pragma unroll
         for (int i = 0; i < HS; ++i) {
           o1[i] = fmaf(del[i], s1[i], Dd * gy[i]);  // du
           float dd = fmaf(uu[i], s1[i], s2[i]);      // d loss / d step
-          if (g.softplus) dd *= softplus_grad(raw[i] + bias);
+          if (g.softplus) dd *= softplus_grad_from_value(del[i]);
           o2[i] = dd;
           if (i < nv) {
             dD_acc = fmaf(gy[i], uu[i], dD_acc);
@@ -936,20 +903,13 @@ __global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
           store_run<HS>(p.ddelta, g.d_dtype, rbase + qs, nv, g.vec, o2);
         }
         if (has_z && p.dz) {
-          float zz[HS], dy[HS];
-          load_run<HS>(p.z, g.u_dtype, rbase + qs, nv, g.vec, zz);
-          load_run<HS>(p.dout, g.u_dtype, rbase + qs, nv, g.vec, dy);
 #pragma unroll
-          for (int i = 0; i < HS; ++i) {
-            const float sg = sigmoid(zz[i]);
-            const float yfull = fmaf(Dd, uu[i], ya[i]);
-            o1[i] = dy[i] * yfull * sg * (1.0f + zz[i] * (1.0f - sg));
-          }
+          for (int i = 0; i < HS; ++i) o1[i] = dzs[wave][i * kWave + lane] * fmaf(Dd, uu[i], ya[i]);
           if (li.active) store_run<HS>(p.dz, g.u_dtype, rbase + qs, nv, g.vec, o1);
         }
       }
       if (UNI) {
-        // The workgroup's dB/dC sums of this quarter, column k*HS + i of state n:
+        // The workgroup's dB/dC sums of this block, column k*HS + i of state n:
         // wavefronts in order, each as (first half of rows) + (second half).
         __syncthreads();
         float* dst = p.pbc + ((li.bg * g.ncb + cb) * g.length + qs) * NS * 2;
@@ -1069,7 +1029,7 @@ struct Plan {
   int ns;
   bool uni;
   size_t off_bt, off_ct, off_bn, off_cn, off_drive, off_sumd, off_adj, off_pbc, off_dap, off_ddp,
-      off_dbp, off_hcs, off_qx;
+      off_dbp;
   size_t fwd_bytes, bwd_bytes;
 };
 
@@ -1153,15 +1113,13 @@ static int make_plan(const mko_selscan_params* p, Plan* pl) {
   pl->off_sumd = o; o = align_up(o + rk * 4);
   pl->fwd_bytes = o;
   // backward workspace (extends the forward layout: bt/ct are used by both)
-  pl->off_bn = o; o = align_up(o + (bgl * ns + HS) * 4);  // + one row tail: quarters read HS steps
+  pl->off_bn = o; o = align_up(o + (bgl * ns + HS) * 4);  // + one row tail: blocks read HS steps
   pl->off_cn = o; o = align_up(o + (bgl * ns + HS) * 4);
   pl->off_adj = o; o = align_up(o + rk * g.dstate * 4);
   pl->off_pbc = o; o = align_up(o + bgl * g.ncb * ns * 2 * 4);
   pl->off_dap = o; o = align_up(o + rk * ns * 4);
   pl->off_ddp = o; o = align_up(o + rk * 4);
   pl->off_dbp = o; o = align_up(o + rk * 4);
-  pl->off_hcs = o; o = align_up(o + rk * ns * 4);
-  pl->off_qx = o; o = align_up(o + (CK > HS ? rk * 3 * ns * 4 : 0));  // quarter-entry states (only when saves are sparser than 16 steps)
   pl->bwd_bytes = o;
   return MKO_OK;
 }
@@ -1204,8 +1162,6 @@ static Ptrs make_ptrs(const mko_selscan_params* p, const Plan& pl) {
   q.dap = reinterpret_cast<float*>(ws + pl.off_dap);
   q.ddp = reinterpret_cast<float*>(ws + pl.off_ddp);
   q.dbp = reinterpret_cast<float*>(ws + pl.off_dbp);
-  q.hcs = reinterpret_cast<float*>(ws + pl.off_hcs);
-  q.qx = reinterpret_cast<float*>(ws + pl.off_qx);
   return q;
 }
 
