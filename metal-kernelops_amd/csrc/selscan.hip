@@ -696,6 +696,9 @@ __global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
   // per wavefront, the block's dz factor dy sigma(z) (1 + z (1 - sigma(z))) per step and
   // lane, computed from the block's first loads so the gradients need no second read
   __shared__ float dzs[4][HS * kWave];
+  // and u's raw 16-bit values when u is 16-bit (fp32 u is read again)
+  __shared__ uint16_t us16[4][HS * kWave];
+  const bool u16 = g.u_dtype != MKO_F32;
   // non-uniform mode: per wavefront, the first lane and the (batch, group) of each run
   // of lanes that share a group (segment s covers lanes seg_first[s] .. seg_first[s+1])
   __shared__ int seg_first[UNI ? 1 : 4][kWave + 1], seg_bg[UNI ? 1 : 4][kWave];
@@ -773,6 +776,13 @@ __global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
         float uu[HS];
         load_run<HS>(p.delta, g.d_dtype, rbase + qs, nv, g.vec, del);
         load_run<HS>(p.u, g.u_dtype, rbase + qs, nv, g.vec, uu);
+        if (u16) {
+          // exact: the floats came from 16-bit values
+#pragma unroll
+          for (int i = 0; i < HS; ++i)
+            us16[wave][i * kWave + lane] = g.u_dtype == MKO_BF16 ? __builtin_bit_cast(uint16_t, from_f32<bf16>(uu[i]))
+                                                                 : __builtin_bit_cast(uint16_t, from_f32<_Float16>(uu[i]));
+        }
         load_run<HS>(p.dout, g.u_dtype, rbase + qs, nv, g.vec, gy);
         if (has_z) {
           float zz[HS];
@@ -886,7 +896,15 @@ __global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
       // ---- per-step gradients of the block
       {
         float uu[HS], o1[HS], o2[HS];
-        load_run<HS>(p.u, g.u_dtype, rbase + qs, nv, g.vec, uu);
+        if (u16) {
+#pragma unroll
+          for (int i = 0; i < HS; ++i) {
+            const uint16_t v = us16[wave][i * kWave + lane];
+            uu[i] = g.u_dtype == MKO_BF16 ? to_f32(__builtin_bit_cast(bf16, v)) : to_f32(__builtin_bit_cast(_Float16, v));
+          }
+        } else {
+          load_run<HS>(p.u, g.u_dtype, rbase + qs, nv, g.vec, uu);
+        }
 #pragma unroll
         for (int i = 0; i < HS; ++i) {
           o1[i] = fmaf(del[i], s1[i], Dd * gy[i]);  // du
