@@ -48,6 +48,8 @@ size_t mko_sizeof_selscan_params(void);
 size_t mko_sizeof_state_update_params(void);
 size_t mko_sizeof_ssd_params(void);
 size_t mko_sizeof_path_params(void);
+size_t mko_sizeof_conv1d_params(void);
+size_t mko_sizeof_conv1d_update_params(void);
 
 /* Kernel timing (observability).  While enabled, every kernel the library
  * launches is bracketed by HIP events on its launch stream; the per-kernel totals
@@ -265,6 +267,63 @@ int mko_path_stack(const mko_path_params* p, void* stream);
  * in its permuting form; the reference's forward merges per-pixel slices, this
  * build's forward merges step-ordered ones like its backward. */
 int mko_path_merge(const mko_path_params* p, void* stream);
+
+/* ======================================================================== */
+/* Causal depthwise conv1d (cv/causal_conv1d.py)                              */
+/* ======================================================================== */
+
+#define MKO_CONV_SILU 1u /* out = silu(pre) instead of pre */
+
+/* With z = cat(initial_state or zeros(width-1), x) along time:
+ *   out[b][c][t] = act(bias[c] + sum_{j < width} weight[c][j] * z[b][c][t + j])
+ *   final_state  = z[..., length : length + width - 1]
+ * Every tensor is contiguous and of `dtype`; arithmetic is float32. */
+typedef struct mko_conv1d_params {
+  const void* x;             /* (batch, channels, length) */
+  const void* weight;        /* (channels, width), width <= 32 */
+  const void* bias;          /* (channels,) or NULL */
+  const void* initial_state; /* (batch, channels, width - 1) or NULL (zeros) */
+  void* out;                 /* forward: (batch, channels, length) */
+  void* final_state;         /* forward: (batch, channels, width - 1), written when non-NULL */
+  const void* dout;          /* backward: (batch, channels, length) */
+  void* dx;                  /* backward: (batch, channels, length) */
+  void* dweight;             /* backward: (channels, width) or NULL */
+  void* dbias;               /* backward: (channels,) or NULL */
+  void* dinitial;            /* backward: (batch, channels, width - 1) or NULL */
+  void* workspace;           /* backward, when dweight or dbias: mko_conv1d_bwd_workspace_size() */
+  size_t workspace_bytes;
+  int64_t batch, channels, length, width;
+  int32_t dtype;
+  uint32_t flags;            /* MKO_CONV_SILU */
+} mko_conv1d_params;
+
+/* Replaces the Metal causal_conv1d_fwd kernel and _forward_metal
+ * (cv/causal_conv1d.py:79-160, 533-549). */
+int mko_conv1d_fwd(const mko_conv1d_params* p, void* stream);
+/* Replaces _CausalConv1d.backward with the Metal causal_conv1d_bwd and
+ * causal_conv1d_dwfinal kernels (cv/causal_conv1d.py:161-338, 562-607): dx, dinitial,
+ * and dweight/dbias reduced over batch and time in a fixed order.  The gradient through
+ * final_state is the caller's (it is a slice of cat(initial_state, x)). */
+size_t mko_conv1d_bwd_workspace_size(const mko_conv1d_params* p);
+int mko_conv1d_bwd(const mko_conv1d_params* p, void* stream);
+
+/* Decode: x (batch, channels, q) advances a rolling state (batch, channels, span),
+ * span >= width - 1, element (b, c, i) at b * state_stride_b + c * state_stride_c + i
+ * (a slice of a larger cache).  out (batch, channels, q) is the convolution of
+ * cat(state, x) at the q new tokens; state becomes cat(state, x)[..., q : q + span].
+ * Replaces the Metal causal_conv1d_update kernel (cv/causal_conv1d.py:340-390, 690-756). */
+typedef struct mko_conv1d_update_params {
+  const void* x;
+  void* state;
+  const void* weight; /* (channels, width) */
+  const void* bias;   /* (channels,) or NULL */
+  void* out;
+  int64_t batch, channels, q, span, width, state_stride_b, state_stride_c;
+  int32_t dtype; /* of every tensor */
+  uint32_t flags;
+} mko_conv1d_update_params;
+
+int mko_conv1d_update(const mko_conv1d_update_params* p, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,391 @@
+// Causal depthwise conv1d (the convolution ahead of every Mamba block) for gfx950.
+//
+// With z = cat(initial_state or zeros(K-1), x) along time and m = K - 1:
+//   pre[b, c, t] = bias[c] + sum_{j < K} w[c, j] z[b, c, t + j]      (z index t + j = time t - m + j)
+//   out          = act(pre),  act = identity or silu
+//   final_state  = z[..., L : L + m]
+// Forward: one lane per 8-step block of a row; the block is a 16-byte vector load on
+// aligned rows and the m look-back steps are scalar loads from the row (or from the
+// initial state / zero padding before t = 0).  Backward: a lane recomputes pre over its
+// block's window (m steps either side), writes dx for its 8 steps, and the taps'
+// gradients dw[c, j] = sum_t g[t] z[t - m + j] and dbias = sum_t g[t] (g = dout act'(pre))
+// are reduced over the lanes of a row segment, then over batch and segments in a fixed
+// order by `finalize`, so they are deterministic.  Decode: one lane per row advances a
+// rolling state of `span` columns by q tokens in place.
+#include "common.hpp"
+#include "io.hpp"
+
+namespace mko {
+namespace conv {
+namespace {
+
+constexpr int BS = 8;  // steps per lane
+
+struct Geo {
+  int64_t batch, channels, length, rows;  // rows = batch * channels
+  int width, taps;                          // taps = width - 1
+  int64_t nblk;                             // blocks of BS steps per row
+  int tpr;                                  // lanes per row segment (power of two <= 256)
+  int64_t nseg;                             // segments per row = ceil(nblk / tpr)
+  int dtype;
+  int silu;
+  int vec;                                  // rows are 16-byte aligned whole blocks
+};
+
+// z at time t of row `row`: x for 0 <= t < length, the initial state (or zero padding)
+// for -taps <= t < 0, zero elsewhere.
+__device__ __forceinline__ float z_at(const Geo& g, const void* x, const void* init, int64_t row, int64_t t) {
+  if (t >= 0) return t < g.length ? load_one(x, g.dtype, row * g.length + t) : 0.0f;
+  if (!init || t < -g.taps) return 0.0f;
+  return load_one(init, g.dtype, row * g.taps + (g.taps + t));
+}
+
+// The taps left-padded to KMAX: wp[j'] = w[j' - (KMAX - width)], zero below, so that
+// pre(t) = bias + sum_{j' < KMAX} wp[j'] z(t - (KMAX - 1) + j') with compile-time indices.
+template <int KMAX>
+__device__ __forceinline__ void load_taps(const Geo& g, const void* weight, int64_t c, float (&wp)[KMAX]) {
+  const int lead = KMAX - g.width;
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) wp[j] = j >= lead ? load_one(weight, g.dtype, c * g.width + (j - lead)) : 0.0f;
+}
+
+// The BS steps of a block at t0 (t0 + BS <= length when vec).
+__device__ __forceinline__ void load_block(const Geo& g, const void* x, int64_t row, int64_t t0, float (&v)[BS]) {
+  if (g.vec) {
+    load_run<BS>(x, g.dtype, row * g.length + t0, BS, true, v);
+  } else {
+#pragma unroll
+    for (int e = 0; e < BS; ++e) v[e] = t0 + e < g.length ? load_one(x, g.dtype, row * g.length + t0 + e) : 0.0f;
+  }
+}
+
+__device__ __forceinline__ float act(const Geo& g, float v) { return g.silu ? v * sigmoid(v) : v; }
+__device__ __forceinline__ float act_grad(const Geo& g, float v) {
+  if (!g.silu) return 1.0f;
+  const float s = sigmoid(v);
+  return s * (1.0f + v * (1.0f - s));
+}
+
+template <int KMAX>
+__global__ void __launch_bounds__(256) forward(Geo g, mko_conv1d_params p) {
+  constexpr int H = KMAX - 1;
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (e >= g.rows * g.nblk) return;
+  const int64_t row = e / g.nblk, blk = e % g.nblk, c = row % g.channels;
+  const int64_t t0 = blk * BS;
+  float wp[KMAX];
+  load_taps<KMAX>(g, p.weight, c, wp);
+  const float bias = p.bias ? load_one(p.bias, g.dtype, c) : 0.0f;
+  // zz[i] = z(t0 - H + i)
+  float zz[H + BS];
+#pragma unroll
+  for (int i = 0; i < H; ++i) zz[i] = i >= H - g.taps ? z_at(g, p.x, p.initial_state, row, t0 - H + i) : 0.0f;
+  float cur[BS];
+  load_block(g, p.x, row, t0, cur);
+#pragma unroll
+  for (int i = 0; i < BS; ++i) zz[H + i] = cur[i];
+  float o[BS];
+#pragma unroll
+  for (int s = 0; s < BS; ++s) {
+    float acc = bias;
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) acc = fmaf(wp[j], zz[s + j], acc);
+    o[s] = act(g, acc);
+  }
+  if (g.vec) {
+    store_run<BS>(p.out, g.dtype, row * g.length + t0, BS, true, o);
+  } else {
+#pragma unroll
+    for (int s = 0; s < BS; ++s)
+      if (t0 + s < g.length) store_one(p.out, g.dtype, row * g.length + t0 + s, o[s]);
+  }
+  if (p.final_state && blk == g.nblk - 1) {
+    for (int m = 0; m < g.taps; ++m)
+      store_one(p.final_state, g.dtype, row * g.taps + m, z_at(g, p.x, p.initial_state, row, g.length - g.taps + m));
+  }
+}
+
+// Sum over the `tpr` lanes of a row segment (lanes tpr-aligned within the workgroup);
+// every lane of the segment gets it.  red: 256 floats of LDS, barrier-protected.
+__device__ __forceinline__ float segment_sum(float v, int tpr, float* red) {
+  const int lane = threadIdx.x & 63;
+  const int span = tpr < 64 ? tpr : 64;
+  for (int off = 1; off < span; off <<= 1) v += __shfl_xor(v, off);
+  if (tpr <= 64) return v;
+  // segments wider than a wavefront: add the wavefront sums of the segment in order
+  __syncthreads();
+  if (lane == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  const int first = (static_cast<int>(threadIdx.x) / tpr) * (tpr / 64);
+  float s = 0.0f;
+  for (int w = 0; w < tpr / 64; ++w) s += red[first + w];
+  return s;
+}
+
+template <int KMAX>
+__global__ void __launch_bounds__(256) backward(Geo g, mko_conv1d_params p, float* partial) {
+  constexpr int H = KMAX - 1;
+  __shared__ float red[4];
+  const int rpw = 256 / g.tpr;  // row segments per workgroup
+  const int64_t seg_id = static_cast<int64_t>(blockIdx.x) * rpw + threadIdx.x / g.tpr;
+  const bool live_seg = seg_id < g.rows * g.nseg;
+  const int64_t row = live_seg ? seg_id / g.nseg : 0, seg = live_seg ? seg_id % g.nseg : 0;
+  const int64_t blk = seg * g.tpr + threadIdx.x % g.tpr;
+  const bool live = live_seg && blk < g.nblk;
+  const int64_t c = row % g.channels;
+  const int64_t t0 = blk * BS;
+  float wp[KMAX];
+  load_taps<KMAX>(g, p.weight, c, wp);
+  const float bias = p.bias ? load_one(p.bias, g.dtype, c) : 0.0f;
+  float dwp[KMAX], dbp = 0.0f;
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) dwp[j] = 0.0f;
+  if (live) {
+    // zz[i] = z(t0 - H + i) over the window pre(t0 .. t0 + BS - 1 + H) reads
+    float zz[BS + 2 * H];
+#pragma unroll
+    for (int i = 0; i < BS + 2 * H; ++i) zz[i] = z_at(g, p.x, p.initial_state, row, t0 - H + i);
+    // gg[i] = g(t0 + i) = dout act'(pre), zero from the end of the row
+    float gg[BS + H];
+#pragma unroll
+    for (int i = 0; i < BS + H; ++i) {
+      const int64_t t = t0 + i;
+      float gv = 0.0f;
+      if (t < g.length) {
+        float pre = bias;
+#pragma unroll
+        for (int j = 0; j < KMAX; ++j) pre = fmaf(wp[j], zz[i + j], pre);
+        gv = load_one(p.dout, g.dtype, row * g.length + t) * act_grad(g, pre);
+      }
+      gg[i] = gv;
+    }
+    // dx(t) = sum_j' wp[j'] g(t + H - j')
+    float dxo[BS];
+#pragma unroll
+    for (int s = 0; s < BS; ++s) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < KMAX; ++j) acc = fmaf(wp[j], gg[s + H - j], acc);
+      dxo[s] = acc;
+    }
+    if (g.vec) {
+      store_run<BS>(p.dx, g.dtype, row * g.length + t0, BS, true, dxo);
+    } else {
+#pragma unroll
+      for (int s = 0; s < BS; ++s)
+        if (t0 + s < g.length) store_one(p.dx, g.dtype, row * g.length + t0 + s, dxo[s]);
+    }
+    // taps (padded index) and bias over this block's own steps
+#pragma unroll
+    for (int s = 0; s < BS; ++s) {
+      dbp += gg[s];
+#pragma unroll
+      for (int j = 0; j < KMAX; ++j) dwp[j] = fmaf(gg[s], zz[s + j], dwp[j]);
+    }
+    // initial state: z(tau), -taps <= tau < 0, feeds pre(t) at t = tau + H - j'
+    if (p.dinitial && blk == 0) {
+#pragma unroll
+      for (int k = 1; k <= H; ++k) {  // tau = -k
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < KMAX; ++j) {
+          const int i = H - k - j;  // t = tau + H - j' relative to t0 = 0
+          if (i >= 0) acc = fmaf(wp[j], gg[i], acc);
+        }
+        if (k <= g.taps) store_one(p.dinitial, g.dtype, row * g.taps + (g.taps - k), acc);
+      }
+    }
+  }
+  if (!partial) return;
+  // one partial per (row, segment): the K taps, then the bias
+  float* dst = partial + (live_seg ? seg_id : 0) * (g.width + 1);
+  const int lead = KMAX - g.width;
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) {
+    if (j < lead) continue;  // uniform
+    const float v = segment_sum(dwp[j], g.tpr, red);
+    if (live_seg && threadIdx.x % g.tpr == 0) dst[j - lead] = v;
+  }
+  const float vb = segment_sum(dbp, g.tpr, red);
+  if (live_seg && threadIdx.x % g.tpr == 0) dst[g.width] = vb;
+}
+
+// dweight[c, j] and dbias[c]: partials summed over batch then segments, in order.
+__global__ void __launch_bounds__(256) finalize(Geo g, mko_conv1d_params p, const float* partial) {
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (e >= g.channels * (g.width + 1)) return;
+  const int64_t c = e / (g.width + 1);
+  const int j = static_cast<int>(e % (g.width + 1));
+  float s = 0.0f;
+  for (int64_t b = 0; b < g.batch; ++b) {
+    const int64_t row = b * g.channels + c;
+    for (int64_t seg = 0; seg < g.nseg; ++seg) s += partial[(row * g.nseg + seg) * (g.width + 1) + j];
+  }
+  if (j < g.width) {
+    if (p.dweight) store_one(p.dweight, g.dtype, c * g.width + j, s);
+  } else if (p.dbias) {
+    store_one(p.dbias, g.dtype, c, s);
+  }
+}
+
+// Decode: per row, joined = cat(state[0..span), x[0..q)); out[t] = act(bias + sum_j
+// w[j] joined[span + t - taps + j]); then state = joined[q .. q + span).
+__global__ void __launch_bounds__(256) update(mko_conv1d_update_params p) {
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (row >= p.batch * p.channels) return;
+  const int64_t b = row / p.channels, c = row % p.channels;
+  const int dt = p.dtype;
+  const int64_t sb = b * p.state_stride_b + c * p.state_stride_c;
+  const int64_t taps = p.width - 1;
+  const float bias = p.bias ? load_one(p.bias, dt, c) : 0.0f;
+  const bool silu = (p.flags & MKO_CONV_SILU) != 0;
+  // joined index i: state column i (i < span), else token i - span
+  auto joined = [&](int64_t i) -> float {
+    return i < p.span ? load_one(p.state, dt, sb + i) : load_one(p.x, dt, row * p.q + (i - p.span));
+  };
+  for (int64_t t = 0; t < p.q; ++t) {
+    float acc = bias;
+    for (int64_t j = 0; j < p.width; ++j) acc = fmaf(load_one(p.weight, dt, c * p.width + j), joined(p.span + t - taps + j), acc);
+    store_one(p.out, dt, row * p.q + t, silu ? acc * sigmoid(acc) : acc);
+  }
+  // shift: the new column i is joined[q + i]; ascending order never overwrites a state
+  // column that a later i still reads (q + i > i)
+  for (int64_t i = 0; i < p.span; ++i) store_one(p.state, dt, sb + i, joined(p.q + i));
+}
+
+int make_geo(const mko_conv1d_params* p, Geo* g) {
+  if (!p) {
+    mko_set_error("conv1d: null parameters");
+    return MKO_EINVAL;
+  }
+  if (p->batch < 0 || p->channels < 0 || p->length < 0 || p->width < 1) {
+    mko_set_error("conv1d: bad sizes batch=%lld channels=%lld length=%lld width=%lld",
+                  static_cast<long long>(p->batch), static_cast<long long>(p->channels),
+                  static_cast<long long>(p->length), static_cast<long long>(p->width));
+    return MKO_EINVAL;
+  }
+  if (p->width > 32) {
+    mko_set_error("conv1d: width=%lld > 32 is not supported", static_cast<long long>(p->width));
+    return MKO_EUNSUPPORTED;
+  }
+  if (p->dtype != MKO_F32 && p->dtype != MKO_F16 && p->dtype != MKO_BF16) {
+    mko_set_error("conv1d: unknown dtype %d", p->dtype);
+    return MKO_EINVAL;
+  }
+  g->batch = p->batch;
+  g->channels = p->channels;
+  g->length = p->length;
+  g->rows = p->batch * p->channels;
+  g->width = static_cast<int>(p->width);
+  g->taps = g->width - 1;
+  g->nblk = (p->length + BS - 1) / BS;
+  int tpr = 1;
+  while (tpr < 256 && tpr < g->nblk) tpr <<= 1;
+  g->tpr = tpr;
+  g->nseg = (g->nblk + tpr - 1) / tpr;
+  g->dtype = p->dtype;
+  g->silu = (p->flags & MKO_CONV_SILU) != 0;
+  const int esz = p->dtype == MKO_F32 ? 4 : 2;
+  const uintptr_t mask = 15u;
+  g->vec = p->length % BS == 0 && (reinterpret_cast<uintptr_t>(p->x) & mask) == 0 &&
+           (reinterpret_cast<uintptr_t>(p->out) & mask) == 0 && (reinterpret_cast<uintptr_t>(p->dx) & mask) == 0 &&
+           (reinterpret_cast<uintptr_t>(p->dout) & mask) == 0 && (p->length * esz) % 16 == 0;
+  return MKO_OK;
+}
+
+template <int KMAX>
+void launch_fwd(const Geo& g, const mko_conv1d_params& p, hipStream_t s) {
+  const int64_t n = g.rows * g.nblk;
+  MKO_TIMED("conv1d_fwd", s, forward<KMAX><<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(g, p));
+}
+
+template <int KMAX>
+void launch_bwd(const Geo& g, const mko_conv1d_params& p, float* partial, hipStream_t s) {
+  const int rpw = 256 / g.tpr;
+  const int64_t segs = g.rows * g.nseg;
+  MKO_TIMED("conv1d_bwd", s, backward<KMAX><<<static_cast<unsigned>((segs + rpw - 1) / rpw), 256, 0, s>>>(g, p, partial));
+}
+
+size_t partial_bytes(const Geo& g) { return static_cast<size_t>(g.rows * g.nseg) * (g.width + 1) * sizeof(float); }
+
+}  // namespace
+}  // namespace conv
+}  // namespace mko
+
+using namespace mko;
+
+extern "C" size_t mko_sizeof_conv1d_params(void) { return sizeof(mko_conv1d_params); }
+extern "C" size_t mko_sizeof_conv1d_update_params(void) { return sizeof(mko_conv1d_update_params); }
+
+extern "C" int mko_conv1d_fwd(const mko_conv1d_params* p, void* stream) {
+  conv::Geo g;
+  int st = conv::make_geo(p, &g);
+  if (st != MKO_OK) return st;
+  if (g.rows == 0 || g.length == 0) return MKO_OK;
+  if (!p->x || !p->weight || !p->out) {
+    mko_set_error("conv1d_fwd: x, weight and out are required");
+    return MKO_EINVAL;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (g.width <= 4) conv::launch_fwd<4>(g, *p, s);
+  else if (g.width <= 8) conv::launch_fwd<8>(g, *p, s);
+  else conv::launch_fwd<32>(g, *p, s);
+  return mko_check_launch("conv1d_fwd");
+}
+
+extern "C" size_t mko_conv1d_bwd_workspace_size(const mko_conv1d_params* p) {
+  conv::Geo g;
+  if (conv::make_geo(p, &g) != MKO_OK) return 0;
+  return conv::partial_bytes(g);
+}
+
+extern "C" int mko_conv1d_bwd(const mko_conv1d_params* p, void* stream) {
+  conv::Geo g;
+  int st = conv::make_geo(p, &g);
+  if (st != MKO_OK) return st;
+  if (g.rows == 0 || g.length == 0) return MKO_OK;  // the caller zero-fills the gradients of an empty input
+  if (!p->x || !p->weight || !p->dout || !p->dx) {
+    mko_set_error("conv1d_bwd: x, weight, dout and dx are required");
+    return MKO_EINVAL;
+  }
+  const bool params = p->dweight || p->dbias;
+  const size_t need = conv::partial_bytes(g);
+  if (params && (!p->workspace || p->workspace_bytes < need)) {
+    mko_set_error("conv1d_bwd: workspace of %zu bytes needed, %zu given", need, p->workspace_bytes);
+    return MKO_EWORKSPACE;
+  }
+  float* partial = params ? static_cast<float*>(p->workspace) : nullptr;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (g.width <= 4) conv::launch_bwd<4>(g, *p, partial, s);
+  else if (g.width <= 8) conv::launch_bwd<8>(g, *p, partial, s);
+  else conv::launch_bwd<32>(g, *p, partial, s);
+  if (params) {
+    const int64_t n = g.channels * (g.width + 1);
+    MKO_TIMED("conv1d_finalize", s, conv::finalize<<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(g, *p, partial));
+  }
+  return mko_check_launch("conv1d_bwd");
+}
+
+extern "C" int mko_conv1d_update(const mko_conv1d_update_params* p, void* stream) {
+  if (!p) {
+    mko_set_error("conv1d_update: null parameters");
+    return MKO_EINVAL;
+  }
+  if (p->batch < 0 || p->channels < 0 || p->q < 0 || p->width < 1 || p->span < p->width - 1) {
+    mko_set_error("conv1d_update: bad sizes (span must be at least width - 1)");
+    return MKO_EINVAL;
+  }
+  if (p->dtype != MKO_F32 && p->dtype != MKO_F16 && p->dtype != MKO_BF16) {
+    mko_set_error("conv1d_update: unknown dtype %d", p->dtype);
+    return MKO_EINVAL;
+  }
+  const int64_t rows = p->batch * p->channels;
+  if (rows == 0 || p->q == 0) return MKO_OK;
+  if (!p->x || !p->state || !p->weight || !p->out) {
+    mko_set_error("conv1d_update: x, state, weight and out are required");
+    return MKO_EINVAL;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  MKO_TIMED("conv1d_update", s, conv::update<<<static_cast<unsigned>((rows + 255) / 256), 256, 0, s>>>(*p));
+  return mko_check_launch("conv1d_update");
+}

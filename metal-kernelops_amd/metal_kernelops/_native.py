@@ -86,6 +86,29 @@ class PathParams(ctypes.Structure):
     ]
 
 
+class Conv1dParams(ctypes.Structure):
+    """Mirror of ``mko_conv1d_params``."""
+
+    _fields_ = [
+        ("x", _vp), ("weight", _vp), ("bias", _vp), ("initial_state", _vp), ("out", _vp),
+        ("final_state", _vp), ("dout", _vp), ("dx", _vp), ("dweight", _vp), ("dbias", _vp),
+        ("dinitial", _vp), ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
+        ("batch", ctypes.c_int64), ("channels", ctypes.c_int64), ("length", ctypes.c_int64),
+        ("width", ctypes.c_int64), ("dtype", ctypes.c_int32), ("flags", ctypes.c_uint32),
+    ]
+
+
+class Conv1dUpdateParams(ctypes.Structure):
+    """Mirror of ``mko_conv1d_update_params``."""
+
+    _fields_ = [
+        ("x", _vp), ("state", _vp), ("weight", _vp), ("bias", _vp), ("out", _vp),
+        ("batch", ctypes.c_int64), ("channels", ctypes.c_int64), ("q", ctypes.c_int64),
+        ("span", ctypes.c_int64), ("width", ctypes.c_int64), ("state_stride_b", ctypes.c_int64),
+        ("state_stride_c", ctypes.c_int64), ("dtype", ctypes.c_int32), ("flags", ctypes.c_uint32),
+    ]
+
+
 _SIGNATURES = {
     "mko_abi_version": ([], ctypes.c_int),
     "mko_last_error": ([], ctypes.c_char_p),
@@ -95,6 +118,12 @@ _SIGNATURES = {
     "mko_sizeof_path_params": ([], ctypes.c_size_t),
     "mko_path_stack": ([ctypes.POINTER(PathParams), _vp], ctypes.c_int),
     "mko_path_merge": ([ctypes.POINTER(PathParams), _vp], ctypes.c_int),
+    "mko_sizeof_conv1d_params": ([], ctypes.c_size_t),
+    "mko_sizeof_conv1d_update_params": ([], ctypes.c_size_t),
+    "mko_conv1d_fwd": ([ctypes.POINTER(Conv1dParams), _vp], ctypes.c_int),
+    "mko_conv1d_bwd_workspace_size": ([ctypes.POINTER(Conv1dParams)], ctypes.c_size_t),
+    "mko_conv1d_bwd": ([ctypes.POINTER(Conv1dParams), _vp], ctypes.c_int),
+    "mko_conv1d_update": ([ctypes.POINTER(Conv1dUpdateParams), _vp], ctypes.c_int),
     "mko_ssd_saved_bytes": ([ctypes.POINTER(SsdParams)], ctypes.c_size_t),
     "mko_ssd_fwd_workspace_size": ([ctypes.POINTER(SsdParams)], ctypes.c_size_t),
     "mko_ssd_fwd": ([ctypes.POINTER(SsdParams), _vp], ctypes.c_int),
@@ -143,7 +172,9 @@ def lib():
         for struct, fn in ((SelscanParams, handle.mko_sizeof_selscan_params),
                            (StateUpdateParams, handle.mko_sizeof_state_update_params),
                            (SsdParams, handle.mko_sizeof_ssd_params),
-                           (PathParams, handle.mko_sizeof_path_params)):
+                           (PathParams, handle.mko_sizeof_path_params),
+                           (Conv1dParams, handle.mko_sizeof_conv1d_params),
+                           (Conv1dUpdateParams, handle.mko_sizeof_conv1d_update_params)):
             if ctypes.sizeof(struct) != fn():
                 raise RuntimeError(f"{struct.__name__} layout does not match libmko.so")
         _lib = handle

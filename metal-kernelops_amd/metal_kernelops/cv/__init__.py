@@ -2,12 +2,14 @@
 
 Same names as the reference's ``cv/__init__.py:15-40`` for the SSM scan path:
 the chunked SSD scan and the single-token decode update, each with its pure-torch
-reference twin, and the four-path 2D scan (VMamba's ss2d) built on the Mamba-1
-scan kernels.  The reference's other ``cv`` operators (causal conv, gated RMSNorm,
-NSA selection, RoIAlign) are not part of this package.
+reference twin, the four-path 2D scan (VMamba's ss2d) built on the Mamba-1 scan
+kernels, and the causal depthwise conv1d that precedes the scan in a Mamba block.
+The reference's other ``cv`` operators (gated RMSNorm, NSA selection, RoIAlign) are
+not part of this package.
 Importing it registers the ``mko::`` custom ops and launches nothing.
 """
 
+from .causal_conv1d import causal_conv1d_fn, causal_conv1d_ref, causal_conv1d_update
 from .mamba2_chunk import last_path, mamba2_chunk_scan, mamba2_chunk_scan_reference
 from .mamba2_state import CHECKED_TORCH, mamba2_state_update, mamba2_state_update_reference
 from .path_scan import MAX_STATES, MERGE_MODES, path_orders, ss2d_scan, ss2d_scan_reference
@@ -16,6 +18,9 @@ __all__ = [
     "CHECKED_TORCH",
     "MAX_STATES",
     "MERGE_MODES",
+    "causal_conv1d_fn",
+    "causal_conv1d_ref",
+    "causal_conv1d_update",
     "last_path",
     "mamba2_chunk_scan",
     "mamba2_chunk_scan_reference",

@@ -1,0 +1,317 @@
+"""Causal depthwise conv1d on MI355X: the convolution ahead of every Mamba block.
+
+Public surface, as in dbydd/metal-kernelops ``cv/causal_conv1d.py:495-756``:
+``causal_conv1d_fn`` (prefill over a sequence, with an analytic backward),
+``causal_conv1d_update`` (decode: q tokens against a rolling state, in place) and
+``causal_conv1d_ref`` (the pure-torch definition).
+
+With ``z = cat(initial_state or zeros(K-1), x)`` along time::
+
+    out[b, c, t] = act(bias[c] + sum_{j < K} weight[c, j] * z[b, c, t + j])
+    final_state  = z[..., L : L + K - 1]
+
+``act`` is ``None`` or SiLU (``"silu"`` / ``"swish"``).  Arithmetic follows
+``weight.dtype`` (x, bias and the state are cast to it) and the result comes back
+in ``x.dtype``, as in the reference; the HIP kernels compute in float32 and round
+once on the store.
+
+How it runs: ``mko::conv1d_fwd`` fuses the taps, the bias, the SiLU and (without
+autograd) the final state in one pass; ``mko::conv1d_bwd`` recomputes the
+pre-activation over each lane's window and writes dx, the initial-state gradient and
+deterministic per-segment tap/bias partials that a second kernel sums in a fixed
+order.  With a gradient in play the final state is a slice of ``cat(initial_state,
+x)`` taken in torch, so its gradient flows to both, as in the reference
+(``:483-492, 642-673``).  ``mko::conv1d_update`` advances the state through its
+strides in place.
+
+Differences from the reference: tensors live on the ROCm GPU (the reference's other
+devices and dtypes run an ATen composition, ``:471-480, 676-687``); float32, float16
+and bfloat16 run the kernels and other dtypes raise ``ValueError``; ``K <= 32``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Tuple
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor
+
+from .. import _native as nat
+from ..scan import _require_gpu
+
+__all__ = ["causal_conv1d_fn", "causal_conv1d_ref", "causal_conv1d_update"]
+
+_ACTIVATIONS = (None, "silu", "swish")
+_FLOATS = (torch.float32, torch.float16, torch.bfloat16)
+_SILU = 1
+_MAX_WIDTH = 32
+
+
+def _as_depthwise(weight):
+    """``(channels, 1, K)`` (nn.Conv1d with groups == channels) or ``(channels, K)`` -> ``(channels, K)``."""
+    if weight.dim() == 3:
+        if weight.shape[1] != 1:
+            raise ValueError(f"weight must be (channels, 1, K) for a depthwise convolution, got {tuple(weight.shape)}")
+        weight = weight[:, 0, :]
+    elif weight.dim() != 2:
+        raise ValueError(f"weight must be (channels, 1, K) or (channels, K), got {tuple(weight.shape)}")
+    if weight.shape[1] < 1:
+        raise ValueError("the kernel width must be at least 1")
+    return weight
+
+
+def _check_activation(activation):
+    if activation not in _ACTIVATIONS:
+        raise NotImplementedError(f"activation must be one of {_ACTIVATIONS}, got {activation!r}")
+
+
+def _final_state(z_input, initial_state, taps):
+    """The last ``taps`` columns of ``cat(initial_state or zeros, x)``, differentiable."""
+    length = z_input.shape[-1]
+    if length >= taps:
+        return z_input[..., length - taps:].contiguous()
+    head = (initial_state[..., length:] if initial_state is not None
+            else z_input.new_zeros(z_input.shape[:-1] + (taps - length,)))
+    return torch.cat([head, z_input], dim=-1)
+
+
+# --------------------------------------------------------------------------- kernels
+
+
+def _params(x, weight, bias, init, silu):
+    p = nat.Conv1dParams()
+    p.x, p.weight, p.bias, p.initial_state = nat.ptr(x), nat.ptr(weight), nat.ptr(bias), nat.ptr(init)
+    p.batch, p.channels, p.length = x.shape
+    p.width = weight.shape[1]
+    p.dtype = nat.code(x.dtype)
+    p.flags = _SILU if silu else 0
+    return p
+
+
+@torch.library.custom_op("mko::conv1d_fwd", mutates_args=(), device_types="cuda")
+def _conv1d_fwd(x: Tensor, weight: Tensor, bias: Optional[Tensor], init: Optional[Tensor], silu: bool,
+                write_final: bool) -> Tuple[Tensor, Tensor]:
+    out = torch.empty_like(x)
+    final = x.new_empty(x.shape[0], x.shape[1], weight.shape[1] - 1 if write_final else 0)
+    if x.numel() == 0:
+        return out, final
+    p = _params(x, weight, bias, init, silu)
+    p.out = out.data_ptr()
+    p.final_state = final.data_ptr() if write_final and final.numel() else None
+    nat.check(nat.lib().mko_conv1d_fwd(ctypes.byref(p), nat.stream_of(x.device)), "mko_conv1d_fwd")
+    return out, final
+
+
+@_conv1d_fwd.register_fake
+def _(x, weight, bias, init, silu, write_final):
+    return torch.empty_like(x), x.new_empty(x.shape[0], x.shape[1], weight.shape[1] - 1 if write_final else 0)
+
+
+@torch.library.custom_op("mko::conv1d_bwd", mutates_args=(), device_types="cuda")
+def _conv1d_bwd(dout: Tensor, x: Tensor, weight: Tensor, bias: Optional[Tensor], init: Optional[Tensor],
+                silu: bool, need_weight: bool, need_bias: bool, need_init: bool
+                ) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+    channels, width = weight.shape
+    dx = torch.empty_like(x)
+    dweight = weight.new_zeros(weight.shape) if need_weight else weight.new_empty(0)
+    dbias = weight.new_zeros(channels) if need_bias else weight.new_empty(0)
+    dinit = x.new_zeros(x.shape[0], channels, width - 1) if need_init else x.new_empty(0)
+    if x.numel() == 0:
+        return dx, dweight, dbias, dinit
+    p = _params(x, weight, bias, init, silu)
+    p.dout, p.dx = dout.data_ptr(), dx.data_ptr()
+    p.dweight = dweight.data_ptr() if need_weight else None
+    p.dbias = dbias.data_ptr() if need_bias else None
+    p.dinitial = dinit.data_ptr() if need_init and dinit.numel() else None
+    ws = nat.workspace(nat.lib().mko_conv1d_bwd_workspace_size(ctypes.byref(p)), x.device)
+    p.workspace, p.workspace_bytes = ws.data_ptr(), ws.numel()
+    nat.check(nat.lib().mko_conv1d_bwd(ctypes.byref(p), nat.stream_of(x.device)), "mko_conv1d_bwd")
+    return dx, dweight, dbias, dinit
+
+
+@_conv1d_bwd.register_fake
+def _(dout, x, weight, bias, init, silu, need_weight, need_bias, need_init):
+    channels, width = weight.shape
+    return (torch.empty_like(x), weight.new_empty(weight.shape if need_weight else (0,)),
+            weight.new_empty(channels if need_bias else 0),
+            x.new_empty((x.shape[0], channels, width - 1) if need_init else (0,)))
+
+
+def _setup(ctx, inputs, output):
+    x, weight, bias, init, silu, _ = inputs
+    ctx.save_for_backward(x, weight, bias, init)
+    ctx.silu = silu
+
+
+def _backward(ctx, dout, _dfinal):
+    x, weight, bias, init = ctx.saved_tensors
+    need = ctx.needs_input_grad
+    dx, dweight, dbias, dinit = torch.ops.mko.conv1d_bwd(
+        dout.contiguous(), x, weight, bias, init, ctx.silu, bool(need[1]), bool(need[2] and bias is not None),
+        bool(need[3] and init is not None))
+    return (dx, dweight if need[1] else None, dbias if need[2] and bias is not None else None,
+            dinit if need[3] and init is not None else None, None, None)
+
+
+torch.library.register_autograd("mko::conv1d_fwd", _backward, setup_context=_setup)
+
+
+@torch.library.custom_op("mko::conv1d_update", mutates_args=("state",), device_types="cuda")
+def _conv1d_update(x: Tensor, state: Tensor, weight: Tensor, bias: Optional[Tensor], silu: bool) -> Tensor:
+    out = torch.empty_like(x)
+    if x.numel() == 0:
+        return out
+    p = nat.Conv1dUpdateParams()
+    p.x, p.state, p.weight, p.bias, p.out = x.data_ptr(), state.data_ptr(), weight.data_ptr(), nat.ptr(bias), \
+        out.data_ptr()
+    p.batch, p.channels, p.q = x.shape
+    p.span, p.width = state.shape[-1], weight.shape[1]
+    p.state_stride_b, p.state_stride_c = state.stride(0), state.stride(1)
+    p.dtype, p.flags = nat.code(x.dtype), _SILU if silu else 0
+    nat.check(nat.lib().mko_conv1d_update(ctypes.byref(p), nat.stream_of(x.device)), "mko_conv1d_update")
+    return out
+
+
+@_conv1d_update.register_fake
+def _(x, state, weight, bias, silu):
+    return torch.empty_like(x)
+
+
+# --------------------------------------------------------------------------- public API
+
+
+def causal_conv1d_ref(x, weight, bias=None, activation=None, initial_state=None, return_final_state=False):
+    """Reference definition, explicit taps on any device and dtype, differentiable.
+
+    Same contract as :func:`causal_conv1d_fn` (``cv/causal_conv1d.py:495-530``):
+    computed in ``weight.dtype``, rounded to ``x.dtype``, then the SiLU.
+    """
+    weight = _as_depthwise(weight)
+    _check_activation(activation)
+    channels, width = weight.shape
+    if x.dim() != 3 or x.shape[1] != channels:
+        raise ValueError(f"x must be (batch, {channels}, length), got {tuple(x.shape)}")
+    taps, length = width - 1, x.shape[-1]
+    z = x.to(weight.dtype)
+    lead = initial_state.to(weight.dtype) if initial_state is not None else z.new_zeros(z.shape[:-1] + (taps,))
+    z = torch.cat([lead, z], dim=-1)
+    out = sum(z[..., j:j + length] * weight[:, j].view(1, channels, 1) for j in range(width))
+    if bias is not None:
+        out = out + bias.to(weight.dtype).view(1, channels, 1)
+    out = out.to(x.dtype)
+    if activation is not None:
+        out = F.silu(out)
+    if return_final_state:
+        return out, z[..., length:].to(x.dtype)
+    return out
+
+
+def causal_conv1d_fn(x, weight, bias=None, activation=None, initial_state=None, return_final_state=False):
+    """Causal depthwise conv1d over a whole sequence on the ROCm GPU.
+
+    Args:
+        x: ``(batch, channels, length)``.
+        weight: ``(channels, 1, K)`` depthwise, or ``(channels, K)``; ``K <= 32``.
+        bias: ``(channels,)`` or ``None``.
+        activation: ``None``, ``"silu"`` or ``"swish"``.
+        initial_state: ``(batch, channels, K-1)`` entering the sequence.
+        return_final_state: also return the state leaving the sequence.
+
+    Returns:
+        ``(batch, channels, length)`` in ``x.dtype``, or ``(out, final_state)`` with
+        ``final_state`` of shape ``(batch, channels, K-1)``.
+    """
+    weight = _as_depthwise(weight)
+    _check_activation(activation)
+    if x.dim() != 3:
+        raise ValueError(f"x must be (batch, channels, length), got {tuple(x.shape)}")
+    channels, width = weight.shape
+    if x.shape[1] != channels:
+        raise ValueError(f"x has {x.shape[1]} channels, weight has {channels}")
+    if bias is not None and (bias.dim() != 1 or bias.shape[0] != channels):
+        raise ValueError(f"bias must be ({channels},), got {tuple(bias.shape)}")
+    if initial_state is not None:
+        expected = (x.shape[0], channels, width - 1)
+        if tuple(initial_state.shape) != expected:
+            raise ValueError(f"initial_state must be {expected}, got {tuple(initial_state.shape)}")
+    for name, t in (("x", x), ("weight", weight), ("bias", bias), ("initial_state", initial_state)):
+        if t is not None:
+            _require_gpu(t)
+    if weight.dtype not in _FLOATS:
+        raise ValueError(f"causal_conv1d_fn computes in weight.dtype; float32, float16 or bfloat16, got {weight.dtype}")
+    if width > _MAX_WIDTH:
+        raise ValueError(f"the kernel width must be at most {_MAX_WIDTH}, got {width}")
+
+    compute = weight.dtype
+    work = x.to(compute).contiguous()
+    init = initial_state.to(compute).contiguous() if initial_state is not None else None
+    shift = bias.to(compute).contiguous() if bias is not None else None
+    grads = torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (work, weight, init, shift))
+    # without autograd the kernel writes the final state; with it, the final state is a
+    # slice of cat(initial_state, x) so that its gradient reaches both
+    fused_final = return_final_state and not grads
+    out, final = torch.ops.mko.conv1d_fwd(work, weight.contiguous(), shift, init, activation is not None,
+                                          bool(fused_final and work.numel()))
+    out = out.to(x.dtype)
+    if not return_final_state:
+        return out
+    if not (fused_final and work.numel()):
+        final = _final_state(work, init, width - 1)
+    return out, final.to(x.dtype)
+
+
+def causal_conv1d_update(x, state, weight, bias=None, activation=None):
+    """Advance the causal convolution by ``q`` tokens, updating ``state`` in place.
+
+    Args:
+        x: ``(batch, channels)`` or ``(batch, channels, q)``.
+        state: ``(batch, channels, s)``, ``s >= K-1``, last stride 1 (it may be a slice of a
+            larger cache), overwritten with ``cat(state, x)[..., -s:]``.
+        weight: ``(channels, 1, K)`` or ``(channels, K)``.
+        bias: ``(channels,)`` or ``None``.
+        activation: ``None``, ``"silu"`` or ``"swish"``.
+
+    Returns:
+        ``(batch, channels)`` or ``(batch, channels, q)``, matching the rank of ``x``.  The
+        decode path carries no autograd (``cv/causal_conv1d.py:690-756``).
+    """
+    weight = _as_depthwise(weight)
+    _check_activation(activation)
+    squeezed = x.dim() == 2
+    if squeezed:
+        x = x.unsqueeze(-1)
+    if x.dim() != 3:
+        raise ValueError(f"x must be (batch, channels) or (batch, channels, q), got {tuple(x.shape)}")
+    channels, width = weight.shape
+    taps = width - 1
+    batch, xchannels, _ = x.shape
+    if xchannels != channels:
+        raise ValueError(f"x has {xchannels} channels, weight has {channels}")
+    if state.dim() != 3 or state.shape[0] != batch or state.shape[1] != channels:
+        raise ValueError(f"state must be ({batch}, {channels}, s) with s >= {taps}, got {tuple(state.shape)}")
+    span = state.shape[-1]
+    if span < taps:
+        raise ValueError(f"state must hold at least K-1 = {taps} columns, got {span}")
+    if state.stride(-1) != 1:
+        raise ValueError(f"state must have stride 1 in its last dimension, got {state.stride()}")
+    if bias is not None and (bias.dim() != 1 or bias.shape[0] != channels):
+        raise ValueError(f"bias must be ({channels},), got {tuple(bias.shape)}")
+    if x.requires_grad or weight.requires_grad or state.requires_grad:
+        raise RuntimeError("causal_conv1d_update is the decode path and carries no autograd")
+    for t in (x, state, weight, bias):
+        if t is not None:
+            _require_gpu(t)
+    if state.dtype not in _FLOATS:
+        raise ValueError(f"state must be float32, float16 or bfloat16, got {state.dtype}")
+    if width > _MAX_WIDTH:
+        raise ValueError(f"the kernel width must be at most {_MAX_WIDTH}, got {width}")
+    # the kernel reads and writes every tensor in the state's dtype, computing in float32
+    dtype = state.dtype
+    work = x.to(dtype).contiguous()
+    out = torch.ops.mko.conv1d_update(work, state, weight.to(dtype).contiguous(),
+                                      bias.to(dtype).contiguous() if bias is not None else None,
+                                      activation is not None)
+    out = out.to(x.dtype)
+    return out.squeeze(-1) if squeezed else out

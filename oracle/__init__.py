@@ -23,3 +23,4 @@ from .ssm import (  # noqa: F401
     ss2d_scan,
     ssd_minimal_discrete,
 )
+from .conv1d import causal_conv1d, causal_conv1d_update  # noqa: F401,E402
