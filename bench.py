@@ -15,8 +15,8 @@ bytes per launch over its average launch time, both measured live with HIP event
 recorded by libmko on the kernel's own stream.  ``cpu_baseline`` times the float64
 oracle's restatement (run in float32 with autograd) on a bounded sample on this
 host.  ``also`` carries the other workloads of the path (Mamba-1 130M layer,
-Mamba-2 decode, Mamba-2 SSD chunk scan, the four-path 2D scan) with their own
-rooflines.
+Mamba-2 decode, Mamba-2 SSD chunk scan, the four-path 2D scan, the causal conv1d
+ahead of the scan) with their own rooflines.
 """
 
 from __future__ import annotations
@@ -401,6 +401,80 @@ def ss2d_cpu_baseline(shape=(1, 96, 1, 16, 28, 28)):
                       f"{best:.2f} s"}
 
 
+# --------------------------------------------------------------------- causal conv1d
+
+CONV_SHAPE = (4, 5120, 4096, 4)  # batch, channels, length, width: the conv ahead of the c3 scan
+
+
+def conv1d_bytes(batch, channels, length, width, esz=2):
+    """Algorithmic bytes (fwd, bwd): x in, out; x, dout in, dx out (weights negligible)."""
+    e = batch * channels * length
+    return 2 * e * esz, 3 * e * esz
+
+
+def conv1d_case(steps, warmup, shape=CONV_SHAPE):
+    from metal_kernelops.cv import causal_conv1d_fn, causal_conv1d_update
+    batch, channels, length, width = shape
+    g = torch.Generator().manual_seed(0)
+    dev = torch.device("cuda")
+    x = torch.randn(batch, channels, length, generator=g).bfloat16().to(dev).requires_grad_(True)
+    w = (0.5 * torch.randn(channels, 1, width, generator=g)).bfloat16().to(dev).requires_grad_(True)
+    b = torch.randn(channels, generator=g).bfloat16().to(dev).requires_grad_(True)
+    dout = torch.randn(batch, channels, length, generator=g).bfloat16().to(dev)
+
+    def step():
+        out = causal_conv1d_fn(x, w, b, "silu")
+        torch.autograd.grad(out, (x, w, b), dout)
+
+    ms, wall, kernels = timed(step, steps, warmup)
+    fwd_b, bwd_b = conv1d_bytes(*shape)
+    name, avg, count = dominant(kernels)
+    per_kernel = {"conv1d_bwd": bwd_b, "conv1d_fwd": fwd_b}
+    roof = roofline(per_kernel.get(name, fwd_b + bwd_b), avg)
+    roof["kernel"] = name
+    roof["algorithmic_bytes"] = per_kernel.get(name, fwd_b + bwd_b)
+    # decode: one token against a 3-column state, 64 x 2048 (the reference's update-64x2048x1)
+    xs = torch.randn(64, 2048, generator=g).to(dev)
+    state = torch.randn(64, 2048, 3, generator=g).to(dev)
+    wd, bd = (0.5 * torch.randn(2048, 4, generator=g)).to(dev), torch.randn(2048, generator=g).to(dev)
+    with torch.no_grad():
+        dms, _, _ = timed(lambda: causal_conv1d_update(xs, state, wd, bd, "silu"), 200, 20)
+    del x, w, b, dout
+    torch.cuda.empty_cache()
+    return {"ms_per_step": ms, "wall_ms_per_step": wall, "gbs": (fwd_b + bwd_b) / (ms * 1e-3) / 1e9,
+            "bytes_per_step": fwd_b + bwd_b, "roofline": roof, "update_us": dms * 1e3,
+            "kernels_ms": {k: round(v[0] / max(v[1], 1), 4) for k, v in sorted(kernels.items())}}
+
+
+def conv1d_cpu_baseline(shape=(1, 1024, 4096, 4)):
+    """The oracle's window product in float32 with autograd, on a bounded sample."""
+    import oracle
+    torch.set_num_threads(os.cpu_count() or 1)
+    batch, channels, length, width = shape
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(batch, channels, length, generator=g).requires_grad_(True)
+    w = (0.5 * torch.randn(channels, 1, width, generator=g)).requires_grad_(True)
+    b = torch.randn(channels, generator=g).requires_grad_(True)
+    dout = torch.randn(batch, channels, length, generator=g)
+
+    def run():
+        out, _ = oracle.causal_conv1d(x, w, b, "silu", dtype=torch.float32)
+        torch.autograd.grad(out, (x, w, b), dout)
+
+    run()
+    best = None
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run()
+        dt = time.perf_counter() - t0
+        best = dt if best is None else min(best, dt)
+    fwd_b, bwd_b = conv1d_bytes(*shape, esz=4)
+    return {"value": round((fwd_b + bwd_b) / best / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"causal conv1d fwd+bwd at {shape} (batch, channels, length, width), float32 window "
+                      f"product with autograd (oracle/conv1d.py), best of 3 after 1 warm-up: {best * 1e3:.1f} ms"}
+
+
 # --------------------------------------------------------------------- main
 
 
@@ -410,7 +484,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-cpu", action="store_true", help="skip the CPU baseline legs")
-    ap.add_argument("--only", choices=["mamba1", "ssd", "decode", "ss2d", "copy", "all"], default="all",
+    ap.add_argument("--only", choices=["mamba1", "ssd", "decode", "ss2d", "conv1d", "copy", "all"], default="all",
                     help="one workload (mamba1 = the config-3 headline alone) or all of them; copy = "
                          "a plain 1 GiB device copy, the calibration point of the PMC byte counters")
     args = ap.parse_args()
@@ -484,6 +558,19 @@ def main():
                            dtype="f32"),
             "roofline": s2["roofline"], "kernels_ms": s2["kernels_ms"]}
         log(f"  {s2['ms_per_step']:.3f} ms/step, {s2['gbs']:.1f} GB/s; kernels {s2['kernels_ms']}")
+    if want("conv1d"):
+        log(f"causal conv1d {CONV_SHAPE} (batch, channels, length, width) fwd+bwd, bf16, silu")
+        cv = conv1d_case(args.steps, args.warmup)
+        also["causal_conv1d_fwd_bwd"] = {
+            "value": round(cv["gbs"], 1), "unit": "GB/s", "ms_per_step": round(cv["ms_per_step"], 4),
+            "config": dict(zip(("batch", "channels", "length", "width"), CONV_SHAPE), dtype="bf16",
+                           activation="silu"),
+            "roofline": cv["roofline"], "kernels_ms": cv["kernels_ms"],
+            "decode_update_us": round(cv["update_us"], 2),
+            "decode_update_config": {"batch": 64, "channels": 2048, "q": 1, "width": 4, "state_columns": 3,
+                                     "dtype": "f32"}}
+        log(f"  {cv['ms_per_step']:.3f} ms/step, {cv['gbs']:.1f} GB/s; decode update {cv['update_us']:.1f} us; "
+            f"kernels {cv['kernels_ms']}")
     if head is None:  # a single non-headline workload: print its own record
         print(json.dumps(also), flush=True)
         return
@@ -498,6 +585,8 @@ def main():
             also["mamba2_ssd_chunk_scan_fwd_bwd"]["cpu_baseline"] = ssd_cpu_baseline()
         if "ss2d_four_path_scan_fwd_bwd" in also:
             also["ss2d_four_path_scan_fwd_bwd"]["cpu_baseline"] = ss2d_cpu_baseline()
+        if "causal_conv1d_fwd_bwd" in also:
+            also["causal_conv1d_fwd_bwd"]["cpu_baseline"] = conv1d_cpu_baseline()
     line = {
         "metric": METRIC,
         "value": round(head["gbs"], 1),

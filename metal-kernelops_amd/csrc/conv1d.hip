@@ -4,14 +4,16 @@
 //   pre[b, c, t] = bias[c] + sum_{j < K} w[c, j] z[b, c, t + j]      (z index t + j = time t - m + j)
 //   out          = act(pre),  act = identity or silu
 //   final_state  = z[..., L : L + m]
-// Forward: one lane per 8-step block of a row; the block is a 16-byte vector load on
-// aligned rows and the m look-back steps are scalar loads from the row (or from the
-// initial state / zero padding before t = 0).  Backward: a lane recomputes pre over its
-// block's window (m steps either side), writes dx for its 8 steps, and the taps'
+// The forward gives a lane one 8-step block (one 16-byte vector load on aligned rows, so
+// a wavefront's loads are whole lines) plus the look-back steps.  In the backward a lane
+// walks RB consecutive blocks of one row with sliding register windows: one vector load
+// of x and of dout per block, the look-back and look-ahead steps carried over.
+// Backward: the lane recomputes pre over its window, writes dx, and sums the taps'
 // gradients dw[c, j] = sum_t g[t] z[t - m + j] and dbias = sum_t g[t] (g = dout act'(pre))
-// are reduced over the lanes of a row segment, then over batch and segments in a fixed
-// order by `finalize`, so they are deterministic.  Decode: one lane per row advances a
-// rolling state of `span` columns by q tokens in place.
+// over its steps; 16 lanes of a row add theirs with DPP, and `finalize` adds those
+// partials over batch and along the row in a fixed order, so the sums are deterministic.
+// Decode: one lane per row advances a rolling state of `span` columns by q tokens in
+// place.
 #include "common.hpp"
 #include "io.hpp"
 
@@ -19,14 +21,16 @@ namespace mko {
 namespace conv {
 namespace {
 
-constexpr int BS = 8;  // steps per lane
+constexpr int BS = 8;  // steps per block
+constexpr int RB = 4;  // blocks per lane in the backward (the forward takes one: its loads
+                       // are whole-wavefront lines only when neighbouring lanes hold
+                       // neighbouring blocks)
 
 struct Geo {
   int64_t batch, channels, length, rows;  // rows = batch * channels
   int width, taps;                          // taps = width - 1
   int64_t nblk;                             // blocks of BS steps per row
-  int tpr;                                  // lanes per row segment (power of two <= 256)
-  int64_t nseg;                             // segments per row = ceil(nblk / tpr)
+  int64_t lpr;                              // lanes per row: ceil(nblk / RB), rounded up to 16
   int dtype;
   int silu;
   int vec;                                  // rows are 16-byte aligned whole blocks
@@ -49,13 +53,27 @@ __device__ __forceinline__ void load_taps(const Geo& g, const void* weight, int6
   for (int j = 0; j < KMAX; ++j) wp[j] = j >= lead ? load_one(weight, g.dtype, c * g.width + (j - lead)) : 0.0f;
 }
 
-// The BS steps of a block at t0 (t0 + BS <= length when vec).
-__device__ __forceinline__ void load_block(const Geo& g, const void* x, int64_t row, int64_t t0, float (&v)[BS]) {
-  if (g.vec) {
-    load_run<BS>(x, g.dtype, row * g.length + t0, BS, true, v);
+// The BS steps of block `blk` of a row as floats (zero past the end of the row).
+__device__ __forceinline__ void row_block(const Geo& g, const void* src, int64_t row, int64_t blk, float (&v)[BS]) {
+  const int64_t t0 = blk * BS;
+  if (blk >= g.nblk) {
+#pragma unroll
+    for (int e = 0; e < BS; ++e) v[e] = 0.0f;
+  } else if (g.vec) {
+    load_run<BS>(src, g.dtype, row * g.length + t0, BS, true, v);
   } else {
 #pragma unroll
-    for (int e = 0; e < BS; ++e) v[e] = t0 + e < g.length ? load_one(x, g.dtype, row * g.length + t0 + e) : 0.0f;
+    for (int e = 0; e < BS; ++e) v[e] = t0 + e < g.length ? load_one(src, g.dtype, row * g.length + t0 + e) : 0.0f;
+  }
+}
+
+__device__ __forceinline__ void row_store(const Geo& g, void* dst, int64_t row, int64_t t0, const float (&v)[BS]) {
+  if (g.vec) {
+    store_run<BS>(dst, g.dtype, row * g.length + t0, BS, true, v);
+  } else {
+#pragma unroll
+    for (int s = 0; s < BS; ++s)
+      if (t0 + s < g.length) store_one(dst, g.dtype, row * g.length + t0 + s, v[s]);
   }
 }
 
@@ -69,157 +87,174 @@ __device__ __forceinline__ float act_grad(const Geo& g, float v) {
 template <int KMAX>
 __global__ void __launch_bounds__(256) forward(Geo g, mko_conv1d_params p) {
   constexpr int H = KMAX - 1;
+  constexpr int RF = 1;  // blocks per lane
   const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (e >= g.rows * g.nblk) return;
-  const int64_t row = e / g.nblk, blk = e % g.nblk, c = row % g.channels;
-  const int64_t t0 = blk * BS;
+  const int64_t row = e / g.nblk, blk0 = e % g.nblk, c = row % g.channels;
   float wp[KMAX];
   load_taps<KMAX>(g, p.weight, c, wp);
   const float bias = p.bias ? load_one(p.bias, g.dtype, c) : 0.0f;
-  // zz[i] = z(t0 - H + i)
+  // zz[i] = z(t0 - H + i); the first H carry over from the previous block
   float zz[H + BS];
 #pragma unroll
-  for (int i = 0; i < H; ++i) zz[i] = i >= H - g.taps ? z_at(g, p.x, p.initial_state, row, t0 - H + i) : 0.0f;
-  float cur[BS];
-  load_block(g, p.x, row, t0, cur);
+  for (int i = 0; i < H; ++i) zz[i] = i >= H - g.taps ? z_at(g, p.x, p.initial_state, row, blk0 * BS - H + i) : 0.0f;
+  float nxt[BS];
+  row_block(g, p.x, row, blk0, nxt);
+  for (int r = 0; r < RF; ++r) {
+    const int64_t blk = blk0 + r;
+    if (blk >= g.nblk) break;
+    const int64_t t0 = blk * BS;
 #pragma unroll
-  for (int i = 0; i < BS; ++i) zz[H + i] = cur[i];
-  float o[BS];
+    for (int i = 0; i < BS; ++i) zz[H + i] = nxt[i];
+    if (r + 1 < RF) row_block(g, p.x, row, blk + 1, nxt);  // in flight during this block
+    float o[BS];
 #pragma unroll
-  for (int s = 0; s < BS; ++s) {
-    float acc = bias;
+    for (int s = 0; s < BS; ++s) {
+      float acc = bias;
 #pragma unroll
-    for (int j = 0; j < KMAX; ++j) acc = fmaf(wp[j], zz[s + j], acc);
-    o[s] = act(g, acc);
-  }
-  if (g.vec) {
-    store_run<BS>(p.out, g.dtype, row * g.length + t0, BS, true, o);
-  } else {
+      for (int j = 0; j < KMAX; ++j) acc = fmaf(wp[j], zz[s + j], acc);
+      o[s] = act(g, acc);
+    }
+    row_store(g, p.out, row, t0, o);
 #pragma unroll
-    for (int s = 0; s < BS; ++s)
-      if (t0 + s < g.length) store_one(p.out, g.dtype, row * g.length + t0 + s, o[s]);
-  }
-  if (p.final_state && blk == g.nblk - 1) {
-    for (int m = 0; m < g.taps; ++m)
-      store_one(p.final_state, g.dtype, row * g.taps + m, z_at(g, p.x, p.initial_state, row, g.length - g.taps + m));
+    for (int i = 0; i < H; ++i) zz[i] = zz[BS + i];
+    if (p.final_state && blk == g.nblk - 1) {
+      for (int m = 0; m < g.taps; ++m)
+        store_one(p.final_state, g.dtype, row * g.taps + m, z_at(g, p.x, p.initial_state, row, g.length - g.taps + m));
+    }
   }
 }
 
-// Sum over the `tpr` lanes of a row segment (lanes tpr-aligned within the workgroup);
-// every lane of the segment gets it.  red: 256 floats of LDS, barrier-protected.
-__device__ __forceinline__ float segment_sum(float v, int tpr, float* red) {
-  const int lane = threadIdx.x & 63;
-  const int span = tpr < 64 ? tpr : 64;
-  for (int off = 1; off < span; off <<= 1) v += __shfl_xor(v, off);
-  if (tpr <= 64) return v;
-  // segments wider than a wavefront: add the wavefront sums of the segment in order
-  __syncthreads();
-  if (lane == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  const int first = (static_cast<int>(threadIdx.x) / tpr) * (tpr / 64);
-  float s = 0.0f;
-  for (int w = 0; w < tpr / 64; ++w) s += red[first + w];
-  return s;
+// Sum over the 16 lanes of a DPP row, every one of them gets it: swap neighbours and
+// pairs (quad_perm), then add the other quad (row_half_mirror), then the other half
+// row (row_mirror).
+__device__ __forceinline__ float row16_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xb1, 0xf, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4e, 0xf, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xf, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xf, 0xf, false));
+  return v;
 }
 
 template <int KMAX>
 __global__ void __launch_bounds__(256) backward(Geo g, mko_conv1d_params p, float* partial) {
   constexpr int H = KMAX - 1;
-  __shared__ float red[4];
-  const int rpw = 256 / g.tpr;  // row segments per workgroup
-  const int64_t seg_id = static_cast<int64_t>(blockIdx.x) * rpw + threadIdx.x / g.tpr;
-  const bool live_seg = seg_id < g.rows * g.nseg;
-  const int64_t row = live_seg ? seg_id / g.nseg : 0, seg = live_seg ? seg_id % g.nseg : 0;
-  const int64_t blk = seg * g.tpr + threadIdx.x % g.tpr;
-  const bool live = live_seg && blk < g.nblk;
+  // The grid covers whole 16-lane groups of one row each (lpr is a multiple of 16), and
+  // every lane reaches the DPP sums at the end.
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const bool in_grid = e < g.rows * g.lpr;
+  const int64_t row = in_grid ? e / g.lpr : 0, blk0 = in_grid ? (e % g.lpr) * RB : g.nblk;
   const int64_t c = row % g.channels;
-  const int64_t t0 = blk * BS;
   float wp[KMAX];
   load_taps<KMAX>(g, p.weight, c, wp);
   const float bias = p.bias ? load_one(p.bias, g.dtype, c) : 0.0f;
   float dwp[KMAX], dbp = 0.0f;
 #pragma unroll
   for (int j = 0; j < KMAX; ++j) dwp[j] = 0.0f;
-  if (live) {
-    // zz[i] = z(t0 - H + i) over the window pre(t0 .. t0 + BS - 1 + H) reads
-    float zz[BS + 2 * H];
+  if (blk0 < g.nblk) {
+    // zz[i] = z(t0 - H + i) over [t0 - H, t0 + BS + H); zn, dn: the next block of x, dout
+    float zz[BS + 2 * H], zn[BS], dc[BS], dn[BS];
 #pragma unroll
-    for (int i = 0; i < BS + 2 * H; ++i) zz[i] = z_at(g, p.x, p.initial_state, row, t0 - H + i);
-    // gg[i] = g(t0 + i) = dout act'(pre), zero from the end of the row
-    float gg[BS + H];
+    for (int i = 0; i < H; ++i) zz[i] = z_at(g, p.x, p.initial_state, row, blk0 * BS - H + i);
+    {
+      float cur[BS];
+      row_block(g, p.x, row, blk0, cur);
 #pragma unroll
-    for (int i = 0; i < BS + H; ++i) {
-      const int64_t t = t0 + i;
-      float gv = 0.0f;
-      if (t < g.length) {
+      for (int i = 0; i < BS; ++i) zz[H + i] = cur[i];
+    }
+    row_block(g, p.x, row, blk0 + 1, zn);
+    row_block(g, p.dout, row, blk0, dc);
+    row_block(g, p.dout, row, blk0 + 1, dn);
+    for (int r = 0; r < RB; ++r) {
+      const int64_t blk = blk0 + r;
+      if (blk >= g.nblk) break;
+      const int64_t t0 = blk * BS;
+      // look-ahead z: the next block, then (taps beyond a block) single steps
+#pragma unroll
+      for (int i = 0; i < H; ++i) zz[H + BS + i] = i < BS ? zn[i] : z_at(g, p.x, p.initial_state, row, t0 + BS + i);
+      // gg[i] = g(t0 + i) = dout act'(pre), zero from the end of the row
+      float gg[BS + H];
+#pragma unroll
+      for (int i = 0; i < BS + H; ++i) {
         float pre = bias;
 #pragma unroll
         for (int j = 0; j < KMAX; ++j) pre = fmaf(wp[j], zz[i + j], pre);
-        gv = load_one(p.dout, g.dtype, row * g.length + t) * act_grad(g, pre);
+        const bool in_row = t0 + i < g.length;
+        const float d = i < BS ? dc[i]
+                               : (i - BS < BS ? dn[i - BS] : (in_row ? load_one(p.dout, g.dtype, row * g.length + t0 + i) : 0.0f));
+        gg[i] = in_row ? d * act_grad(g, pre) : 0.0f;
       }
-      gg[i] = gv;
-    }
-    // dx(t) = sum_j' wp[j'] g(t + H - j')
-    float dxo[BS];
+      // dx(t) = sum_j' wp[j'] g(t + H - j')
+      float dxo[BS];
 #pragma unroll
-    for (int s = 0; s < BS; ++s) {
-      float acc = 0.0f;
-#pragma unroll
-      for (int j = 0; j < KMAX; ++j) acc = fmaf(wp[j], gg[s + H - j], acc);
-      dxo[s] = acc;
-    }
-    if (g.vec) {
-      store_run<BS>(p.dx, g.dtype, row * g.length + t0, BS, true, dxo);
-    } else {
-#pragma unroll
-      for (int s = 0; s < BS; ++s)
-        if (t0 + s < g.length) store_one(p.dx, g.dtype, row * g.length + t0 + s, dxo[s]);
-    }
-    // taps (padded index) and bias over this block's own steps
-#pragma unroll
-    for (int s = 0; s < BS; ++s) {
-      dbp += gg[s];
-#pragma unroll
-      for (int j = 0; j < KMAX; ++j) dwp[j] = fmaf(gg[s], zz[s + j], dwp[j]);
-    }
-    // initial state: z(tau), -taps <= tau < 0, feeds pre(t) at t = tau + H - j'
-    if (p.dinitial && blk == 0) {
-#pragma unroll
-      for (int k = 1; k <= H; ++k) {  // tau = -k
+      for (int s = 0; s < BS; ++s) {
         float acc = 0.0f;
 #pragma unroll
-        for (int j = 0; j < KMAX; ++j) {
-          const int i = H - k - j;  // t = tau + H - j' relative to t0 = 0
-          if (i >= 0) acc = fmaf(wp[j], gg[i], acc);
+        for (int j = 0; j < KMAX; ++j) acc = fmaf(wp[j], gg[s + H - j], acc);
+        dxo[s] = acc;
+      }
+      row_store(g, p.dx, row, t0, dxo);
+      // taps (padded index) and bias over this block's own steps
+#pragma unroll
+      for (int s = 0; s < BS; ++s) {
+        dbp += gg[s];
+#pragma unroll
+        for (int j = 0; j < KMAX; ++j) dwp[j] = fmaf(gg[s], zz[s + j], dwp[j]);
+      }
+      // initial state: z(tau), -taps <= tau < 0, feeds pre(t) at t = tau + H - j'
+      if (p.dinitial && blk == 0) {
+#pragma unroll
+        for (int k = 1; k <= H; ++k) {
+          float acc = 0.0f;
+#pragma unroll
+          for (int j = 0; j < KMAX; ++j) {
+            const int i = H - k - j;
+            if (i >= 0) acc = fmaf(wp[j], gg[i], acc);
+          }
+          if (k <= g.taps) store_one(p.dinitial, g.dtype, row * g.taps + (g.taps - k), acc);
         }
-        if (k <= g.taps) store_one(p.dinitial, g.dtype, row * g.taps + (g.taps - k), acc);
+      }
+      // slide by one block; the loads of the block after next fly during the next one
+#pragma unroll
+      for (int i = 0; i < H; ++i) zz[i] = zz[BS + i];
+#pragma unroll
+      for (int i = 0; i < BS; ++i) {
+        zz[H + i] = zn[i];
+        dc[i] = dn[i];
+      }
+      if (r + 1 < RB) {
+        row_block(g, p.x, row, blk + 2, zn);
+        row_block(g, p.dout, row, blk + 2, dn);
       }
     }
   }
   if (!partial) return;
-  // one partial per (row, segment): the K taps, then the bias
-  float* dst = partial + (live_seg ? seg_id : 0) * (g.width + 1);
+  // one partial per 16-lane group of a row: the K taps, then the bias
   const int lead = KMAX - g.width;
+  float* dst = partial + (in_grid ? e / 16 : 0) * (g.width + 1);
+  const bool writer = in_grid && (threadIdx.x & 15) == 0;
 #pragma unroll
   for (int j = 0; j < KMAX; ++j) {
     if (j < lead) continue;  // uniform
-    const float v = segment_sum(dwp[j], g.tpr, red);
-    if (live_seg && threadIdx.x % g.tpr == 0) dst[j - lead] = v;
+    const float v = row16_sum(dwp[j]);
+    if (writer) dst[j - lead] = v;
   }
-  const float vb = segment_sum(dbp, g.tpr, red);
-  if (live_seg && threadIdx.x % g.tpr == 0) dst[g.width] = vb;
+  const float vb = row16_sum(dbp);
+  if (writer) dst[g.width] = vb;
 }
 
-// dweight[c, j] and dbias[c]: partials summed over batch then segments, in order.
+// dweight[c, j] and dbias[c]: the 16-lane partials summed over batch, then along the
+// row, in order.
 __global__ void __launch_bounds__(256) finalize(Geo g, mko_conv1d_params p, const float* partial) {
   const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (e >= g.channels * (g.width + 1)) return;
   const int64_t c = e / (g.width + 1);
   const int j = static_cast<int>(e % (g.width + 1));
+  const int64_t groups = g.lpr / 16;
   float s = 0.0f;
   for (int64_t b = 0; b < g.batch; ++b) {
     const int64_t row = b * g.channels + c;
-    for (int64_t seg = 0; seg < g.nseg; ++seg) s += partial[(row * g.nseg + seg) * (g.width + 1) + j];
+    for (int64_t k = 0; k < groups; ++k) s += partial[(row * groups + k) * (g.width + 1) + j];
   }
   if (j < g.width) {
     if (p.dweight) store_one(p.dweight, g.dtype, c * g.width + j, s);
@@ -245,7 +280,8 @@ __global__ void __launch_bounds__(256) update(mko_conv1d_update_params p) {
   };
   for (int64_t t = 0; t < p.q; ++t) {
     float acc = bias;
-    for (int64_t j = 0; j < p.width; ++j) acc = fmaf(load_one(p.weight, dt, c * p.width + j), joined(p.span + t - taps + j), acc);
+    for (int64_t j = 0; j < p.width; ++j)
+      acc = fmaf(load_one(p.weight, dt, c * p.width + j), joined(p.span + t - taps + j), acc);
     store_one(p.out, dt, row * p.q + t, silu ? acc * sigmoid(acc) : acc);
   }
   // shift: the new column i is joined[q + i]; ascending order never overwrites a state
@@ -279,17 +315,13 @@ int make_geo(const mko_conv1d_params* p, Geo* g) {
   g->width = static_cast<int>(p->width);
   g->taps = g->width - 1;
   g->nblk = (p->length + BS - 1) / BS;
-  int tpr = 1;
-  while (tpr < 256 && tpr < g->nblk) tpr <<= 1;
-  g->tpr = tpr;
-  g->nseg = (g->nblk + tpr - 1) / tpr;
+  g->lpr = ((g->nblk + RB - 1) / RB + 15) / 16 * 16;
   g->dtype = p->dtype;
   g->silu = (p->flags & MKO_CONV_SILU) != 0;
-  const int esz = p->dtype == MKO_F32 ? 4 : 2;
   const uintptr_t mask = 15u;
   g->vec = p->length % BS == 0 && (reinterpret_cast<uintptr_t>(p->x) & mask) == 0 &&
            (reinterpret_cast<uintptr_t>(p->out) & mask) == 0 && (reinterpret_cast<uintptr_t>(p->dx) & mask) == 0 &&
-           (reinterpret_cast<uintptr_t>(p->dout) & mask) == 0 && (p->length * esz) % 16 == 0;
+           (reinterpret_cast<uintptr_t>(p->dout) & mask) == 0;
   return MKO_OK;
 }
 
@@ -301,12 +333,13 @@ void launch_fwd(const Geo& g, const mko_conv1d_params& p, hipStream_t s) {
 
 template <int KMAX>
 void launch_bwd(const Geo& g, const mko_conv1d_params& p, float* partial, hipStream_t s) {
-  const int rpw = 256 / g.tpr;
-  const int64_t segs = g.rows * g.nseg;
-  MKO_TIMED("conv1d_bwd", s, backward<KMAX><<<static_cast<unsigned>((segs + rpw - 1) / rpw), 256, 0, s>>>(g, p, partial));
+  const int64_t n = g.rows * g.lpr;
+  MKO_TIMED("conv1d_bwd", s, backward<KMAX><<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(g, p, partial));
 }
 
-size_t partial_bytes(const Geo& g) { return static_cast<size_t>(g.rows * g.nseg) * (g.width + 1) * sizeof(float); }
+size_t partial_bytes(const Geo& g) {
+  return static_cast<size_t>(g.rows * (g.lpr / 16)) * (g.width + 1) * sizeof(float);
+}
 
 }  // namespace
 }  // namespace conv
@@ -361,7 +394,8 @@ extern "C" int mko_conv1d_bwd(const mko_conv1d_params* p, void* stream) {
   else conv::launch_bwd<32>(g, *p, partial, s);
   if (params) {
     const int64_t n = g.channels * (g.width + 1);
-    MKO_TIMED("conv1d_finalize", s, conv::finalize<<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(g, *p, partial));
+    MKO_TIMED("conv1d_finalize", s,
+              conv::finalize<<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(g, *p, partial));
   }
   return mko_check_launch("conv1d_bwd");
 }
