@@ -16,7 +16,7 @@ recorded by libmko on the kernel's own stream.  ``cpu_baseline`` times the float
 oracle's restatement (run in float32 with autograd) on a bounded sample on this
 host.  ``also`` carries the other workloads of the path (Mamba-1 130M layer,
 Mamba-2 decode, Mamba-2 SSD chunk scan, the four-path 2D scan, the causal conv1d
-ahead of the scan) with their own rooflines.
+ahead of the scan, the gated RMSNorm after it) with their own rooflines.
 """
 
 from __future__ import annotations
@@ -475,6 +475,78 @@ def conv1d_cpu_baseline(shape=(1, 1024, 4096, 4)):
                       f"product with autograd (oracle/conv1d.py), best of 3 after 1 warm-up: {best * 1e3:.1f} ms"}
 
 
+NORM_SHAPE = (8192, 2560)  # rows, features: the reference's first gated-norm bench shape, one group per row
+
+
+def norm_bytes(rows, features, esz=2):
+    """Algorithmic bytes (fwd, bwd) with z and no parameter gradients: x, z in, out;
+    x, z, dout in, dx, dz out (weight, bias and the per-row rstd are negligible)."""
+    e = rows * features
+    return 3 * e * esz, 5 * e * esz
+
+
+def norm_case(steps, warmup, shape=NORM_SHAPE):
+    from metal_kernelops.cv import rmsnorm_gated
+    rows, features = shape
+    g = torch.Generator().manual_seed(0)
+    dev = torch.device("cuda")
+    x = torch.randn(rows, features, generator=g).bfloat16().to(dev).requires_grad_(True)
+    z = torch.randn(rows, features, generator=g).bfloat16().to(dev).requires_grad_(True)
+    w = torch.randn(features, generator=g).bfloat16().to(dev)
+    b = torch.randn(features, generator=g).bfloat16().to(dev)
+    dout = torch.randn(rows, features, generator=g).bfloat16().to(dev)
+
+    def step():
+        out = rmsnorm_gated(x, w, b, z)
+        torch.autograd.grad(out, (x, z), dout)
+
+    ms, wall, kernels = timed(step, steps, warmup)
+    fwd_b, bwd_b = norm_bytes(*shape)
+    name, avg, count = dominant(kernels)
+    per_kernel = {"gated_norm_bwd": bwd_b, "gated_norm_fwd": fwd_b}
+    roof = roofline(per_kernel.get(name, fwd_b + bwd_b), avg, load_traffic(name))
+    roof["kernel"] = name
+    roof["algorithmic_bytes"] = per_kernel.get(name, fwd_b + bwd_b)
+    with torch.no_grad():
+        fms, _, fk = timed(lambda: rmsnorm_gated(x, w, b, z), steps, warmup)
+    del x, z, w, b, dout
+    torch.cuda.empty_cache()
+    return {"ms_per_step": ms, "wall_ms_per_step": wall, "gbs": (fwd_b + bwd_b) / (ms * 1e-3) / 1e9,
+            "bytes_per_step": fwd_b + bwd_b, "roofline": roof, "fwd_us": fms * 1e3,
+            "fwd_gbs": fwd_b / (fms * 1e-3) / 1e9,
+            "kernels_ms": {k: round(v[0] / max(v[1], 1), 4) for k, v in sorted(kernels.items())}}
+
+
+def norm_cpu_baseline(shape=(2048, 2560)):
+    """The oracle's forward in float32 with autograd (dx, dz), on a bounded sample."""
+    import oracle
+    torch.set_num_threads(os.cpu_count() or 1)
+    rows, features = shape
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(rows, features, generator=g).requires_grad_(True)
+    z = torch.randn(rows, features, generator=g).requires_grad_(True)
+    w, b = torch.randn(features, generator=g), torch.randn(features, generator=g)
+    dout = torch.randn(rows, features, generator=g)
+
+    def run():
+        out, _ = oracle.rmsnorm_gated(x, w, b, z, dtype=torch.float32)
+        torch.autograd.grad(out, (x, z), dout)
+
+    run()
+    best = None
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run()
+        dt = time.perf_counter() - t0
+        best = dt if best is None else min(best, dt)
+    fwd_b, bwd_b = norm_bytes(*shape, esz=4)
+    return {"value": round((fwd_b + bwd_b) / best / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"gated RMSNorm fwd+bwd (dx, dz) at {shape} (rows, features), gate after the norm, "
+                      f"float32 composition with autograd (oracle/norm.py), best of 3 after 1 warm-up: "
+                      f"{best * 1e3:.1f} ms"}
+
+
 # --------------------------------------------------------------------- main
 
 
@@ -484,7 +556,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-cpu", action="store_true", help="skip the CPU baseline legs")
-    ap.add_argument("--only", choices=["mamba1", "ssd", "decode", "ss2d", "conv1d", "copy", "all"], default="all",
+    ap.add_argument("--only", choices=["mamba1", "ssd", "decode", "ss2d", "conv1d", "norm", "copy", "all"],
+                    default="all",
                     help="one workload (mamba1 = the config-3 headline alone) or all of them; copy = "
                          "a plain 1 GiB device copy, the calibration point of the PMC byte counters")
     args = ap.parse_args()
@@ -571,6 +644,18 @@ def main():
                                      "dtype": "f32"}}
         log(f"  {cv['ms_per_step']:.3f} ms/step, {cv['gbs']:.1f} GB/s; decode update {cv['update_us']:.1f} us; "
             f"kernels {cv['kernels_ms']}")
+    if want("norm"):
+        log(f"gated RMSNorm {NORM_SHAPE} (rows, features) fwd+bwd, bf16, z and bias, gate after the norm")
+        nm = norm_case(args.steps, args.warmup)
+        also["gated_rmsnorm_fwd_bwd"] = {
+            "value": round(nm["gbs"], 1), "unit": "GB/s", "ms_per_step": round(nm["ms_per_step"], 4),
+            "fwd_us": round(nm["fwd_us"], 2), "fwd_gbs": round(nm["fwd_gbs"], 1),
+            "config": {"rows": NORM_SHAPE[0], "features": NORM_SHAPE[1], "group_size": NORM_SHAPE[1],
+                       "dtype": "bf16", "z": True, "bias": True, "norm_before_gate": True,
+                       "grads": "x, z"},
+            "roofline": nm["roofline"], "kernels_ms": nm["kernels_ms"]}
+        log(f"  {nm['ms_per_step'] * 1e3:.1f} us/step, {nm['gbs']:.1f} GB/s; forward {nm['fwd_us']:.1f} us; "
+            f"kernels {nm['kernels_ms']}")
     if head is None:  # a single non-headline workload: print its own record
         print(json.dumps(also), flush=True)
         return
@@ -587,6 +672,8 @@ def main():
             also["ss2d_four_path_scan_fwd_bwd"]["cpu_baseline"] = ss2d_cpu_baseline()
         if "causal_conv1d_fwd_bwd" in also:
             also["causal_conv1d_fwd_bwd"]["cpu_baseline"] = conv1d_cpu_baseline()
+        if "gated_rmsnorm_fwd_bwd" in also:
+            also["gated_rmsnorm_fwd_bwd"]["cpu_baseline"] = norm_cpu_baseline()
     line = {
         "metric": METRIC,
         "value": round(head["gbs"], 1),

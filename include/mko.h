@@ -50,6 +50,7 @@ size_t mko_sizeof_ssd_params(void);
 size_t mko_sizeof_path_params(void);
 size_t mko_sizeof_conv1d_params(void);
 size_t mko_sizeof_conv1d_update_params(void);
+size_t mko_sizeof_gated_norm_params(void);
 
 /* Kernel timing (observability).  While enabled, every kernel the library
  * launches is bracketed by HIP events on its launch stream; the per-kernel totals
@@ -324,6 +325,51 @@ typedef struct mko_conv1d_update_params {
 } mko_conv1d_update_params;
 
 int mko_conv1d_update(const mko_conv1d_update_params* p, void* stream);
+
+/* ======================================================================== */
+/* Gated RMSNorm (cv/gated_norm.py)                                          */
+/* ======================================================================== */
+
+/* Where silu(z) enters; the numbering of the reference's _GATE_* constants
+ * (cv/gated_norm.py:63-66). */
+#define MKO_GATE_NONE 0   /* no z */
+#define MKO_GATE_BEFORE 1 /* norm_before_gate=False: x' = x * silu(z) is normalised */
+#define MKO_GATE_AFTER 2  /* norm_before_gate=True: the normalised output is multiplied by silu(z) */
+
+/* Per (row, group) of `group` consecutive features:
+ *   x'  = x * silu(z) (MKO_GATE_BEFORE) or x
+ *   r   = 1 / sqrt(mean(x'^2) + eps)                       (biased mean over the group)
+ *   out = (x' * r * weight + bias) * silu(z) (MKO_GATE_AFTER), or without the gate
+ * x, z, out, dout, dx and dz are (rows, features) of `dtype`; weight, bias, rstd,
+ * dweight and dbias are float32.  Arithmetic is float32. */
+typedef struct mko_gated_norm_params {
+  const void* x;
+  const void* z;        /* NULL with MKO_GATE_NONE */
+  const float* weight;  /* (features,) */
+  const float* bias;    /* (features,) or NULL */
+  void* out;            /* forward */
+  float* rstd;          /* (rows, features / group): the forward writes it when non-NULL, the backward reads it */
+  const void* dout;     /* backward */
+  void* dx;             /* backward */
+  void* dz;             /* backward, with a gate */
+  float* dweight;       /* backward: (features,), summed over rows, or NULL */
+  float* dbias;         /* backward: (features,), summed over rows, or NULL */
+  void* workspace;      /* backward: mko_gated_norm_bwd_workspace_size() bytes */
+  size_t workspace_bytes;
+  int64_t rows, features, group; /* group divides features */
+  float eps;
+  int32_t dtype;
+  int32_t gate;         /* MKO_GATE_* */
+} mko_gated_norm_params;
+
+/* Replaces the Metal fwd_* / fwd_stream_* kernels and _GatedRMSNorm.forward
+ * (cv/gated_norm.py:154-183, 252-281, 565-604). */
+int mko_gated_norm_fwd(const mko_gated_norm_params* p, void* stream);
+/* Replaces _GatedRMSNorm.backward with the Metal bwd_*, bwd_c1_* and bwd_apply_*
+ * kernels and the partial sums (cv/gated_norm.py:185-250, 283-340, 606-645): dx, dz,
+ * and dweight/dbias reduced over rows in a fixed order. */
+size_t mko_gated_norm_bwd_workspace_size(const mko_gated_norm_params* p);
+int mko_gated_norm_bwd(const mko_gated_norm_params* p, void* stream);
 
 #ifdef __cplusplus
 }

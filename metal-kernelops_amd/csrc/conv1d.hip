@@ -125,17 +125,6 @@ __global__ void __launch_bounds__(256) forward(Geo g, mko_conv1d_params p) {
   }
 }
 
-// Sum over the 16 lanes of a DPP row, every one of them gets it: swap neighbours and
-// pairs (quad_perm), then add the other quad (row_half_mirror), then the other half
-// row (row_mirror).
-__device__ __forceinline__ float row16_sum(float v) {
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xb1, 0xf, 0xf, false));
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4e, 0xf, 0xf, false));
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xf, 0xf, false));
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xf, 0xf, false));
-  return v;
-}
-
 template <int KMAX>
 __global__ void __launch_bounds__(256) backward(Geo g, mko_conv1d_params p, float* partial) {
   constexpr int H = KMAX - 1;

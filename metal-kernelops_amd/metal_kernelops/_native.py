@@ -109,6 +109,18 @@ class Conv1dUpdateParams(ctypes.Structure):
     ]
 
 
+class GatedNormParams(ctypes.Structure):
+    """Mirror of ``mko_gated_norm_params``."""
+
+    _fields_ = [
+        ("x", _vp), ("z", _vp), ("weight", _vp), ("bias", _vp), ("out", _vp), ("rstd", _vp),
+        ("dout", _vp), ("dx", _vp), ("dz", _vp), ("dweight", _vp), ("dbias", _vp),
+        ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
+        ("rows", ctypes.c_int64), ("features", ctypes.c_int64), ("group", ctypes.c_int64),
+        ("eps", ctypes.c_float), ("dtype", ctypes.c_int32), ("gate", ctypes.c_int32),
+    ]
+
+
 _SIGNATURES = {
     "mko_abi_version": ([], ctypes.c_int),
     "mko_last_error": ([], ctypes.c_char_p),
@@ -124,6 +136,10 @@ _SIGNATURES = {
     "mko_conv1d_bwd_workspace_size": ([ctypes.POINTER(Conv1dParams)], ctypes.c_size_t),
     "mko_conv1d_bwd": ([ctypes.POINTER(Conv1dParams), _vp], ctypes.c_int),
     "mko_conv1d_update": ([ctypes.POINTER(Conv1dUpdateParams), _vp], ctypes.c_int),
+    "mko_sizeof_gated_norm_params": ([], ctypes.c_size_t),
+    "mko_gated_norm_fwd": ([ctypes.POINTER(GatedNormParams), _vp], ctypes.c_int),
+    "mko_gated_norm_bwd_workspace_size": ([ctypes.POINTER(GatedNormParams)], ctypes.c_size_t),
+    "mko_gated_norm_bwd": ([ctypes.POINTER(GatedNormParams), _vp], ctypes.c_int),
     "mko_ssd_saved_bytes": ([ctypes.POINTER(SsdParams)], ctypes.c_size_t),
     "mko_ssd_fwd_workspace_size": ([ctypes.POINTER(SsdParams)], ctypes.c_size_t),
     "mko_ssd_fwd": ([ctypes.POINTER(SsdParams), _vp], ctypes.c_int),
@@ -174,7 +190,8 @@ def lib():
                            (SsdParams, handle.mko_sizeof_ssd_params),
                            (PathParams, handle.mko_sizeof_path_params),
                            (Conv1dParams, handle.mko_sizeof_conv1d_params),
-                           (Conv1dUpdateParams, handle.mko_sizeof_conv1d_update_params)):
+                           (Conv1dUpdateParams, handle.mko_sizeof_conv1d_update_params),
+                           (GatedNormParams, handle.mko_sizeof_gated_norm_params)):
             if ctypes.sizeof(struct) != fn():
                 raise RuntimeError(f"{struct.__name__} layout does not match libmko.so")
         _lib = handle

@@ -10,6 +10,7 @@ Importing it registers the ``mko::`` custom ops and launches nothing.
 """
 
 from .causal_conv1d import causal_conv1d_fn, causal_conv1d_ref, causal_conv1d_update
+from .gated_norm import rmsnorm_gated, rmsnorm_gated_reference
 from .mamba2_chunk import last_path, mamba2_chunk_scan, mamba2_chunk_scan_reference
 from .mamba2_state import CHECKED_TORCH, mamba2_state_update, mamba2_state_update_reference
 from .path_scan import MAX_STATES, MERGE_MODES, path_orders, ss2d_scan, ss2d_scan_reference
@@ -27,6 +28,8 @@ __all__ = [
     "mamba2_state_update",
     "mamba2_state_update_reference",
     "path_orders",
+    "rmsnorm_gated",
+    "rmsnorm_gated_reference",
     "ss2d_scan",
     "ss2d_scan_reference",
 ]

@@ -1,0 +1,217 @@
+"""Gated RMSNorm on MI355X: the normalisation after the SSM scan in a Mamba-2 block.
+
+Public surface, as in dbydd/metal-kernelops ``cv/gated_norm.py:647-721``:
+``rmsnorm_gated`` (fused HIP forward, analytic backward) and
+``rmsnorm_gated_reference`` (the float64 torch definition it is checked against).
+
+Per ``(row, group)`` of ``group_size`` consecutive features (the whole feature axis
+when ``group_size`` is None)::
+
+    gate = silu(z)                         when z is given
+    x'   = x * gate                        if norm_before_gate is False
+    r    = rsqrt(mean(x'^2 over the group) + eps)     (biased mean)
+    out  = (x' * r * weight + bias) * gate  if norm_before_gate is True
+
+Every intermediate is float32 and the result comes back in ``x.dtype``, as in the
+reference (``:537-561``).
+
+How it runs: ``mko::gated_norm_fwd`` gives each ``(row, group)`` to a team of
+wavefronts that holds the group in registers from the load to the store (x and z
+read once, out written once) and saves ``r`` per group; ``mko::gated_norm_bwd``
+walks blocks of rows per group, writes dx and dz in the same pass and sums
+``dweight``/``dbias`` in a fixed order.  Groups wider than the register set
+(32768 elements forward, 8192 backward, fewer for unaligned groups) stream.
+
+Differences from the reference: tensors live on the ROCm GPU; float32, float16 and
+bfloat16 run the kernels and float64 raises ``ValueError`` (the reference's composed
+float64/CPU path, ``:471-480, 537-561``, is :func:`rmsnorm_gated_reference` here).  A
+``z`` of another dtype than ``x`` makes both float32 for the kernel, which is the
+reference's composed arithmetic for that case.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Tuple
+
+import torch
+from torch import Tensor
+
+from .. import _native as nat
+from ..scan import _require_gpu
+
+__all__ = ["rmsnorm_gated", "rmsnorm_gated_reference"]
+
+GATE_NONE = 0
+"""No z."""
+GATE_BEFORE = 1
+"""``norm_before_gate=False``: silu(z) multiplies x before the mean square."""
+GATE_AFTER = 2
+"""``norm_before_gate=True``: silu(z) multiplies the normalised, scaled output."""
+
+_FLOATS = (torch.float32, torch.float16, torch.bfloat16)
+
+
+def _params(x, weight, bias, z, eps, group, gate):
+    p = nat.GatedNormParams()
+    p.x, p.z, p.weight, p.bias = x.data_ptr(), nat.ptr(z), weight.data_ptr(), nat.ptr(bias)
+    p.rows, p.features = x.shape
+    p.group, p.eps = group, eps
+    p.dtype, p.gate = nat.code(x.dtype), gate
+    return p
+
+
+@torch.library.custom_op("mko::gated_norm_fwd", mutates_args=(), device_types="cuda")
+def _gated_norm_fwd(x: Tensor, weight: Tensor, bias: Optional[Tensor], z: Optional[Tensor], eps: float,
+                    group: int, gate: int) -> Tuple[Tensor, Tensor]:
+    rows, features = x.shape
+    out = torch.empty_like(x)
+    rstd = x.new_empty(rows * (features // group), dtype=torch.float32)
+    if x.numel() == 0:
+        return out, rstd
+    p = _params(x, weight, bias, z, eps, group, gate)
+    p.out, p.rstd = out.data_ptr(), rstd.data_ptr()
+    nat.check(nat.lib().mko_gated_norm_fwd(ctypes.byref(p), nat.stream_of(x.device)), "mko_gated_norm_fwd")
+    return out, rstd
+
+
+@_gated_norm_fwd.register_fake
+def _(x, weight, bias, z, eps, group, gate):
+    rows, features = x.shape
+    return torch.empty_like(x), x.new_empty(rows * (features // group), dtype=torch.float32)
+
+
+@torch.library.custom_op("mko::gated_norm_bwd", mutates_args=(), device_types="cuda")
+def _gated_norm_bwd(dout: Tensor, x: Tensor, weight: Tensor, bias: Optional[Tensor], z: Optional[Tensor],
+                    rstd: Tensor, group: int, gate: int, need_weight: bool, need_bias: bool
+                    ) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+    features = x.shape[1]
+    dx = torch.empty_like(x)
+    dz = torch.empty_like(z) if z is not None else x.new_empty(0)
+    dweight = weight.new_zeros(features) if need_weight else weight.new_empty(0)
+    dbias = weight.new_zeros(features) if need_bias else weight.new_empty(0)
+    if x.numel() == 0:
+        return dx, dz, dweight, dbias
+    p = _params(x, weight, bias, z, 0.0, group, gate)
+    p.rstd, p.dout, p.dx = rstd.data_ptr(), dout.data_ptr(), dx.data_ptr()
+    p.dz = dz.data_ptr() if z is not None else None
+    p.dweight = dweight.data_ptr() if need_weight else None
+    p.dbias = dbias.data_ptr() if need_bias else None
+    ws = nat.workspace(nat.lib().mko_gated_norm_bwd_workspace_size(ctypes.byref(p)), x.device)
+    p.workspace, p.workspace_bytes = ws.data_ptr(), ws.numel()
+    nat.check(nat.lib().mko_gated_norm_bwd(ctypes.byref(p), nat.stream_of(x.device)), "mko_gated_norm_bwd")
+    return dx, dz, dweight, dbias
+
+
+@_gated_norm_bwd.register_fake
+def _(dout, x, weight, bias, z, rstd, group, gate, need_weight, need_bias):
+    features = x.shape[1]
+    return (torch.empty_like(x), torch.empty_like(z) if z is not None else x.new_empty(0),
+            weight.new_empty(features if need_weight else 0), weight.new_empty(features if need_bias else 0))
+
+
+def _setup(ctx, inputs, output):
+    x, weight, bias, z, _eps, group, gate = inputs
+    ctx.save_for_backward(x, weight, bias, z, output[1])
+    ctx.group, ctx.gate = group, gate
+
+
+def _backward(ctx, dout, _drstd):
+    x, weight, bias, z, rstd = ctx.saved_tensors
+    need = ctx.needs_input_grad
+    need_bias = bool(need[2] and bias is not None)
+    dx, dz, dweight, dbias = torch.ops.mko.gated_norm_bwd(
+        dout.contiguous(), x, weight, bias, z, rstd, ctx.group, ctx.gate, bool(need[1]), need_bias)
+    return (dx, dweight if need[1] else None, dbias if need_bias else None,
+            dz if z is not None and need[3] else None, None, None, None)
+
+
+torch.library.register_autograd("mko::gated_norm_fwd", _backward, setup_context=_setup)
+
+
+def _checked_group(x, weight, bias, z, group_size):
+    """The reference's argument checks on a non-empty feature axis (``cv/gated_norm.py:674-684``);
+    returns the group width."""
+    features = x.shape[-1]
+    group = features if group_size is None else int(group_size)
+    if group <= 0 or features % group:
+        raise ValueError(f"group_size {group} does not divide {features}")
+    if tuple(weight.shape) != (features,):
+        raise ValueError(f"weight must be ({features},), got {tuple(weight.shape)}")
+    if bias is not None and tuple(bias.shape) != (features,):
+        raise ValueError(f"bias must be ({features},), got {tuple(bias.shape)}")
+    if z is not None and z.shape != x.shape:
+        raise ValueError(f"z must match x {tuple(x.shape)}, got {tuple(z.shape)}")
+    return group
+
+
+def rmsnorm_gated(x, weight, bias=None, z=None, eps=1e-5, group_size=None, norm_before_gate=True):
+    """Gated RMSNorm over the last axis, as in ``mamba_ssm``'s ``RMSNorm``.
+
+    Args:
+        x: ``(..., features)``, float32, float16 or bfloat16 on the ROCm GPU.
+        weight: ``(features,)`` scale, any float dtype (used as float32; its gradient
+            comes back in its own dtype).
+        bias: ``(features,)`` shift, added before the gate, or None.
+        z: the gate, shaped like ``x``, or None.
+        eps: added to the mean square before the reciprocal square root.
+        group_size: elements per normalisation group; None means the whole feature
+            axis.  Must divide ``features``.
+        norm_before_gate: True applies silu(z) after the normalisation, False to the
+            input before it.
+
+    Returns:
+        ``(..., features)`` in ``x.dtype``.
+    """
+    if x.dim() < 1:
+        raise ValueError("rmsnorm_gated needs a feature axis")
+    features = x.shape[-1]
+    if features == 0:
+        return x.clone()  # nothing to average over, as in the reference
+    group = _checked_group(x, weight, bias, z, group_size)
+    for t in (x, weight, bias, z):
+        if t is not None:
+            _require_gpu(t)
+    if x.dtype not in _FLOATS:
+        raise ValueError(f"rmsnorm_gated runs float32, float16 or bfloat16 on the GPU, got {x.dtype}; "
+                         "rmsnorm_gated_reference evaluates other dtypes")
+    if z is not None and z.dtype not in _FLOATS:
+        raise ValueError(f"z must be float32, float16 or bfloat16, got {z.dtype}")
+    work = x.dtype if z is None or z.dtype == x.dtype else torch.float32
+    shape = x.shape
+    rows_x = x.reshape(-1, features).to(work).contiguous()
+    rows_z = z.reshape(-1, features).to(work).contiguous() if z is not None else None
+    gate = GATE_NONE if z is None else (GATE_AFTER if norm_before_gate else GATE_BEFORE)
+    out, _ = torch.ops.mko.gated_norm_fwd(
+        rows_x, weight.float().contiguous(), bias.float().contiguous() if bias is not None else None, rows_z,
+        float(eps), group, gate)
+    return out.reshape(shape).to(x.dtype)
+
+
+def rmsnorm_gated_reference(x, weight, bias=None, z=None, eps=1e-5, group_size=None, norm_before_gate=True):
+    """``rms_norm_ref`` of mamba's ``layernorm_gated.py``, evaluated in float64 with torch.
+
+    The specification the kernels are checked against (``cv/gated_norm.py:689-721``):
+    gate before the mean, scale, shift, gate after, biased mean.  Like the
+    reference it runs on the CPU and returns a CPU tensor of ``x.dtype``;
+    differentiable.
+    """
+    out_dtype = x.dtype
+    xf = x.to("cpu").double()
+    weightf = weight.to("cpu").double()
+    biasf = bias.to("cpu").double() if bias is not None else None
+    zf = z.to("cpu").double() if z is not None else None
+    features = xf.shape[-1]
+    if features == 0:
+        return torch.empty(x.shape, dtype=out_dtype)
+    group = features if group_size is None else group_size
+    if zf is not None and not norm_before_gate:
+        xf = xf * torch.nn.functional.silu(zf)
+    grouped = xf.reshape(xf.shape[:-1] + (features // group, group))
+    rstd = torch.rsqrt(grouped.square().mean(-1, keepdim=True) + eps)
+    out = (grouped * rstd).reshape(xf.shape) * weightf
+    if biasf is not None:
+        out = out + biasf
+    if zf is not None and norm_before_gate:
+        out = out * torch.nn.functional.silu(zf)
+    return out.to(out_dtype)

@@ -24,3 +24,4 @@ from .ssm import (  # noqa: F401
     ssd_minimal_discrete,
 )
 from .conv1d import causal_conv1d, causal_conv1d_update  # noqa: F401,E402
+from .norm import rmsnorm_gated, rmsnorm_gated_bwd  # noqa: F401,E402

@@ -78,3 +78,39 @@ def test_host_side_validation_without_gpu(native):
     q = native.StateUpdateParams()
     q.batch, q.nheads, q.headdim, q.dstate, q.ngroups = 1, 4, 8, 16, 3
     assert lib.mko_state_update_fwd(ctypes.byref(q), None) == 1
+
+
+def test_gated_norm_validation_without_gpu(native):
+    lib = native.lib()
+    assert ctypes.sizeof(native.GatedNormParams) == lib.mko_sizeof_gated_norm_params()
+    p = native.GatedNormParams()
+    p.rows, p.features, p.group, p.eps, p.dtype, p.gate = 4, 300, 7, 1e-5, 0, 0  # 300 % 7 != 0
+    assert lib.mko_gated_norm_fwd(ctypes.byref(p), None) == 1
+    assert b"divide" in lib.mko_last_error()
+    p.group, p.gate = 100, 5
+    assert lib.mko_gated_norm_fwd(ctypes.byref(p), None) == 1
+    assert b"gate" in lib.mko_last_error()
+    p.gate, p.dtype = 2, 9
+    assert lib.mko_gated_norm_bwd(ctypes.byref(p), None) == 1
+    assert b"dtype" in lib.mko_last_error()
+    p.dtype, p.eps = 2, -1.0
+    assert lib.mko_gated_norm_fwd(ctypes.byref(p), None) == 1
+    p.eps = 1e-5
+    assert lib.mko_gated_norm_fwd(ctypes.byref(p), None) == 1  # x, weight, out, z missing
+    assert b"required" in lib.mko_last_error()
+    p.rows = 0  # no rows: nothing to launch, no pointers needed
+    assert lib.mko_gated_norm_fwd(ctypes.byref(p), None) == 0
+    assert lib.mko_gated_norm_bwd(ctypes.byref(p), None) == 0
+    assert lib.mko_gated_norm_bwd_workspace_size(ctypes.byref(p)) == 0
+    # dweight wanted: a partial row per row block; a group past the register set adds c1
+    p.rows, p.features, p.group, p.gate = 256, 2560, 2560, 2
+    for name in ("x", "z", "weight", "dout", "dx", "dz", "rstd"):
+        setattr(p, name, 256)  # 16-byte aligned, never dereferenced
+    p.dweight = 256
+    dense = lib.mko_gated_norm_bwd_workspace_size(ctypes.byref(p))
+    assert dense > 0 and dense % (2 * 2560 * 4) == 0
+    p.features = p.group = 32768
+    wide = lib.mko_gated_norm_bwd_workspace_size(ctypes.byref(p))
+    assert wide > 0 and (wide - 256 * 4) % (2 * 32768 * 4) == 0
+    p.workspace, p.workspace_bytes = None, 0
+    assert lib.mko_gated_norm_bwd(ctypes.byref(p), None) == 4
