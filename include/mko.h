@@ -340,13 +340,13 @@ int mko_conv1d_update(const mko_conv1d_update_params* p, void* stream);
  *   x'  = x * silu(z) (MKO_GATE_BEFORE) or x
  *   r   = 1 / sqrt(mean(x'^2) + eps)                       (biased mean over the group)
  *   out = (x' * r * weight + bias) * silu(z) (MKO_GATE_AFTER), or without the gate
- * x, z, out, dout, dx and dz are (rows, features) of `dtype`; weight, bias, rstd,
- * dweight and dbias are float32.  Arithmetic is float32. */
+ * x, z, out, dout, dx and dz are (rows, features) of `dtype`; weight and bias are
+ * (features,) of `wdtype`; rstd, dweight and dbias are float32.  Arithmetic is float32. */
 typedef struct mko_gated_norm_params {
   const void* x;
   const void* z;        /* NULL with MKO_GATE_NONE */
-  const float* weight;  /* (features,) */
-  const float* bias;    /* (features,) or NULL */
+  const void* weight;   /* (features,) */
+  const void* bias;     /* (features,) or NULL */
   void* out;            /* forward */
   float* rstd;          /* (rows, features / group): the forward writes it when non-NULL, the backward reads it */
   const void* dout;     /* backward */
@@ -358,8 +358,9 @@ typedef struct mko_gated_norm_params {
   size_t workspace_bytes;
   int64_t rows, features, group; /* group divides features */
   float eps;
-  int32_t dtype;
+  int32_t dtype;        /* of x, z, out, dout, dx, dz */
   int32_t gate;         /* MKO_GATE_* */
+  int32_t wdtype;       /* of weight and bias */
 } mko_gated_norm_params;
 
 /* Replaces the Metal fwd_* / fwd_stream_* kernels and _GatedRMSNorm.forward

@@ -32,7 +32,9 @@ constexpr int kStream = 1024;       // threads of the streaming kernels' team
 constexpr int kFwdElems = 32;       // register elements per thread, forward
 constexpr int kBwdElems = 8;        // register elements per thread, backward
 constexpr int kBwdTeamWaves = 8;    // waves per backward workgroup when teams are narrow
-constexpr int kBwdWaveTarget = 2048;  // backward waves in flight across the chip
+constexpr int kBwdWaveTarget = 8192;  // backward waves across the chip without parameter gradients
+constexpr int kBwdWaveTargetParams = 4096;  // ... with them (each row block adds a partial row)
+constexpr int kMaxBlocks = 4096;      // row blocks per group: two column-sum passes of 64 rows
 constexpr int kColThreads = 256;    // workgroup of the per-column backward kernel
 
 struct Geo {
@@ -42,6 +44,7 @@ struct Geo {
   int64_t blocks;   // backward: row blocks per group (partial rows)
   int64_t rpb;      // backward: rows per block
   int gate, bias;
+  int wd;           // dtype of weight and bias
   int want_dw, want_db;
   float eps;
 };
@@ -72,6 +75,7 @@ __device__ __forceinline__ void zero(Raw<T, VEC>& r) {
 // a load at or past `bytes` return zero and drops such a store, which masks the lanes
 // past the group and the teams without a row (bytes = 0).
 typedef uint32_t v4u32 __attribute__((ext_vector_type(4)));
+typedef uint32_t v2u32 __attribute__((ext_vector_type(2)));
 constexpr int kRsrcWord3 = 0x00020000;  // raw buffer, 32-bit data format (gfx9)
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
@@ -219,6 +223,66 @@ __device__ __forceinline__ void load_param(const float* p, float (&o)[VEC]) {
   }
 }
 
+// 16-bit weights packed two to a word, as float32.
+template <int VEC>
+__device__ __forceinline__ void unpack16(const uint32_t (&w)[(VEC + 1) / 2], bool bf, float (&o)[VEC]) {
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) {
+    const uint32_t h = (i & 1) ? (w[i / 2] >> 16) : (w[i / 2] & 0xffffu);
+    o[i] = bf ? __uint_as_float(h << 16) : static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
+  }
+}
+
+// VEC consecutive weights from element `elem` of a buffer of dtype `wd`, as float32.
+template <int VEC>
+__device__ __forceinline__ void bload_w(__amdgpu_buffer_rsrc_t r, uint32_t elem, int wd, float (&o)[VEC]) {
+  if (wd == MKO_F32) {
+    bload_param<VEC>(r, elem * 4, o);
+    return;
+  }
+  uint32_t w[(VEC + 1) / 2];
+  const uint32_t off = elem * 2;
+  if constexpr (VEC == 8) {
+    const v4u32 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    w[0] = v.x;
+    w[1] = v.y;
+    w[2] = v.z;
+    w[3] = v.w;
+  } else if constexpr (VEC == 4) {
+    const v2u32 v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    w[0] = v.x;
+    w[1] = v.y;
+  } else {
+    static_assert(VEC == 1, "weights come in 1, 4 or 8");
+    w[0] = __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+  }
+  unpack16<VEC>(w, wd == MKO_BF16, o);
+}
+
+template <int VEC>
+__device__ __forceinline__ void load_w(const void* p, int wd, int64_t elem, float (&o)[VEC]) {
+  if (wd == MKO_F32) {
+    load_param<VEC>(static_cast<const float*>(p) + elem, o);
+    return;
+  }
+  const uint16_t* q = static_cast<const uint16_t*>(p) + elem;
+  uint32_t w[(VEC + 1) / 2];
+  if constexpr (VEC == 8) {
+    const uint4 v = *reinterpret_cast<const uint4*>(q);
+    w[0] = v.x;
+    w[1] = v.y;
+    w[2] = v.z;
+    w[3] = v.w;
+  } else if constexpr (VEC == 4) {
+    const uint2 v = *reinterpret_cast<const uint2*>(q);
+    w[0] = v.x;
+    w[1] = v.y;
+  } else {
+    w[0] = q[0];
+  }
+  unpack16<VEC>(w, wd == MKO_BF16, o);
+}
+
 template <int VEC>
 __device__ __forceinline__ void store_param(float* p, const float (&v)[VEC]) {
   if constexpr (VEC >= 4) {
@@ -262,8 +326,10 @@ __global__ void __launch_bounds__(1024) forward(Geo g, mko_gated_norm_params p) 
   constexpr bool gate = GATE != MKO_GATE_NONE;
   const auto rx = rsrc(static_cast<const char*>(p.x) + base, bytes);
   const auto rz = rsrc(gate ? static_cast<const char*>(p.z) + base : static_cast<const char*>(p.x), gate ? bytes : 0u);
-  const auto rw = rsrc(p.weight + gi * g.group, static_cast<uint32_t>(g.group * 4));
-  const auto rb = rsrc(p.bias ? p.bias + gi * g.group : p.weight, p.bias ? static_cast<uint32_t>(g.group * 4) : 0u);
+  const int64_t wsz = g.wd == MKO_F32 ? 4 : 2;
+  const auto rw = rsrc(static_cast<const char*>(p.weight) + gi * g.group * wsz, static_cast<uint32_t>(g.group * wsz));
+  const auto rb = rsrc(p.bias ? static_cast<const char*>(p.bias) + gi * g.group * wsz : p.weight,
+                       p.bias ? static_cast<uint32_t>(g.group * wsz) : 0u);
 
   float v[NV][VEC], w[NV][VEC];
   Raw<T, VEC> zr[NV];
@@ -277,7 +343,7 @@ __global__ void __launch_bounds__(1024) forward(Geo g, mko_gated_norm_params p) 
   }
   // the weights are in flight during the reduction
 #pragma unroll
-  for (int k = 0; k < NV; ++k) bload_param<VEC>(rw, static_cast<uint32_t>(lt + k * g.tw) * (VEC * 4), w[k]);
+  for (int k = 0; k < NV; ++k) bload_w<VEC>(rw, static_cast<uint32_t>(lt + k * g.tw) * VEC, g.wd, w[k]);
   float ss = 0.0f;
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
@@ -306,7 +372,7 @@ __global__ void __launch_bounds__(1024) forward(Geo g, mko_gated_norm_params p) 
     for (int e = 0; e < VEC; ++e) o[e] = v[k][e] * r * w[k][e];
     if (p.bias) {
       float b[VEC];
-      bload_param<VEC>(rb, i * (VEC * 4), b);
+      bload_w<VEC>(rb, i * VEC, g.wd, b);
 #pragma unroll
       for (int e = 0; e < VEC; ++e) o[e] += b[e];
     }
@@ -351,13 +417,12 @@ __global__ void __launch_bounds__(kStream) forward_stream(Geo g, mko_gated_norm_
   const float r = rsqrtf(team_sum(ss, slots, kStream, 0) / static_cast<float>(g.group) + g.eps);
   if (threadIdx.x == 0 && p.rstd) p.rstd[u] = r;
   T* out = static_cast<T*>(p.out) + base;
-  const float* wp = p.weight + gi * g.group;
-  const float* bp = p.bias ? p.bias + gi * g.group : nullptr;
+  const int64_t col0 = gi * g.group;
   for (int64_t i = threadIdx.x; i < g.nvec; i += kStream) {
     float v[VEC], zf[VEC], w[VEC];
     load_vec<T, VEC>(x + i * VEC, v);
     if (g.gate != MKO_GATE_NONE) load_vec<T, VEC>(z + i * VEC, zf);
-    load_param<VEC>(wp + i * VEC, w);
+    load_w<VEC>(p.weight, g.wd, col0 + i * VEC, w);
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
       float sig;
@@ -365,9 +430,9 @@ __global__ void __launch_bounds__(kStream) forward_stream(Geo g, mko_gated_norm_
       if (g.gate == MKO_GATE_BEFORE) v[e] *= s;
       v[e] = v[e] * r * w[e];
     }
-    if (bp) {
+    if (p.bias) {
       float b[VEC];
-      load_param<VEC>(bp + i * VEC, b);
+      load_w<VEC>(p.bias, g.wd, col0 + i * VEC, b);
 #pragma unroll
       for (int e = 0; e < VEC; ++e) v[e] += b[e];
     }
@@ -452,13 +517,15 @@ __global__ void __launch_bounds__(1024) backward(Geo g, mko_gated_norm_params p,
 
   float w[NV][VEC], b[NV][VEC], dw[NV][VEC], db[NV][VEC];
   {
-    const auto rw = rsrc(p.weight + col0, static_cast<uint32_t>(g.group * 4));
-    const auto rb = rsrc(p.bias ? p.bias + col0 : p.weight, p.bias ? static_cast<uint32_t>(g.group * 4) : 0u);
+    const int64_t wsz = g.wd == MKO_F32 ? 4 : 2;
+    const auto rw = rsrc(static_cast<const char*>(p.weight) + col0 * wsz, static_cast<uint32_t>(g.group * wsz));
+    const auto rb = rsrc(p.bias ? static_cast<const char*>(p.bias) + col0 * wsz : p.weight,
+                         p.bias ? static_cast<uint32_t>(g.group * wsz) : 0u);
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
-      const uint32_t off = static_cast<uint32_t>(lt + k * g.tw) * (VEC * 4);
-      bload_param<VEC>(rw, off, w[k]);
-      if constexpr (GATE == MKO_GATE_AFTER) bload_param<VEC>(rb, off, b[k]);
+      const uint32_t elem = static_cast<uint32_t>(lt + k * g.tw) * VEC;
+      bload_w<VEC>(rw, elem, g.wd, w[k]);
+      if constexpr (GATE == MKO_GATE_AFTER) bload_w<VEC>(rb, elem, g.wd, b[k]);
 #pragma unroll
       for (int e = 0; e < VEC; ++e) dw[k][e] = db[k][e] = 0.0f;
     }
@@ -584,7 +651,7 @@ __global__ void __launch_bounds__(kStream) c1_stream(Geo g, mko_gated_norm_param
     load_vec<T, VEC>(static_cast<const T*>(p.x) + base + i * VEC, x);
     load_vec<T, VEC>(static_cast<const T*>(p.dout) + base + i * VEC, dy);
     if (g.gate != MKO_GATE_NONE) load_vec<T, VEC>(static_cast<const T*>(p.z) + base + i * VEC, z);
-    load_param<VEC>(p.weight + gi * g.group + i * VEC, w);
+    load_w<VEC>(p.weight, g.wd, gi * g.group + i * VEC, w);
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
       float sig;
@@ -609,10 +676,10 @@ __global__ void __launch_bounds__(kColThreads) columns(Geo g, mko_gated_norm_par
   if (blk >= g.blocks) return;
   const int64_t f0 = j * VEC, gi = f0 / g.group;
   float w[VEC], b[VEC], dw[VEC], db[VEC];
-  load_param<VEC>(p.weight + f0, w);
+  load_w<VEC>(p.weight, g.wd, f0, w);
 #pragma unroll
   for (int e = 0; e < VEC; ++e) b[e] = dw[e] = db[e] = 0.0f;
-  if (p.bias) load_param<VEC>(p.bias + f0, b);
+  if (p.bias) load_w<VEC>(p.bias, g.wd, f0, b);
   const int64_t r0 = blk * g.rpb;
   const int64_t r1 = r0 + g.rpb < g.rows ? r0 + g.rpb : g.rows;
   for (int64_t row = r0; row < r1; ++row) {
@@ -646,32 +713,29 @@ __global__ void __launch_bounds__(kColThreads) columns(Geo g, mko_gated_norm_par
   if (g.want_db) store_param<VEC>(part + (g.blocks + blk) * g.features + f0, db);
 }
 
-// dweight and dbias: the partial rows summed over the blocks.  64 columns per
-// workgroup; wave v adds blocks v, v + 16, ... in order, then the 16 wave sums are
-// added in order.
-__global__ void __launch_bounds__(1024) finalize(Geo g, mko_gated_norm_params p, const float* part) {
-  __shared__ float s[2][kMaxWaves][kWave];
+// dweight and dbias from the partial rows: column sums of a (rows, cols) float32 matrix,
+// 64 rows by 64 columns per workgroup.  Wave v adds rows 16 v .. 16 v + 15 of the
+// workgroup's 64 in order (the 16 loads issued together), then the four wave sums are
+// added in order into out[blockIdx.y][col]; a second pass over the per-64-row sums
+// finishes blocks > 64.  The order is fixed, so the sums are deterministic.
+constexpr int kSumRows = 64;
+
+__global__ void __launch_bounds__(256) colsum(const float* in, int64_t rows, int64_t cols, float* out) {
+  __shared__ float s[4][kWave];
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
   const int64_t col = static_cast<int64_t>(blockIdx.x) * kWave + lane;
-  float a = 0.0f, b = 0.0f;
-  if (col < g.features) {
-    for (int64_t k = wave; k < g.blocks; k += kMaxWaves) {
-      if (g.want_dw) a += part[k * g.features + col];
-      if (g.want_db) b += part[(g.blocks + k) * g.features + col];
-    }
-  }
-  s[0][wave][lane] = a;
-  s[1][wave][lane] = b;
-  __syncthreads();
-  if (wave != 0 || col >= g.features) return;
-  float ta = 0.0f, tb = 0.0f;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * kSumRows + wave * 16;
+  float a = 0.0f;
+  if (col < cols) {
+    float v[16];
 #pragma unroll
-  for (int v = 0; v < kMaxWaves; ++v) {
-    ta += s[0][v][lane];
-    tb += s[1][v][lane];
+    for (int j = 0; j < 16; ++j) v[j] = r0 + j < rows ? in[(r0 + j) * cols + col] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) a += v[j];
   }
-  if (g.want_dw) p.dweight[col] = ta;
-  if (g.want_db) p.dbias[col] = tb;
+  s[wave][lane] = a;
+  __syncthreads();
+  if (wave == 0 && col < cols) out[blockIdx.y * cols + col] = (s[0][lane] + s[1][lane]) + (s[2][lane] + s[3][lane]);
 }
 
 // ------------------------------------------------------------------ host side
@@ -708,6 +772,10 @@ int check_common(const mko_gated_norm_params* p, const char* what) {
     mko_set_error("%s: unknown dtype %d", what, p->dtype);
     return MKO_EINVAL;
   }
+  if (p->wdtype != MKO_F32 && p->wdtype != MKO_F16 && p->wdtype != MKO_BF16) {
+    mko_set_error("%s: unknown weight dtype %d", what, p->wdtype);
+    return MKO_EINVAL;
+  }
   if (p->gate != MKO_GATE_NONE && p->gate != MKO_GATE_BEFORE && p->gate != MKO_GATE_AFTER) {
     mko_set_error("%s: unknown gate %d", what, p->gate);
     return MKO_EINVAL;
@@ -731,6 +799,7 @@ Plan make_plan(const mko_gated_norm_params* p, bool bwd) {
   g.units = g.rows * g.ngroups;
   g.gate = p->gate;
   g.bias = p->bias != nullptr;
+  g.wd = p->wdtype;
   g.eps = p->eps;
   g.want_dw = bwd && p->dweight != nullptr;
   g.want_db = bwd && p->dbias != nullptr;
@@ -768,7 +837,9 @@ Plan make_plan(const mko_gated_norm_params* p, bool bwd) {
   if (bwd) {
     if (pl.path == kDense) {
       const int64_t wg_waves = static_cast<int64_t>(g.tpw) * (g.tw / kWave);
-      int64_t blocks = cdiv(cdiv(kBwdWaveTarget, wg_waves), g.ngroups);
+      const int64_t target = g.want_dw || g.want_db ? kBwdWaveTargetParams : kBwdWaveTarget;
+      int64_t blocks = cdiv(cdiv(target, wg_waves), g.ngroups);
+      blocks = blocks > kMaxBlocks ? kMaxBlocks : blocks;
       const int64_t most = cdiv(g.rows, g.tpw);
       blocks = blocks > most ? most : blocks;
       blocks = blocks < 1 ? 1 : blocks;
@@ -779,6 +850,7 @@ Plan make_plan(const mko_gated_norm_params* p, bool bwd) {
       const int64_t cols = g.features / pl.vec;
       int64_t blocks = cdiv(65536, cols);
       blocks = blocks > g.rows ? g.rows : blocks;
+      blocks = blocks > kMaxBlocks ? kMaxBlocks : blocks;
       blocks = blocks < 1 ? 1 : blocks;
       g.rpb = cdiv(g.rows, blocks);
       g.blocks = cdiv(g.rows, g.rpb);
@@ -787,12 +859,29 @@ Plan make_plan(const mko_gated_norm_params* p, bool bwd) {
   return pl;
 }
 
+// Workspace: the dw/db partial rows (2 x blocks x features), their per-64-row sums when
+// blocks > 64 (2 x sums x features), and c1 per (row, group) on the wide path.
+int64_t sum_rows(const Geo& g) { return g.blocks > kSumRows ? cdiv(g.blocks, kSumRows) : 0; }
+
 size_t workspace_bytes(const Plan& pl) {
   const Geo& g = pl.g;
   size_t n = 0;
-  if (g.want_dw || g.want_db) n += static_cast<size_t>(2 * g.blocks * g.features) * sizeof(float);
+  if (g.want_dw || g.want_db) n += static_cast<size_t>(2 * (g.blocks + sum_rows(g)) * g.features) * sizeof(float);
   if (pl.path == kWide) n += static_cast<size_t>(g.units) * sizeof(float);
   return n;
+}
+
+// dst = column sums of the (rows, features) partials: one colsum pass for rows <= 64,
+// two (through `tmp`, cdiv(rows, 64) rows) otherwise.
+void column_sums(const float* part, int64_t rows, int64_t features, float* tmp, float* dst, hipStream_t s) {
+  const unsigned gx = static_cast<unsigned>(cdiv(features, kWave));
+  if (rows <= kSumRows) {
+    colsum<<<dim3(gx, 1), 256, 0, s>>>(part, rows, features, dst);
+    return;
+  }
+  const int64_t mid = cdiv(rows, kSumRows);
+  colsum<<<dim3(gx, static_cast<unsigned>(mid)), 256, 0, s>>>(part, rows, features, tmp);
+  colsum<<<dim3(gx, 1), 256, 0, s>>>(tmp, mid, features, dst);
 }
 
 template <typename T, int VEC, int NV>
@@ -929,9 +1018,11 @@ extern "C" int mko_gated_norm_bwd(const mko_gated_norm_params* p, void* stream) 
     mko_set_error("gated_norm_bwd: workspace of %zu bytes needed, %zu given", need, p->workspace_bytes);
     return MKO_EWORKSPACE;
   }
-  const bool params = pl.g.want_dw || pl.g.want_db;
+  const gnorm::Geo& g = pl.g;
+  const bool params = g.want_dw || g.want_db;
   float* part = static_cast<float*>(p->workspace);
-  float* c1 = params ? part + 2 * pl.g.blocks * pl.g.features : part;
+  float* sums = part + 2 * g.blocks * g.features;
+  float* c1 = params ? sums + 2 * gnorm::sum_rows(g) * g.features : part;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (p->dtype == MKO_F32)
     st = gnorm::launch_bwd<float>(pl, *p, part, c1, s);
@@ -941,9 +1032,11 @@ extern "C" int mko_gated_norm_bwd(const mko_gated_norm_params* p, void* stream) 
     st = gnorm::launch_bwd<_Float16>(pl, *p, part, c1, s);
   if (st != MKO_OK) return st;
   if (params) {
-    MKO_TIMED("gated_norm_bwd_finalize", s,
-              gnorm::finalize<<<static_cast<unsigned>(gnorm::cdiv(p->features, kWave)), 1024, 0, s>>>(pl.g, *p,
-                                                                                                       part));
+    const int64_t mid = gnorm::sum_rows(g) * g.features;
+    MKO_TIMED("gated_norm_bwd_sums", s, {
+      if (g.want_dw) gnorm::column_sums(part, g.blocks, g.features, sums, p->dweight, s);
+      if (g.want_db) gnorm::column_sums(part + g.blocks * g.features, g.blocks, g.features, sums + mid, p->dbias, s);
+    });
   }
   return mko_check_launch("gated_norm_bwd");
 }

@@ -118,6 +118,7 @@ class GatedNormParams(ctypes.Structure):
         ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
         ("rows", ctypes.c_int64), ("features", ctypes.c_int64), ("group", ctypes.c_int64),
         ("eps", ctypes.c_float), ("dtype", ctypes.c_int32), ("gate", ctypes.c_int32),
+        ("wdtype", ctypes.c_int32),
     ]
 
 

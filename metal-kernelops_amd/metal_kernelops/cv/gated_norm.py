@@ -15,11 +15,12 @@ when ``group_size`` is None)::
 Every intermediate is float32 and the result comes back in ``x.dtype``, as in the
 reference (``:537-561``).
 
-How it runs: ``mko::gated_norm_fwd`` gives each ``(row, group)`` to a team of
+How it runs: ``mko_gated_norm_fwd`` gives each ``(row, group)`` to a team of
 wavefronts that holds the group in registers from the load to the store (x and z
-read once, out written once) and saves ``r`` per group; ``mko::gated_norm_bwd``
+read once, out written once) and saves ``r`` per group; ``mko_gated_norm_bwd``
 walks blocks of rows per group, writes dx and dz in the same pass and sums
-``dweight``/``dbias`` in a fixed order.  Groups wider than the register set
+``dweight``/``dbias`` in a fixed order.  Both are called through the C ABI from a
+plain autograd Function (first-order, as in the reference).  Groups wider than the register set
 (32768 elements forward, 8192 backward, fewer for unaligned groups) stream.
 
 Differences from the reference: tensors live on the ROCm GPU; float32, float16 and
@@ -32,10 +33,9 @@ reference's composed arithmetic for that case.
 from __future__ import annotations
 
 import ctypes
-from typing import Optional, Tuple
 
 import torch
-from torch import Tensor
+from torch.autograd.function import once_differentiable
 
 from .. import _native as nat
 from ..scan import _require_gpu
@@ -57,76 +57,62 @@ def _params(x, weight, bias, z, eps, group, gate):
     p.x, p.z, p.weight, p.bias = x.data_ptr(), nat.ptr(z), weight.data_ptr(), nat.ptr(bias)
     p.rows, p.features = x.shape
     p.group, p.eps = group, eps
-    p.dtype, p.gate = nat.code(x.dtype), gate
+    p.dtype, p.gate, p.wdtype = nat.code(x.dtype), gate, nat.code(weight.dtype)
     return p
 
 
-@torch.library.custom_op("mko::gated_norm_fwd", mutates_args=(), device_types="cuda")
-def _gated_norm_fwd(x: Tensor, weight: Tensor, bias: Optional[Tensor], z: Optional[Tensor], eps: float,
-                    group: int, gate: int) -> Tuple[Tensor, Tensor]:
+def _forward(x, weight, bias, z, eps, group, gate):
+    """``(out, rstd)`` for contiguous ``(rows, features)`` x (and z) on the GPU."""
     rows, features = x.shape
     out = torch.empty_like(x)
-    rstd = x.new_empty(rows * (features // group), dtype=torch.float32)
-    if x.numel() == 0:
-        return out, rstd
-    p = _params(x, weight, bias, z, eps, group, gate)
-    p.out, p.rstd = out.data_ptr(), rstd.data_ptr()
-    nat.check(nat.lib().mko_gated_norm_fwd(ctypes.byref(p), nat.stream_of(x.device)), "mko_gated_norm_fwd")
+    rstd = torch.empty(rows * (features // group), dtype=torch.float32, device=x.device)
+    if x.numel():
+        p = _params(x, weight, bias, z, eps, group, gate)
+        p.out, p.rstd = out.data_ptr(), rstd.data_ptr()
+        nat.check(nat.lib().mko_gated_norm_fwd(ctypes.byref(p), nat.stream_of(x.device)), "mko_gated_norm_fwd")
     return out, rstd
 
 
-@_gated_norm_fwd.register_fake
-def _(x, weight, bias, z, eps, group, gate):
-    rows, features = x.shape
-    return torch.empty_like(x), x.new_empty(rows * (features // group), dtype=torch.float32)
-
-
-@torch.library.custom_op("mko::gated_norm_bwd", mutates_args=(), device_types="cuda")
-def _gated_norm_bwd(dout: Tensor, x: Tensor, weight: Tensor, bias: Optional[Tensor], z: Optional[Tensor],
-                    rstd: Tensor, group: int, gate: int, need_weight: bool, need_bias: bool
-                    ) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+def _backward(dout, x, weight, bias, z, rstd, group, gate, need_weight, need_bias):
+    """``(dx, dz, dweight, dbias)``; dz is None without z, dweight/dbias float32 or None."""
     features = x.shape[1]
     dx = torch.empty_like(x)
-    dz = torch.empty_like(z) if z is not None else x.new_empty(0)
-    dweight = weight.new_zeros(features) if need_weight else weight.new_empty(0)
-    dbias = weight.new_zeros(features) if need_bias else weight.new_empty(0)
-    if x.numel() == 0:
-        return dx, dz, dweight, dbias
-    p = _params(x, weight, bias, z, 0.0, group, gate)
-    p.rstd, p.dout, p.dx = rstd.data_ptr(), dout.data_ptr(), dx.data_ptr()
-    p.dz = dz.data_ptr() if z is not None else None
-    p.dweight = dweight.data_ptr() if need_weight else None
-    p.dbias = dbias.data_ptr() if need_bias else None
-    ws = nat.workspace(nat.lib().mko_gated_norm_bwd_workspace_size(ctypes.byref(p)), x.device)
-    p.workspace, p.workspace_bytes = ws.data_ptr(), ws.numel()
-    nat.check(nat.lib().mko_gated_norm_bwd(ctypes.byref(p), nat.stream_of(x.device)), "mko_gated_norm_bwd")
+    dz = torch.empty_like(z) if z is not None else None
+    dweight = torch.zeros(features, dtype=torch.float32, device=x.device) if need_weight else None
+    dbias = torch.zeros(features, dtype=torch.float32, device=x.device) if need_bias else None
+    if x.numel():
+        p = _params(x, weight, bias, z, 0.0, group, gate)
+        p.rstd, p.dout, p.dx = rstd.data_ptr(), dout.data_ptr(), dx.data_ptr()
+        p.dz, p.dweight, p.dbias = nat.ptr(dz), nat.ptr(dweight), nat.ptr(dbias)
+        size = nat.lib().mko_gated_norm_bwd_workspace_size(ctypes.byref(p))
+        ws = nat.workspace(size, x.device) if size else None
+        p.workspace, p.workspace_bytes = nat.ptr(ws), size
+        nat.check(nat.lib().mko_gated_norm_bwd(ctypes.byref(p), nat.stream_of(x.device)), "mko_gated_norm_bwd")
     return dx, dz, dweight, dbias
 
 
-@_gated_norm_bwd.register_fake
-def _(dout, x, weight, bias, z, rstd, group, gate, need_weight, need_bias):
-    features = x.shape[1]
-    return (torch.empty_like(x), torch.empty_like(z) if z is not None else x.new_empty(0),
-            weight.new_empty(features if need_weight else 0), weight.new_empty(features if need_bias else 0))
+class _GatedRMSNorm(torch.autograd.Function):
+    """Fused forward, analytic first-order backward (as the reference's ``_GatedRMSNorm``,
+    ``cv/gated_norm.py:563-645``).  A plain autograd Function calling the C ABI: the
+    host cost per call is a few microseconds, which is what a layer this short needs."""
 
+    @staticmethod
+    def forward(ctx, x, weight, bias, z, eps, group, gate):
+        out, rstd = _forward(x, weight, bias, z, eps, group, gate)
+        ctx.save_for_backward(x, weight, bias, z, rstd)
+        ctx.group, ctx.gate = group, gate
+        return out
 
-def _setup(ctx, inputs, output):
-    x, weight, bias, z, _eps, group, gate = inputs
-    ctx.save_for_backward(x, weight, bias, z, output[1])
-    ctx.group, ctx.gate = group, gate
-
-
-def _backward(ctx, dout, _drstd):
-    x, weight, bias, z, rstd = ctx.saved_tensors
-    need = ctx.needs_input_grad
-    need_bias = bool(need[2] and bias is not None)
-    dx, dz, dweight, dbias = torch.ops.mko.gated_norm_bwd(
-        dout.contiguous(), x, weight, bias, z, rstd, ctx.group, ctx.gate, bool(need[1]), need_bias)
-    return (dx, dweight if need[1] else None, dbias if need_bias else None,
-            dz if z is not None and need[3] else None, None, None, None)
-
-
-torch.library.register_autograd("mko::gated_norm_fwd", _backward, setup_context=_setup)
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, dout):
+        x, weight, bias, z, rstd = ctx.saved_tensors
+        need = ctx.needs_input_grad
+        need_bias = bool(need[2] and bias is not None)
+        dx, dz, dweight, dbias = _backward(dout.contiguous(), x, weight, bias, z, rstd, ctx.group, ctx.gate,
+                                           bool(need[1]), need_bias)
+        return (dx, dweight.to(weight.dtype) if need[1] else None, dbias.to(bias.dtype) if need_bias else None,
+                dz if z is not None and need[3] else None, None, None, None)
 
 
 def _checked_group(x, weight, bias, z, group_size):
@@ -150,7 +136,7 @@ def rmsnorm_gated(x, weight, bias=None, z=None, eps=1e-5, group_size=None, norm_
 
     Args:
         x: ``(..., features)``, float32, float16 or bfloat16 on the ROCm GPU.
-        weight: ``(features,)`` scale, any float dtype (used as float32; its gradient
+        weight: ``(features,)`` scale, any float dtype (read as float32; its gradient
             comes back in its own dtype).
         bias: ``(features,)`` shift, added before the gate, or None.
         z: the gate, shaped like ``x``, or None.
@@ -182,9 +168,11 @@ def rmsnorm_gated(x, weight, bias=None, z=None, eps=1e-5, group_size=None, norm_
     rows_x = x.reshape(-1, features).to(work).contiguous()
     rows_z = z.reshape(-1, features).to(work).contiguous() if z is not None else None
     gate = GATE_NONE if z is None else (GATE_AFTER if norm_before_gate else GATE_BEFORE)
-    out, _ = torch.ops.mko.gated_norm_fwd(
-        rows_x, weight.float().contiguous(), bias.float().contiguous() if bias is not None else None, rows_z,
-        float(eps), group, gate)
+    # weight and bias are read in their own dtype when it is one the kernels take
+    pdtype = weight.dtype if weight.dtype in _FLOATS else torch.float32
+    w = weight.to(pdtype).contiguous()
+    b = bias.to(pdtype).contiguous() if bias is not None else None
+    out = _GatedRMSNorm.apply(rows_x, w, b, rows_z, float(eps), group, gate)
     return out.reshape(shape).to(x.dtype)
 
 

@@ -320,6 +320,23 @@ def test_mixed_weight_and_gate_dtypes():
         outb = rmsnorm_gated(xb.to(DEV), wb.to(DEV), z=zf.to(DEV), norm_before_gate=False)
     wantb, _ = oracle.rmsnorm_gated(xb, wb, None, zf, norm_before_gate=False)
     assert outb.dtype == torch.bfloat16 and fwd_error(outb, wantb) < 4e-2
+    # bfloat16 parameters on float32 activations (read as 4-element, 8-byte vectors), and
+    # float64 parameters (made float32 for the kernel); gradients come back in their dtype
+    for pdtype in (torch.bfloat16, torch.float64):
+        x4, z4 = make((48, 640), 37, 1.0, torch.float32), make((48, 640), 38, 1.0, torch.float32)
+        w4, b4 = make((640,), 39, 1.0, pdtype), make((640,), 40, 1.0, pdtype)
+        dy = make((48, 640), 41, 1.0, torch.float32)
+        leaves = [t.to(DEV).requires_grad_(True) for t in (x4, w4, b4, z4)]
+        out4 = rmsnorm_gated(*leaves, group_size=160, norm_before_gate=False)
+        out4.backward(dy.to(DEV))
+        want4, _ = oracle.rmsnorm_gated(x4, w4, b4, z4, group_size=160, norm_before_gate=False)
+        assert fwd_error(out4, want4) <= 2e-5
+        grads = oracle.rmsnorm_gated_bwd(dy, x4, w4, b4, z4, group_size=160, norm_before_gate=False)
+        for leaf, want in zip(leaves, (grads[0], grads[1], grads[2], grads[3])):
+            assert leaf.grad.dtype == leaf.dtype
+            # the parameter gradients are float32 sums rounded once to the parameter dtype
+            tol = 1e-6 if leaf.dtype != torch.bfloat16 else 2 ** -8
+            assert rel(leaf.grad, want) <= tol, (pdtype, leaf.dtype, rel(leaf.grad, want))
 
 
 @pytest.mark.gpu
