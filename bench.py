@@ -430,7 +430,8 @@ def conv1d_case(steps, warmup, shape=CONV_SHAPE):
     fwd_b, bwd_b = conv1d_bytes(*shape)
     name, avg, count = dominant(kernels)
     per_kernel = {"conv1d_bwd": bwd_b, "conv1d_fwd": fwd_b}
-    roof = roofline(per_kernel.get(name, fwd_b + bwd_b), avg)
+    roof = roofline(per_kernel.get(name, fwd_b + bwd_b), avg,
+                    load_traffic(f"{name}@{batch}x{channels}x{length}x{width}"))
     roof["kernel"] = name
     roof["algorithmic_bytes"] = per_kernel.get(name, fwd_b + bwd_b)
     # decode: one token against a 3-column state, 64 x 2048 (the reference's update-64x2048x1)
@@ -504,7 +505,7 @@ def norm_case(steps, warmup, shape=NORM_SHAPE):
     fwd_b, bwd_b = norm_bytes(*shape)
     name, avg, count = dominant(kernels)
     per_kernel = {"gated_norm_bwd": bwd_b, "gated_norm_fwd": fwd_b}
-    roof = roofline(per_kernel.get(name, fwd_b + bwd_b), avg, load_traffic(name))
+    roof = roofline(per_kernel.get(name, fwd_b + bwd_b), avg, load_traffic(f"{name}@{rows}x{features}"))
     roof["kernel"] = name
     roof["algorithmic_bytes"] = per_kernel.get(name, fwd_b + bwd_b)
     with torch.no_grad():
