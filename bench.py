@@ -16,7 +16,8 @@ recorded by libmko on the kernel's own stream.  ``cpu_baseline`` times the float
 oracle's restatement (run in float32 with autograd) on a bounded sample on this
 host.  ``also`` carries the other workloads of the path (Mamba-1 130M layer,
 Mamba-2 decode, Mamba-2 SSD chunk scan, the four-path 2D scan, the causal conv1d
-ahead of the scan, the gated RMSNorm after it) with their own rooflines.
+ahead of the scan, the gated RMSNorm after it, and the integration verifier's blocks with a
+Mamba-2 2.7B layer) with their own rooflines where a kernel dominates.
 """
 
 from __future__ import annotations
@@ -548,6 +549,104 @@ def norm_cpu_baseline(shape=(2048, 2560)):
                       f"{best * 1e3:.1f} ms"}
 
 
+class Mamba2Layer(torch.nn.Module):
+    """The reference verifier's Mamba-2 block (``benchmarks/verify_cv_integration.py:38-78``):
+    in_proj, causal conv1d with SiLU, chunked SSD scan with skip, step bias and softplus, gated
+    RMSNorm (gate before the norm), out_proj -- on the package's kernels."""
+
+    def __init__(self, d_model, heads, head_dim, d_state, conv=4, chunk=256):
+        super().__init__()
+        self.heads, self.head_dim, self.d_state, self.chunk = heads, head_dim, d_state, chunk
+        inner = heads * head_dim
+        self.inner = inner
+        self.in_proj = torch.nn.Linear(d_model, 2 * inner + 2 * d_state + heads)
+        self.conv_weight = torch.nn.Parameter(torch.randn(inner + 2 * d_state, 1, conv) * .3)
+        self.conv_bias = torch.nn.Parameter(torch.randn(inner + 2 * d_state) * .1)
+        self.a_log = torch.nn.Parameter(torch.randn(heads) * .2)
+        self.d_skip = torch.nn.Parameter(torch.ones(heads))
+        self.dt_bias = torch.nn.Parameter(torch.randn(heads) * .2)
+        self.norm_weight = torch.nn.Parameter(torch.ones(inner))
+        self.out_proj = torch.nn.Linear(inner, d_model)
+
+    def forward(self, x):
+        from metal_kernelops.cv import causal_conv1d_fn, mamba2_chunk_scan, rmsnorm_gated
+        inner, n = self.inner, self.d_state
+        zxbcdt = self.in_proj(x)
+        z, xbc, dt = zxbcdt[..., :inner], zxbcdt[..., inner:2 * inner + 2 * n], zxbcdt[..., 2 * inner + 2 * n:]
+        xbc = causal_conv1d_fn(xbc.transpose(1, 2), self.conv_weight.reshape(inner + 2 * n, -1), self.conv_bias,
+                               activation="silu").transpose(1, 2)
+        x_ssm = xbc[..., :inner].reshape(x.shape[0], x.shape[1], self.heads, self.head_dim)
+        y, _ = mamba2_chunk_scan(x_ssm, dt, -torch.exp(self.a_log), xbc[..., inner:inner + n].unsqueeze(2),
+                                 xbc[..., inner + n:].unsqueeze(2), chunk_size=self.chunk, D=self.d_skip,
+                                 dt_bias=self.dt_bias, dt_softplus=True)
+        y = rmsnorm_gated(y.reshape(x.shape[0], x.shape[1], inner), self.norm_weight, z=z, norm_before_gate=False)
+        return self.out_proj(y)
+
+
+class PathLayer(torch.nn.Module):
+    """The verifier's VMamba-style block (``benchmarks/verify_cv_integration.py:81-100``)."""
+
+    def __init__(self, channels=6, groups=2, states=4):
+        super().__init__()
+        self.groups, self.states = groups, states
+        self.u = torch.nn.Conv2d(channels, channels, 3, padding=1)
+        self.dt = torch.nn.Conv2d(channels, channels, 1)
+        self.b = torch.nn.Conv2d(channels, groups * states, 1)
+        self.c = torch.nn.Conv2d(channels, groups * states, 1)
+        self.a = torch.nn.Parameter(-torch.rand(channels, states))
+
+    def forward(self, x):
+        from metal_kernelops.cv import ss2d_scan
+        shape = (x.shape[0], self.groups, self.states, x.shape[2], x.shape[3])
+        return ss2d_scan(self.u(x), torch.nn.functional.softplus(self.dt(x)), self.a,
+                         self.b(x).reshape(shape), self.c(x).reshape(shape), merge="sum")
+
+
+BLOCK_LAYER = dict(d_model=2560, heads=80, head_dim=64, d_state=128)  # Mamba-2 2.7B layer
+BLOCK_TOKENS = (2, 4096)
+
+
+def block_case(steps, warmup):
+    """The verifier's two blocks at its shapes (fwd + bwd + zero_grad per step, as its timing
+    loop, ``verify_cv_integration.py:141-155``), and a Mamba-2 2.7B layer in bf16."""
+    torch.manual_seed(17)
+    dev = torch.device("cuda")
+    out = {}
+    with torch.backends.cudnn.flags(enabled=False):  # torch's own convolutions, no MIOpen tuning
+        for name, layer, shape in (("mamba2_block", Mamba2Layer(24, 2, 6, 5, chunk=8), (2, 19, 24)),
+                                   ("path_block", PathLayer(), (2, 6, 9, 11))):
+            layer = layer.to(dev)
+            x = torch.randn(*shape, device=dev)
+
+            def step():
+                layer(x).square().mean().backward()
+                layer.zero_grad(set_to_none=True)
+
+            ms, _, _ = timed(step, steps, warmup)
+            out[name] = {"ms_per_step": round(ms, 4), "shape": list(shape)}
+    layer = Mamba2Layer(**BLOCK_LAYER).to(dev).bfloat16()
+    for p in (layer.a_log, layer.d_skip, layer.dt_bias):
+        p.data = p.data.float()
+    batch, length = BLOCK_TOKENS
+    x = torch.randn(batch, length, BLOCK_LAYER["d_model"], device=dev, dtype=torch.bfloat16)
+    gy = torch.randn_like(x)
+
+    def layer_step():
+        layer(x).backward(gy)
+        layer.zero_grad(set_to_none=True)
+
+    ms, _, kernels = timed(layer_step, max(steps // 2, 3), warmup)
+    tokens = batch * length
+    out["mamba2_2.7b_layer"] = {
+        "value": round(tokens / (ms * 1e-3), 1), "unit": "tokens/s", "ms_per_step": round(ms, 4),
+        "config": dict(BLOCK_LAYER, batch=batch, seqlen=length, conv=4, dtype="bf16", ngroups=1),
+        "kernels_ms": {k: round(v[0] / max(v[1], 1), 4) for k, v in sorted(kernels.items())},
+        "mko_kernels_ms_per_step": round(sum(v[0] for v in kernels.values()) / max(steps // 2, 3), 4)}
+    del layer, x, gy
+    torch.cuda.empty_cache()
+    return out
+
+
 # --------------------------------------------------------------------- main
 
 
@@ -557,7 +656,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-cpu", action="store_true", help="skip the CPU baseline legs")
-    ap.add_argument("--only", choices=["mamba1", "ssd", "decode", "ss2d", "conv1d", "norm", "copy", "all"],
+    ap.add_argument("--only", choices=["mamba1", "ssd", "decode", "ss2d", "conv1d", "norm", "block", "copy", "all"],
                     default="all",
                     help="one workload (mamba1 = the config-3 headline alone) or all of them; copy = "
                          "a plain 1 GiB device copy, the calibration point of the PMC byte counters")
@@ -657,6 +756,13 @@ def main():
             "roofline": nm["roofline"], "kernels_ms": nm["kernels_ms"]}
         log(f"  {nm['ms_per_step'] * 1e3:.1f} us/step, {nm['gbs']:.1f} GB/s; forward {nm['fwd_us']:.1f} us; "
             f"kernels {nm['kernels_ms']}")
+    if want("block"):
+        log("Mamba-2 block and path-scan block at the integration verifier's shapes; Mamba-2 2.7B layer bf16")
+        bl = block_case(args.steps, args.warmup)
+        also["integration_blocks_fwd_bwd"] = bl
+        log(f"  verifier blocks {bl['mamba2_block']['ms_per_step']:.3f} / {bl['path_block']['ms_per_step']:.3f} ms; "
+            f"2.7B layer {bl['mamba2_2.7b_layer']['ms_per_step']:.3f} ms/step, "
+            f"{bl['mamba2_2.7b_layer']['value'] / 1e6:.2f} M tokens/s; kernels {bl['mamba2_2.7b_layer']['kernels_ms']}")
     if head is None:  # a single non-headline workload: print its own record
         print(json.dumps(also), flush=True)
         return
