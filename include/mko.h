@@ -83,8 +83,8 @@ typedef struct mko_selscan_params {
   const float* delta_bias;  /* (dim,) or NULL                                     */
   /* forward outputs */
   void* out;                /* (batch, dim, length) u_dtype                        */
-  float* states;            /* (batch, mko_selscan_num_checkpoints(length), dstate, dim):
-                               the state entering every 16-step block, channel-fastest;
+  float* states;            /* (batch, mko_selscan_num_checkpoints(length), dim, dstate):
+                               the state entering every 16-step block, state-fastest;
                                written by the forward, read by the backward         */
   /* backward input */
   const void* dout;         /* (batch, dim, length) u_dtype                        */
@@ -105,7 +105,7 @@ typedef struct mko_selscan_params {
   uint32_t flags;
 } mko_selscan_params;
 
-/* ceil(length / MKO_SS_CHECKPOINT): the third extent of params.states. */
+/* ceil(length / MKO_SS_CHECKPOINT): the second extent of params.states. */
 int64_t mko_selscan_num_checkpoints(int64_t length);
 
 /* Replaces _Scan.forward (scan.py:237-255) together with the pointwise pre/post

@@ -108,11 +108,12 @@ __device__ __forceinline__ float step_of(const Geo& g, float raw, float bias) {
   return g.softplus ? softplus(v) : v;
 }
 
-// Saved scan states, (batch, checkpoint, state, dim): channel-fastest, so a
-// wavefront's 64 rows (consecutive channels) read or write 256 contiguous bytes.
+// Saved scan states, (batch, checkpoint, dim, state): a channel's states are contiguous, so
+// a lane-per-channel wavefront reads or writes 64 consecutive channels' states as one run,
+// and the lane-per-state kernels' 4 channels x 16 states are 256 contiguous bytes.
 __device__ __forceinline__ int64_t ck_index(const Geo& g, int64_t row, int64_t k, int64_t n) {
   const int64_t b = row / g.dim, d = row - b * g.dim;
-  return ((b * g.nck + k) * g.dstate + n) * g.dim + d;
+  return ((b * g.nck + k) * g.dim + d) * g.dstate + n;
 }
 
 // ---------------------------------------------------------------- layout prep
@@ -513,10 +514,15 @@ __global__ void __launch_bounds__(256) fwd_replay(Geo g, Ptrs p) {
     static_assert(CK == HS, "one saved state per block");
     {
       float* sp = p.states + ck_index(g, li.row, t0 / CK, 0);
-      const int sd = static_cast<int>(g.dim);
+      if constexpr (FULL) {
 #pragma unroll
-      for (int n = 0; n < NS; ++n)
-        if (FULL || n < N) sp[n * sd] = x[n];
+        for (int v = 0; v < NS / 4; ++v)
+          reinterpret_cast<float4*>(sp)[v] = make_float4(x[4 * v], x[4 * v + 1], x[4 * v + 2], x[4 * v + 3]);
+      } else {
+#pragma unroll
+        for (int n = 0; n < NS; ++n)
+          if (n < N) sp[n] = x[n];
+      }
     }
     const int nv = min(HS, t_end - t0);
     float raw[HS], uu[HS], zz[HS], del[HS], du[HS], y[HS];
@@ -544,6 +550,117 @@ __global__ void __launch_bounds__(256) fwd_replay(Geo g, Ptrs p) {
       for (int i = 0; i < HS; ++i) y[i] *= zz[i] * sigmoid(zz[i]);
     }
     if (li.active) store_u<TU>(g, p.out, rbase + t0, nv, y);
+  }
+}
+
+// ---------------------------------------------------------------- forward, lane per (channel, state)
+//
+// With dstate <= 16 and enough rows, a wavefront holds 4 channels x 16 states, lane (c, n),
+// and walks the whole sequence once, 16 steps a block: no time chunks, so no summary pass
+// and no replay.  Per block:
+//   - lane (c, n) loads step t0 + n of its channel's delta, u and z (a wavefront reads 4 rows
+//     x 16 consecutive steps) and forms that step's size and du = step * u;
+//   - it advances its one state over the 16 steps, reading step i's size and du from lane i
+//     of its row (DPP row_newbcast, folded into the multiplies) and B_n, C_n of those steps
+//     from 16 consecutive values of its state's row of the caller's B and C (as stored:
+//     16-bit rows are half the vector-memory traffic of float32 copies);
+//   - the 16 states' C_n x_n per step go through a per-wavefront LDS transpose, so lane
+//     (c, n) sums step t0 + n's, adds the skip, applies the gate and stores it;
+//   - the state entering the block is saved (4 channels x 16 states: 256 contiguous bytes).
+// The next block's loads are issued before the current block is computed.
+
+template <int I, int END, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < END) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, END>(f);
+  }
+}
+
+// The value held by lane I of each 16-lane row, in every lane of that row.
+template <int I>
+__device__ __forceinline__ float row_newbcast(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + I, 0xf, 0xf, false));
+}
+
+constexpr int kLaneChannels = 4;  // channels per wavefront in the lane-per-state kernels
+
+template <class TU, class TB>
+__global__ void __launch_bounds__(256) fwd_lane(Geo g, Ptrs p) {
+  constexpr int kRow = HS + 1;   // a step's 16 states, padded so the transposed reads miss no bank
+  constexpr int kCS = HS * kRow; // one channel's [step][state] block (272 floats: 16 banks apart)
+  __shared__ float sy[4][kLaneChannels * kCS];
+  const int wave = uniform(static_cast<int>(threadIdx.x >> 6));
+  const int lane = threadIdx.x & 63, cl = lane >> 4, n = lane & 15;
+  const int64_t row = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * kLaneChannels + cl;
+  const bool active = row < g.rows;
+  const int64_t r = active ? row : g.rows - 1;
+  const int64_t bb = r / g.dim, d = r - bb * g.dim;
+  const int64_t bg = bb * g.ngroups + d / g.dg;
+  const int N = static_cast<int>(g.dstate);
+  const bool sn = n < N;
+  const float a2 = sn ? p.A[d * N + n] * kLog2e : 0.0f;
+  const float bias = p.bias ? p.bias[d] : 0.0f;
+  const float Dd = p.D ? p.D[d] : 0.0f;
+  const bool has_z = p.z != nullptr;
+  const int64_t L = g.length;
+  const int64_t rbase = r * L + n;  // this lane's step of every block
+  const int64_t bcrow = (bg * N + (sn ? n : 0)) * L;
+  const float* dp = static_cast<const float*>(p.delta) + rbase;
+  const TU* up = static_cast<const TU*>(p.u) + rbase;
+  const TU* zp = static_cast<const TU*>(has_z ? p.z : p.u) + rbase;
+  TU* op = static_cast<TU*>(p.out) + rbase;
+  float* sp = p.states + ck_index(g, r, 0, sn ? n : 0);
+  const int64_t sstep = g.dim * N;  // one saved state further
+  float* sw = sy[wave] + cl * kCS;
+
+  struct In {
+    float dl;
+    TU u, z;
+    RawRun<TB> b, c;
+  };
+  auto load = [&](int64_t t0, In& in) {
+    in.dl = dp[t0];
+    in.u = up[t0];
+    in.z = zp[t0];
+    in.b.load(g, p.B, 0, bcrow + t0, HS);
+    in.c.load(g, p.C, 0, bcrow + t0, HS);
+  };
+  In cur, nxt;
+  load(0, cur);
+  float x = 0.0f;
+  const int64_t nblk = L / HS;
+  for (int64_t k = 0; k < nblk; ++k) {
+    const int64_t t0 = k * HS;
+    load((k + 1 < nblk ? k + 1 : k) * HS, nxt);  // the last block loads itself again
+    if (active && sn) sp[k * sstep] = x;
+    const float uu = to_f32(cur.u);
+    const float del = step_of(g, cur.dl, bias);
+    const float du = del * uu;
+    float bv[HS], cv[HS];
+    cur.b.get(bv);
+    cur.c.get(cv);
+    if (N < HS && !sn) {  // a padded state adds nothing (its B row is state 0's)
+#pragma unroll
+      for (int i = 0; i < HS; ++i) bv[i] = cv[i] = 0.0f;
+    }
+    static_for<0, HS>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      x = fmaf(fast_exp2(a2 * row_newbcast<i>(del)), x, row_newbcast<i>(du) * bv[i]);
+      sw[i * kRow + n] = cv[i] * x;
+    });
+    wave_lds_sync();
+    float ys = 0.0f;
+#pragma unroll
+    for (int m = 0; m < HS; ++m) ys += sw[n * kRow + m];
+    wave_lds_sync();
+    float y = fmaf(Dd, uu, ys);
+    if (has_z) {
+      const float zz = to_f32(cur.z);
+      y *= zz * sigmoid(zz);
+    }
+    if (active) op[t0] = from_f32<TU>(y);
+    cur = nxt;
   }
 }
 
@@ -766,9 +883,8 @@ __global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
   // blocks in reverse, states one at a time
   for (int j = je - 1; j >= jb; --j) {
     const int qs = j * CK;
-    // saved state entering block j, element n at srow[n * srow_stride]
+    // saved state entering block j, element n at srow[n]
     const float* srow = p.states + ck_index(g, li.row, j, 0);
-    const int srow_stride = static_cast<int>(g.dim);
     {
       const int nv = min(HS, t_end - qs);
       float del[HS], du[HS], gy[HS];
@@ -817,7 +933,7 @@ __global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
         __syncthreads();
       }
       const float* xin_p = srow;
-      const int xin_stride = srow_stride;
+      const int xin_stride = 1;
       const float* bn_p = p.bn + (li.bg * NS) * g.length + qs;
       const float* cn_p = p.cn + (li.bg * NS) * g.length + qs;
       float xin_n = xin_p[0];
@@ -1046,6 +1162,7 @@ struct Plan {
   Geo g;
   int ns;
   bool uni;
+  bool lane;  // forward through fwd_lane (set per call from pointer alignment and shape)
   size_t off_bt, off_ct, off_bn, off_cn, off_drive, off_sumd, off_adj, off_pbc, off_dap, off_ddp,
       off_dbp;
   size_t fwd_bytes, bwd_bytes;
@@ -1187,9 +1304,29 @@ static inline unsigned blocks_for(int64_t n, int per = 256) {
   return static_cast<unsigned>((n + per - 1) / per);
 }
 
+// Rows from which the lane-per-state forward has enough wavefronts (rows / 4 of them) to
+// fill the chip without time chunks.
+constexpr int64_t kLaneRows = 6144;
+
+template <class TU>
+static int launch_fwd_lane(const Plan& pl, const Ptrs& q, hipStream_t s) {
+  const Geo& g = pl.g;
+  const unsigned grid = static_cast<unsigned>((g.rows + 4 * kLaneChannels - 1) / (4 * kLaneChannels));
+  if (g.bc_dtype == MKO_BF16)
+    MKO_TIMED("selscan_fwd_lane", s, fwd_lane<TU, bf16><<<grid, 256, 0, s>>>(g, q));
+  else if (g.bc_dtype == MKO_F16)
+    MKO_TIMED("selscan_fwd_lane", s, fwd_lane<TU, _Float16><<<grid, 256, 0, s>>>(g, q));
+  else
+    MKO_TIMED("selscan_fwd_lane", s, fwd_lane<TU, float><<<grid, 256, 0, s>>>(g, q));
+  return mko_check_launch("selscan_fwd");
+}
+
 template <int NS, bool UNI, class TU>
 static int launch_fwd(const Plan& pl, const Ptrs& q, hipStream_t s) {
   const Geo& g = pl.g;
+  if constexpr (NS == 16 && !__is_same(TU, Dyn)) {
+    if (pl.lane) return launch_fwd_lane<TU>(pl, q, s);
+  }
   const dim3 block(g.wpg * kWave);
   const unsigned gx = static_cast<unsigned>((g.nwr + g.wpg - 1) / g.wpg);
   const int64_t bgl = g.batch * g.ngroups * g.length;
@@ -1281,6 +1418,8 @@ extern "C" int mko_selscan_fwd(const mko_selscan_params* p, void* stream) {
   }
   pl.g.vec = rows_vectorisable(pl.g, {{p->u, p->u_dtype}, {p->delta, p->delta_dtype}, {p->z, p->u_dtype},
                                       {p->out, p->u_dtype}}) ? 1 : 0;
+  pl.lane = pl.ns == 16 && pl.g.rows >= kLaneRows && pl.g.length % HS == 0 &&
+            rows_vectorisable(pl.g, {{p->B, p->bc_dtype}, {p->C, p->bc_dtype}});
   Ptrs q = make_ptrs(p, pl);
   hipStream_t s = static_cast<hipStream_t>(stream);
   return dispatch_types(pl, p->u_dtype, p->delta_dtype, [&](auto tag) {

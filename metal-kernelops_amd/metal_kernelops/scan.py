@@ -63,7 +63,7 @@ def _selscan_fwd(u: Tensor, delta: Tensor, A: Tensor, B: Tensor, C: Tensor, D: O
                  ) -> Tuple[Tensor, Tensor]:
     batch, dim, length = u.shape
     out = torch.empty_like(u)
-    states = torch.empty(batch, _num_checkpoints(length), A.shape[1], dim, dtype=torch.float32,
+    states = torch.empty(batch, _num_checkpoints(length), dim, A.shape[1], dtype=torch.float32,
                          device=u.device)
     if out.numel() == 0:
         return out, states
@@ -79,7 +79,7 @@ def _selscan_fwd(u: Tensor, delta: Tensor, A: Tensor, B: Tensor, C: Tensor, D: O
 @_selscan_fwd.register_fake
 def _(u, delta, A, B, C, D, z, delta_bias, softplus):
     batch, dim, length = u.shape
-    return torch.empty_like(u), u.new_empty(batch, _num_checkpoints(length), A.shape[1], dim,
+    return torch.empty_like(u), u.new_empty(batch, _num_checkpoints(length), dim, A.shape[1],
                                             dtype=torch.float32)
 
 

@@ -128,6 +128,45 @@ def test_bf16_delta_and_fp16():
     _compare(inputs, dy, True, 2e-2, 2e-2)
 
 
+# At 6144 channels (batch x dim) and more, dstate <= 16 and whole 16-step blocks, the forward
+# runs one lane per (channel, state) over the whole sequence; its saved states feed the backward.
+LANE_SHAPES = [
+    (2, 3072, 64, 16, 1),   # the smallest lane-path problem
+    (2, 3072, 48, 12, 2),   # dstate 12 (lanes 12..15 idle), two groups
+    (1, 6200, 32, 16, 4),   # a ragged last wavefront, four groups of 1550 channels
+]
+
+
+@pytest.mark.parametrize("shape", LANE_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_lane_forward_shapes_fp32(shape):
+    inputs, dy = _random_problem(*shape, seed=sum(shape))
+    _compare(inputs, dy, True, 1e-5, 1e-4)
+
+
+@pytest.mark.parametrize("opts", [dict(d=False), dict(z=False), dict(bias=False),
+                                  dict(d=False, z=False, bias=False)],
+                         ids=["noD", "noz", "nobias", "bare"])
+@pytest.mark.parametrize("softplus", [True, False])
+def test_lane_forward_options(opts, softplus):
+    inputs, dy = _random_problem(2, 3072, 32, 16, 1, seed=17, **opts)
+    if not softplus:
+        inputs["dt"] = torch.rand(inputs["dt"].shape) * 0.3
+        if inputs["delta_bias"] is not None:
+            inputs["delta_bias"] = inputs["delta_bias"].abs() * 0.1
+    _compare(inputs, dy, softplus, 1e-5, 1e-4)
+
+
+def test_lane_forward_16bit():
+    inputs, dy = _random_problem(2, 3072, 64, 16, 1, seed=19, act=torch.bfloat16)
+    _compare(inputs, dy, True, 2e-2, 2e-2)
+    inputs, dy = _random_problem(2, 3072, 64, 16, 1, seed=20, act=torch.float16)
+    _compare(inputs, dy, True, 2e-2, 2e-2)
+    # 16-bit u and z with float32 B and C
+    inputs, dy = _random_problem(2, 3072, 64, 16, 1, seed=21, act=torch.bfloat16)
+    inputs["B"], inputs["C"] = inputs["B"].float(), inputs["C"].float()
+    _compare(inputs, dy, True, 2e-2, 2e-2)
+
+
 def test_deterministic_backward():
     inputs, dy = _random_problem(2, 256, 300, 16, 1, seed=12)
     runs = [_gpu(inputs, dy, True) for _ in range(2)]
