@@ -1227,15 +1227,19 @@ static int make_plan(const mko_selscan_params* p, Plan* pl) {
   }
   // Coarse chunks: about eight wavefronts per SIMD over the chip's 1024 SIMDs
   // (the state-inner loops hide their scalar-load waits with other waves), the
-  // chunk a multiple of the save interval and at least 128 steps: shorter chunks
-  // cost more in per-chunk summaries and dA partials than their parallelism buys
-  // (c2, 8 x 1536 x 2048: 64 chunks of 32 steps 1.07 ms, 16 of 128 0.95 ms).
+  // chunk a multiple of the save interval and, while that still leaves about 2048
+  // wavefronts, at least 128 steps: shorter chunks cost more in per-chunk summaries
+  // and dA partials than their parallelism buys (c2, 8 x 1536 x 2048: 64 chunks of 32
+  // steps 1.07 ms, 16 of 128 0.95 ms), but a problem of few channel rows (the 2D scan's
+  // 384 rows) needs the short chunks for its wavefronts.
   int64_t want = (8192 + g.nwr - 1) / (g.nwr > 0 ? g.nwr : 1);
   int64_t k = 1;
   while (k < want) k <<= 1;
   int64_t lc = (g.length + k - 1) / k;
   lc = ((lc + CK - 1) / CK) * CK;
-  if (lc < 128) lc = 128;
+  int64_t lmin = 128;
+  while (lmin > CK && g.nwr * ((g.length + lmin - 1) / lmin) < 2048) lmin /= 2;
+  if (lc < lmin) lc = lmin;
   g.lc = static_cast<int>(lc);
   g.nchunks = static_cast<int>(g.length > 0 ? (g.length + lc - 1) / lc : 0);
   g.vec = 0;
