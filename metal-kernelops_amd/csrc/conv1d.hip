@@ -4,14 +4,16 @@
 //   pre[b, c, t] = bias[c] + sum_{j < K} w[c, j] z[b, c, t + j]      (z index t + j = time t - m + j)
 //   out          = act(pre),  act = identity or silu
 //   final_state  = z[..., L : L + m]
-// The forward gives a lane one 8-step block (one 16-byte vector load on aligned rows, so
-// a wavefront's loads are whole lines) plus the look-back steps.  In the backward a lane
-// walks RB consecutive blocks of one row with sliding register windows: one vector load
-// of x and of dout per block, the look-back and look-ahead steps carried over.
+// Widths up to 8: a wavefront covers 64 * WB consecutive 8-step blocks of one row, lane l
+// taking blocks l, l + 64, ... (one 16-byte vector load per block on aligned rows, so every
+// wavefront access is 64 consecutive blocks); the look-back (and, in the backward,
+// look-ahead) steps come from the neighbouring lanes.  Wider kernels: the forward gives a
+// lane one block; the backward walks RB consecutive blocks with sliding register windows.
 // Backward: the lane recomputes pre over its window, writes dx, and sums the taps'
 // gradients dw[c, j] = sum_t g[t] z[t - m + j] and dbias = sum_t g[t] (g = dout act'(pre))
-// over its steps; 16 lanes of a row add theirs with DPP, and `finalize` adds those
-// partials over batch and along the row in a fixed order, so the sums are deterministic.
+// over its steps; the lanes of a wavefront (or of a 16-lane group, wider kernels) add
+// theirs with DPP, and `finalize_il` / `finalize` add those partials over batch and along
+// the row in a fixed order, so the sums are deterministic.
 // Decode: one lane per row advances a rolling state of `span` columns by q tokens in
 // place.
 #include "common.hpp"
@@ -22,15 +24,16 @@ namespace conv {
 namespace {
 
 constexpr int BS = 8;  // steps per block
-constexpr int RB = 4;  // blocks per lane in the backward (the forward takes one: its loads
-                       // are whole-wavefront lines only when neighbouring lanes hold
-                       // neighbouring blocks)
+constexpr int RB = 4;  // blocks per lane in the wide-kernel backward (width > 8)
+constexpr int WB = 4;  // iterations of the interleaved backward: a wavefront covers 64 * WB
+                       // consecutive blocks of a row, lane l taking blocks l, l + 64, ...
 
 struct Geo {
   int64_t batch, channels, length, rows;  // rows = batch * channels
   int width, taps;                          // taps = width - 1
   int64_t nblk;                             // blocks of BS steps per row
   int64_t lpr;                              // lanes per row: ceil(nblk / RB), rounded up to 16
+  int64_t nseg;                             // interleaved backward: wavefronts per row
   int dtype;
   int silu;
   int vec;                                  // rows are 16-byte aligned whole blocks
@@ -232,6 +235,215 @@ __global__ void __launch_bounds__(256) backward(Geo g, mko_conv1d_params p, floa
   if (writer) dst[g.width] = vb;
 }
 
+// Forward for widths up to 8, blocks interleaved across lanes as in `backward_il`: a
+// wavefront covers 64 * WB consecutive blocks of one row, every load and store is 64
+// consecutive blocks, and the H steps before a block come from lane l - 1 (lane 0: the
+// carry of lane 63's previous block, or the initial state).  The per-row setup (index
+// arithmetic, taps, bias) is paid once per four blocks.
+template <int KMAX>
+__global__ void __launch_bounds__(256) forward_il(Geo g, mko_conv1d_params p) {
+  constexpr int H = KMAX - 1;
+  static_assert(H < BS, "look-back within one neighbouring block");
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t wv = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + (threadIdx.x >> 6);
+  if (wv >= g.rows * g.nseg) return;  // wave-uniform: whole wavefronts leave
+  const int64_t row = wv / g.nseg, seg = wv % g.nseg;
+  const int64_t c = row % g.channels;
+  float wp[KMAX];
+  load_taps<KMAX>(g, p.weight, c, wp);
+  const float bias = p.bias ? load_one(p.bias, g.dtype, c) : 0.0f;
+  const int64_t base = seg * kWave * WB;
+  float carry[H];
+#pragma unroll
+  for (int i = 0; i < H; ++i) carry[i] = z_at(g, p.x, p.initial_state, row, base * BS - H + i);
+  float xc[BS];
+  row_block(g, p.x, row, base + lane, xc);
+  for (int k = 0; k < WB; ++k) {
+    const int64_t blk = base + k * kWave + lane;
+    if (base + k * kWave >= g.nblk) break;  // wave-uniform: no block of this iteration exists
+    float xn[BS];
+    if (k + 1 < WB) row_block(g, p.x, row, blk + kWave, xn);  // in flight during this block
+    float zz[H + BS];
+#pragma unroll
+    for (int i = 0; i < H; ++i) {
+      const float prev = __shfl_up(xc[BS - H + i], 1);
+      zz[i] = lane == 0 ? carry[i] : prev;
+    }
+#pragma unroll
+    for (int i = 0; i < BS; ++i) zz[H + i] = xc[i];
+    if (blk < g.nblk) {
+      float o[BS];
+#pragma unroll
+      for (int s = 0; s < BS; ++s) {
+        float acc = bias;
+#pragma unroll
+        for (int j = 0; j < KMAX; ++j) acc = fmaf(wp[j], zz[s + j], acc);
+        o[s] = act(g, acc);
+      }
+      row_store(g, p.out, row, blk * BS, o);
+      if (p.final_state && blk == g.nblk - 1) {
+        for (int m = 0; m < g.taps; ++m)
+          store_one(p.final_state, g.dtype, row * g.taps + m,
+                    z_at(g, p.x, p.initial_state, row, g.length - g.taps + m));
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < H; ++i) carry[i] = __shfl(xc[BS - H + i], kWave - 1);
+    if (k + 1 < WB) {
+#pragma unroll
+      for (int i = 0; i < BS; ++i) xc[i] = xn[i];
+    }
+  }
+}
+
+// Backward for widths up to 8 (look-back and look-ahead shorter than a block), blocks
+// interleaved across lanes: at iteration k lane l holds block base + 64 k + l, so every
+// load and store of a wavefront is 64 consecutive blocks (1 KB of 16-bit x).  The H = K - 1
+// steps before a block come from lane l - 1 (lane 0: the carry of lane 63's block one
+// iteration earlier, or the initial state), the H steps after it from lane l + 1 (lane 63
+// loads the next block itself: prefetching it too costs more in registers than the wait).
+// The taps' gradients are summed over the wavefront, which
+// lies in one row, and `finalize_il` adds the wavefronts' partials in order.
+template <int KMAX>
+__global__ void __launch_bounds__(256) backward_il(Geo g, mko_conv1d_params p, float* partial) {
+  constexpr int H = KMAX - 1;
+  static_assert(H < BS, "look-back and look-ahead within one neighbouring block");
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t wv = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + (threadIdx.x >> 6);
+  const bool in_grid = wv < g.rows * g.nseg;
+  const int64_t row = in_grid ? wv / g.nseg : 0, seg = in_grid ? wv % g.nseg : 0;
+  const int64_t c = row % g.channels;
+  float wp[KMAX];
+  load_taps<KMAX>(g, p.weight, c, wp);
+  const float bias = p.bias ? load_one(p.bias, g.dtype, c) : 0.0f;
+  float dwp[KMAX], dbp = 0.0f;
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) dwp[j] = 0.0f;
+  const int64_t base = in_grid ? seg * kWave * WB : g.nblk;  // no row: every block is past the end
+  // z(t0 - H + i), i < H, of lane 0's first block: the initial state (or zeros) for block 0,
+  // else the steps before the segment
+  float carry[H];
+#pragma unroll
+  for (int i = 0; i < H; ++i) carry[i] = z_at(g, p.x, p.initial_state, row, base * BS - H + i);
+  float xc[BS], dc[BS];
+  row_block(g, p.x, row, base + lane, xc);
+  row_block(g, p.dout, row, base + lane, dc);
+  for (int k = 0; k < WB; ++k) {
+    const int64_t blk = base + k * kWave + lane;
+    const int64_t t0 = blk * BS;
+    float xn[BS], dn[BS];
+    if (k + 1 < WB) {  // in flight during this iteration
+      row_block(g, p.x, row, blk + kWave, xn);
+      row_block(g, p.dout, row, blk + kWave, dn);
+    }
+    // the next block's first H steps: from lane + 1, lane 63 reads them
+    float xa[BS], da[BS];
+#pragma unroll
+    for (int i = 0; i < H; ++i) {
+      xa[i] = __shfl_down(xc[i], 1);
+      da[i] = __shfl_down(dc[i], 1);
+    }
+    if (lane == kWave - 1) {
+      row_block(g, p.x, row, blk + 1, xa);
+      row_block(g, p.dout, row, blk + 1, da);
+    }
+    // zz[i] = z(t0 - H + i) over [t0 - H, t0 + BS + H)
+    float zz[BS + 2 * H];
+#pragma unroll
+    for (int i = 0; i < H; ++i) {
+      const float prev = __shfl_up(xc[BS - H + i], 1);
+      zz[i] = lane == 0 ? carry[i] : prev;
+    }
+#pragma unroll
+    for (int i = 0; i < BS; ++i) zz[H + i] = xc[i];
+#pragma unroll
+    for (int i = 0; i < H; ++i) zz[H + BS + i] = xa[i];
+    // gg[i] = g(t0 + i) = dout act'(pre), zero from the end of the row
+    float gg[BS + H];
+#pragma unroll
+    for (int i = 0; i < BS + H; ++i) {
+      float pre = bias;
+#pragma unroll
+      for (int j = 0; j < KMAX; ++j) pre = fmaf(wp[j], zz[i + j], pre);
+      const bool in_row = t0 + i < g.length;
+      const float d = i < BS ? dc[i] : da[i - BS];
+      gg[i] = in_row ? d * act_grad(g, pre) : 0.0f;
+    }
+    if (blk < g.nblk) {
+      float dxo[BS];
+#pragma unroll
+      for (int s = 0; s < BS; ++s) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < KMAX; ++j) acc = fmaf(wp[j], gg[s + H - j], acc);
+        dxo[s] = acc;
+      }
+      row_store(g, p.dx, row, t0, dxo);
+      if (p.dinitial && blk == 0) {
+#pragma unroll
+        for (int kk = 1; kk <= H; ++kk) {
+          float acc = 0.0f;
+#pragma unroll
+          for (int j = 0; j < KMAX; ++j) {
+            const int i = H - kk - j;
+            if (i >= 0) acc = fmaf(wp[j], gg[i], acc);
+          }
+          if (kk <= g.taps) store_one(p.dinitial, g.dtype, row * g.taps + (g.taps - kk), acc);
+        }
+      }
+    }
+    // taps (padded index) and bias over this block's own steps (zero past the row)
+#pragma unroll
+    for (int s = 0; s < BS; ++s) {
+      dbp += gg[s];
+#pragma unroll
+      for (int j = 0; j < KMAX; ++j) dwp[j] = fmaf(gg[s], zz[s + j], dwp[j]);
+    }
+    // lane 63's last H steps precede lane 0's next block
+#pragma unroll
+    for (int i = 0; i < H; ++i) carry[i] = __shfl(xc[BS - H + i], kWave - 1);
+    if (k + 1 < WB) {
+#pragma unroll
+      for (int i = 0; i < BS; ++i) {
+        xc[i] = xn[i];
+        dc[i] = dn[i];
+      }
+    }
+  }
+  if (!partial) return;
+  // one partial per wavefront: the K taps, then the bias
+  const int lead = KMAX - g.width;
+  float* dst = partial + (in_grid ? wv : 0) * (g.width + 1);
+  const bool writer = in_grid && lane == 0;
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) {
+    if (j < lead) continue;  // uniform
+    const float v = wave_sum(dwp[j]);
+    if (writer) dst[j - lead] = v;
+  }
+  const float vb = wave_sum(dbp);
+  if (writer) dst[g.width] = vb;
+}
+
+// dweight[c, j] and dbias[c] from the interleaved backward: the wavefronts' partials summed
+// over batch, then along the row, in order.
+__global__ void __launch_bounds__(256) finalize_il(Geo g, mko_conv1d_params p, const float* partial) {
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (e >= g.channels * (g.width + 1)) return;
+  const int64_t c = e / (g.width + 1);
+  const int j = static_cast<int>(e % (g.width + 1));
+  float s = 0.0f;
+  for (int64_t b = 0; b < g.batch; ++b) {
+    const int64_t row = b * g.channels + c;
+    for (int64_t k = 0; k < g.nseg; ++k) s += partial[(row * g.nseg + k) * (g.width + 1) + j];
+  }
+  if (j < g.width) {
+    if (p.dweight) store_one(p.dweight, g.dtype, c * g.width + j, s);
+  } else if (p.dbias) {
+    store_one(p.dbias, g.dtype, c, s);
+  }
+}
+
 // dweight[c, j] and dbias[c]: the 16-lane partials summed over batch, then along the
 // row, in order.
 __global__ void __launch_bounds__(256) finalize(Geo g, mko_conv1d_params p, const float* partial) {
@@ -305,6 +517,7 @@ int make_geo(const mko_conv1d_params* p, Geo* g) {
   g->taps = g->width - 1;
   g->nblk = (p->length + BS - 1) / BS;
   g->lpr = ((g->nblk + RB - 1) / RB + 15) / 16 * 16;
+  g->nseg = (g->nblk + kWave * WB - 1) / (kWave * WB);
   g->dtype = p->dtype;
   g->silu = (p->flags & MKO_CONV_SILU) != 0;
   const uintptr_t mask = 15u;
@@ -316,18 +529,31 @@ int make_geo(const mko_conv1d_params* p, Geo* g) {
 
 template <int KMAX>
 void launch_fwd(const Geo& g, const mko_conv1d_params& p, hipStream_t s) {
-  const int64_t n = g.rows * g.nblk;
-  MKO_TIMED("conv1d_fwd", s, forward<KMAX><<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(g, p));
+  if constexpr (KMAX <= BS) {
+    const int64_t waves = g.rows * g.nseg;
+    MKO_TIMED("conv1d_fwd", s, forward_il<KMAX><<<static_cast<unsigned>((waves + 3) / 4), 256, 0, s>>>(g, p));
+  } else {
+    const int64_t n = g.rows * g.nblk;
+    MKO_TIMED("conv1d_fwd", s, forward<KMAX><<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(g, p));
+  }
 }
 
 template <int KMAX>
 void launch_bwd(const Geo& g, const mko_conv1d_params& p, float* partial, hipStream_t s) {
-  const int64_t n = g.rows * g.lpr;
-  MKO_TIMED("conv1d_bwd", s, backward<KMAX><<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(g, p, partial));
+  if constexpr (KMAX <= BS) {
+    const int64_t waves = g.rows * g.nseg;
+    MKO_TIMED("conv1d_bwd", s,
+              backward_il<KMAX><<<static_cast<unsigned>((waves + 3) / 4), 256, 0, s>>>(g, p, partial));
+  } else {
+    const int64_t n = g.rows * g.lpr;
+    MKO_TIMED("conv1d_bwd", s, backward<KMAX><<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(g, p, partial));
+  }
 }
 
+// One partial per interleaved wavefront (width <= 8) or per 16-lane group (wider).
 size_t partial_bytes(const Geo& g) {
-  return static_cast<size_t>(g.rows * (g.lpr / 16)) * (g.width + 1) * sizeof(float);
+  const int64_t parts = g.width <= BS ? g.rows * g.nseg : g.rows * (g.lpr / 16);
+  return static_cast<size_t>(parts) * (g.width + 1) * sizeof(float);
 }
 
 }  // namespace
@@ -383,8 +609,11 @@ extern "C" int mko_conv1d_bwd(const mko_conv1d_params* p, void* stream) {
   else conv::launch_bwd<32>(g, *p, partial, s);
   if (params) {
     const int64_t n = g.channels * (g.width + 1);
-    MKO_TIMED("conv1d_finalize", s,
-              conv::finalize<<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(g, *p, partial));
+    const unsigned grid = static_cast<unsigned>((n + 255) / 256);
+    if (g.width <= conv::BS)
+      MKO_TIMED("conv1d_finalize", s, conv::finalize_il<<<grid, 256, 0, s>>>(g, *p, partial));
+    else
+      MKO_TIMED("conv1d_finalize", s, conv::finalize<<<grid, 256, 0, s>>>(g, *p, partial));
   }
   return mko_check_launch("conv1d_bwd");
 }
