@@ -70,6 +70,68 @@ __device__ __forceinline__ void row_block(const Geo& g, const void* src, int64_t
   }
 }
 
+// One BS-step block of a row of T, kept as loaded until `get`, so that a block fetched a
+// step ahead stays in flight until its first use (converting at the load would wait for
+// it there).  The load always reads inside the row (a block past the end reads the last
+// one again) and `get` zeroes the steps past the end.  VEC: whole 16-byte aligned blocks.
+template <class T, bool VEC>
+struct RawBlk {
+  static constexpr int W = VEC ? BS * static_cast<int>(sizeof(T)) / 4 : BS;
+  static_assert(!VEC || W % 4 == 0, "a block is whole 16-byte vectors");
+  uint32_t w[W];
+  int nok;  // steps of the block inside the row
+  __device__ __forceinline__ void load(const Geo& g, const T* __restrict__ src, int64_t row, int64_t blk) {
+    const int64_t b = blk < g.nblk ? blk : g.nblk - 1;
+    const int64_t t0 = b * BS;
+    const T* q = src + row * g.length + t0;
+    if constexpr (VEC) {
+      nok = blk < g.nblk ? BS : 0;
+      const uint4* v = reinterpret_cast<const uint4*>(q);
+#pragma unroll
+      for (int i = 0; i < W / 4; ++i) {
+        const uint4 t = v[i];
+        w[4 * i] = t.x;
+        w[4 * i + 1] = t.y;
+        w[4 * i + 2] = t.z;
+        w[4 * i + 3] = t.w;
+      }
+    } else {
+      const int64_t left = g.length - t0;  // at least 1
+      nok = blk < g.nblk ? (left < BS ? static_cast<int>(left) : BS) : 0;
+#pragma unroll
+      for (int e = 0; e < BS; ++e) w[e] = __float_as_uint(to_f32(q[e < left ? e : left - 1]));
+    }
+  }
+  __device__ __forceinline__ void get(float (&v)[BS]) const {
+    float f[BS];
+    if constexpr (!VEC || sizeof(T) == 4) {
+#pragma unroll
+      for (int i = 0; i < BS; ++i) f[i] = __uint_as_float(w[i]);
+    } else if constexpr (__is_same(T, bf16)) {
+#pragma unroll
+      for (int i = 0; i < W; ++i) {
+        f[2 * i] = __uint_as_float(w[i] << 16);
+        f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < W; ++i) {
+        f[2 * i] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w[i] & 0xffffu)));
+        f[2 * i + 1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w[i] >> 16)));
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < BS; ++i) v[i] = i < nok ? f[i] : 0.0f;
+  }
+};
+
+// The BS steps at t0 of a typed row (those inside the row).
+template <class T, bool VEC>
+__device__ __forceinline__ void typed_store(const Geo& g, void* dst, int64_t row, int64_t t0, const float (&v)[BS]) {
+  const int64_t left = g.length - t0;
+  store_run_t<T, BS>(static_cast<T*>(dst) + row * g.length + t0, left < BS ? static_cast<int>(left) : BS, VEC, v);
+}
+
 __device__ __forceinline__ void row_store(const Geo& g, void* dst, int64_t row, int64_t t0, const float (&v)[BS]) {
   if (g.vec) {
     store_run<BS>(dst, g.dtype, row * g.length + t0, BS, true, v);
@@ -240,7 +302,7 @@ __global__ void __launch_bounds__(256) backward(Geo g, mko_conv1d_params p, floa
 // consecutive blocks, and the H steps before a block come from lane l - 1 (lane 0: the
 // carry of lane 63's previous block, or the initial state).  The per-row setup (index
 // arithmetic, taps, bias) is paid once per four blocks.
-template <int KMAX>
+template <int KMAX, class T, bool VEC>
 __global__ void __launch_bounds__(256) forward_il(Geo g, mko_conv1d_params p) {
   constexpr int H = KMAX - 1;
   static_assert(H < BS, "look-back within one neighbouring block");
@@ -256,13 +318,16 @@ __global__ void __launch_bounds__(256) forward_il(Geo g, mko_conv1d_params p) {
   float carry[H];
 #pragma unroll
   for (int i = 0; i < H; ++i) carry[i] = z_at(g, p.x, p.initial_state, row, base * BS - H + i);
-  float xc[BS];
-  row_block(g, p.x, row, base + lane, xc);
+  const T* xs = static_cast<const T*>(p.x);
+  RawBlk<T, VEC> cur;
+  cur.load(g, xs, row, base + lane);
   for (int k = 0; k < WB; ++k) {
     const int64_t blk = base + k * kWave + lane;
     if (base + k * kWave >= g.nblk) break;  // wave-uniform: no block of this iteration exists
-    float xn[BS];
-    if (k + 1 < WB) row_block(g, p.x, row, blk + kWave, xn);  // in flight during this block
+    RawBlk<T, VEC> nxt;
+    if (k + 1 < WB) nxt.load(g, xs, row, blk + kWave);  // in flight during this block
+    float xc[BS];
+    cur.get(xc);
     float zz[H + BS];
 #pragma unroll
     for (int i = 0; i < H; ++i) {
@@ -280,7 +345,7 @@ __global__ void __launch_bounds__(256) forward_il(Geo g, mko_conv1d_params p) {
         for (int j = 0; j < KMAX; ++j) acc = fmaf(wp[j], zz[s + j], acc);
         o[s] = act(g, acc);
       }
-      row_store(g, p.out, row, blk * BS, o);
+      typed_store<T, VEC>(g, p.out, row, blk * BS, o);
       if (p.final_state && blk == g.nblk - 1) {
         for (int m = 0; m < g.taps; ++m)
           store_one(p.final_state, g.dtype, row * g.taps + m,
@@ -289,10 +354,7 @@ __global__ void __launch_bounds__(256) forward_il(Geo g, mko_conv1d_params p) {
     }
 #pragma unroll
     for (int i = 0; i < H; ++i) carry[i] = __shfl(xc[BS - H + i], kWave - 1);
-    if (k + 1 < WB) {
-#pragma unroll
-      for (int i = 0; i < BS; ++i) xc[i] = xn[i];
-    }
+    if (k + 1 < WB) cur = nxt;
   }
 }
 
@@ -300,11 +362,12 @@ __global__ void __launch_bounds__(256) forward_il(Geo g, mko_conv1d_params p) {
 // interleaved across lanes: at iteration k lane l holds block base + 64 k + l, so every
 // load and store of a wavefront is 64 consecutive blocks (1 KB of 16-bit x).  The H = K - 1
 // steps before a block come from lane l - 1 (lane 0: the carry of lane 63's block one
-// iteration earlier, or the initial state), the H steps after it from lane l + 1 (lane 63
-// loads the next block itself: prefetching it too costs more in registers than the wait).
+// iteration earlier, or the initial state), the H steps after it from lane l + 1 (lane 63:
+// from lane 0's next block, which is in flight as the next iteration's prefetch).  The
+// loop stays rolled: unrolled, the four iterations' registers cost a wavefront per SIMD.
 // The taps' gradients are summed over the wavefront, which
 // lies in one row, and `finalize_il` adds the wavefronts' partials in order.
-template <int KMAX>
+template <int KMAX, class T, bool VEC>
 __global__ void __launch_bounds__(256) backward_il(Geo g, mko_conv1d_params p, float* partial) {
   constexpr int H = KMAX - 1;
   static_assert(H < BS, "look-back and look-ahead within one neighbouring block");
@@ -325,29 +388,28 @@ __global__ void __launch_bounds__(256) backward_il(Geo g, mko_conv1d_params p, f
   float carry[H];
 #pragma unroll
   for (int i = 0; i < H; ++i) carry[i] = z_at(g, p.x, p.initial_state, row, base * BS - H + i);
-  float xc[BS], dc[BS];
-  row_block(g, p.x, row, base + lane, xc);
-  row_block(g, p.dout, row, base + lane, dc);
+  const T* xs = static_cast<const T*>(p.x);
+  const T* ds = static_cast<const T*>(p.dout);
+  RawBlk<T, VEC> xr, dr;
+  xr.load(g, xs, row, base + lane);
+  dr.load(g, ds, row, base + lane);
+#pragma unroll 1
   for (int k = 0; k < WB; ++k) {
     const int64_t blk = base + k * kWave + lane;
     const int64_t t0 = blk * BS;
-    float xn[BS], dn[BS];
-    if (k + 1 < WB) {  // in flight during this iteration
-      row_block(g, p.x, row, blk + kWave, xn);
-      row_block(g, p.dout, row, blk + kWave, dn);
+    // The next iteration's blocks, in flight during this one.  Lane 0's is also the block
+    // after lane 63's, so in the last iteration lane 0 alone needs it (the other lanes'
+    // loads re-read the row's last block and come out as zeros).
+    RawBlk<T, VEC> xnr, dnr;
+    {
+      const int64_t nb = (k + 1 < WB || lane == 0) ? blk + kWave : g.nblk;
+      xnr.load(g, xs, row, nb);
+      dnr.load(g, ds, row, nb);
     }
-    // the next block's first H steps: from lane + 1, lane 63 reads them
-    float xa[BS], da[BS];
-#pragma unroll
-    for (int i = 0; i < H; ++i) {
-      xa[i] = __shfl_down(xc[i], 1);
-      da[i] = __shfl_down(dc[i], 1);
-    }
-    if (lane == kWave - 1) {
-      row_block(g, p.x, row, blk + 1, xa);
-      row_block(g, p.dout, row, blk + 1, da);
-    }
-    // zz[i] = z(t0 - H + i) over [t0 - H, t0 + BS + H)
+    float xc[BS], dc[BS];
+    xr.get(xc);
+    dr.get(dc);
+    // zz[i] = z(t0 - H + i) over [t0 - H, t0 + BS + H); the last H (look-ahead) further down
     float zz[BS + 2 * H];
 #pragma unroll
     for (int i = 0; i < H; ++i) {
@@ -356,19 +418,43 @@ __global__ void __launch_bounds__(256) backward_il(Geo g, mko_conv1d_params p, f
     }
 #pragma unroll
     for (int i = 0; i < BS; ++i) zz[H + i] = xc[i];
-#pragma unroll
-    for (int i = 0; i < H; ++i) zz[H + BS + i] = xa[i];
-    // gg[i] = g(t0 + i) = dout act'(pre), zero from the end of the row
+    // gg[i] = g(t0 + i) = dout act'(pre), zero from the end of the row.  The block's own
+    // steps first: they and the tap and bias gradients need no look-ahead.
     float gg[BS + H];
-#pragma unroll
-    for (int i = 0; i < BS + H; ++i) {
+    auto grad_at = [&](int i, float d) {
       float pre = bias;
 #pragma unroll
       for (int j = 0; j < KMAX; ++j) pre = fmaf(wp[j], zz[i + j], pre);
-      const bool in_row = t0 + i < g.length;
-      const float d = i < BS ? dc[i] : da[i - BS];
-      gg[i] = in_row ? d * act_grad(g, pre) : 0.0f;
+      return t0 + i < g.length ? d * act_grad(g, pre) : 0.0f;
+    };
+#pragma unroll
+    for (int i = 0; i < BS; ++i) gg[i] = grad_at(i, dc[i]);
+    // taps (padded index) and bias over this block's own steps (zero past the row)
+#pragma unroll
+    for (int s = 0; s < BS; ++s) {
+      dbp += gg[s];
+#pragma unroll
+      for (int j = 0; j < KMAX; ++j) dwp[j] = fmaf(gg[s], zz[s + j], dwp[j]);
     }
+    // The next block's first H steps: from lane + 1; lane 63 takes them from lane 0's next
+    // block.  Kept after the work above, so that load has had that long to arrive.
+    __builtin_amdgcn_sched_barrier(0);
+    {
+      float xn[BS], dn[BS];
+      xnr.get(xn);
+      dnr.get(dn);
+      const bool last = lane == kWave - 1;
+#pragma unroll
+      for (int i = 0; i < H; ++i) {
+        const float x0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(xn[i]), 0));
+        const float d0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dn[i]), 0));
+        const float xd = __shfl_down(xc[i], 1), dd = __shfl_down(dc[i], 1);
+        zz[H + BS + i] = last ? x0 : xd;
+        gg[BS + i] = last ? d0 : dd;  // dout for now, the gradient just below
+      }
+    }
+#pragma unroll
+    for (int i = BS; i < BS + H; ++i) gg[i] = grad_at(i, gg[i]);
     if (blk < g.nblk) {
       float dxo[BS];
 #pragma unroll
@@ -378,7 +464,7 @@ __global__ void __launch_bounds__(256) backward_il(Geo g, mko_conv1d_params p, f
         for (int j = 0; j < KMAX; ++j) acc = fmaf(wp[j], gg[s + H - j], acc);
         dxo[s] = acc;
       }
-      row_store(g, p.dx, row, t0, dxo);
+      typed_store<T, VEC>(g, p.dx, row, t0, dxo);
       if (p.dinitial && blk == 0) {
 #pragma unroll
         for (int kk = 1; kk <= H; ++kk) {
@@ -392,23 +478,11 @@ __global__ void __launch_bounds__(256) backward_il(Geo g, mko_conv1d_params p, f
         }
       }
     }
-    // taps (padded index) and bias over this block's own steps (zero past the row)
-#pragma unroll
-    for (int s = 0; s < BS; ++s) {
-      dbp += gg[s];
-#pragma unroll
-      for (int j = 0; j < KMAX; ++j) dwp[j] = fmaf(gg[s], zz[s + j], dwp[j]);
-    }
     // lane 63's last H steps precede lane 0's next block
 #pragma unroll
     for (int i = 0; i < H; ++i) carry[i] = __shfl(xc[BS - H + i], kWave - 1);
-    if (k + 1 < WB) {
-#pragma unroll
-      for (int i = 0; i < BS; ++i) {
-        xc[i] = xn[i];
-        dc[i] = dn[i];
-      }
-    }
+    xr = xnr;
+    dr = dnr;
   }
   if (!partial) return;
   // one partial per wavefront: the K taps, then the bias
@@ -531,7 +605,16 @@ template <int KMAX>
 void launch_fwd(const Geo& g, const mko_conv1d_params& p, hipStream_t s) {
   if constexpr (KMAX <= BS) {
     const int64_t waves = g.rows * g.nseg;
-    MKO_TIMED("conv1d_fwd", s, forward_il<KMAX><<<static_cast<unsigned>((waves + 3) / 4), 256, 0, s>>>(g, p));
+    const unsigned grid = static_cast<unsigned>((waves + 3) / 4);
+#define MKO_CONV_FWD(T, V) MKO_TIMED("conv1d_fwd", s, (forward_il<KMAX, T, V><<<grid, 256, 0, s>>>(g, p)))
+    if (g.dtype == MKO_F32) {
+      if (g.vec) MKO_CONV_FWD(float, true); else MKO_CONV_FWD(float, false);
+    } else if (g.dtype == MKO_BF16) {
+      if (g.vec) MKO_CONV_FWD(bf16, true); else MKO_CONV_FWD(bf16, false);
+    } else {
+      if (g.vec) MKO_CONV_FWD(_Float16, true); else MKO_CONV_FWD(_Float16, false);
+    }
+#undef MKO_CONV_FWD
   } else {
     const int64_t n = g.rows * g.nblk;
     MKO_TIMED("conv1d_fwd", s, forward<KMAX><<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(g, p));
@@ -542,8 +625,16 @@ template <int KMAX>
 void launch_bwd(const Geo& g, const mko_conv1d_params& p, float* partial, hipStream_t s) {
   if constexpr (KMAX <= BS) {
     const int64_t waves = g.rows * g.nseg;
-    MKO_TIMED("conv1d_bwd", s,
-              backward_il<KMAX><<<static_cast<unsigned>((waves + 3) / 4), 256, 0, s>>>(g, p, partial));
+    const unsigned grid = static_cast<unsigned>((waves + 3) / 4);
+#define MKO_CONV_BWD(T, V) MKO_TIMED("conv1d_bwd", s, (backward_il<KMAX, T, V><<<grid, 256, 0, s>>>(g, p, partial)))
+    if (g.dtype == MKO_F32) {
+      if (g.vec) MKO_CONV_BWD(float, true); else MKO_CONV_BWD(float, false);
+    } else if (g.dtype == MKO_BF16) {
+      if (g.vec) MKO_CONV_BWD(bf16, true); else MKO_CONV_BWD(bf16, false);
+    } else {
+      if (g.vec) MKO_CONV_BWD(_Float16, true); else MKO_CONV_BWD(_Float16, false);
+    }
+#undef MKO_CONV_BWD
   } else {
     const int64_t n = g.rows * g.lpr;
     MKO_TIMED("conv1d_bwd", s, backward<KMAX><<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(g, p, partial));

@@ -586,7 +586,7 @@ __device__ __forceinline__ float row_newbcast(float v) {
 constexpr int kLaneChannels = 4;  // channels per wavefront in the lane-per-state kernels
 
 template <class TU, class TB>
-__global__ void __launch_bounds__(256) fwd_lane(Geo g, Ptrs p) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) fwd_lane(Geo g, Ptrs p) {
   constexpr int kRow = HS + 1;   // a step's 16 states, padded so the transposed reads miss no bank
   constexpr int kCS = HS * kRow; // one channel's [step][state] block (272 floats: 16 banks apart)
   __shared__ float sy[4][kLaneChannels * kCS];
@@ -626,20 +626,29 @@ __global__ void __launch_bounds__(256) fwd_lane(Geo g, Ptrs p) {
     in.b.load(g, p.B, 0, bcrow + t0, HS);
     in.c.load(g, p.C, 0, bcrow + t0, HS);
   };
-  In cur, nxt;
-  load(0, cur);
-  float x = 0.0f;
   const int64_t nblk = L / HS;
-  for (int64_t k = 0; k < nblk; ++k) {
+  // Two buffers of raw inputs: a block's raw words are unpacked first and then
+  // reloaded with the block two further on (the last ones reload the last block), so
+  // each load has two blocks of work to arrive.  32-bit B/C need no unpacking (the
+  // raw words are the values), so their reload waits for the end of the block
+  // instead of holding a second copy: one block of work, as many registers as one
+  // buffer ahead.
+  auto ahead = [&](int64_t k) { return (k < nblk ? k : nblk - 1) * HS; };
+  In ra, rb;
+  load(0, ra);
+  load(ahead(1), rb);
+  float x = 0.0f;
+  auto block = [&](int64_t k, In& in) {
     const int64_t t0 = k * HS;
-    load((k + 1 < nblk ? k + 1 : k) * HS, nxt);  // the last block loads itself again
     if (active && sn) sp[k * sstep] = x;
-    const float uu = to_f32(cur.u);
-    const float del = step_of(g, cur.dl, bias);
-    const float du = del * uu;
+    const float uu = to_f32(in.u);
+    const float zz = to_f32(in.z);
+    const float del = step_of(g, in.dl, bias);
     float bv[HS], cv[HS];
-    cur.b.get(bv);
-    cur.c.get(cv);
+    in.b.get(bv);
+    in.c.get(cv);
+    if constexpr (sizeof(TB) == 2) load(ahead(k + 2), in);
+    const float du = del * uu;
     if (N < HS && !sn) {  // a padded state adds nothing (its B row is state 0's)
 #pragma unroll
       for (int i = 0; i < HS; ++i) bv[i] = cv[i] = 0.0f;
@@ -650,17 +659,20 @@ __global__ void __launch_bounds__(256) fwd_lane(Geo g, Ptrs p) {
       sw[i * kRow + n] = cv[i] * x;
     });
     wave_lds_sync();
-    float ys = 0.0f;
+    float s4[4];
 #pragma unroll
-    for (int m = 0; m < HS; ++m) ys += sw[n * kRow + m];
+    for (int m = 0; m < 4; ++m) s4[m] = sw[n * kRow + m];
+#pragma unroll
+    for (int m = 4; m < HS; ++m) s4[m & 3] += sw[n * kRow + m];
     wave_lds_sync();
-    float y = fmaf(Dd, uu, ys);
-    if (has_z) {
-      const float zz = to_f32(cur.z);
-      y *= zz * sigmoid(zz);
-    }
+    float y = fmaf(Dd, uu, (s4[0] + s4[1]) + (s4[2] + s4[3]));
+    if (has_z) y *= zz * sigmoid(zz);
     if (active) op[t0] = from_f32<TU>(y);
-    cur = nxt;
+    if constexpr (sizeof(TB) == 4) load(ahead(k + 2), in);
+  };
+  for (int64_t k = 0; k < nblk; k += 2) {
+    block(k, ra);
+    if (k + 1 < nblk) block(k + 1, rb);
   }
 }
 
