@@ -674,12 +674,22 @@ def main():
         # A device-to-device copy of 1 GiB, three times: under rocprofv3 --pmc its
         # FETCH_SIZE / WRITE_SIZE per dispatch calibrate the counters against a known
         # 1 GiB read and 1 GiB write.
+        # The timed copies give the practical read+write bandwidth of the part.
         src = torch.empty(1 << 28, dtype=torch.float32, device="cuda").fill_(1.0)
         dst = torch.empty_like(src)
         for _ in range(3):
             dst.copy_(src)
         torch.cuda.synchronize()
-        print(json.dumps({"copy_bytes_read": src.numel() * 4, "copy_bytes_written": dst.numel() * 4}), flush=True)
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(10):
+            dst.copy_(src)
+        t1.record()
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / 10
+        nbytes = src.numel() * 4
+        print(json.dumps({"copy_bytes_read": nbytes, "copy_bytes_written": nbytes, "copy_ms": round(ms, 4),
+                          "copy_gbs": round(2 * nbytes / ms / 1e6, 1)}), flush=True)
         return
     also = {}
     want = (lambda w: args.only in (w, "all"))
