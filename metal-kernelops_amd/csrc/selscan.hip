@@ -453,18 +453,43 @@ __global__ void __launch_bounds__(256) chain(Geo g, const float* __restrict__ A,
   const int n = static_cast<int>(i % N);
   const float a2 = A[(row % g.dim) * N + n] * kLog2e;
   const int k = g.nchunks;
+  // The chunk maps (decay, drive) do not depend on the carried state: they are fetched
+  // PB chunks at a time (clamped indices, so every load is issued), then composed.
+  constexpr int PB = 16;
+  float dec[PB], drv[PB];
+  auto fetch = [&](int c0, int dir) {
+#pragma unroll
+    for (int q = 0; q < PB; ++q) {
+      int c = c0 + dir * q;
+      c = c < 0 ? 0 : (c >= k ? k - 1 : c);
+      dec[q] = sumd[row * k + c];
+      drv[q] = drive[(row * k + c) * N + n];
+    }
+  };
   if (!REV) {
     const int per = g.lc / CK;
     float x = 0.0f;
-    for (int c = 0; c < k; ++c) {
-      out[ck_index(g, row, static_cast<int64_t>(c) * per, n)] = x;
-      if (c + 1 < k) x = fmaf(fast_exp2(a2 * sumd[row * k + c]), x, drive[(row * k + c) * N + n]);
+    for (int c0 = 0; c0 < k; c0 += PB) {
+      fetch(c0, 1);
+#pragma unroll
+      for (int q = 0; q < PB; ++q) {
+        const int c = c0 + q;
+        if (c >= k) break;
+        out[ck_index(g, row, static_cast<int64_t>(c) * per, n)] = x;
+        if (c + 1 < k) x = fmaf(fast_exp2(a2 * dec[q]), x, drv[q]);
+      }
     }
   } else {
     float h = 0.0f;
-    for (int c = k - 1; c >= 0; --c) {
-      out[(row * k + c) * N + n] = h;
-      if (c > 0) h = fmaf(fast_exp2(a2 * sumd[row * k + c]), h, drive[(row * k + c) * N + n]);
+    for (int c0 = k - 1; c0 >= 0; c0 -= PB) {
+      fetch(c0, -1);
+#pragma unroll
+      for (int q = 0; q < PB; ++q) {
+        const int c = c0 - q;
+        if (c < 0) break;
+        out[(row * k + c) * N + n] = h;
+        if (c > 0) h = fmaf(fast_exp2(a2 * dec[q]), h, drv[q]);
+      }
     }
   }
 }
@@ -1134,16 +1159,34 @@ __global__ void __launch_bounds__(256) reduce_params(Geo g, int ns, const float*
   const int n = static_cast<int>(blockIdx.x / dblocks);  // 0..N (N: the dD / dbias row)
   const int64_t d = (blockIdx.x % dblocks) * 64 + (threadIdx.x & 63);
   const int grp = threadIdx.x >> 6;
-  const int64_t npart = static_cast<int64_t>(g.nchunks) * g.batch;
+  const int npart = g.nchunks * static_cast<int>(g.batch);
+  const int nb = static_cast<int>(g.batch);
   float s0 = 0.0f, s1 = 0.0f;
   if (d < g.dim) {
-    for (int64_t k = grp; k < npart; k += 4) {
-      const int64_t c = k / g.batch, b = k % g.batch;
-      if (n < N) {
-        s0 += dap[(c * ns + n) * g.rows + b * g.dim + d];
-      } else {
-        s0 += ddp[c * g.rows + b * g.dim + d];
-        s1 += dbp[c * g.rows + b * g.dim + d];
+    // partials grp, grp + 4, ... added in that order, four loads in flight at a time
+    // (the bounds are wave-uniform)
+    constexpr int PF = 4;
+    for (int k0 = grp; k0 < npart; k0 += 4 * PF) {
+      float v0[PF], v1[PF];
+#pragma unroll
+      for (int q = 0; q < PF; ++q) {
+        const int k = k0 + 4 * q;
+        v0[q] = v1[q] = 0.0f;
+        if (k < npart) {
+          const int64_t c = k / nb, b = k % nb;
+          if (n < N) {
+            v0[q] = dap[(c * ns + n) * g.rows + b * g.dim + d];
+          } else {
+            v0[q] = ddp[c * g.rows + b * g.dim + d];
+            v1[q] = dbp[c * g.rows + b * g.dim + d];
+          }
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < PF; ++q) {
+        if (k0 + 4 * q >= npart) break;
+        s0 += v0[q];
+        s1 += v1[q];
       }
     }
   }
