@@ -36,7 +36,7 @@ import torch
 from torch import Tensor
 
 from .. import _native as nat
-from ..scan import _require_gpu
+from ..scan import _require_gpu, selscan_bwd_impl, selscan_fwd_impl
 
 __all__ = ["MAX_STATES", "MERGE_MODES", "path_orders", "ss2d_scan", "ss2d_scan_reference"]
 
@@ -117,8 +117,7 @@ def _path_call(fn, x, out, height, width, scale):
     nat.check(getattr(lib, fn)(ctypes.byref(p), nat.stream_of(x.device)), fn)
 
 
-@torch.library.custom_op("mko::path_stack", mutates_args=(), device_types="cuda")
-def _path_stack(x: Tensor, height: int, width: int, scale: float) -> Tensor:
+def _stack_impl(x: Tensor, height: int, width: int, scale: float) -> Tensor:
     """(batch, rows, H*W) -> (batch, 4 rows, H*W): the four paths in step order."""
     out = x.new_empty(x.shape[0], 4 * x.shape[1], x.shape[2])
     if out.numel():
@@ -126,18 +125,24 @@ def _path_stack(x: Tensor, height: int, width: int, scale: float) -> Tensor:
     return out
 
 
-@_path_stack.register_fake
-def _(x, height, width, scale):
-    return x.new_empty(x.shape[0], 4 * x.shape[1], x.shape[2])
-
-
-@torch.library.custom_op("mko::path_merge", mutates_args=(), device_types="cuda")
-def _path_merge(x: Tensor, height: int, width: int, scale: float) -> Tensor:
+def _merge_impl(x: Tensor, height: int, width: int, scale: float) -> Tensor:
     """(batch, 4 rows, H*W) in step order -> (batch, rows, H*W) per pixel."""
     out = x.new_empty(x.shape[0], x.shape[1] // 4, x.shape[2])
     if out.numel():
         _path_call("mko_path_merge", x, out, height, width, scale)
     return out
+
+
+# The layout launches as torch ops; the 2D scan's own autograd function calls the
+# implementations directly (a dispatcher round trip per launch costs more host time than
+# the launch itself on these small maps).
+_path_stack = torch.library.custom_op("mko::path_stack", _stack_impl, mutates_args=(), device_types="cuda")
+_path_merge = torch.library.custom_op("mko::path_merge", _merge_impl, mutates_args=(), device_types="cuda")
+
+
+@_path_stack.register_fake
+def _(x, height, width, scale):
+    return x.new_empty(x.shape[0], 4 * x.shape[1], x.shape[2])
 
 
 @_path_merge.register_fake
@@ -150,7 +155,7 @@ def _stacked(u, dt, A, B, C):
     batch, channels, height, width = u.shape
     groups, states = B.shape[1], A.shape[1]
     length = height * width
-    stack = torch.ops.mko.path_stack
+    stack = _stack_impl
     su = stack(u.reshape(batch, channels, length), height, width, 1.0)
     sdt = stack(dt.reshape(batch, channels, length), height, width, 1.0)
     sb = stack(B.reshape(batch, groups * states, length), height, width, 1.0)
@@ -164,8 +169,8 @@ class _PathScan(torch.autograd.Function):
     def forward(ctx, u, dt, A, B, C, scale):
         batch, channels, height, width = u.shape
         su, sdt, sa, sb, sc = _stacked(u, dt, A, B, C)
-        ys, ck = torch.ops.mko.selscan_fwd(su, sdt, sa, sb, sc, None, None, None, False)
-        out = torch.ops.mko.path_merge(ys, height, width, scale)
+        ys, ck = selscan_fwd_impl(su, sdt, sa, sb, sc, None, None, None, False)
+        out = _merge_impl(ys, height, width, scale)
         ctx.scale = scale
         ctx.save_for_backward(u, dt, A, B, C, ck)
         return out.view(batch, channels, height, width)
@@ -178,11 +183,9 @@ class _PathScan(torch.autograd.Function):
         groups, states = B.shape[1], A.shape[1]
         length = height * width
         su, sdt, sa, sb, sc = _stacked(u, dt, A, B, C)
-        sdy = torch.ops.mko.path_stack(dy.to(u.dtype).contiguous().reshape(batch, channels, length),
-                                       height, width, ctx.scale)
-        dus, ddts, das, dbs, dcs, _, _, _ = torch.ops.mko.selscan_bwd(
-            sdy, su, sdt, sa, sb, sc, None, None, None, False, ck)
-        merge = torch.ops.mko.path_merge
+        sdy = _stack_impl(dy.to(u.dtype).contiguous().reshape(batch, channels, length), height, width, ctx.scale)
+        dus, ddts, das, dbs, dcs, _, _, _ = selscan_bwd_impl(sdy, su, sdt, sa, sb, sc, None, None, None, False, ck)
+        merge = _merge_impl
         du = merge(dus, height, width, 1.0).view(batch, channels, height, width)
         ddt = merge(ddts, height, width, 1.0).view(batch, channels, height, width)
         rows = (batch, 4 * groups * states, length)

@@ -57,10 +57,11 @@ def _num_checkpoints(length):
     return (length + _CHECKPOINT - 1) // _CHECKPOINT
 
 
-@torch.library.custom_op("mko::selscan_fwd", mutates_args=(), device_types="cuda")
-def _selscan_fwd(u: Tensor, delta: Tensor, A: Tensor, B: Tensor, C: Tensor, D: Optional[Tensor],
-                 z: Optional[Tensor], delta_bias: Optional[Tensor], softplus: bool
-                 ) -> Tuple[Tensor, Tensor]:
+def selscan_fwd_impl(u: Tensor, delta: Tensor, A: Tensor, B: Tensor, C: Tensor, D: Optional[Tensor],
+                     z: Optional[Tensor], delta_bias: Optional[Tensor], softplus: bool
+                     ) -> Tuple[Tensor, Tensor]:
+    """The forward launch behind ``mko::selscan_fwd``; callers that compose several launches
+    in their own autograd function (the 2D scan) call it without the dispatcher."""
     batch, dim, length = u.shape
     out = torch.empty_like(u)
     states = torch.empty(batch, _num_checkpoints(length), dim, A.shape[1], dtype=torch.float32,
@@ -76,6 +77,9 @@ def _selscan_fwd(u: Tensor, delta: Tensor, A: Tensor, B: Tensor, C: Tensor, D: O
     return out, states
 
 
+_selscan_fwd = torch.library.custom_op("mko::selscan_fwd", selscan_fwd_impl, mutates_args=(), device_types="cuda")
+
+
 @_selscan_fwd.register_fake
 def _(u, delta, A, B, C, D, z, delta_bias, softplus):
     batch, dim, length = u.shape
@@ -83,11 +87,11 @@ def _(u, delta, A, B, C, D, z, delta_bias, softplus):
                                             dtype=torch.float32)
 
 
-@torch.library.custom_op("mko::selscan_bwd", mutates_args=(), device_types="cuda")
-def _selscan_bwd(dout: Tensor, u: Tensor, delta: Tensor, A: Tensor, B: Tensor, C: Tensor,
-                 D: Optional[Tensor], z: Optional[Tensor], delta_bias: Optional[Tensor],
-                 softplus: bool, states: Tensor
-                 ) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+def selscan_bwd_impl(dout: Tensor, u: Tensor, delta: Tensor, A: Tensor, B: Tensor, C: Tensor,
+                     D: Optional[Tensor], z: Optional[Tensor], delta_bias: Optional[Tensor],
+                     softplus: bool, states: Tensor
+                     ) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """The backward launch behind ``mko::selscan_bwd`` (see ``selscan_fwd_impl``)."""
     dim = u.shape[1]
     f32 = dict(dtype=torch.float32, device=u.device)
     du, ddelta = torch.empty_like(u), torch.empty_like(delta)
@@ -113,6 +117,9 @@ def _selscan_bwd(dout: Tensor, u: Tensor, delta: Tensor, A: Tensor, B: Tensor, C
     p.workspace, p.workspace_bytes = ws.data_ptr(), ws.numel()
     nat.check(lib.mko_selscan_bwd(ctypes.byref(p), nat.stream_of(u.device)), "mko_selscan_bwd")
     return du, ddelta, dA, dB, dC, dD, dz, dbias
+
+
+_selscan_bwd = torch.library.custom_op("mko::selscan_bwd", selscan_bwd_impl, mutates_args=(), device_types="cuda")
 
 
 @_selscan_bwd.register_fake
