@@ -115,10 +115,14 @@ def _conv1d_bwd(dout: Tensor, x: Tensor, weight: Tensor, bias: Optional[Tensor],
                 ) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
     channels, width = weight.shape
     dx = torch.empty_like(x)
-    dweight = weight.new_zeros(weight.shape) if need_weight else weight.new_empty(0)
-    dbias = weight.new_zeros(channels) if need_bias else weight.new_empty(0)
-    dinit = x.new_zeros(x.shape[0], channels, width - 1) if need_init else x.new_empty(0)
-    if x.numel() == 0:
+    # the kernels write every element of these; an empty input launches nothing and
+    # leaves zeros
+    empty = x.numel() == 0
+    wnew = weight.new_zeros if empty else weight.new_empty
+    dweight = wnew(weight.shape) if need_weight else weight.new_empty(0)
+    dbias = wnew(channels) if need_bias else weight.new_empty(0)
+    dinit = (x.new_zeros if empty else x.new_empty)(x.shape[0], channels, width - 1) if need_init else x.new_empty(0)
+    if empty:
         return dx, dweight, dbias, dinit
     p = _params(x, weight, bias, init, silu)
     p.dout, p.dx = dout.data_ptr(), dx.data_ptr()
