@@ -175,6 +175,33 @@ def test_gradients(case):
 
 
 @pytest.mark.gpu
+def test_bench_shape_full_size_channel_subset():
+    """The bench's prefill shape at full size (4 x 5120 x 4096, width 4, bf16, SiLU).  Channels
+    are independent in the output, dx and the tap and bias gradients, so the full-size run is
+    checked on 64 channels spread over the width against the oracle."""
+    from metal_kernelops.cv import causal_conv1d_fn
+    batch, channels, length, width = 4, 5120, 4096, 4
+    g = torch.Generator().manual_seed(50)
+    x = torch.randn(batch, channels, length, generator=g).bfloat16()
+    w = (0.5 * torch.randn(channels, width, generator=g)).bfloat16()
+    b = torch.randn(channels, generator=g).bfloat16()
+    dy = torch.randn(batch, channels, length, generator=g).bfloat16()
+    leaves = [t.to(DEV).requires_grad_(True) for t in (x, w, b)]
+    out = causal_conv1d_fn(leaves[0], leaves[1], leaves[2], activation="silu")
+    out.backward(dy.to(DEV))
+    torch.cuda.synchronize()
+    sel = torch.arange(0, channels, 80)
+    xs, ws, bs = (t.double().requires_grad_(True) for t in (x[:, sel], w[sel], b[sel]))
+    want, _ = oracle.causal_conv1d(xs, ws, bs, "silu")
+    want.backward(dy[:, sel].double())
+    on = sel.to(DEV)
+    assert rel(out.detach()[:, on], want) <= TOL[torch.bfloat16]
+    for name, got, ref in (("x", leaves[0].grad[:, on], xs.grad), ("weight", leaves[1].grad[on], ws.grad),
+                           ("bias", leaves[2].grad[on], bs.grad)):
+        assert rel(got, ref) <= 10 * TOL[torch.bfloat16], (name, rel(got, ref))
+
+
+@pytest.mark.gpu
 def test_backward_deterministic():
     from metal_kernelops.cv import causal_conv1d_fn
     x, w, b, s = _inputs(4, 256, 777, 4, True, torch.float32, seed=30)

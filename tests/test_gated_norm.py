@@ -233,6 +233,27 @@ def test_gradients(case, dtype):
 
 
 @pytest.mark.gpu
+def test_bench_shape_full_size():
+    """The bench's shape at full size (8192 x 2560 bf16, z and bias, gate after the norm, as
+    ``benchmarks/verify_gated_norm.py:518-555`` times it): every row of the output and of dx,
+    dz, and the weight and bias gradients summed over all 8192 rows."""
+    from metal_kernelops.cv import rmsnorm_gated
+    shape = (8192, 2560)
+    x, w, b, z = _inputs(shape, True, True, torch.bfloat16, seed=500)
+    dy = make(shape, 501, 1.0, torch.bfloat16)
+    leaves = [t.to(DEV).requires_grad_(True) for t in (x, w, b, z)]
+    out = rmsnorm_gated(*leaves, norm_before_gate=True)
+    out.backward(dy.to(DEV))
+    torch.cuda.synchronize()
+    want, _ = oracle.rmsnorm_gated(x, w, b, z, norm_before_gate=True)
+    assert fwd_error(out, want) <= FWD_TOL[torch.bfloat16]
+    dx, dw, db, dz = oracle.rmsnorm_gated_bwd(dy, x, w, b, z, eps=1e-5, norm_before_gate=True)
+    for name, leaf, ref in (("x", leaves[0], dx), ("weight", leaves[1], dw), ("bias", leaves[2], db),
+                            ("z", leaves[3], dz)):
+        assert rel(leaf.grad, ref) <= GRAD_TOL[torch.bfloat16], (name, rel(leaf.grad, ref))
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("shape,group,before", [((4, 300), 100, True), ((4, 128), 32, False)])
 def test_central_differences_of_the_kernel(shape, group, before):
     """The kernels' analytic dx and dz against central differences of their own forward."""
