@@ -301,9 +301,9 @@ __device__ __forceinline__ void forward_block_lds(const float* sb, const float* 
 // while the previous block is computed.
 struct Dyn {};
 
-template <class T>
-struct RawRun {  // HS consecutive elements of a row, raw
-  static constexpr int W = HS * static_cast<int>(sizeof(T)) / 4;
+template <class T, int NE = HS>
+struct RawRun {  // NE consecutive elements of a row, raw
+  static constexpr int W = NE * static_cast<int>(sizeof(T)) / 4;
   uint32_t w[W];
   __device__ __forceinline__ void load(const Geo&, const void* base, int, int64_t off, int) {
     const uint4* q = reinterpret_cast<const uint4*>(static_cast<const T*>(base) + off);
@@ -316,10 +316,10 @@ struct RawRun {  // HS consecutive elements of a row, raw
       w[4 * i + 3] = t.w;
     }
   }
-  __device__ __forceinline__ void get(float (&f)[HS]) const {
+  __device__ __forceinline__ void get(float (&f)[NE]) const {
     if constexpr (sizeof(T) == 4) {
 #pragma unroll
-      for (int i = 0; i < HS; ++i) f[i] = __uint_as_float(w[i]);
+      for (int i = 0; i < NE; ++i) f[i] = __uint_as_float(w[i]);
     } else if constexpr (__is_same(T, bf16)) {
 #pragma unroll
       for (int i = 0; i < W; ++i) {
@@ -337,7 +337,7 @@ struct RawRun {  // HS consecutive elements of a row, raw
 };
 
 template <>
-struct RawRun<Dyn> {
+struct RawRun<Dyn, HS> {
   float f[HS];
   __device__ __forceinline__ void load(const Geo& g, const void* base, int dtype, int64_t off, int nv) {
     load_run<HS>(base, dtype, off, nv, g.vec, f);
@@ -630,7 +630,6 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) f
   const bool has_z = p.z != nullptr;
   const int64_t L = g.length;
   const int64_t rbase = r * L + n;  // this lane's step of every block
-  const int64_t bcrow = (bg * N + (sn ? n : 0)) * L;
   const float* dp = static_cast<const float*>(p.delta) + rbase;
   const TU* up = static_cast<const TU*>(p.u) + rbase;
   const TU* zp = static_cast<const TU*>(has_z ? p.z : p.u) + rbase;
@@ -638,18 +637,30 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) f
   float* sp = p.states + ck_index(g, r, 0, sn ? n : 0);
   const int64_t sstep = g.dim * N;  // one saved state further
   float* sw = sy[wave] + cl * kCS;
+  // The wavefront's 4 channels share one (batch, group), so one 16-step block of B and C
+  // serves all of them: lane l fetches 8 values of it (matrix l / 32, state (l / 2) mod 16,
+  // steps 8 (l mod 2) ..), stages them in LDS as float32 (zeros for padded states), and
+  // lane (c, n) reads its state's 16 steps back.  Rows are 20 floats: 16-byte aligned, and
+  // the 16 rows' reads fall in distinct banks.
+  constexpr int kBcRow = 20;
+  __shared__ __align__(16) float sbc[4][2][HS][kBcRow];
+  const int sm = lane >> 5, sst = (lane >> 1) & 15, shf = lane & 1;
+  const bool sok = sst < N;
+  const TB* bcsrc = static_cast<const TB*>(sm ? p.C : p.B) + (bg * N + (sok ? sst : 0)) * L + 8 * shf;
+  float* stg = &sbc[wave][sm][sst][8 * shf];
+  const float* brow = &sbc[wave][0][n][0];
+  const float* crow = &sbc[wave][1][n][0];
 
   struct In {
     float dl;
     TU u, z;
-    RawRun<TB> b, c;
+    RawRun<TB, 8> bc;
   };
   auto load = [&](int64_t t0, In& in) {
     in.dl = dp[t0];
     in.u = up[t0];
     in.z = zp[t0];
-    in.b.load(g, p.B, 0, bcrow + t0, HS);
-    in.c.load(g, p.C, 0, bcrow + t0, HS);
+    in.bc.load(g, bcsrc, 0, t0, 8);
   };
   const int64_t nblk = L / HS;
   // Two buffers of raw inputs: a block's raw words are unpacked first and then
@@ -669,15 +680,22 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) f
     const float uu = to_f32(in.u);
     const float zz = to_f32(in.z);
     const float del = step_of(g, in.dl, bias);
-    float bv[HS], cv[HS];
-    in.b.get(bv);
-    in.c.get(cv);
-    if constexpr (sizeof(TB) == 2) load(ahead(k + 2), in);
-    const float du = del * uu;
-    if (N < HS && !sn) {  // a padded state adds nothing (its B row is state 0's)
+    {
+      float sv[8];
+      in.bc.get(sv);
+      if (!sok) {  // a padded state adds nothing
 #pragma unroll
-      for (int i = 0; i < HS; ++i) bv[i] = cv[i] = 0.0f;
+        for (int i = 0; i < 8; ++i) sv[i] = 0.0f;
+      }
+      reinterpret_cast<float4*>(stg)[0] = make_float4(sv[0], sv[1], sv[2], sv[3]);
+      reinterpret_cast<float4*>(stg)[1] = make_float4(sv[4], sv[5], sv[6], sv[7]);
     }
+    if constexpr (sizeof(TB) == 2) load(ahead(k + 2), in);
+    wave_lds_sync();
+    float bv[HS], cv[HS];
+    lds_row<HS>(brow, bv);
+    lds_row<HS>(crow, cv);
+    const float du = del * uu;
     static_for<0, HS>([&](auto ic) {
       constexpr int i = decltype(ic)::value;
       x = fmaf(fast_exp2(a2 * row_newbcast<i>(del)), x, row_newbcast<i>(du) * bv[i]);
@@ -1479,7 +1497,7 @@ extern "C" int mko_selscan_fwd(const mko_selscan_params* p, void* stream) {
   }
   pl.g.vec = rows_vectorisable(pl.g, {{p->u, p->u_dtype}, {p->delta, p->delta_dtype}, {p->z, p->u_dtype},
                                       {p->out, p->u_dtype}}) ? 1 : 0;
-  pl.lane = pl.ns == 16 && pl.g.rows >= kLaneRows && pl.g.length % HS == 0 &&
+  pl.lane = pl.ns == 16 && pl.g.rows >= kLaneRows && pl.g.length % HS == 0 && pl.g.dg % kLaneChannels == 0 &&
             rows_vectorisable(pl.g, {{p->B, p->bc_dtype}, {p->C, p->bc_dtype}});
   Ptrs q = make_ptrs(p, pl);
   hipStream_t s = static_cast<hipStream_t>(stream);

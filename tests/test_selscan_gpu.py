@@ -133,13 +133,38 @@ def test_bf16_delta_and_fp16():
 LANE_SHAPES = [
     (2, 3072, 64, 16, 1),   # the smallest lane-path problem
     (2, 3072, 48, 12, 2),   # dstate 12 (lanes 12..15 idle), two groups
-    (1, 6200, 32, 16, 4),   # a ragged last wavefront, four groups of 1550 channels
+    (1, 6200, 32, 16, 2),   # a ragged last workgroup, two groups of 3100 channels
 ]
+
+
+def _forward_kernels(inputs, softplus):
+    """The library's kernels that one forward launches (its per-kernel timing names)."""
+    from metal_kernelops import _native as nat
+    from metal_kernelops import selective_scan
+    dev = {k: (v.to(DEV) if v is not None else None) for k, v in inputs.items()}
+    nat.kernel_timing_reset()
+    nat.kernel_timing(True)
+    try:
+        with torch.no_grad():
+            selective_scan(**dev, delta_softplus=softplus)
+        return set(nat.kernel_times())
+    finally:
+        nat.kernel_timing(False)
 
 
 @pytest.mark.parametrize("shape", LANE_SHAPES, ids=lambda s: "x".join(map(str, s)))
 def test_lane_forward_shapes_fp32(shape):
     inputs, dy = _random_problem(*shape, seed=sum(shape))
+    assert "selscan_fwd_lane" in _forward_kernels(inputs, True)
+    _compare(inputs, dy, True, 1e-5, 1e-4)
+
+
+def test_unaligned_groups_take_the_chunked_forward():
+    """Groups of 1550 channels (not a multiple of the 4 a lane-path wavefront shares): the
+    chunked forward runs instead, to the same result."""
+    inputs, dy = _random_problem(1, 6200, 32, 16, 4, seed=6252)
+    kernels = _forward_kernels(inputs, True)
+    assert "selscan_fwd_lane" not in kernels and "selscan_fwd_replay" in kernels
     _compare(inputs, dy, True, 1e-5, 1e-4)
 
 
