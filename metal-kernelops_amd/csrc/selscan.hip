@@ -662,20 +662,20 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) f
     in.z = zp[t0];
     in.bc.load(g, bcsrc, 0, t0, 8);
   };
-  const int64_t nblk = L / HS;
+  const int nblk = static_cast<int>(L / HS);
   // Two buffers of raw inputs: a block's raw words are unpacked first and then
   // reloaded with the block two further on (the last ones reload the last block), so
   // each load has two blocks of work to arrive.  32-bit B/C need no unpacking (the
   // raw words are the values), so their reload waits for the end of the block
   // instead of holding a second copy: one block of work, as many registers as one
   // buffer ahead.
-  auto ahead = [&](int64_t k) { return (k < nblk ? k : nblk - 1) * HS; };
+  auto ahead = [&](int k) { return static_cast<int64_t>(k < nblk ? k : nblk - 1) * HS; };
   In ra, rb;
   load(0, ra);
   load(ahead(1), rb);
   float x = 0.0f;
-  auto block = [&](int64_t k, In& in) {
-    const int64_t t0 = k * HS;
+  auto block = [&](int k, In& in) {
+    const int64_t t0 = static_cast<int64_t>(k) * HS;
     if (active && sn) sp[k * sstep] = x;
     const float uu = to_f32(in.u);
     const float zz = to_f32(in.z);
@@ -713,7 +713,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) f
     if (active) op[t0] = from_f32<TU>(y);
     if constexpr (sizeof(TB) == 4) load(ahead(k + 2), in);
   };
-  for (int64_t k = 0; k < nblk; k += 2) {
+  for (int k = 0; k < nblk; k += 2) {
     block(k, ra);
     if (k + 1 < nblk) block(k + 1, rb);
   }
