@@ -4,8 +4,9 @@
 //   pre[b, c, t] = bias[c] + sum_{j < K} w[c, j] z[b, c, t + j]      (z index t + j = time t - m + j)
 //   out          = act(pre),  act = identity or silu
 //   final_state  = z[..., L : L + m]
-// Widths up to 8: a wavefront covers 64 * WB consecutive 8-step blocks of one row, lane l
-// taking blocks l, l + 64, ... (one 16-byte vector load per block on aligned rows, so every
+// Widths up to 8: a wavefront covers 64 * WF (forward) or 64 * WB (backward) consecutive
+// 8-step blocks of one row, lane l taking blocks l, l + 64, ... (one 16-byte vector load per
+// block on aligned rows, so every
 // wavefront access is 64 consecutive blocks); the look-back (and, in the backward,
 // look-ahead) steps come from the neighbouring lanes.  Wider kernels: the forward gives a
 // lane one block; the backward walks RB consecutive blocks with sliding register windows.
@@ -25,15 +26,18 @@ namespace {
 
 constexpr int BS = 8;  // steps per block
 constexpr int RB = 4;  // blocks per lane in the wide-kernel backward (width > 8)
-constexpr int WB = 4;  // iterations of the interleaved backward: a wavefront covers 64 * WB
+constexpr int WF = 4;  // iterations of the interleaved forward: a wavefront covers 64 * WF
                        // consecutive blocks of a row, lane l taking blocks l, l + 64, ...
+constexpr int WB = 8;  // iterations of the interleaved backward (more, so that its longer
+                       // per-wavefront setup and tap sums are paid over more blocks)
 
 struct Geo {
   int64_t batch, channels, length, rows;  // rows = batch * channels
   int width, taps;                          // taps = width - 1
   int64_t nblk;                             // blocks of BS steps per row
   int64_t lpr;                              // lanes per row: ceil(nblk / RB), rounded up to 16
-  int64_t nseg;                             // interleaved backward: wavefronts per row
+  int64_t nseg;                             // interleaved forward: wavefronts per row
+  int64_t nsegb;                            // interleaved backward: wavefronts per row
   int dtype;
   int silu;
   int vec;                                  // rows are 16-byte aligned whole blocks
@@ -124,6 +128,42 @@ struct RawBlk {
     for (int i = 0; i < BS; ++i) v[i] = i < nok ? f[i] : 0.0f;
   }
 };
+
+// The taps (left-padded to KMAX as in load_taps) and the bias of channel c, and the carry
+// z(t_first + i), i < H (x for t >= 0, else the initial state or zero padding), in the
+// element type: every load reads a valid address and is issued before any is converted,
+// so they arrive together (through load_one's dtype branches they would be waited for one
+// at a time).
+template <int KMAX, class T>
+__device__ __forceinline__ void load_setup_t(const Geo& g, const mko_conv1d_params& p, int64_t row, int64_t c,
+                                             int64_t t_first, float (&wp)[KMAX], float& bias,
+                                             float (&carry)[KMAX - 1]) {
+  constexpr int H = KMAX - 1;
+  const int lead = KMAX - g.width;
+  const T* w = static_cast<const T*>(p.weight) + c * g.width;
+  const T* b = p.bias ? static_cast<const T*>(p.bias) + c : w;
+  const T* xr = static_cast<const T*>(p.x) + row * g.length;
+  const bool has_init = p.initial_state != nullptr && g.taps > 0;  // width 1: an empty state
+  const T* ir = has_init ? static_cast<const T*>(p.initial_state) + row * g.taps : xr;
+  T rw[KMAX], rx[H], ri[H];
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) rw[j] = w[j >= lead ? j - lead : 0];
+  const T rb = *b;
+#pragma unroll
+  for (int i = 0; i < H; ++i) {
+    const int64_t t = t_first + i, ti = g.taps + t;
+    rx[i] = xr[t < 0 ? 0 : (t < g.length ? t : g.length - 1)];
+    ri[i] = ir[has_init && ti >= 0 && ti < g.taps ? ti : 0];
+  }
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) wp[j] = j >= lead ? to_f32(rw[j]) : 0.0f;
+  bias = p.bias ? to_f32(rb) : 0.0f;
+#pragma unroll
+  for (int i = 0; i < H; ++i) {
+    const int64_t t = t_first + i;
+    carry[i] = t >= 0 ? (t < g.length ? to_f32(rx[i]) : 0.0f) : (has_init && t >= -g.taps ? to_f32(ri[i]) : 0.0f);
+  }
+}
 
 // The BS steps at t0 of a typed row (those inside the row).
 template <class T, bool VEC>
@@ -298,7 +338,7 @@ __global__ void __launch_bounds__(256) backward(Geo g, mko_conv1d_params p, floa
 }
 
 // Forward for widths up to 8, blocks interleaved across lanes as in `backward_il`: a
-// wavefront covers 64 * WB consecutive blocks of one row, every load and store is 64
+// wavefront covers 64 * WF consecutive blocks of one row, every load and store is 64
 // consecutive blocks, and the H steps before a block come from lane l - 1 (lane 0: the
 // carry of lane 63's previous block, or the initial state).  The per-row setup (index
 // arithmetic, taps, bias) is paid once per four blocks.
@@ -311,21 +351,18 @@ __global__ void __launch_bounds__(256) forward_il(Geo g, mko_conv1d_params p) {
   if (wv >= g.rows * g.nseg) return;  // wave-uniform: whole wavefronts leave
   const int64_t row = wv / g.nseg, seg = wv % g.nseg;
   const int64_t c = row % g.channels;
-  float wp[KMAX];
-  load_taps<KMAX>(g, p.weight, c, wp);
-  const float bias = p.bias ? load_one(p.bias, g.dtype, c) : 0.0f;
-  const int64_t base = seg * kWave * WB;
-  float carry[H];
-#pragma unroll
-  for (int i = 0; i < H; ++i) carry[i] = z_at(g, p.x, p.initial_state, row, base * BS - H + i);
+  const int64_t base = seg * kWave * WF;
+  // the carry: z(t0 - H + i) of lane 0's first block
+  float wp[KMAX], bias, carry[H];
+  load_setup_t<KMAX, T>(g, p, row, c, base * BS - H, wp, bias, carry);
   const T* xs = static_cast<const T*>(p.x);
   RawBlk<T, VEC> cur;
   cur.load(g, xs, row, base + lane);
-  for (int k = 0; k < WB; ++k) {
+  for (int k = 0; k < WF; ++k) {
     const int64_t blk = base + k * kWave + lane;
     if (base + k * kWave >= g.nblk) break;  // wave-uniform: no block of this iteration exists
     RawBlk<T, VEC> nxt;
-    if (k + 1 < WB) nxt.load(g, xs, row, blk + kWave);  // in flight during this block
+    if (k + 1 < WF) nxt.load(g, xs, row, blk + kWave);  // in flight during this block
     float xc[BS];
     cur.get(xc);
     float zz[H + BS];
@@ -354,7 +391,7 @@ __global__ void __launch_bounds__(256) forward_il(Geo g, mko_conv1d_params p) {
     }
 #pragma unroll
     for (int i = 0; i < H; ++i) carry[i] = __shfl(xc[BS - H + i], kWave - 1);
-    if (k + 1 < WB) cur = nxt;
+    if (k + 1 < WF) cur = nxt;
   }
 }
 
@@ -373,21 +410,17 @@ __global__ void __launch_bounds__(256) backward_il(Geo g, mko_conv1d_params p, f
   static_assert(H < BS, "look-back and look-ahead within one neighbouring block");
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t wv = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + (threadIdx.x >> 6);
-  const bool in_grid = wv < g.rows * g.nseg;
-  const int64_t row = in_grid ? wv / g.nseg : 0, seg = in_grid ? wv % g.nseg : 0;
+  const bool in_grid = wv < g.rows * g.nsegb;
+  const int64_t row = in_grid ? wv / g.nsegb : 0, seg = in_grid ? wv % g.nsegb : 0;
   const int64_t c = row % g.channels;
-  float wp[KMAX];
-  load_taps<KMAX>(g, p.weight, c, wp);
-  const float bias = p.bias ? load_one(p.bias, g.dtype, c) : 0.0f;
   float dwp[KMAX], dbp = 0.0f;
 #pragma unroll
   for (int j = 0; j < KMAX; ++j) dwp[j] = 0.0f;
   const int64_t base = in_grid ? seg * kWave * WB : g.nblk;  // no row: every block is past the end
-  // z(t0 - H + i), i < H, of lane 0's first block: the initial state (or zeros) for block 0,
-  // else the steps before the segment
-  float carry[H];
-#pragma unroll
-  for (int i = 0; i < H; ++i) carry[i] = z_at(g, p.x, p.initial_state, row, base * BS - H + i);
+  // the carry: z(t0 - H + i), i < H, of lane 0's first block (the initial state or zeros for
+  // block 0, else the steps before the segment)
+  float wp[KMAX], bias, carry[H];
+  load_setup_t<KMAX, T>(g, p, row, c, base * BS - H, wp, bias, carry);
   const T* xs = static_cast<const T*>(p.x);
   const T* ds = static_cast<const T*>(p.dout);
   RawBlk<T, VEC> xr, dr;
@@ -509,7 +542,7 @@ __global__ void __launch_bounds__(256) finalize_il(Geo g, mko_conv1d_params p, c
   float s = 0.0f;
   for (int64_t b = 0; b < g.batch; ++b) {
     const int64_t row = b * g.channels + c;
-    for (int64_t k = 0; k < g.nseg; ++k) s += partial[(row * g.nseg + k) * (g.width + 1) + j];
+    for (int64_t k = 0; k < g.nsegb; ++k) s += partial[(row * g.nsegb + k) * (g.width + 1) + j];
   }
   if (j < g.width) {
     if (p.dweight) store_one(p.dweight, g.dtype, c * g.width + j, s);
@@ -591,7 +624,8 @@ int make_geo(const mko_conv1d_params* p, Geo* g) {
   g->taps = g->width - 1;
   g->nblk = (p->length + BS - 1) / BS;
   g->lpr = ((g->nblk + RB - 1) / RB + 15) / 16 * 16;
-  g->nseg = (g->nblk + kWave * WB - 1) / (kWave * WB);
+  g->nseg = (g->nblk + kWave * WF - 1) / (kWave * WF);
+  g->nsegb = (g->nblk + kWave * WB - 1) / (kWave * WB);
   g->dtype = p->dtype;
   g->silu = (p->flags & MKO_CONV_SILU) != 0;
   const uintptr_t mask = 15u;
@@ -624,7 +658,7 @@ void launch_fwd(const Geo& g, const mko_conv1d_params& p, hipStream_t s) {
 template <int KMAX>
 void launch_bwd(const Geo& g, const mko_conv1d_params& p, float* partial, hipStream_t s) {
   if constexpr (KMAX <= BS) {
-    const int64_t waves = g.rows * g.nseg;
+    const int64_t waves = g.rows * g.nsegb;
     const unsigned grid = static_cast<unsigned>((waves + 3) / 4);
 #define MKO_CONV_BWD(T, V) MKO_TIMED("conv1d_bwd", s, (backward_il<KMAX, T, V><<<grid, 256, 0, s>>>(g, p, partial)))
     if (g.dtype == MKO_F32) {
@@ -643,7 +677,7 @@ void launch_bwd(const Geo& g, const mko_conv1d_params& p, float* partial, hipStr
 
 // One partial per interleaved wavefront (width <= 8) or per 16-lane group (wider).
 size_t partial_bytes(const Geo& g) {
-  const int64_t parts = g.width <= BS ? g.rows * g.nseg : g.rows * (g.lpr / 16);
+  const int64_t parts = g.width <= BS ? g.rows * g.nsegb : g.rows * (g.lpr / 16);
   return static_cast<size_t>(parts) * (g.width + 1) * sizeof(float);
 }
 
