@@ -585,14 +585,15 @@ __global__ void __launch_bounds__(256) fwd_replay(Geo g, Ptrs p) {
 // and no replay.  Per block:
 //   - lane (c, n) loads step t0 + n of its channel's delta, u and z (a wavefront reads 4 rows
 //     x 16 consecutive steps) and forms that step's size and du = step * u;
-//   - it advances its one state over the 16 steps, reading step i's size and du from lane i
-//     of its row (DPP row_newbcast, folded into the multiplies) and B_n, C_n of those steps
-//     from 16 consecutive values of its state's row of the caller's B and C (as stored:
-//     16-bit rows are half the vector-memory traffic of float32 copies);
+//   - the 4 channels share one (batch, group), so the block's B and C (16 states x 16 steps
+//     each) are fetched once per wavefront, 8 values a lane, and staged in LDS as float32;
+//   - lane (c, n) advances its one state over the 16 steps, reading step i's size and du
+//     from lane i of its row (DPP row_newbcast, folded into the multiplies) and B_n, C_n of
+//     those steps from the staged block;
 //   - the 16 states' C_n x_n per step go through a per-wavefront LDS transpose, so lane
 //     (c, n) sums step t0 + n's, adds the skip, applies the gate and stores it;
 //   - the state entering the block is saved (4 channels x 16 states: 256 contiguous bytes).
-// The next block's loads are issued before the current block is computed.
+// A block's inputs are requested two blocks ahead.
 
 template <int I, int END, class F>
 __device__ __forceinline__ void static_for(F&& f) {
