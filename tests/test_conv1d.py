@@ -123,6 +123,10 @@ CASES = [
     ("k1-2x64x33", 2, 64, 33, 1, None, True, torch.float32),
     ("ragged-3x40x37-k3", 3, 40, 37, 3, "silu", True, torch.float32),
     ("wide-2x16x90-k20", 2, 16, 90, 20, "silu", True, torch.float32),
+    # this build's own boundaries: rows longer than one interleaved wavefront's span in both
+    # directions (the carry crosses segments), aligned and ragged, and width 8
+    ("long-2x64x9000-k4", 2, 64, 9000, 4, "silu", True, torch.float32),
+    ("long-2x32x12288-k8-bf16", 2, 32, 12288, 8, "silu", True, torch.bfloat16),
 ]
 
 
