@@ -31,19 +31,31 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 template <typename TM>
 constexpr int tile_ld() { return sizeof(TM) == 2 ? 72 : 66; }
 
+// A compact 16-bit tile, 64 elements a row, for kernels whose LDS bounds their
+// occupancy.  Every row is 0 mod 32 banks, so the 16-byte units of row r are XOR-swizzled
+// by (r mod 8) ^ (r / 8 mod 8): the operand reads (32 consecutive rows at one k) and the
+// transposed staging stores (rows 8m + j at one k) both spread over eight 4-bank groups.
+// fp32 tiles keep their padded pitch.
 template <typename TM>
+constexpr int compact_ld() { return sizeof(TM) == 2 ? 64 : tile_ld<TM>(); }
+
+template <typename TM, int LD = tile_ld<TM>()>
 struct LdsTile {
-  static constexpr int ld = tile_ld<TM>();
+  static constexpr int ld = LD;
   static constexpr int elems = 64 * ld;
 };
 
 // Element offset of (row, k) in an LDS operand tile (k: the contiguous dimension).
-template <typename TM>
+template <typename TM, int LD = tile_ld<TM>()>
 __device__ __forceinline__ int lds_idx(int row, int k) {
-  if constexpr (sizeof(TM) == 2)
-    return row * tile_ld<TM>() + (k ^ (row & 0x38));
-  else
-    return row * tile_ld<TM>() + k;
+  if constexpr (sizeof(TM) == 2) {
+    if constexpr (LD == 64)
+      return row * 64 + (k ^ (((row & 7) ^ ((row >> 3) & 7)) << 3));
+    else
+      return row * LD + (k ^ (row & 0x38));
+  } else {
+    return row * LD + k;
+  }
 }
 
 __device__ __forceinline__ void quadrant(int lane_wave, int& wm, int& wn) {
@@ -58,15 +70,15 @@ __device__ __forceinline__ int acc_row(int wm, int lane, int r) {
 __device__ __forceinline__ int acc_col(int wn, int lane) { return wn * 32 + (lane & 31); }
 
 // acc += A[wm*32 .. +32][0..k_len) * B[0..k_len)[wn*32 .. +32], with A and B^T in LDS.
-template <typename TM>
+template <typename TM, int LD = tile_ld<TM>()>
 __device__ __forceinline__ void mma_tile(f32x16& acc, const TM* A, const TM* Bt, int wm, int wn, int lane,
                                          int k_len) {
-  constexpr int ld = tile_ld<TM>();
+  constexpr int ld = LD;
   if constexpr (sizeof(TM) == 2) {
     const int ra = wm * 32 + (lane & 31), rb = wn * 32 + (lane & 31), kh = (lane >> 5) * 8;
     for (int k = 0; k < k_len; k += 16) {
-      const uint4 av = *reinterpret_cast<const uint4*>(A + lds_idx<TM>(ra, k + kh));
-      const uint4 bv = *reinterpret_cast<const uint4*>(Bt + lds_idx<TM>(rb, k + kh));
+      const uint4 av = *reinterpret_cast<const uint4*>(A + lds_idx<TM, LD>(ra, k + kh));
+      const uint4 bv = *reinterpret_cast<const uint4*>(Bt + lds_idx<TM, LD>(rb, k + kh));
       if constexpr (__is_same(TM, bf16)) {
         acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(mfma_bf16x8, av),
                                                       __builtin_bit_cast(mfma_bf16x8, bv), acc, 0, 0, 0);

@@ -170,7 +170,8 @@ __device__ __forceinline__ void scale8(const V8<TM>& v, float s, float (&f)[8]) 
 // flight during the products of the current ones.
 template <typename TM, bool VEC, bool BWD>
 __global__ void __launch_bounds__(256) chunk_state(Geo g, Ptrs p, void* out_) {
-  constexpr int TE = LdsTile<TM>::elems;
+  constexpr int LD = compact_ld<TM>();  // LDS bounds this kernel: the compact tiles
+  constexpr int TE = LdsTile<TM, LD>::elems;
   __shared__ __align__(16) TM sbuf[2][3 * TE];
   __shared__ float s1[256];
   const WgId id = wg_id(g.npt * g.nnp, g.nc);
@@ -204,9 +205,9 @@ __global__ void __launch_bounds__(256) chunk_state(Geo g, Ptrs p, void* out_) {
     float a[8], bb[8];
     scale8(r.x[0], s1[64 * kb + r0], a);
     scale8(r.x[1], s1[64 * kb + r0 + 1], bb);
-    put2x8<TM, true>(buf, r0, c0, a, bb);                     // A[p][l]
-    put_raw<TM, true>(buf + TE, r0, c0, r.y0[0], r.y0[1]);      // Bt[n][l]
-    put_raw<TM, true>(buf + 2 * TE, r0, c0, r.y1[0], r.y1[1]);
+    put2x8<TM, true, LD>(buf, r0, c0, a, bb);                     // A[p][l]
+    put_raw<TM, true, LD>(buf + TE, r0, c0, r.y0[0], r.y0[1]);      // Bt[n][l]
+    put_raw<TM, true, LD>(buf + 2 * TE, r0, c0, r.y1[0], r.y1[1]);
   };
   f32x16 acc0, acc1;
   zero(acc0);
@@ -215,8 +216,8 @@ __global__ void __launch_bounds__(256) chunk_state(Geo g, Ptrs p, void* out_) {
   Regs ra, rb;
   pipeline2(g.qb, ra, rb, fetch, put, [&](int kb) {
     TM* buf = sbuf[kb & 1];
-    mma_tile<TM>(acc0, buf, buf + TE, wm, wn, lane, 64);
-    mma_tile<TM>(acc1, buf, buf + 2 * TE, wm, wn, lane, 64);
+    mma_tile<TM, LD>(acc0, buf, buf + TE, wm, wn, lane, 64);
+    mma_tile<TM, LD>(acc1, buf, buf + 2 * TE, wm, wn, lane, 64);
   });
   TM* out = static_cast<TM*>(out_) + (bh * g.nc + c) * g.headdim * g.dstate;
 #pragma unroll

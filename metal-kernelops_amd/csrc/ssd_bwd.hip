@@ -474,7 +474,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) d
 // block of the group's heads.
 template <typename TM, bool VEC>
 __global__ void __launch_bounds__(256) dbc_state(Geo g, BwdPlan pl, Ptrs p) {
-  constexpr int TE = LdsTile<TM>::elems;
+  constexpr int LD = compact_ld<TM>();  // LDS bounds this kernel: the compact tiles
+  constexpr int TE = LdsTile<TM, LD>::elems;
   __shared__ __align__(16) TM sbuf[2][3 * TE];
   const WgId id = wg_id(g.qb * g.nnp * 2 * pl.hb2, g.nc * g.ngroups);
   int idx = id.x;
@@ -523,9 +524,9 @@ __global__ void __launch_bounds__(256) dbc_state(Geo g, BwdPlan pl, Ptrs p) {
     const float sc1 = which ? fast_exp(r.cl[1]) : r.dl[1] * fast_exp(r.T - r.cl[1]);
     scale8(r.src[0], sc0, a);
     scale8(r.src[1], sc1, bb);
-    put2x8<TM, false>(buf, r0, c0, a, bb);                    // A[l][p]
-    put_raw<TM, true>(buf + TE, r0, c0, r.s0[0], r.s0[1]);      // Bt[n][p] = S[p][n]
-    put_raw<TM, true>(buf + 2 * TE, r0, c0, r.s1[0], r.s1[1]);
+    put2x8<TM, false, LD>(buf, r0, c0, a, bb);                    // A[l][p]
+    put_raw<TM, true, LD>(buf + TE, r0, c0, r.s0[0], r.s0[1]);      // Bt[n][p] = S[p][n]
+    put_raw<TM, true, LD>(buf + 2 * TE, r0, c0, r.s1[0], r.s1[1]);
   };
   f32x16 acc0, acc1;
   zero(acc0);
@@ -533,8 +534,8 @@ __global__ void __launch_bounds__(256) dbc_state(Geo g, BwdPlan pl, Ptrs p) {
   Regs ra, rb;
   pipeline2(nst, ra, rb, fetch, put, [&](int k) {
     TM* buf = sbuf[k & 1];
-    mma_tile<TM>(acc0, buf, buf + TE, wm, wn, lane, 64);
-    mma_tile<TM>(acc1, buf, buf + 2 * TE, wm, wn, lane, 64);
+    mma_tile<TM, LD>(acc0, buf, buf + TE, wm, wn, lane, 64);
+    mma_tile<TM, LD>(acc1, buf, buf + 2 * TE, wm, wn, lane, 64);
   });
 #pragma unroll
   for (int r = 0; r < 16; ++r) {

@@ -123,19 +123,19 @@ __device__ __forceinline__ void v8_store(T* p, int n, bool vec, const float (&f)
 
 // Writes the thread's block (row r0 = a, row r0+1 = b, columns c0..c0+7) into an LDS
 // operand tile, as is or transposed.
-template <typename TM, bool TRANS>
+template <typename TM, bool TRANS, int LD = tile_ld<TM>()>
 __device__ __forceinline__ void put2x8(TM* dst, int r0, int c0, const float (&a)[8], const float (&b)[8]) {
-  constexpr int ld = tile_ld<TM>();
+  constexpr int ld = LD;
   if constexpr (sizeof(TM) == 2) {
     if constexpr (!TRANS) {
-      *reinterpret_cast<uint4*>(dst + lds_idx<TM>(r0, c0)) =
+      *reinterpret_cast<uint4*>(dst + lds_idx<TM, LD>(r0, c0)) =
           make_uint4(pack2<TM>(a[0], a[1]), pack2<TM>(a[2], a[3]), pack2<TM>(a[4], a[5]), pack2<TM>(a[6], a[7]));
-      *reinterpret_cast<uint4*>(dst + lds_idx<TM>(r0 + 1, c0)) =
+      *reinterpret_cast<uint4*>(dst + lds_idx<TM, LD>(r0 + 1, c0)) =
           make_uint4(pack2<TM>(b[0], b[1]), pack2<TM>(b[2], b[3]), pack2<TM>(b[4], b[5]), pack2<TM>(b[6], b[7]));
     } else {
 #pragma unroll
       for (int k = 0; k < 8; ++k)
-        *reinterpret_cast<uint32_t*>(dst + lds_idx<TM>(c0 + k, r0)) = pack2<TM>(a[k], b[k]);
+        *reinterpret_cast<uint32_t*>(dst + lds_idx<TM, LD>(c0 + k, r0)) = pack2<TM>(a[k], b[k]);
     }
   } else {
     if constexpr (!TRANS) {
@@ -199,9 +199,9 @@ __device__ __forceinline__ void store_win(T* base, int ld, int nrows, int ncols,
 }
 
 // Writes the thread's raw block (rows a, b) into an LDS operand tile without conversion.
-template <typename TM, bool TRANS>
+template <typename TM, bool TRANS, int LD = tile_ld<TM>()>
 __device__ __forceinline__ void put_raw(TM* dst, int r0, int c0, const V8<TM>& a, const V8<TM>& b) {
-  constexpr int ld = tile_ld<TM>();
+  constexpr int ld = LD;
   constexpr int W = V8<TM>::kWords;
   uint32_t aw[W], bw[W];
 #pragma unroll
@@ -211,14 +211,14 @@ __device__ __forceinline__ void put_raw(TM* dst, int r0, int c0, const V8<TM>& a
   }
   if constexpr (sizeof(TM) == 2) {
     if constexpr (!TRANS) {
-      *reinterpret_cast<uint4*>(dst + lds_idx<TM>(r0, c0)) = make_uint4(aw[0], aw[1], aw[2], aw[3]);
-      *reinterpret_cast<uint4*>(dst + lds_idx<TM>(r0 + 1, c0)) = make_uint4(bw[0], bw[1], bw[2], bw[3]);
+      *reinterpret_cast<uint4*>(dst + lds_idx<TM, LD>(r0, c0)) = make_uint4(aw[0], aw[1], aw[2], aw[3]);
+      *reinterpret_cast<uint4*>(dst + lds_idx<TM, LD>(r0 + 1, c0)) = make_uint4(bw[0], bw[1], bw[2], bw[3]);
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         // column 2i: low halves of a and b; column 2i+1: high halves
-        *reinterpret_cast<uint32_t*>(dst + lds_idx<TM>(c0 + 2 * i, r0)) = __builtin_amdgcn_perm(bw[i], aw[i], 0x05040100u);
-        *reinterpret_cast<uint32_t*>(dst + lds_idx<TM>(c0 + 2 * i + 1, r0)) =
+        *reinterpret_cast<uint32_t*>(dst + lds_idx<TM, LD>(c0 + 2 * i, r0)) = __builtin_amdgcn_perm(bw[i], aw[i], 0x05040100u);
+        *reinterpret_cast<uint32_t*>(dst + lds_idx<TM, LD>(c0 + 2 * i + 1, r0)) =
             __builtin_amdgcn_perm(bw[i], aw[i], 0x07060302u);
       }
     }
