@@ -169,7 +169,8 @@ __device__ __forceinline__ void scale8(const V8<TM>& v, float s, float (&f)[8]) 
 // are staged transposed.  Double-buffered: the loads of the next 64 tokens are in
 // flight during the products of the current ones.
 template <typename TM, bool VEC, bool BWD>
-__global__ void __launch_bounds__(256) chunk_state(Geo g, Ptrs p, void* out_) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(sizeof(TM) == 2 ? 3 : 1)))
+chunk_state(Geo g, Ptrs p, void* out_) {
   constexpr int LD = compact_ld<TM>();  // LDS bounds this kernel: the compact tiles
   constexpr int TE = LdsTile<TM, LD>::elems;
   __shared__ __align__(16) TM sbuf[2][3 * TE];

@@ -473,7 +473,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) d
 // sum_h e^{cs_l} gy_l S_in) for one 64-token tile and two d_state tiles, over a
 // block of the group's heads.
 template <typename TM, bool VEC>
-__global__ void __launch_bounds__(256) dbc_state(Geo g, BwdPlan pl, Ptrs p) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(sizeof(TM) == 2 ? 3 : 1)))
+dbc_state(Geo g, BwdPlan pl, Ptrs p) {
   constexpr int LD = compact_ld<TM>();  // LDS bounds this kernel: the compact tiles
   constexpr int TE = LdsTile<TM, LD>::elems;
   __shared__ __align__(16) TM sbuf[2][3 * TE];
