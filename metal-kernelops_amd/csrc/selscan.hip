@@ -118,45 +118,47 @@ __device__ __forceinline__ int64_t ck_index(const Geo& g, int64_t row, int64_t k
 
 // ---------------------------------------------------------------- layout prep
 
-// B, C (bg, N, L) any dtype -> time-major fp32 (bg, L, NS), states >= N zeroed.
+// B, C (bg, N, L) any dtype -> the fp32 copies the scan kernels read: time-major
+// (bg, L, NS) in bt/ct and state-major (bg, NS, L) in bn/cn, states >= N zeroed. Any
+// output may be null. A workgroup converts one kPrepSteps-step tile of one (batch,
+// group): the loads and the state-major stores run along L, and the time-major stores
+// go through an LDS transpose so that they run along the states.
+constexpr int kPrepSteps = 64;
+
 template <int NS>
-__global__ void __launch_bounds__(256) prep_time_major(Geo g, const void* B, const void* C,
-                                                       float* bt, float* ct) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int64_t total = g.batch * g.ngroups * g.length;
-  if (i >= total) return;
-  const int64_t bg = i / g.length, t = i % g.length;
+__global__ void __launch_bounds__(256) prep_layouts(Geo g, int64_t ntiles, const void* B, const void* C,
+                                                    float* bt, float* ct, float* bn, float* cn) {
+  __shared__ float tile[2][kPrepSteps][NS + 1];
+  const int64_t bg = blockIdx.x / ntiles;
+  const int64_t t0 = (blockIdx.x % ntiles) * kPrepSteps;
+  const int tl = threadIdx.x & (kPrepSteps - 1);
+  const int64_t t = t0 + tl;
+  const bool in_t = t < g.length;
   const int N = static_cast<int>(g.dstate);
-#pragma unroll
-  for (int n = 0; n < NS; ++n) {
+  for (int n = static_cast<int>(threadIdx.x) / kPrepSteps; n < NS; n += 256 / kPrepSteps) {
     float vb = 0.0f, vc = 0.0f;
-    if (n < N) {
+    if (in_t && n < N) {
       const int64_t src = (bg * N + n) * g.length + t;
       if (B) vb = load_one(B, g.bc_dtype, src);
       if (C) vc = load_one(C, g.bc_dtype, src);
     }
-    if (bt) bt[i * NS + n] = vb;
-    if (ct) ct[i * NS + n] = vc;
+    tile[0][tl][n] = vb;
+    tile[1][tl][n] = vc;
+    if (in_t) {
+      const int64_t dst = (bg * NS + n) * g.length + t;
+      if (bn) bn[dst] = vb;
+      if (cn) cn[dst] = vc;
+    }
   }
-}
-
-// B, C (bg, N, L) any dtype -> state-major fp32 (bg, NS, L), padded states zeroed.
-__global__ void __launch_bounds__(256) prep_state_major(Geo g, int ns, const void* B, const void* C,
-                                                        float* bn, float* cn) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int64_t total = g.batch * g.ngroups * ns * g.length;
-  if (i >= total) return;
-  const int64_t t = i % g.length;
-  const int64_t n = (i / g.length) % ns;
-  const int64_t bg = i / (g.length * ns);
-  float vb = 0.0f, vc = 0.0f;
-  if (n < g.dstate) {
-    const int64_t src = (bg * g.dstate + n) * g.length + t;
-    vb = load_one(B, g.bc_dtype, src);
-    vc = load_one(C, g.bc_dtype, src);
+  if (!bt && !ct) return;  // the same for the whole grid
+  __syncthreads();
+  const int64_t base = (bg * g.length + t0) * NS;
+  const int nt = static_cast<int>(min(static_cast<int64_t>(kPrepSteps), g.length - t0));
+  for (int e = threadIdx.x; e < nt * NS; e += 256) {
+    const int tt = e / NS, n = e % NS;
+    if (bt) bt[base + e] = tile[0][tt][n];
+    if (ct) ct[base + e] = tile[1][tt][n];
   }
-  bn[i] = vb;
-  cn[i] = vc;
 }
 
 // ---------------------------------------------------------------- forward
@@ -1409,8 +1411,10 @@ static int launch_fwd(const Plan& pl, const Ptrs& q, hipStream_t s) {
   }
   const dim3 block(g.wpg * kWave);
   const unsigned gx = static_cast<unsigned>((g.nwr + g.wpg - 1) / g.wpg);
-  const int64_t bgl = g.batch * g.ngroups * g.length;
-  MKO_TIMED("selscan_prep", s, prep_time_major<NS><<<blocks_for(bgl), 256, 0, s>>>(g, q.B, q.C, q.bt, q.ct));
+  const int64_t ntiles = (g.length + kPrepSteps - 1) / kPrepSteps;
+  const unsigned gprep = static_cast<unsigned>(g.batch * g.ngroups * ntiles);
+  MKO_TIMED("selscan_prep", s,
+            prep_layouts<NS><<<gprep, 256, 0, s>>>(g, ntiles, q.B, q.C, q.bt, q.ct, nullptr, nullptr));
   if (g.nchunks > 1) {
     MKO_TIMED("selscan_fwd_summary", s, fwd_summary<NS, UNI, TU><<<dim3(gx, g.nchunks - 1), block, 0, s>>>(g, q));
   }
@@ -1428,8 +1432,11 @@ static int launch_bwd(const Plan& pl, const Ptrs& q, const mko_selscan_params* p
   const dim3 block(g.wpg * kWave);
   const unsigned gx = static_cast<unsigned>((g.nwr + g.wpg - 1) / g.wpg);
   const int64_t bgl = g.batch * g.ngroups * g.length;
-  MKO_TIMED("selscan_prep", s, prep_time_major<NS><<<blocks_for(bgl), 256, 0, s>>>(g, q.B, q.C, q.bt, q.ct);
-            prep_state_major<<<blocks_for(bgl * NS), 256, 0, s>>>(g, NS, q.B, q.C, q.bn, q.cn));
+  const int64_t ntiles = (g.length + kPrepSteps - 1) / kPrepSteps;
+  const unsigned gprep = static_cast<unsigned>(g.batch * g.ngroups * ntiles);
+  // the backward reads C time-major (summaries) and B, C state-major (main pass)
+  MKO_TIMED("selscan_prep", s,
+            prep_layouts<NS><<<gprep, 256, 0, s>>>(g, ntiles, q.B, q.C, nullptr, q.ct, q.bn, q.cn));
   if (g.nchunks > 1) {
     MKO_TIMED("selscan_bwd_summary", s, bwd_summary<NS, UNI, TU><<<dim3(gx, g.nchunks - 1), block, 0, s>>>(g, q));
   }
