@@ -1147,8 +1147,24 @@ __global__ void __launch_bounds__(256) reduce_bc(Geo g, int ncb, const float* __
     const int64_t t = t0 + tl;
     float vb = 0.0f, vc = 0.0f;
     if (t < g.length) {
-      for (int cbk = 0; cbk < ncb; ++cbk) {
-        const float2 q = *reinterpret_cast<const float2*>(pbc + (((bg * ncb + cbk) * g.length + t) * NS + n) * 2);
+      // channel blocks in order: whole batches of eight issue their loads together,
+      // the rest one at a time
+      constexpr int PF = 8;
+      const float2* src = reinterpret_cast<const float2*>(pbc + ((bg * ncb * g.length + t) * NS + n) * 2);
+      const int64_t stride = g.length * NS;  // float2 elements between channel blocks
+      int cbk = 0;
+      for (; cbk + PF <= ncb; cbk += PF) {
+        float2 q[PF];
+#pragma unroll
+        for (int j = 0; j < PF; ++j) q[j] = src[(cbk + j) * stride];
+#pragma unroll
+        for (int j = 0; j < PF; ++j) {
+          vb += q[j].x;
+          vc += q[j].y;
+        }
+      }
+      for (; cbk < ncb; ++cbk) {
+        const float2 q = src[cbk * stride];
         vb += q.x;
         vc += q.y;
       }
@@ -1163,6 +1179,38 @@ __global__ void __launch_bounds__(256) reduce_bc(Geo g, int ncb, const float* __
     const int64_t o = (bg * g.dstate + n) * g.length + t;
     if (dB) store_one(dB, g.bc_dtype, o, sb[n][tl]);
     if (dC) store_one(dC, g.bc_dtype, o, sc[n][tl]);
+  }
+}
+
+// Partials grp, grp + 4, ... of one channel (partial k = chunk k / nb, batch k % nb, at
+// k / nb * cstride + k % nb * dim), added in that order. Whole batches of eight issue
+// their loads together and the rest go one at a time; the bounds are wave-uniform. TWO:
+// p1 is summed into s1 alongside.
+template <bool TWO>
+__device__ __forceinline__ void sum_partials(const Geo& g, int grp, int npart, int nb, int64_t cstride,
+                                             const float* __restrict__ p0, const float* __restrict__ p1,
+                                             float& s0, float& s1) {
+  constexpr int PF = 8;
+  auto at = [&](int k) { return (k / nb) * cstride + (k % nb) * g.dim; };
+  int k = grp;
+  for (; k + 4 * (PF - 1) < npart; k += 4 * PF) {
+    float v0[PF], v1[PF];
+#pragma unroll
+    for (int q = 0; q < PF; ++q) {
+      const int64_t o = at(k + 4 * q);
+      v0[q] = p0[o];
+      if constexpr (TWO) v1[q] = p1[o];
+    }
+#pragma unroll
+    for (int q = 0; q < PF; ++q) {
+      s0 += v0[q];
+      if constexpr (TWO) s1 += v1[q];
+    }
+  }
+  for (; k < npart; k += 4) {
+    const int64_t o = at(k);
+    s0 += p0[o];
+    if constexpr (TWO) s1 += p1[o];
   }
 }
 
@@ -1184,32 +1232,11 @@ __global__ void __launch_bounds__(256) reduce_params(Geo g, int ns, const float*
   const int nb = static_cast<int>(g.batch);
   float s0 = 0.0f, s1 = 0.0f;
   if (d < g.dim) {
-    // partials grp, grp + 4, ... added in that order, four loads in flight at a time
-    // (the bounds are wave-uniform)
-    constexpr int PF = 4;
-    for (int k0 = grp; k0 < npart; k0 += 4 * PF) {
-      float v0[PF], v1[PF];
-#pragma unroll
-      for (int q = 0; q < PF; ++q) {
-        const int k = k0 + 4 * q;
-        v0[q] = v1[q] = 0.0f;
-        if (k < npart) {
-          const int64_t c = k / nb, b = k % nb;
-          if (n < N) {
-            v0[q] = dap[(c * ns + n) * g.rows + b * g.dim + d];
-          } else {
-            v0[q] = ddp[c * g.rows + b * g.dim + d];
-            v1[q] = dbp[c * g.rows + b * g.dim + d];
-          }
-        }
-      }
-#pragma unroll
-      for (int q = 0; q < PF; ++q) {
-        if (k0 + 4 * q >= npart) break;
-        s0 += v0[q];
-        s1 += v1[q];
-      }
-    }
+    const int64_t cstride = static_cast<int64_t>(n < N ? ns : 1) * g.rows;  // between chunks
+    if (n < N)
+      sum_partials<false>(g, grp, npart, nb, cstride, dap + n * g.rows + d, nullptr, s0, s1);
+    else
+      sum_partials<true>(g, grp, npart, nb, cstride, ddp + d, dbp + d, s0, s1);
   }
   part[0][grp][threadIdx.x & 63] = s0;
   part[1][grp][threadIdx.x & 63] = s1;
