@@ -127,10 +127,13 @@ __global__ void __launch_bounds__(256) chunk_scan(Geo g, Ptrs p) {
   constexpr int TE = LdsTile<TM>::elems;
   __shared__ __align__(16) TM sbuf[2][2 * TE];
   __shared__ __align__(16) float csc[256], dlc[256], ecol[256], dcol[64];
-  const WgId id = wg_id(g.qb * g.npt, g.nc);
-  const int i = id.x % g.qb, pt = id.x / g.qb;
-  const int c = id.y;
-  const int64_t bh = id.z, b = bh / g.nheads, h = bh % g.nheads;
+  // Heads fastest: the workgroups that run together share the group's C and C B^T
+  // tiles and cover whole token rows of x and the outputs.
+  const WgId id = wg_id(g.nheads, g.qb * g.npt);
+  const int64_t h = id.x, b = id.z / g.nc;
+  const int i = id.y % g.qb, pt = id.y / g.qb;
+  const int c = static_cast<int>(id.z % g.nc);
+  const int64_t bh = b * g.nheads + h;
   const int lane = threadIdx.x & 63;
   int wm, wn;
   quadrant(threadIdx.x >> 6, wm, wn);

@@ -52,10 +52,14 @@ __global__ void __launch_bounds__(256) gate(Geo g, BwdPlan pl, Ptrs p) {
   __shared__ __align__(16) TM sbuf[2][2 * TE];
   __shared__ __align__(16) float csc[256], dlc[256], ecol[256];
   __shared__ float colred[4][64];
-  const WgId id = wg_id(g.qb * g.npt, g.nc);
-  const int i = id.x % g.qb, pt = id.x / g.qb;
-  const int c = id.y;
-  const int64_t bh = id.z, b = bh / g.nheads, h = bh % g.nheads;
+  // Heads fastest: the workgroups that run together cover whole token rows (a row's
+  // heads are adjacent in x, dy, z and the outputs) instead of one head's columns of
+  // many rows.
+  const WgId id = wg_id(g.nheads, g.qb * g.npt);
+  const int64_t h = id.x, b = id.z / g.nc;
+  const int i = id.y % g.qb, pt = id.y / g.qb;
+  const int c = static_cast<int>(id.z % g.nc);
+  const int64_t bh = b * g.nheads + h;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int wm, wn;
   quadrant(wave, wm, wn);
@@ -203,11 +207,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) d
   __shared__ __align__(16) TM sbuf[2][2 * TE];
   __shared__ __align__(16) float csc[256], dlc[256], ecol[256], dcol[64];
   const int nj = (g.qb + 1) / 2;
-  const WgId id = wg_id(nj * g.npt, g.nc);
-  const int jx = id.x % nj, pt = id.x / nj;
+  // heads fastest, as in the forward's chunk_scan
+  const WgId id = wg_id(g.nheads, nj * g.npt);
+  const int jx = id.y % nj, pt = id.y / nj;
   const int ja = jx, jb = g.qb - 1 - jx;
-  const int c = id.y;
-  const int64_t bh = id.z, b = bh / g.nheads, h = bh % g.nheads, gg = h / g.hpg;
+  const int c = static_cast<int>(id.z % g.nc);
+  const int64_t h = id.x, b = id.z / g.nc, gg = h / g.hpg;
+  const int64_t bh = b * g.nheads + h;
   const int lane = threadIdx.x & 63;
   int wm, wn;
   quadrant(threadIdx.x >> 6, wm, wn);
