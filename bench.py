@@ -228,8 +228,8 @@ def ssd_flops(batch, length, nheads, headdim, ngroups, dstate, q):
 
     Per token and head: P(Q+1) for the masked scores . X product, 2NP for the chunk
     state and 2NP for C . state; per token and group N(Q+1) for C . B^T.  The backward
-    does two gradient contractions per forward one.  The backward's recompute of the
-    chunk output (ssd_gate) is not algorithmic work and is reported apart.
+    does two gradient contractions per forward one.  ssd_gate is element-wise here: the
+    forward saves the chunk output for it when a gradient will be taken.
     """
     tok = batch * length
     P, N, H, G = headdim, dstate, nheads, ngroups
@@ -240,7 +240,7 @@ def ssd_flops(batch, length, nheads, headdim, ngroups, dstate, q):
         "ssd_cb": cb, "ssd_chunk_state": state, "ssd_chunk_scan": tri_x + state,
         "ssd_chunk_state_bwd": state, "ssd_du": tri_x + state, "ssd_dcb": tri_x,
         "ssd_dbc_state": 2 * state, "ssd_dbc_final": 2 * cb,
-    }, {"ssd_gate": tri_x + state}
+    }
 
 
 def ssd_bytes(batch, length, nheads, headdim, ngroups, dstate, act=2):
@@ -272,16 +272,16 @@ def ssd_case(steps, warmup, batch=4, length=4096, nheads=64, headdim=64, ngroups
         torch.autograd.grad((y, s), order, (dy, dfinal))
 
     ms, wall, kernels = timed(step, steps, warmup)
-    flops, recompute = ssd_flops(batch, length, nheads, headdim, ngroups, dstate, chunk)
+    flops = ssd_flops(batch, length, nheads, headdim, ngroups, dstate, chunk)
     total = sum(flops.values())
     fwd_b, bwd_b = ssd_bytes(batch, length, nheads, headdim, ngroups, dstate)
     per = {k: v[0] / max(v[1], 1) for k, v in kernels.items()}
     mfma = {}
-    for k, f in {**flops, **recompute}.items():
+    for k, f in flops.items():
         if k in per:
             tf = f / (per[k] * 1e-3) / 1e12
             mfma[k] = {"ms": round(per[k], 4), "gflop": round(f / 1e9, 2), "tflops": round(tf, 1),
-                       "frac": round(tf / BF16_PEAK_TFLOPS, 4), "recompute": k in recompute}
+                       "frac": round(tf / BF16_PEAK_TFLOPS, 4)}
     name = max((k for k in per if k in flops), key=lambda k: per[k])
     achieved = flops[name] / (per[name] * 1e-3) / 1e12
     roof = {"bound": "mfma", "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
