@@ -192,6 +192,14 @@ def test_lane_forward_16bit():
     _compare(inputs, dy, True, 2e-2, 2e-2)
 
 
+def test_partial_reductions_whole_batches_and_tail():
+    # One group of 2304 channels: 9 blocks of 256 channels feed each dB/dC value (a batch
+    # of eight partials plus one), and the 256 steps run as 16 chunks of 16, so each
+    # dA/dD/ddelta_bias value sums 16 chunks x 2 batches = 32 partials in whole batches.
+    inputs, dy = _random_problem(2, 2304, 256, 16, 1, seed=23)
+    _compare(inputs, dy, True, 1e-5, 1e-4)
+
+
 def test_deterministic_backward():
     inputs, dy = _random_problem(2, 256, 300, 16, 1, seed=12)
     runs = [_gpu(inputs, dy, True) for _ in range(2)]
