@@ -497,6 +497,80 @@ __global__ void __launch_bounds__(256) chain(Geo g, const float* __restrict__ A,
 }
 
 // FULL: dstate == NS (no padded states), so the saved-state stores need no guards.
+// The same chain with one wavefront per (row, state), for problems of few rows and many
+// chunks, where one thread per pair walking the chunks in turn leaves most of the chip
+// idle. Each lane composes the maps x -> e x + d of a run of consecutive chunks (in walk
+// order), a scan across the wavefront composes the runs before each lane, and each lane
+// walks its run again from that entering value to write the states. The map of the last
+// chunk in walk order is never applied (its summary is not computed), so no run reads it.
+template <bool REV>
+__global__ void __launch_bounds__(256) chain_wave(Geo g, const float* __restrict__ A,
+                                                  const float* __restrict__ drive,
+                                                  const float* __restrict__ sumd, float* __restrict__ out) {
+  const int64_t pair = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int N = static_cast<int>(g.dstate);
+  if (pair >= g.rows * N) return;  // the same for the whole wavefront
+  const int lane = threadIdx.x & 63;
+  const int64_t row = pair / N;
+  const int n = static_cast<int>(pair % N);
+  const float a2 = A[(row % g.dim) * N + n] * kLog2e;
+  const int k = g.nchunks;
+  const int run = (k + kWave - 1) / kWave;
+  const int r0 = min(lane * run, k), r1 = min(r0 + run, k);
+  // the maps of walk positions b0 .. b0 + PB - 1, fetched together (clamped positions:
+  // every load is issued; values past the run are not used)
+  constexpr int PB = 8;
+  float e[PB], d[PB];
+  auto fetch = [&](int b0) {
+#pragma unroll
+    for (int q = 0; q < PB; ++q) {
+      const int r = min(b0 + q, k - 1);
+      const int64_t c = row * k + (REV ? k - 1 - r : r);
+      e[q] = sumd[c];
+      d[q] = drive[c * N + n];
+    }
+#pragma unroll
+    for (int q = 0; q < PB; ++q) e[q] = fast_exp2(a2 * e[q]);
+  };
+  const int rc = min(r1, k - 1);  // the maps this run applies
+  float E = 1.0f, D = 0.0f;
+  for (int b0 = r0; b0 < rc; b0 += PB) {
+    fetch(b0);
+#pragma unroll
+    for (int q = 0; q < PB; ++q) {
+      const bool use = b0 + q < rc;
+      const float eq = use ? e[q] : 1.0f, dq = use ? d[q] : 0.0f;
+      E *= eq;
+      D = fmaf(eq, D, dq);
+    }
+  }
+  // inclusive scan: the maps of lanes below apply first
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const float Ep = __shfl_up(E, off), Dp = __shfl_up(D, off);
+    if (lane >= off) {
+      D = fmaf(E, Dp, D);
+      E *= Ep;
+    }
+  }
+  float x = __shfl_up(D, 1);  // every earlier run applied to the zero entering state
+  if (lane == 0) x = 0.0f;
+  const int per = g.lc / CK;
+  for (int b0 = r0; b0 < r1; b0 += PB) {
+    if (run > PB || b0 != r0) fetch(b0);  // a run of at most PB maps is still held
+#pragma unroll
+    for (int q = 0; q < PB; ++q) {
+      const int r = b0 + q;
+      if (r >= r1) break;
+      if (REV)
+        out[(row * k + (k - 1 - r)) * N + n] = x;
+      else
+        out[ck_index(g, row, static_cast<int64_t>(r) * per, n)] = x;
+      if (r + 1 < k) x = fmaf(e[q], x, d[q]);
+    }
+  }
+}
+
 template <int NS, bool UNI, class TU, bool FULL>
 __global__ void __launch_bounds__(256) fwd_replay(Geo g, Ptrs p) {
   const LaneInfo li = lane_info(g, UNI);
@@ -1413,6 +1487,12 @@ static inline unsigned blocks_for(int64_t n, int per = 256) {
   return static_cast<unsigned>((n + per - 1) / per);
 }
 
+// The wavefront-per-pair chain pays off when a thread per (row, state) would walk many
+// chunks and fill fewer than 1024 workgroups.
+static bool chain_by_wave(const Geo& g) {
+  return g.nchunks > 32 && g.rows * g.dstate < 1024 * 256;
+}
+
 // Rows from which the lane-per-state forward has enough wavefronts (rows / 4 of them) to
 // fill the chip without time chunks.
 constexpr int64_t kLaneRows = 6144;
@@ -1445,7 +1525,11 @@ static int launch_fwd(const Plan& pl, const Ptrs& q, hipStream_t s) {
   if (g.nchunks > 1) {
     MKO_TIMED("selscan_fwd_summary", s, fwd_summary<NS, UNI, TU><<<dim3(gx, g.nchunks - 1), block, 0, s>>>(g, q));
   }
-  MKO_TIMED("selscan_chain", s, chain<false><<<blocks_for(g.rows * g.dstate), 256, 0, s>>>(g, q.A, q.drive, q.sumd, q.states));
+  if (chain_by_wave(g))
+    MKO_TIMED("selscan_chain", s,
+              chain_wave<false><<<blocks_for(g.rows * g.dstate, 4), 256, 0, s>>>(g, q.A, q.drive, q.sumd, q.states));
+  else
+    MKO_TIMED("selscan_chain", s, chain<false><<<blocks_for(g.rows * g.dstate), 256, 0, s>>>(g, q.A, q.drive, q.sumd, q.states));
   if (g.dstate == NS)
     MKO_TIMED("selscan_fwd_replay", s, fwd_replay<NS, UNI, TU, true><<<dim3(gx, g.nchunks), block, 0, s>>>(g, q));
   else
@@ -1467,7 +1551,11 @@ static int launch_bwd(const Plan& pl, const Ptrs& q, const mko_selscan_params* p
   if (g.nchunks > 1) {
     MKO_TIMED("selscan_bwd_summary", s, bwd_summary<NS, UNI, TU><<<dim3(gx, g.nchunks - 1), block, 0, s>>>(g, q));
   }
-  MKO_TIMED("selscan_chain", s, chain<true><<<blocks_for(g.rows * g.dstate), 256, 0, s>>>(g, q.A, q.drive, q.sumd, q.adj));
+  if (chain_by_wave(g))
+    MKO_TIMED("selscan_chain", s,
+              chain_wave<true><<<blocks_for(g.rows * g.dstate, 4), 256, 0, s>>>(g, q.A, q.drive, q.sumd, q.adj));
+  else
+    MKO_TIMED("selscan_chain", s, chain<true><<<blocks_for(g.rows * g.dstate), 256, 0, s>>>(g, q.A, q.drive, q.sumd, q.adj));
   if (!UNI) {
     const int64_t n = bgl * NS * 2;
     MKO_TIMED("selscan_zero", s, zero_f32<<<blocks_for(n), 256, 0, s>>>(q.pbc, n));

@@ -155,6 +155,7 @@ SHAPES = [
     (1, 4, 1, 3, 1, 7),     # single row
     (1, 4, 1, 3, 7, 1),     # single column
     (2, 64, 1, 16, 8, 12),  # a full 64-channel wavefront per group
+    (1, 8, 1, 16, 28, 28),  # 784 steps: 49 chunks, chained by a wavefront per (row, state)
 ]
 
 

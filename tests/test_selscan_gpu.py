@@ -192,6 +192,15 @@ def test_lane_forward_16bit():
     _compare(inputs, dy, True, 2e-2, 2e-2)
 
 
+@pytest.mark.parametrize("shape", [(1, 64, 2000, 16, 1), (2, 24, 1500, 20, 3)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_long_sequences_few_channels(shape):
+    # Few rows and 16-step chunks: 125 (94) chunks, more than 32, so the chunk chains run
+    # a wavefront per (row, state) with the chunks split into runs across its lanes.
+    inputs, dy = _random_problem(*shape, seed=sum(shape))
+    _compare(inputs, dy, True, 1e-5, 1e-4)
+
+
 def test_partial_reductions_whole_batches_and_tail():
     # One group of 2304 channels: 9 blocks of 256 channels feed each dB/dC value (a batch
     # of eight partials plus one), and the 256 steps run as 16 chunks of 16, so each
