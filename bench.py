@@ -134,31 +134,46 @@ def mamba1_case(batch, dim, length, steps, warmup, seed=0):
     }
 
 
-def mamba1_cpu_baseline(batch=1, dim=256, length=2048):
-    """The oracle's per-timestep recurrence in float32 with autograd on the host cores."""
+def host_cpu():
+    """The host's CPU model (lscpu's "Model name"), the cores it reports and the threads torch uses."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "os_cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads()}
+
+
+def mamba1_cpu_baseline(batch, dim, length):
+    """The oracle's per-timestep recurrence in float32 on the host cores, forward only, at
+    the full layer shape.
+
+    The forward+backward with autograd is out of reach on the host: at config 2 it ran past
+    15 minutes on 8 cores, and at config 3 autograd would hold about 16 GB of per-step
+    tensors.  So the baseline is the forward at the full shape, one timed run after a
+    warm-up over a 256-step prefix, against the forward's algorithmic bytes."""
     import oracle
     from cases import mamba1_layer
     torch.set_num_threads(os.cpu_count() or 1)
-    inputs, dout = mamba1_layer(batch, dim, length, seed=0, act=torch.float32)
-    leaves = {k: v.float().requires_grad_(True) for k, v in inputs.items()}
-
-    def run():
-        out = oracle.selective_scan(**leaves, delta_softplus=True, dtype=torch.float32)
-        torch.autograd.grad(out, list(leaves.values()), dout.float())
-
-    run()  # warm-up
-    best = None
-    for _ in range(2):
+    inputs, _ = mamba1_layer(batch, dim, length, seed=0, act=torch.float32)
+    inputs = {k: v.float() for k, v in inputs.items()}
+    prefix = {k: (v[..., :256].contiguous() if k in ("u", "dt", "z", "B", "C") else v) for k, v in inputs.items()}
+    with torch.no_grad():
+        oracle.selective_scan(**prefix, delta_softplus=True, dtype=torch.float32)
         t0 = time.perf_counter()
-        run()
-        dt = time.perf_counter() - t0
-        best = dt if best is None else min(best, dt)
-    fwd_b, bwd_b = mamba1_bytes(batch, dim, length, 16, 1)
-    return {"value": round((fwd_b + bwd_b) / best / 1e9, 6), "unit": "GB/s",
-            "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"Mamba-1 fwd+bwd, batch {batch} x dim {dim} x seqlen {length}, d_state 16, "
-                      f"float32 per-step recurrence with autograd (oracle/ssm.py), best of 2 after "
-                      f"1 warm-up: {best:.2f} s per step"}
+        oracle.selective_scan(**inputs, delta_softplus=True, dtype=torch.float32)
+        sec = time.perf_counter() - t0
+    fwd_b, _ = mamba1_bytes(batch, dim, length, 16, 1)
+    return {"value": round(fwd_b / sec / 1e9, 4), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port", **host_cpu(),
+            "sample": f"Mamba-1 forward only at the full {batch} x {dim} x {length} shape (d_state 16), "
+                      f"float32 per-step recurrence of oracle/ssm.py on the host, one run after a 256-step "
+                      f"warm-up: {sec:.2f} s for {fwd_b / 1e6:.1f} MB of forward algorithmic bytes "
+                      f"(forward+backward with autograd does not fit a bench run on the host)"}
 
 
 # --------------------------------------------------------------------- decode
@@ -202,7 +217,9 @@ def decode_case(steps=1024, warmup=16):
             "kernels_ms": {k: round(v[0] / max(v[1], 1), 4) for k, v in sorted(kernels.items())}}
 
 
-def decode_cpu_baseline(steps=4):
+def decode_cpu_baseline(steps=16):
+    """The oracle's decode step in float32 on the host cores at the config-5 shape, timed
+    over ``steps`` in-place steps after one warm-up step."""
     import oracle
     from cases import decode_problem
     torch.set_num_threads(os.cpu_count() or 1)
@@ -215,9 +232,9 @@ def decode_cpu_baseline(steps=4):
         _, state = oracle.mamba2_state_update(state, **p, dt_softplus=True, dtype=torch.float32)
     per = (time.perf_counter() - t0) / steps
     return {"value": round(2 * state.numel() * 4 / per / 1e9, 4), "unit": "GB/s",
-            "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"decode step at the config-5 shape in float32 (oracle/ssm.py), {steps} steps, "
-                      f"{per * 1e3:.1f} ms per step"}
+            "cores": torch.get_num_threads(), "kind": "port", **host_cpu(),
+            "sample": f"decode step at the config-5 shape in float32 (oracle/ssm.py), {steps} steps after "
+                      f"1 warm-up, {per * 1e3:.1f} ms per step"}
 
 
 # --------------------------------------------------------------------- Mamba-2 SSD
@@ -321,7 +338,7 @@ def ssd_cpu_baseline(batch=4, length=4096):
         dt = time.perf_counter() - t0
         best = dt if best is None else min(best, dt)
     return {"value": round(batch * length / best, 1), "unit": "tokens/s", "cores": torch.get_num_threads(),
-            "kind": "port",
+            "kind": "port", **host_cpu(),
             "sample": f"SSD fwd+bwd, batch {batch} x seqlen {length} at the c4 head shape (H64 P64 N128, chunk 256), "
                       f"bf16 chunked composition with autograd (oracle/ssm.py), best of 2 after 1 warm-up: "
                       f"{best:.2f} s"}
@@ -778,9 +795,12 @@ def main():
         return
     cpu = None
     if not args.skip_cpu:
-        log("cpu baseline (mamba1 sample)")
-        cpu = mamba1_cpu_baseline()
+        log("cpu baseline (mamba1 config 3, forward)")
+        cpu = mamba1_cpu_baseline(4, 5120, 4096)
         log(f"  {cpu['sample']}")
+        if "mamba1_130m_layer_fwd_bwd" in also:
+            log("cpu baseline (mamba1 config 2, forward)")
+            also["mamba1_130m_layer_fwd_bwd"]["cpu_baseline"] = mamba1_cpu_baseline(8, 1536, 2048)
         if "mamba2_decode_state_rmw" in also:
             also["mamba2_decode_state_rmw"]["cpu_baseline"] = decode_cpu_baseline()
         if "mamba2_ssd_chunk_scan_fwd_bwd" in also:

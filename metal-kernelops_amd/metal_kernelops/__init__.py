@@ -1,22 +1,17 @@
 """MI355X (gfx950) SSM scan kernels behind the dbydd/metal-kernelops API.
 
-Same import names as the reference (``src/metal_kernelops/__init__.py:23-43``):
-``from metal_kernelops import selective_scan`` and ``from metal_kernelops.cv
-import mamba2_chunk_scan, mamba2_state_update``.  The compute runs in hand-written
-HIP kernels (``libmko.so``, C ABI in ``include/mko.h``) on a ROCm GPU; importing
-the package loads nothing and launches nothing.
+The import names match the reference's (``src/metal_kernelops/__init__.py:23-43``):
+``from metal_kernelops import selective_scan`` for the Mamba-1 scan, and
+``from metal_kernelops.cv import mamba2_chunk_scan, mamba2_state_update`` for Mamba-2.
+Hand-written HIP kernels (``libmko.so``, C ABI in ``include/mko.h``) do the work on a
+ROCm GPU; importing the package neither loads the library nor launches anything.
 
-The recurrence is the one from mamba_ssm's ``selective_scan_fn``:
-
-    x_t = exp(dt_t * A) * x_{t-1} + dt_t * B_t * u_t
-    y_t = <x_t, C_t>
-
-Layouts:
-    u, dt:  (batch, dim, length)
-    A:      (dim, dstate)          negative reals
-    B, C:   (batch, groups, dstate, length)
-    D:      (dim,)
-    z:      (batch, dim, length)
+The Mamba-1 scan carries, per channel d and state n, the state
+``h[t] = exp(delta[t] A[d, n]) h[t-1] + delta[t] u[t] B[n, t]`` from ``h[-1] = 0`` and
+reads out ``y[t] = sum_n C[n, t] h[t]``.  ``u``, ``delta`` and ``z`` are laid out
+(batch, dim, length); ``A`` is (dim, dstate) with negative entries; ``B`` and ``C``
+are (batch, groups, dstate, length), one row per group of dim / groups channels;
+``D`` is (dim,).
 """
 
 from . import reference

@@ -1,12 +1,12 @@
 """Mamba-2 operators of ``metal_kernelops.cv`` on MI355X (HIP kernels).
 
-Same names as the reference's ``cv/__init__.py:15-40`` for the SSM scan path:
-the chunked SSD scan and the single-token decode update, each with its pure-torch
-reference twin, the four-path 2D scan (VMamba's ss2d) built on the Mamba-1 scan
-kernels, and the causal depthwise conv1d that precedes the scan in a Mamba block.
-The reference's other ``cv`` operators (gated RMSNorm, NSA selection, RoIAlign) are
-not part of this package.
-Importing it registers the ``mko::`` custom ops and launches nothing.
+The names follow the reference's ``cv/__init__.py:15-40`` for the SSM scan path and
+its neighbours in a Mamba block: the chunked SSD scan and the single-token decode
+update (each with its pure-torch twin), the four-path 2D scan (VMamba's ss2d) built
+on the Mamba-1 scan kernels, the causal depthwise conv1d ahead of the scan and the
+gated RMSNorm after it.  The reference's other ``cv`` operators (NSA selection,
+RoIAlign and the rest) are not part of this package.  Importing it registers the
+``mko::`` custom ops and launches nothing.
 """
 
 from .causal_conv1d import causal_conv1d_fn, causal_conv1d_ref, causal_conv1d_update

@@ -39,6 +39,7 @@ import torch.nn.functional as F
 from torch import Tensor
 
 from .. import _native as nat
+from .._contract import Rules
 from ..scan import _require_gpu
 
 __all__ = ["causal_conv1d_fn", "causal_conv1d_ref", "causal_conv1d_update"]
@@ -49,32 +50,41 @@ _SILU = 1
 _MAX_WIDTH = 32
 
 
-def _as_depthwise(weight):
-    """``(channels, 1, K)`` (nn.Conv1d with groups == channels) or ``(channels, K)`` -> ``(channels, K)``."""
+def _as_depthwise(weight, op="causal_conv1d"):
+    """The taps as a (channels, K) matrix.
+
+    Accepts the (channels, K) matrix itself or the (channels, 1, K) weight of an
+    ``nn.Conv1d`` with ``groups == channels``; K must be at least 1."""
+    rules = Rules(op)
     if weight.dim() == 3:
-        if weight.shape[1] != 1:
-            raise ValueError(f"weight must be (channels, 1, K) for a depthwise convolution, got {tuple(weight.shape)}")
-        weight = weight[:, 0, :]
-    elif weight.dim() != 2:
-        raise ValueError(f"weight must be (channels, 1, K) or (channels, K), got {tuple(weight.shape)}")
-    if weight.shape[1] < 1:
-        raise ValueError("the kernel width must be at least 1")
+        rules.require(weight.shape[1] == 1, "a 3-d weight must be the depthwise (channels, 1, K) layout; "
+                                            f"its shape is {tuple(weight.shape)}")
+        weight = weight.squeeze(1)
+    rules.require(weight.dim() == 2, "weight should be (channels, K) or (channels, 1, K); "
+                                     f"its shape is {tuple(weight.shape)}")
+    rules.require(weight.shape[1] >= 1, "weight has no taps (K = 0)")
     return weight
 
 
-def _check_activation(activation):
+def _check_activation(activation, op="causal_conv1d"):
+    """Only no activation, "silu" or its alias "swish" are implemented."""
     if activation not in _ACTIVATIONS:
-        raise NotImplementedError(f"activation must be one of {_ACTIVATIONS}, got {activation!r}")
+        Rules(op).fail(f"activation {activation!r} is not implemented; use one of {_ACTIVATIONS}",
+                       NotImplementedError)
 
 
 def _final_state(z_input, initial_state, taps):
-    """The last ``taps`` columns of ``cat(initial_state or zeros, x)``, differentiable."""
+    """The state leaving the sequence: the last ``taps`` columns of the concatenation
+    ``[initial_state or zeros, z_input]`` along time, kept in the autograd graph."""
     length = z_input.shape[-1]
-    if length >= taps:
-        return z_input[..., length - taps:].contiguous()
-    head = (initial_state[..., length:] if initial_state is not None
-            else z_input.new_zeros(z_input.shape[:-1] + (taps - length,)))
-    return torch.cat([head, z_input], dim=-1)
+    short = taps - length  # columns that must come from before the sequence
+    if short <= 0:
+        return z_input[..., -taps:].contiguous() if taps else z_input[..., length:].contiguous()
+    if initial_state is None:
+        before = z_input.new_zeros(*z_input.shape[:-1], short)
+    else:
+        before = initial_state[..., initial_state.shape[-1] - short:]
+    return torch.cat([before, z_input], dim=-1)
 
 
 # --------------------------------------------------------------------------- kernels

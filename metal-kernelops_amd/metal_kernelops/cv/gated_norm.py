@@ -38,6 +38,7 @@ import torch
 from torch.autograd.function import once_differentiable
 
 from .. import _native as nat
+from .._contract import Rules
 from ..scan import _require_gpu
 
 __all__ = ["rmsnorm_gated", "rmsnorm_gated_reference"]
@@ -116,18 +117,16 @@ class _GatedRMSNorm(torch.autograd.Function):
 
 
 def _checked_group(x, weight, bias, z, group_size):
-    """The reference's argument checks on a non-empty feature axis (``cv/gated_norm.py:674-684``);
-    returns the group width."""
+    """Width of the normalisation groups after the reference's argument rules
+    (``cv/gated_norm.py:674-684``, same order), for a non-empty feature axis."""
+    rules = Rules("rmsnorm_gated")
     features = x.shape[-1]
-    group = features if group_size is None else int(group_size)
-    if group <= 0 or features % group:
-        raise ValueError(f"group_size {group} does not divide {features}")
-    if tuple(weight.shape) != (features,):
-        raise ValueError(f"weight must be ({features},), got {tuple(weight.shape)}")
-    if bias is not None and tuple(bias.shape) != (features,):
-        raise ValueError(f"bias must be ({features},), got {tuple(bias.shape)}")
-    if z is not None and z.shape != x.shape:
-        raise ValueError(f"z must match x {tuple(x.shape)}, got {tuple(z.shape)}")
+    group = int(group_size) if group_size is not None else features
+    rules.require(group > 0 and features % group == 0,
+                  f"{features} features do not split into whole groups of {group}")
+    rules.shape("weight", weight, (features,))
+    rules.shape("bias", bias, (features,))
+    rules.shape("z", z, tuple(x.shape))
     return group
 
 

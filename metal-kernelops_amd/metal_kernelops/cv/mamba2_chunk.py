@@ -36,6 +36,7 @@ import torch
 from torch import Tensor
 
 from .. import _native as nat
+from .._contract import Rules
 
 __all__ = ["mamba2_chunk_scan", "mamba2_chunk_scan_reference", "last_path"]
 
@@ -51,50 +52,50 @@ def last_path():
     return _path
 
 
+def _initial_layout(rules, states, batch, nheads, headdim, dstate):
+    """``initial_states`` in the (batch, nheads, headdim, dstate) layout the kernels read.
+
+    Besides that layout the reference accepts a 5-D tensor with a unit second axis and,
+    when headdim and dstate differ, the (batch, nheads, dstate, headdim) transpose."""
+    want = (batch, nheads, headdim, dstate)
+    if states.dim() == 5 and states.shape[1] == 1:
+        states = states.squeeze(1)
+    if tuple(states.shape) == want:
+        return states
+    if headdim != dstate and tuple(states.shape) == (batch, nheads, dstate, headdim):
+        return states.transpose(-1, -2)
+    rules.fail(f"initial_states should be (batch, nheads, headdim, dstate) = {want}; "
+               f"its shape is {tuple(states.shape)}")
+
+
 def _check(x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size):
-    """Validation of ``cv/mamba2_chunk.py:398-444``; raises ``ValueError``."""
-    if chunk_size < 1:
-        raise ValueError(f"chunk_size must be positive, got {chunk_size}")
-    if x.dim() != 4:
-        raise ValueError(f"x must be (batch, length, nheads, d_head), got {tuple(x.shape)}")
+    """The reference's argument rules (``cv/mamba2_chunk.py:398-444``), in its order.
+
+    Returns the sizes and ``initial_states`` in the kernels' layout.  float64 ``x``, which
+    the reference's torch composition takes, is refused here: the kernels compute in
+    float32 with float32 or 16-bit operands."""
+    rules = Rules("mamba2_chunk_scan")
+    rules.require(chunk_size >= 1, f"chunk_size must be at least 1 (got {chunk_size})")
+    rules.dims("x", x, 4, "(batch, length, nheads, headdim)")
     batch, length, nheads, headdim = x.shape
-    if tuple(dt.shape) != (batch, length, nheads):
-        raise ValueError(f"dt must be {(batch, length, nheads)}, got {tuple(dt.shape)}")
-    if tuple(A.shape) != (nheads,):
-        raise ValueError(f"A must be ({nheads},), got {tuple(A.shape)}")
-    if B.dim() != 4 or tuple(C.shape) != tuple(B.shape):
-        raise ValueError("B and C must both be (batch, length, ngroups, d_state), got "
-                         f"{tuple(B.shape)} and {tuple(C.shape)}")
-    if tuple(B.shape[:2]) != (batch, length):
-        raise ValueError(f"B/C must start with {(batch, length)}, got {tuple(B.shape)}")
+    rules.shape("dt", dt, (batch, length, nheads))
+    rules.shape("A", A, (nheads,))
+    rules.require(B.dim() == 4 and tuple(C.shape) == tuple(B.shape),
+                  f"B and C should share one (batch, length, ngroups, dstate) shape; "
+                  f"they are {tuple(B.shape)} and {tuple(C.shape)}")
+    rules.require(tuple(B.shape[:2]) == (batch, length),
+                  f"B and C should lead with (batch, length) = {(batch, length)}; they are {tuple(B.shape)}")
     ngroups, dstate = B.shape[2], B.shape[3]
-    if ngroups < 1 or nheads % ngroups:
-        raise ValueError(f"nheads={nheads} must be a multiple of ngroups={ngroups}")
-    if z is not None and tuple(z.shape) != tuple(x.shape):
-        raise ValueError(f"z must be {tuple(x.shape)}, got {tuple(z.shape)}")
-    if D is not None and tuple(D.shape) not in ((nheads,), (nheads, headdim)):
-        raise ValueError(f"D must be ({nheads},) or ({nheads}, {headdim}), got {tuple(D.shape)}")
-    if dt_bias is not None and tuple(dt_bias.shape) != (nheads,):
-        raise ValueError(f"dt_bias must be ({nheads},), got {tuple(dt_bias.shape)}")
+    rules.require(ngroups >= 1 and nheads % ngroups == 0,
+                  f"{nheads} heads do not split evenly into {ngroups} groups")
+    rules.shape("z", z, tuple(x.shape))
+    rules.shape("D", D, (nheads,), (nheads, headdim))
+    rules.shape("dt_bias", dt_bias, (nheads,))
     if initial_states is not None:
-        if initial_states.dim() == 5 and initial_states.shape[1] == 1:
-            initial_states = initial_states[:, 0]
-        if tuple(initial_states.shape) != (batch, nheads, headdim, dstate):
-            if tuple(initial_states.shape) == (batch, nheads, dstate, headdim) and headdim != dstate:
-                initial_states = initial_states.transpose(-1, -2)
-            else:
-                raise ValueError(
-                    "initial_states must be (batch, nheads, d_head, d_state) = "
-                    f"{(batch, nheads, headdim, dstate)}, got {tuple(initial_states.shape)}")
-    if x.dtype not in _FLOATS:
-        raise ValueError(f"x must be float32, float16 or bfloat16 on the GPU path, got {x.dtype}")
-    for name, tensor in (("dt", dt), ("A", A), ("B", B), ("C", C)):
-        if tensor.device != x.device:
-            raise ValueError(f"{name} is on {tensor.device}, x is on {x.device}")
-    for name, tensor in (("dt", dt), ("B", B), ("C", C), ("z", z), ("D", D), ("dt_bias", dt_bias),
-                         ("initial_states", initial_states), ("A", A)):
-        if tensor is not None and tensor.dtype not in _FLOATS:
-            raise ValueError(f"{name} must be float32, float16 or bfloat16, got {tensor.dtype}")
+        initial_states = _initial_layout(rules, initial_states, batch, nheads, headdim, dstate)
+    rules.dtype_in(_FLOATS, x=x)
+    rules.same_device(x.device, dt=dt, A=A, B=B, C=C)
+    rules.dtype_in(_FLOATS, dt=dt, B=B, C=C, z=z, D=D, dt_bias=dt_bias, initial_states=initial_states, A=A)
     return batch, length, nheads, headdim, ngroups, dstate, initial_states
 
 
@@ -199,24 +200,34 @@ def _f32(t):
 
 def mamba2_chunk_scan(x, dt, A, B, C, chunk_size=64, D=None, z=None, dt_bias=None,
                       dt_softplus=False, initial_states=None):
-    """Mamba-2 chunked SSD scan on the ROCm GPU.
+    """Mamba-2 SSD over a whole sequence on the ROCm GPU; returns ``(y, final_state)``.
 
-    Args:
-        x: ``(batch, length, nheads, d_head)``, float32/float16/bfloat16.
-        dt: ``(batch, length, nheads)`` pre-activation time steps.
-        A: ``(nheads,)`` negative state decay.
-        B, C: ``(batch, length, ngroups, d_state)``; ``ngroups`` divides ``nheads``
-            and the heads of a group share both.
-        chunk_size: accepted for signature parity; the result does not depend on it.
-        D: ``(nheads,)`` or ``(nheads, d_head)`` skip connection.
-        z: ``(batch, length, nheads, d_head)`` gate, applied as ``y * silu(z)``.
-        dt_bias: ``(nheads,)`` added to ``dt`` before the softplus.
-        dt_softplus: apply ``softplus`` to ``dt + dt_bias``.
-        initial_states: ``(batch, nheads, d_head, d_state)``.
+    The recurrence runs per head over ``length`` tokens; the heads of one group read
+    the same ``B`` and ``C``.  Shapes (b = batch, L = length, H = nheads, P = headdim,
+    G = ngroups dividing H, N = dstate):
 
-    Returns:
-        ``(y, final_state)``: ``y`` is ``(batch, length, nheads, d_head)`` and
-        ``final_state`` is ``(batch, nheads, d_head, d_state)``, both in ``x.dtype``.
+    ========================  ==============================  ==============================
+    argument                  shape                           meaning
+    ========================  ==============================  ==============================
+    ``x``                     (b, L, H, P)                    input; its dtype (float32,
+                                                              float16, bfloat16) is the
+                                                              operand and output dtype
+    ``dt``                    (b, L, H)                       step sizes before the optional
+                                                              bias and softplus
+    ``A``                     (H,)                            per-head log decay (negative)
+    ``B``, ``C``              (b, L, G, N)                    input and output projections
+    ``chunk_size``            int >= 1                        kept for the reference's
+                                                              signature; the kernels pick
+                                                              their own chunk, and the result
+                                                              does not depend on it
+    ``D``                     (H,) or (H, P), optional        skip weight on ``x``
+    ``z``                     (b, L, H, P), optional          gate: ``y * silu(z)``
+    ``dt_bias``               (H,), optional                  added to ``dt``
+    ``dt_softplus``           bool                            softplus on ``dt + dt_bias``
+    ``initial_states``        (b, H, P, N), optional          state before the first token
+    ========================  ==============================  ==============================
+
+    ``y`` is (b, L, H, P) and ``final_state`` (b, H, P, N), both in ``x.dtype``.
     """
     global _path
     if x.device.type != "cuda" or torch.version.hip is None:

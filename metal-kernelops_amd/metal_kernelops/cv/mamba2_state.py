@@ -32,6 +32,7 @@ import torch
 from torch import Tensor
 
 from .. import _native as nat
+from .._contract import Rules
 
 CHECKED_TORCH = "2.10.0"
 """Torch release this module was written and measured against (ROCm build)."""
@@ -41,51 +42,42 @@ _SOFTPLUS, _DT_PER_ROW, _D_PER_ROW = 1, 2, 4
 
 
 def _check(state, x, dt, A, B, C, D, z, dt_bias, out_state):
-    """Shape contract of ``cv/mamba2_state.py:565-598``; raises ``ValueError``."""
-    if state.dim() != 4:
-        raise ValueError(f"state must be (batch, nheads, dim, dstate), got {tuple(state.shape)}")
+    """The reference's argument rules (``cv/mamba2_state.py:565-598``) in its order, plus
+    this build's limits (3-D B/C, dstate <= 1024, one device, floating inputs) at the
+    points where they first apply."""
+    rules = Rules("mamba2_state_update")
+    rules.dims("state", state, 4, "(batch, nheads, headdim, dstate)")
     batch, nheads, dim, dstate = state.shape
-    if dstate < 1:
-        raise ValueError("state must have a non-empty last dimension")
-    expected = (batch, nheads, dim)
-    for name, tensor in (("x", x), ("z", z)):
-        if tensor is not None and tuple(tensor.shape) != expected:
-            raise ValueError(f"{name} must be {expected}, got {tuple(tensor.shape)}")
-    if tuple(dt.shape) not in ((batch, nheads), expected):
-        raise ValueError(f"dt must be {(batch, nheads)} or {expected}, got {tuple(dt.shape)}")
-    if tuple(A.shape) != (nheads,):
-        raise ValueError(f"A must be {(nheads,)}, got {tuple(A.shape)}")
-    if B.dim() != 3:
-        raise ValueError(f"B and C must be (batch, ngroups, dstate), got {tuple(B.shape)}")
+    rules.require(dstate >= 1, "state has an empty dstate axis")
+    rows = (batch, nheads, dim)
+    rules.shape("x", x, rows)
+    rules.shape("z", z, rows)
+    rules.shape("dt", dt, (batch, nheads), rows)
+    rules.shape("A", A, (nheads,))
+    rules.dims("B", B, 3, "(batch, ngroups, dstate)")
     groups = B.shape[1]
-    if tuple(B.shape) != (batch, groups, dstate) or tuple(C.shape) != tuple(B.shape):
-        raise ValueError(
-            f"B and C must be {(batch, groups, dstate)}, got {tuple(B.shape)}, {tuple(C.shape)}")
-    if groups < 1 or nheads % groups:
-        raise ValueError(f"nheads ({nheads}) must be divisible by ngroups ({groups})")
-    if D is not None and tuple(D.shape) not in ((nheads,), (nheads, dim)):
-        raise ValueError(f"D must be {(nheads,)} or {(nheads, dim)}, got {tuple(D.shape)}")
-    if dt_bias is not None and tuple(dt_bias.shape) != (nheads,):
-        raise ValueError(f"dt_bias must be {(nheads,)}, got {tuple(dt_bias.shape)}")
-    if dstate > 1024:
-        raise ValueError(f"dstate must be at most 1024, got {dstate}")
+    rules.require(tuple(B.shape) == (batch, groups, dstate) and tuple(C.shape) == tuple(B.shape),
+                  f"B and C should both be (batch, ngroups, dstate) = {(batch, groups, dstate)}; "
+                  f"they are {tuple(B.shape)} and {tuple(C.shape)}")
+    rules.require(groups >= 1 and nheads % groups == 0,
+                  f"{nheads} heads do not split evenly into {groups} groups")
+    rules.shape("D", D, (nheads,), (nheads, dim))
+    rules.shape("dt_bias", dt_bias, (nheads,))
+    rules.require(dstate <= 1024, f"dstate is at most 1024 here (got {dstate})")
     for name, tensor in (("x", x), ("dt", dt), ("A", A), ("B", B), ("C", C), ("D", D), ("z", z),
                          ("dt_bias", dt_bias)):
         if tensor is None:
             continue
-        if tensor.device != state.device:
-            raise ValueError(f"{name} is on {tensor.device}, state is on {state.device}")
-        if not tensor.is_floating_point():
-            raise ValueError(f"{name} must be a floating tensor, got {tensor.dtype}")
+        rules.same_device(state.device, **{name: tensor})
+        rules.require(tensor.is_floating_point(), f"{name} should be a floating tensor; it is {tensor.dtype}")
     if out_state is not None:
-        if out_state.device != state.device:
-            raise ValueError("out_state must be on the same device as state")
-        if tuple(out_state.shape) != tuple(state.shape) or out_state.dtype != state.dtype:
-            raise ValueError("out_state must match state in shape and dtype")
-        if not out_state.is_contiguous():
-            raise ValueError("out_state must be contiguous")
-        if out_state.requires_grad:
-            raise ValueError("out_state is written in place and cannot require grad")
+        rules.require(out_state.device == state.device,
+                      f"out_state lives on {out_state.device}, state on {state.device}")
+        rules.require(tuple(out_state.shape) == tuple(state.shape) and out_state.dtype == state.dtype,
+                      "out_state should have the shape and dtype of state")
+        rules.require(out_state.is_contiguous(), "out_state should be contiguous")
+        rules.require(not out_state.requires_grad,
+                      "out_state is overwritten in place, so it may not require grad")
 
 
 def _as_kernel_dtype(t, state_dtype):
@@ -214,26 +206,23 @@ class _StateUpdate(torch.autograd.Function):
 
 def mamba2_state_update(state, x, dt, A, B, C, D=None, z=None, dt_bias=None,
                         dt_softplus=False, out_state=None):
-    """One Mamba-2 selective state update step on the ROCm GPU.
+    """Advance a Mamba-2 decode state by one token on the ROCm GPU; returns ``(y, new_state)``.
 
-    Args:
-        state: ``(batch, nheads, dim, dstate)`` float32/float16/bfloat16, not modified
-            (unless it is also ``out_state``).
-        x: ``(batch, nheads, dim)``.
-        dt: ``(batch, nheads)`` or ``(batch, nheads, dim)``.
-        A: ``(nheads,)`` per-head log decay, normally ``-exp(A_log)``.
-        B, C: ``(batch, ngroups, dstate)``; head ``h`` reads group ``h // (nheads // ngroups)``.
-        D: ``(nheads,)`` or ``(nheads, dim)`` skip connection.
-        z: ``(batch, nheads, dim)`` gate, applied as ``y * silu(z)``.
-        dt_bias: ``(nheads,)`` added to ``dt`` before the optional softplus.
-        dt_softplus: apply softplus to ``dt + dt_bias`` (torch's threshold-20 rule).
-        out_state: optional destination for the new state, written in place (it may
-            be ``state`` itself).  It must not require grad.
+    Per head ``h`` (group ``g = h // (nheads // ngroups)``) and row ``p``:
+    ``delta = softplus(dt + dt_bias)`` (the bias and softplus optional),
+    ``new_state = exp(A[h] * delta) * state + delta * x * B[g]`` and
+    ``y = <new_state, C[g]> + D * x``, times ``silu(z)`` when ``z`` is given.
 
-    Returns:
-        ``(y, updated_state)``; ``y`` is ``(batch, nheads, dim)`` in ``state.dtype``.
-        Without ``out_state`` the input ``state`` is untouched and ``updated_state``
-        is a fresh tensor; with it, ``updated_state`` shares storage with ``out_state``.
+    Shapes (b = batch, H = nheads, P = headdim, N = dstate, G = ngroups):
+    ``state`` (b, H, P, N) in float32, float16 or bfloat16, which fixes the compute and
+    output dtype; ``x`` and ``z`` (b, H, P); ``dt`` (b, H), shared by a head's rows, or
+    (b, H, P); ``A`` and ``dt_bias`` (H,); ``B`` and ``C`` (b, G, N); ``D`` (H,) or (H, P).
+
+    ``state`` is read, never written, unless it is passed again as ``out_state``.  With
+    ``out_state`` (contiguous, the state's shape and dtype, not requiring grad) the new
+    state is written there and returned as that tensor, outside the autograd graph; the
+    state may be its own destination, the in-place form a decode loop uses.  Without it,
+    ``new_state`` is a fresh tensor.  ``y`` is (b, H, P) in the state's dtype.
     """
     if state.device.type != "cuda" or torch.version.hip is None:
         raise ValueError("mamba2_state_update runs on a ROCm GPU (torch device 'cuda')")
@@ -245,6 +234,10 @@ def mamba2_state_update(state, x, dt, A, B, C, D=None, z=None, dt_bias=None,
     kx, kdt, kB, kC, kz = (_as_kernel_dtype(t, dtype) for t in (x, dt, B, C, z))
     if kB.dtype != kC.dtype:
         kB, kC = kB.to(dtype).contiguous(), kC.to(dtype).contiguous()
+    if kz is not None and kz.dtype != kx.dtype:
+        # the kernel reads z in x's element type: meet in the state dtype, which with a
+        # float32 state widens both exactly (what the reference's cast to state.dtype does)
+        kx, kz = kx.to(dtype).contiguous(), kz.to(dtype).contiguous()
     kA, kD, kbias = _f32(A), _f32(D), _f32(dt_bias)
 
     needs_grad = torch.is_grad_enabled() and any(

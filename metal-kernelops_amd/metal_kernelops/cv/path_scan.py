@@ -36,6 +36,7 @@ import torch
 from torch import Tensor
 
 from .. import _native as nat
+from .._contract import Rules
 from ..scan import _require_gpu, selscan_bwd_impl, selscan_fwd_impl
 
 __all__ = ["MAX_STATES", "MERGE_MODES", "path_orders", "ss2d_scan", "ss2d_scan_reference"]
@@ -51,57 +52,44 @@ _FLOATS = (torch.float32, torch.float16, torch.bfloat16)
 
 def _check_merge(merge):
     if merge not in MERGE_MODES:
-        raise ValueError(f"merge must be one of {MERGE_MODES}, got {merge!r}")
+        Rules("ss2d_scan").fail(f"merge={merge!r} is not one of {MERGE_MODES}")
 
 
 def _shape_contract(u, dt, A, B, C, where):
-    """Validate the shared shape contract (``cv/path_scan.py:116-150``); returns the sizes."""
-    if u.dim() != 4:
-        raise ValueError(f"{where}: u must be (batch, channels, height, width), got {tuple(u.shape)}")
+    """The shape rules every 2D-scan entry shares (``cv/path_scan.py:116-150``, same
+    order); returns (batch, channels, groups, states, height, width)."""
+    rules = Rules(where)
+    rules.dims("u", u, 4, "(batch, channels, height, width)")
     batch, channels, height, width = u.shape
-    if dt.shape != u.shape:
-        raise ValueError(f"{where}: dt {tuple(dt.shape)} != u {tuple(u.shape)}")
-    if A.dim() != 2:
-        raise ValueError(f"{where}: A must be (channels, states), got {tuple(A.shape)}")
-    if A.shape[0] != channels:
-        raise ValueError(f"{where}: A has {A.shape[0]} rows for {channels} channels")
-    if B.dim() != 5:
-        raise ValueError(f"{where}: B must be (batch, groups, states, height, width), got {tuple(B.shape)}")
-    if C.shape != B.shape:
-        raise ValueError(f"{where}: C {tuple(C.shape)} != B {tuple(B.shape)}")
-    if B.shape[0] != batch:
-        raise ValueError(f"{where}: B batch {B.shape[0]} != u batch {batch}")
-    if B.shape[2] != A.shape[1]:
-        raise ValueError(f"{where}: B has {B.shape[2]} states, A has {A.shape[1]}")
-    if tuple(B.shape[3:]) != (height, width):
-        raise ValueError(f"{where}: B spatial {tuple(B.shape[3:])} != {(height, width)}")
-    groups = B.shape[1]
-    if channels and groups < 1:
-        raise ValueError(f"{where}: {channels} channels need at least one group")
-    if groups and channels % groups:
-        raise ValueError(f"{where}: {channels} channels do not divide into {groups} groups; "
-                         f"a channel would map to no group")
-    return batch, channels, groups, A.shape[1], height, width
+    rules.shape("dt", dt, tuple(u.shape))
+    rules.dims("A", A, 2, "(channels, states)")
+    rules.require(A.shape[0] == channels, f"A has {A.shape[0]} rows; u has {channels} channels")
+    rules.dims("B", B, 5, "(batch, groups, states, height, width)")
+    rules.shape("C", C, tuple(B.shape))
+    groups, states = B.shape[1], A.shape[1]
+    rules.require(B.shape[0] == batch, f"B holds {B.shape[0]} images; u holds {batch}")
+    rules.require(B.shape[2] == states, f"B carries {B.shape[2]} states per group; A carries {states}")
+    rules.require(tuple(B.shape[3:]) == (height, width),
+                  f"B covers a {tuple(B.shape[3:])} map; u covers {(height, width)}")
+    rules.require(not channels or groups >= 1, f"{channels} channels but no group to read B and C from")
+    rules.require(not groups or channels % groups == 0,
+                  f"{channels} channels do not divide evenly into {groups} groups")
+    return batch, channels, groups, states, height, width
 
 
 def path_orders(height, width, device=None):
-    """Spatial index order of each of the four scan paths, as a list of tensors.
-
-    Entry ``p[i]`` of path ``k`` is the flat ``h * width + w`` index of the pixel at
-    step ``i``; paths 2 and 3 are the reverses of paths 0 and 1 (``:153-162``).
-    """
-    row_major = torch.arange(height * width, device=device).reshape(height, width)
-    flat = row_major.reshape(-1)
-    column_major = row_major.transpose(0, 1).reshape(-1)
-    return [flat, column_major, flat.flip(0), column_major.flip(0)]
+    """For each of the four paths, the pixel (flat index ``h * width + w``) it visits at
+    every step: row-major, down each column, and those two reversed."""
+    step = torch.arange(height * width, device=device)
+    down_columns = (step % height) * width + step // height
+    return [step, down_columns, step.flip(0), down_columns.flip(0)]
 
 
 def _zero_result(shape, tensors):
-    """A zero result that still carries the gradient graph of ``tensors`` (``:191-197``)."""
-    zero = tensors[0].sum() * 0
-    for tensor in tensors[1:]:
-        zero = zero + tensor.sum() * 0
-    return tensors[0].new_zeros(shape) + zero
+    """Zeros of ``shape`` that depend on every tensor in ``tensors`` (each times zero), so
+    a backward through an empty problem still reaches them (``cv/path_scan.py:191-197``)."""
+    tie = sum(t.sum() for t in tensors) * 0
+    return tensors[0].new_zeros(shape) + tie
 
 
 # --------------------------------------------------------------------------- layout ops

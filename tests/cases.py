@@ -7,6 +7,9 @@ cast; ``dt_bias = log(expm1(U(1e-3, 1e-1)))``.
 
 from __future__ import annotations
 
+import json
+import os
+
 import torch
 
 
@@ -100,3 +103,22 @@ def norm_rel(actual, expected):
     actual = actual.detach().double().cpu()
     expected = expected.detach().double().cpu()
     return (actual - expected).norm().item() / max(expected.norm().item(), 1e-30)
+
+
+# Parity bars of the hot path: max relative error of outputs, and norm-relative error of
+# gradients, by the dtype of the tensor compared (float16 follows the reference verifiers'
+# 2e-3, benchmarks/verify_mamba2_chunk.py:62-64).
+OUT_TOL = {torch.float32: 1e-5, torch.float16: 2e-3, torch.bfloat16: 2e-2}
+GRAD_TOL = {torch.float32: 1e-4, torch.float16: 2e-3, torch.bfloat16: 2e-2}
+
+
+def record(case, quantity, err, tol):
+    """Print one measured parity error and return it; with MKO_PARITY_LOG set, also append
+    it to that file as one JSON line, so a run leaves a table of every error it asserted."""
+    print(f"[parity] {case} {quantity}: {err:.3e} (bar {tol:g})", flush=True)
+    path = os.environ.get("MKO_PARITY_LOG")
+    if path:
+        with open(path, "a") as f:
+            f.write(json.dumps({"case": case, "quantity": quantity, "err": float(err),
+                                "bar": float(tol)}) + "\n")
+    return err

@@ -1,8 +1,11 @@
 """Mamba-1 selective scan: HIP kernels against the float64 CPU oracle.
 
-Tolerances (north star): fp32 outputs <= 1e-5 max relative error (max abs error
-over the largest reference magnitude), bf16 outputs <= 2e-2, gradient norms
-<= 1e-4 relative (fp32), 2e-2 for bf16 inputs.
+Bars, by the dtype of the tensor compared (north star): outputs fp32 <= 1e-5 max
+relative error (max abs error over the largest reference magnitude), bf16 <= 2e-2,
+fp16 <= 2e-3; gradient norms fp32 <= 1e-4 relative, bf16 2e-2, fp16 2e-3.  The
+kernels widen 16-bit inputs exactly and compute in float32, so a float32 gradient
+(of delta, A, D, delta_bias) is held to 1e-4 also when the activations are 16-bit.
+Every measured error is printed (and logged to $MKO_PARITY_LOG when set).
 """
 
 import os
@@ -12,7 +15,7 @@ import pytest
 import torch
 
 import oracle
-from cases import mamba1_c1, mamba1_layer, max_rel, norm_rel
+from cases import GRAD_TOL, OUT_TOL, mamba1_c1, mamba1_layer, max_rel, norm_rel, record
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -40,23 +43,26 @@ def _ref(inputs, dy, softplus=True):
     return out.detach(), {k: (None if v is None else v.grad) for k, v in leaves.items()}
 
 
-def _compare(inputs, dy, softplus, out_tol, grad_tol):
+def _compare(inputs, dy, softplus, case):
+    """Forward and every gradient against the oracle, each at the bar of its own dtype."""
     out, grads = _gpu(inputs, dy, softplus)
     ref, rgrads = _ref(inputs, dy, softplus)
     assert out.dtype == inputs["u"].dtype
-    err = max_rel(out, ref)
-    assert err <= out_tol, f"forward max rel {err:.3e}"
+    tol = OUT_TOL[out.dtype]
+    err = record(case, "out", max_rel(out, ref), tol)
+    assert err <= tol, f"forward max rel {err:.3e}"
     for name in NAMES:
         if inputs.get(name) is None:
             continue
         assert grads[name] is not None and grads[name].dtype == inputs[name].dtype, name
-        e = norm_rel(grads[name], rgrads[name])
-        assert e <= grad_tol, f"grad {name}: norm rel {e:.3e}"
+        tol = GRAD_TOL[grads[name].dtype]
+        e = record(case, "d" + name, norm_rel(grads[name], rgrads[name]), tol)
+        assert e <= tol, f"grad {name}: norm rel {e:.3e}"
 
 
 def test_config1_fp32_forward_backward():
     inputs, dy = mamba1_c1()
-    _compare(inputs, dy, True, 1e-5, 1e-4)
+    _compare(inputs, dy, True, "c1")
 
 
 def test_config1_matches_golden_fixture():
@@ -99,7 +105,7 @@ SHAPES = [
 @pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
 def test_shapes_fp32(shape):
     inputs, dy = _random_problem(*shape, seed=sum(shape))
-    _compare(inputs, dy, True, 1e-5, 1e-4)
+    _compare(inputs, dy, True, "x".join(map(str, shape)))
 
 
 @pytest.mark.parametrize("opts", [dict(d=False), dict(z=False), dict(bias=False),
@@ -112,20 +118,20 @@ def test_options(opts, softplus):
         inputs["dt"] = torch.rand(inputs["dt"].shape) * 0.3
         if inputs["delta_bias"] is not None:
             inputs["delta_bias"] = inputs["delta_bias"].abs() * 0.1
-    _compare(inputs, dy, softplus, 1e-5, 1e-4)
+    _compare(inputs, dy, softplus, f"options {opts} softplus={softplus}")
 
 
 def test_bf16_activations():
     inputs, dy = _random_problem(2, 256, 512, 16, 1, seed=9, act=torch.bfloat16)
-    _compare(inputs, dy, True, 2e-2, 2e-2)
+    _compare(inputs, dy, True, "2x256x512 bf16")
 
 
 def test_bf16_delta_and_fp16():
     inputs, dy = _random_problem(1, 128, 200, 16, 1, seed=10, act=torch.float16)
-    _compare(inputs, dy, True, 2e-3 * 10, 2e-2)
+    _compare(inputs, dy, True, "1x128x200 fp16")
     inputs, dy = _random_problem(1, 128, 200, 16, 1, seed=11, act=torch.bfloat16)
     inputs["dt"] = inputs["dt"].bfloat16()
-    _compare(inputs, dy, True, 2e-2, 2e-2)
+    _compare(inputs, dy, True, "1x128x200 bf16 with bf16 delta")
 
 
 # At 6144 channels (batch x dim) and more, dstate <= 16 and whole 16-step blocks, the forward
@@ -156,7 +162,7 @@ def _forward_kernels(inputs, softplus):
 def test_lane_forward_shapes_fp32(shape):
     inputs, dy = _random_problem(*shape, seed=sum(shape))
     assert "selscan_fwd_lane" in _forward_kernels(inputs, True)
-    _compare(inputs, dy, True, 1e-5, 1e-4)
+    _compare(inputs, dy, True, "lane " + "x".join(map(str, shape)))
 
 
 def test_unaligned_groups_take_the_chunked_forward():
@@ -165,7 +171,7 @@ def test_unaligned_groups_take_the_chunked_forward():
     inputs, dy = _random_problem(1, 6200, 32, 16, 4, seed=6252)
     kernels = _forward_kernels(inputs, True)
     assert "selscan_fwd_lane" not in kernels and "selscan_fwd_replay" in kernels
-    _compare(inputs, dy, True, 1e-5, 1e-4)
+    _compare(inputs, dy, True, "1x6200x32 G4")
 
 
 @pytest.mark.parametrize("opts", [dict(d=False), dict(z=False), dict(bias=False),
@@ -178,18 +184,18 @@ def test_lane_forward_options(opts, softplus):
         inputs["dt"] = torch.rand(inputs["dt"].shape) * 0.3
         if inputs["delta_bias"] is not None:
             inputs["delta_bias"] = inputs["delta_bias"].abs() * 0.1
-    _compare(inputs, dy, softplus, 1e-5, 1e-4)
+    _compare(inputs, dy, softplus, f"lane options {opts} softplus={softplus}")
 
 
 def test_lane_forward_16bit():
     inputs, dy = _random_problem(2, 3072, 64, 16, 1, seed=19, act=torch.bfloat16)
-    _compare(inputs, dy, True, 2e-2, 2e-2)
+    _compare(inputs, dy, True, "lane 2x3072x64 bf16")
     inputs, dy = _random_problem(2, 3072, 64, 16, 1, seed=20, act=torch.float16)
-    _compare(inputs, dy, True, 2e-2, 2e-2)
+    _compare(inputs, dy, True, "lane 2x3072x64 fp16")
     # 16-bit u and z with float32 B and C
     inputs, dy = _random_problem(2, 3072, 64, 16, 1, seed=21, act=torch.bfloat16)
     inputs["B"], inputs["C"] = inputs["B"].float(), inputs["C"].float()
-    _compare(inputs, dy, True, 2e-2, 2e-2)
+    _compare(inputs, dy, True, "lane 2x3072x64 bf16 u/z, fp32 B/C")
 
 
 @pytest.mark.parametrize("shape", [(1, 64, 2000, 16, 1), (2, 24, 1500, 20, 3)],
@@ -198,7 +204,7 @@ def test_long_sequences_few_channels(shape):
     # Few rows and 16-step chunks: 125 (94) chunks, more than 32, so the chunk chains run
     # a wavefront per (row, state) with the chunks split into runs across its lanes.
     inputs, dy = _random_problem(*shape, seed=sum(shape))
-    _compare(inputs, dy, True, 1e-5, 1e-4)
+    _compare(inputs, dy, True, "long " + "x".join(map(str, shape)))
 
 
 def test_partial_reductions_whole_batches_and_tail():
@@ -206,7 +212,7 @@ def test_partial_reductions_whole_batches_and_tail():
     # of eight partials plus one), and the 256 steps run as 16 chunks of 16, so each
     # dA/dD/ddelta_bias value sums 16 chunks x 2 batches = 32 partials in whole batches.
     inputs, dy = _random_problem(2, 2304, 256, 16, 1, seed=23)
-    _compare(inputs, dy, True, 1e-5, 1e-4)
+    _compare(inputs, dy, True, "2x2304x256")
 
 
 def test_deterministic_backward():
@@ -217,27 +223,41 @@ def test_deterministic_backward():
         assert torch.equal(runs[0][1][k], runs[1][1][k]), k
 
 
-def test_config3_full_size_channel_subset():
-    # Config 3 at full size: channels are independent in the forward, and with the
-    # upstream gradient zero outside a subset the dB/dC sums only see that subset,
-    # so the oracle only needs the subset.
-    inputs, dy = mamba1_layer(4, 5120, 4096, seed=0)
-    sel = torch.arange(0, 5120, 80)  # 64 channels spread over the width
-    mask = torch.zeros(5120, dtype=torch.bool)
+def _layer_channel_subset(case, batch, dim, length, stride):
+    """A BASELINE layer shape at full size on the GPU, checked on a channel subset.
+
+    Channels are independent in the forward; with the upstream gradient zero outside
+    the subset, the dB/dC sums over channels only see the subset, so the oracle only
+    needs those channels.  bf16 tensors (out, du, dz, dB, dC) are held to 2e-2, the
+    float32 gradients (delta, A, D, delta_bias) to 1e-4."""
+    inputs, dy = mamba1_layer(batch, dim, length, seed=0)
+    sel = torch.arange(0, dim, stride)
+    mask = torch.zeros(dim, dtype=torch.bool)
     mask[sel] = True
     dy = dy * mask[None, :, None].to(dy.dtype)
     out, grads = _gpu(inputs, dy, True)
+    assert torch.isfinite(out).all()
     sub = {k: (v[:, sel] if k in ("u", "dt", "z") else v[sel] if k in ("A", "D", "delta_bias") else v)
            for k, v in inputs.items()}
     ref, rgrads = _ref(sub, dy[:, sel], True)
-    assert max_rel(out[:, sel], ref) <= 2e-2
-    for k in ("u", "dt", "z"):
-        assert norm_rel(grads[k][:, sel], rgrads[k]) <= 2e-2, k
-    for k in ("B", "C"):
-        assert norm_rel(grads[k], rgrads[k]) <= 2e-2, k
-    for k in ("A", "D", "delta_bias"):
-        assert norm_rel(grads[k][sel], rgrads[k]) <= 1e-3, k
-    assert torch.isfinite(out).all()
+    err = record(case, "out", max_rel(out[:, sel], ref), OUT_TOL[out.dtype])
+    assert err <= OUT_TOL[out.dtype], f"out {err:.3e}"
+    for k in NAMES:
+        g = grads[k]
+        got = g[:, sel] if k in ("u", "dt", "z") else g[sel] if k in ("A", "D", "delta_bias") else g
+        tol = GRAD_TOL[g.dtype]
+        e = record(case, "d" + k, norm_rel(got, rgrads[k]), tol)
+        assert e <= tol, f"d{k} {e:.3e} > {tol}"
+
+
+def test_config2_full_size_channel_subset():
+    # Config 2 (130M layer): 8 x 1536 x 2048, 64 channels spread over the width
+    _layer_channel_subset("c2 8x1536x2048", 8, 1536, 2048, 24)
+
+
+def test_config3_full_size_channel_subset():
+    # Config 3 (2.8B layer): 4 x 5120 x 4096, 64 channels spread over the width
+    _layer_channel_subset("c3 4x5120x4096", 4, 5120, 4096, 80)
 
 
 def test_empty_inputs():

@@ -13,7 +13,7 @@ import pytest
 import torch
 
 import oracle
-from cases import max_rel, norm_rel, ssd_problem
+from cases import max_rel, norm_rel, record, ssd_problem
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -66,8 +66,10 @@ def test_forward_option_matrix(shape, dtype):
     y, s = _api()(*args, 64, **options, dt_softplus=True)
     assert y.dtype == dtype and s.dtype == dtype
     assert y.shape == y_ref.shape and s.shape == s_ref.shape
-    assert max_rel(y, y_ref) <= TOL[dtype], f"y {max_rel(y, y_ref):.3e}"
-    assert max_rel(s, s_ref) <= TOL[dtype], f"state {max_rel(s, s_ref):.3e}"
+    case = f"fwd {'x'.join(map(str, shape))} {dtype}"
+    assert record(case, "y", max_rel(y, y_ref), TOL[dtype]) <= TOL[dtype], f"y {max_rel(y, y_ref):.3e}"
+    assert record(case, "final_state", max_rel(s, s_ref), TOL[dtype]) <= TOL[dtype], \
+        f"state {max_rel(s, s_ref):.3e}"
 
 
 def test_defaults_and_each_option_alone():
@@ -117,8 +119,8 @@ def test_config4_shape_batch_slice():
         one["x"].double(), one["dt"].double(), one["A"].double(), one["B"].double(), one["C"].double(),
         chunk_size=256, D=one["D"].double(), z=one["z"].double(), dt_bias=one["dt_bias"].double(),
         dt_softplus=True)
-    assert max_rel(y[:1], y_ref) <= 2e-2
-    assert max_rel(s[:1], s_ref) <= 2e-2
+    assert record("c4 fwd batch 0", "y", max_rel(y[:1], y_ref), 2e-2) <= 2e-2
+    assert record("c4 fwd batch 0", "final_state", max_rel(s[:1], s_ref), 2e-2) <= 2e-2
     assert torch.isfinite(y).all() and torch.isfinite(s).all()
 
 
@@ -126,8 +128,10 @@ def test_config4_shape_batch_slice():
 
 # Gradient norm-relative tolerances against the float64 oracle run on the same (rounded)
 # inputs: 1e-4 for fp32 (the reference's gradient bar); half precision rounds the
-# matrix-core operands, so 1e-2 (fp16) and 3e-2 (bf16).
-GRAD_TOL = {torch.float32: 1e-4, torch.float16: 1e-2, torch.bfloat16: 3e-2}
+# matrix-core operands as the reference's composition does, so every gradient of a
+# half-precision problem (the float32 ones of dt, A, D and dt_bias included) is held to
+# the half-precision output bars, 2e-2 for bf16, and 1e-2 for fp16.
+GRAD_TOL = {torch.float32: 1e-4, torch.float16: 1e-2, torch.bfloat16: 2e-2}
 ACTS = ("x", "B", "C", "z", "initial_states")
 NAMES = ("x", "dt", "A", "B", "C")
 
@@ -188,7 +192,7 @@ def _compare(got, ref, tol, what):
         assert gk is not None, f"{what}: no gradient for {k}"
         assert gk.shape == r.shape, f"{what}: {k} shape {tuple(gk.shape)} vs {tuple(r.shape)}"
         assert torch.isfinite(gk).all(), f"{what}: {k} not finite"
-        err = norm_rel(gk, r)
+        err = record(what, "d" + k, norm_rel(gk, r), tol)
         assert err <= tol, f"{what}: d{k} norm-relative error {err:.3e} > {tol}"
 
 
@@ -220,7 +224,8 @@ def test_reference_gradient_case():
     fast = grads(DEV, torch.float32, lambda *a, **k: _api()(*a[:5], 8, **k))
     slow = grads("cpu", torch.float64, oracle.mamba2_chunk_scan_recurrence)
     for name, got, ref in zip(("x", "dt", "A", "B", "C", "D", "z", "dt_bias", "init"), fast, slow):
-        assert max_rel(got, ref) <= 1e-5, f"grad {name}: {max_rel(got, ref):.3e}"
+        err = record("reference gradient case", "d" + name + " (max rel)", max_rel(got, ref), 1e-5)
+        assert err <= 1e-5, f"grad {name}: {err:.3e}"
 
 
 @pytest.mark.parametrize("case", [
@@ -292,5 +297,5 @@ def test_config4_backward_prefix():
         if k in ("x", "dt", "B", "C", "z"):
             assert torch.count_nonzero(gk[:, cut:]) == 0 and torch.count_nonzero(gk[1:]) == 0, k
             gk = gk[:1, :cut]
-        err = norm_rel(gk, v.grad)
-        assert err <= 3e-2, f"d{k} {err:.3e}"
+        err = record("c4 bwd prefix 384", "d" + k, norm_rel(gk, v.grad), 2e-2)
+        assert err <= 2e-2, f"d{k} {err:.3e}"

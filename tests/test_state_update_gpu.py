@@ -9,7 +9,7 @@ import pytest
 import torch
 
 import oracle
-from cases import decode_problem, max_rel, norm_rel
+from cases import decode_problem, max_rel, norm_rel, record
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -94,15 +94,124 @@ def test_case(tag, dtype, shape, opts):
         assert e <= TOL[dtype], f"{tag}: grad {name} rel {e:.3e}"
 
 
-def test_config5_shape_batch_subset():
-    # Config 5 geometry (nheads 80, headdim 64, dstate 128, fp32 state, bf16 x/B/C/z);
-    # rows of different batches are independent, so a batch slice checks exactly.
-    p = decode_problem(16, 80, 64, 128, 1, seed=0)
+C5 = (256, 80, 64, 128, 1)  # config 5: batch, nheads, headdim, dstate, ngroups
+
+
+def _c5_ring(steps=8):
+    """Per-step x, dt, B, C, z of config 5 from a seeded ring of 8 (the bench's draws)."""
+    batch, nheads, headdim, dstate, _ = C5
+    ring = []
+    for i in range(steps):
+        g = torch.Generator().manual_seed(100 + i)
+        ring.append({"x": torch.randn(batch, nheads, headdim, generator=g).bfloat16(),
+                     "dt": torch.randn(batch, nheads, generator=g),
+                     "B": torch.randn(batch, 1, dstate, generator=g).bfloat16(),
+                     "C": torch.randn(batch, 1, dstate, generator=g).bfloat16(),
+                     "z": torch.randn(batch, nheads, headdim, generator=g).bfloat16()})
+    return ring
+
+
+def test_config5_full_batch_step():
+    # Config 5 at full size (256 x 80 x 64 x 128 fp32 state, bf16 x/B/C/z): one step on
+    # the GPU; batches are independent, so the oracle checks the first and last two.
+    p = decode_problem(*C5, seed=0)
     ys, ss = _api()(*(p[k].to(DEV) for k in ("state", "x", "dt", "A", "B", "C")),
                     D=p["D"].to(DEV), z=p["z"].to(DEV), dt_bias=p["dt_bias"].to(DEV), dt_softplus=True)
-    wy, ws = oracle.mamba2_state_update(**p, dt_softplus=True)
-    assert max_rel(ys, wy) <= 1e-5
-    assert max_rel(ss, ws) <= 1e-5
+    rows = torch.tensor([0, 1, 254, 255])
+    sub = {k: (v[rows] if v.dim() >= 2 else v) for k, v in p.items()}
+    wy, ws = oracle.mamba2_state_update(**sub, dt_softplus=True)
+    e_y = record("c5 full step", "y", max_rel(ys[rows.to(DEV)], wy), 1e-5)
+    e_s = record("c5 full step", "new_state", max_rel(ss[rows.to(DEV)], ws), 1e-5)
+    assert e_y <= 1e-5 and e_s <= 1e-5
+    assert torch.isfinite(ys).all() and torch.isfinite(ss).all()
+
+
+def test_config5_1024_in_place_steps():
+    # The workload the decode metric is quoted on: 1024 in-place steps (out_state=state)
+    # at full size with per-step inputs from a seeded ring of 8.  The oracle steps two
+    # batch rows through the same 1024 steps in float64.
+    p = decode_problem(*C5, seed=0)
+    ring = _c5_ring()
+    ring_dev = [{k: v.to(DEV) for k, v in r.items()} for r in ring]
+    A, D, bias = p["A"], p["D"], p["dt_bias"]
+    state = p["state"].to(DEV)
+    rows = torch.tensor([0, 255])
+    ref_state = p["state"][rows].double()
+    fn = _api()
+    worst_y = 0.0
+    for t in range(1024):
+        r, rd = ring[t % 8], ring_dev[t % 8]
+        y, out = fn(state, rd["x"], rd["dt"], A.to(DEV), rd["B"], rd["C"], D=D.to(DEV), z=rd["z"],
+                    dt_bias=bias.to(DEV), dt_softplus=True, out_state=state)
+        assert out.data_ptr() == state.data_ptr()
+        wy, ref_state = oracle.mamba2_state_update(ref_state, r["x"][rows], r["dt"][rows], A, r["B"][rows],
+                                                   r["C"][rows], D=D, z=r["z"][rows], dt_bias=bias,
+                                                   dt_softplus=True)
+        if t % 64 == 63:
+            worst_y = max(worst_y, max_rel(y[rows.to(DEV)], wy))
+    e_y = record("c5 1024 in-place steps", "y (every 64th step)", worst_y, 1e-5)
+    e_s = record("c5 1024 in-place steps", "final state", max_rel(state[rows.to(DEV)], ref_state), 1e-5)
+    assert e_y <= 1e-5 and e_s <= 1e-5
+    assert torch.isfinite(state).all()
+
+
+def test_config5_backward_batch_slice():
+    # The decode backward at config-5 geometry, full batch on the GPU.  With the upstream
+    # gradients zero outside batch rows 0 and 1, the parameter gradients (summed over the
+    # batch) only see those rows, so the float64 oracle runs on them alone.
+    p = decode_problem(*C5, seed=2)
+    names = ("state", "x", "dt", "A", "B", "C", "D", "z", "dt_bias")
+    g = torch.Generator().manual_seed(3)
+    wy = torch.zeros(C5[0], C5[1], C5[2])
+    ws = torch.zeros(C5[0], C5[1], C5[2], C5[3])
+    wy[:2] = torch.randn(2, C5[1], C5[2], generator=g)
+    ws[:2] = torch.randn(2, C5[1], C5[2], C5[3], generator=g)
+    got = {k: p[k].to(DEV).requires_grad_(True) for k in names}
+    y, s = _api()(*(got[k] for k in names[:6]), D=got["D"], z=got["z"], dt_bias=got["dt_bias"],
+                  dt_softplus=True)
+    ((y.float() * wy.to(DEV)).sum() + (s * ws.to(DEV)).sum()).backward()
+    sub = {k: (p[k][:2] if k in ("state", "x", "dt", "B", "C", "z") else p[k]).double().requires_grad_(True)
+           for k in names}
+    ry, rs = oracle.mamba2_state_update(**sub, dt_softplus=True)
+    ((ry * wy[:2].double()).sum() + (rs * ws[:2].double()).sum()).backward()
+    for k in names:
+        gk = got[k].grad
+        if k in ("state", "x", "dt", "B", "C", "z"):
+            assert torch.count_nonzero(gk[2:]) == 0, k
+            gk = gk[:2]
+        tol = TOL[got[k].dtype]
+        e = record("c5 backward rows 0-1", "d" + k, norm_rel(gk, sub[k].grad), tol)
+        assert e <= tol, f"d{k} {e:.3e}"
+
+
+@pytest.mark.parametrize("x_dtype,z_dtype", [(torch.bfloat16, torch.float32),
+                                             (torch.float32, torch.bfloat16),
+                                             (torch.float16, torch.bfloat16)],
+                         ids=["x-bf16-z-f32", "x-f32-z-bf16", "x-f16-z-bf16"])
+def test_mixed_x_and_z_dtypes(x_dtype, z_dtype):
+    # A float32 state with x and z of different dtypes: the reference casts both to the
+    # state's dtype (exact here), so the oracle sees the rounded values in float64.
+    p = decode_problem(3, 8, 16, 32, 2, seed=5, state_dtype=torch.float32)
+    p["x"], p["z"] = p["x"].float().to(x_dtype), p["z"].float().to(z_dtype)
+    names = ("state", "x", "dt", "A", "B", "C", "D", "z", "dt_bias")
+    got = {k: p[k].to(DEV).requires_grad_(True) for k in names}
+    y, s = _api()(*(got[k] for k in names[:6]), D=got["D"], z=got["z"], dt_bias=got["dt_bias"],
+                  dt_softplus=True)
+    g = torch.Generator().manual_seed(6)
+    wy = torch.randn(y.shape, generator=g)
+    ((y * wy.to(DEV)).sum() + s.square().sum()).backward()
+    ref = {k: p[k].double().requires_grad_(True) for k in names}
+    ry, rs = oracle.mamba2_state_update(**ref, dt_softplus=True)
+    ((ry * wy.double()).sum() + rs.square().sum()).backward()
+    case = f"mixed x {x_dtype} z {z_dtype}"
+    assert y.dtype == torch.float32
+    e = record(case, "y", max_rel(y, ry), 1e-5)
+    assert e <= 1e-5
+    for k in names:
+        assert got[k].grad.dtype == got[k].dtype, k
+        tol = TOL[got[k].dtype]
+        e = record(case, "d" + k, norm_rel(got[k].grad, ref[k].grad), tol)
+        assert e <= tol, f"d{k} {e:.3e}"
 
 
 def test_in_place_decode_loop_matches_recurrence():
