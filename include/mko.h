@@ -8,7 +8,9 @@
  * the failure (thread-local).
  *
  * Ownership: the caller allocates every input, output and workspace; the
- * library never allocates or frees device memory.  Inputs are never written.
+ * library never allocates or frees device memory (its one static device array,
+ * behind mko_state_update_bwd_static, comes with the code object).  Inputs are
+ * never written.
  * All tensors are dense row-major (contiguous) in the layouts documented per
  * field.  dtype fields take MKO_F32 / MKO_F16 / MKO_BF16; every kernel computes
  * in float32 and rounds once when it stores a 16-bit output.
@@ -174,6 +176,22 @@ int mko_state_update_fwd(const mko_state_update_params* p, void* stream);
  * gradient has one writer, so repeated runs are bit-identical. */
 size_t mko_state_update_bwd_workspace_size(const mko_state_update_params* p);
 int mko_state_update_bwd(const mko_state_update_params* p, void* stream);
+
+/* Bytes of the static device array behind mko_state_update_bwd_static (one array per
+ * GPU the library runs on, held until the process ends). */
+#define MKO_SU_STATIC_SCRATCH_BYTES (32u << 20)
+
+/* No counterpart in the reference: for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving or training loops, harnesses that
+ * forbid hipMalloc).  The backward of mko_state_update_bwd, with its per-head partials
+ * in the library's static scratch array instead of p->workspace (ignored); it calls no
+ * allocator.  The problem must need at most MKO_SU_STATIC_SCRATCH_BYTES of partials
+ * (mko_state_update_bwd_workspace_size(p); config 5's 256 x 80 heads need 26.4 MB),
+ * else MKO_EWORKSPACE.  The stream must belong to the current device.  Every call on
+ * one GPU shares that GPU's array: calls that overlap on one GPU (two streams, or two
+ * host threads) race.  Nothing in the array needs clearing between calls: each call
+ * writes every partial it reads. */
+int mko_state_update_bwd_static(const mko_state_update_params* p, void* stream);
 
 /* ======================================================================== */
 /* Mamba-2 SSD chunk scan                                                     */

@@ -11,6 +11,9 @@
 // and dA/dD/ddt over its rows in a fixed order; a second kernel sums the
 // per-head partials over heads (dB/dC) or batch (dA/dD/ddt_bias).  Every output
 // has one writer, so the backward is bit-deterministic.
+#include <mutex>
+#include <vector>
+
 #include "common.hpp"
 
 namespace mko {
@@ -474,24 +477,13 @@ extern "C" size_t mko_state_update_bwd_workspace_size(const mko_state_update_par
   return bwd_layout(g).total;
 }
 
-extern "C" int mko_state_update_bwd(const mko_state_update_params* p, void* stream) {
-  Geo g;
-  int st = make_geo(p, &g);
-  if (st != MKO_OK) return st;
-  if (!p->grad_state || !p->dx || !p->ddt || !p->dA || !p->dB || !p->dC) {
-    mko_set_error("state_update_bwd: grad_state, dx, ddt, dA, dB and dC are required");
-    return MKO_EINVAL;
-  }
-  if ((p->D && !p->dD) || (p->z && !p->dz) || (p->dt_bias && !p->ddt_bias)) {
-    mko_set_error("state_update_bwd: dD/dz/ddt_bias are required when D/z/dt_bias are given");
-    return MKO_EINVAL;
-  }
-  if (g.batch == 0 || g.headdim == 0) return MKO_OK;  // caller zero-fills
+namespace {
+
+// The checks and launches of the backward, with the per-head partials in `ws` (at least
+// bwd_layout(g).total bytes of device memory on the stream's device).
+int run_bwd(const mko_state_update_params* p, void* stream, char* ws, const Geo& geo) {
+  Geo g = geo;
   const BwdLayout l = bwd_layout(g);
-  if (!p->workspace || p->workspace_bytes < l.total) {
-    mko_set_error("state_update_bwd: workspace of %zu bytes needed, %zu given", l.total, p->workspace_bytes);
-    return MKO_EWORKSPACE;
-  }
   g.vec = pick_vec(g, p, true);
   Args a = base_args(p, g);
   a.dy = p->dy;
@@ -500,7 +492,6 @@ extern "C" int mko_state_update_bwd(const mko_state_update_params* p, void* stre
   a.dx = p->dx;
   a.ddt = p->ddt;
   a.dz = p->dz;
-  char* ws = static_cast<char*>(p->workspace);
   a.pb = reinterpret_cast<float*>(ws + l.pb);
   a.pc = reinterpret_cast<float*>(ws + l.pc);
   a.pa = reinterpret_cast<float*>(ws + l.pa);
@@ -518,4 +509,98 @@ extern "C" int mko_state_update_bwd(const mko_state_update_params* p, void* stre
             reduce<<<static_cast<unsigned>((total + 255) / 256), 256, 0, s>>>(a, p->dB, p->dC, p->dA, p->dD,
                                                                                p->ddt_bias));
   return mko_check_launch("state_update_bwd");
+}
+
+// Sizes and pointers every backward call needs; MKO_OK with *empty set when there is
+// nothing to launch.
+int check_bwd(const mko_state_update_params* p, Geo* g, bool* empty) {
+  int st = make_geo(p, g);
+  if (st != MKO_OK) return st;
+  if (!p->grad_state || !p->dx || !p->ddt || !p->dA || !p->dB || !p->dC) {
+    mko_set_error("state_update_bwd: grad_state, dx, ddt, dA, dB and dC are required");
+    return MKO_EINVAL;
+  }
+  if ((p->D && !p->dD) || (p->z && !p->dz) || (p->dt_bias && !p->ddt_bias)) {
+    mko_set_error("state_update_bwd: dD/dz/ddt_bias are required when D/z/dt_bias are given");
+    return MKO_EINVAL;
+  }
+  *empty = g->batch == 0 || g->headdim == 0;  // the caller zero-fills
+  return MKO_OK;
+}
+
+// The partials of mko_state_update_bwd_static: one copy of this array per GPU, held until
+// the process ends.  In host code `scratch` only names the symbol; its device address on
+// each GPU comes from hipGetSymbolAddress (scratch_address) and is what kernels receive.
+__device__ __align__(256) unsigned char scratch[MKO_SU_STATIC_SCRATCH_BYTES];
+
+std::mutex g_scratch_mu;
+std::vector<void*> g_scratch_at;  // per device ordinal; null until first resolved
+
+// The device address of `scratch` on the current device (resolved once per device).
+int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess || dev < 0) {
+    mko_set_error("state_update_bwd_static: no current device: %s", hipGetErrorString(err));
+    return MKO_ELAUNCH;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (static_cast<size_t>(dev) >= g_scratch_at.size()) g_scratch_at.resize(dev + 1, nullptr);
+  if (!g_scratch_at[dev]) {
+    void* ptr = nullptr;
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !ptr) {
+      mko_set_error("state_update_bwd_static: scratch address on device %d: %s", dev, hipGetErrorString(err));
+      return MKO_ELAUNCH;
+    }
+    g_scratch_at[dev] = ptr;
+  }
+  *out = g_scratch_at[dev];
+  return MKO_OK;
+}
+
+}  // namespace
+
+extern "C" int mko_state_update_bwd(const mko_state_update_params* p, void* stream) {
+  Geo g;
+  bool empty = false;
+  int st = check_bwd(p, &g, &empty);
+  if (st != MKO_OK || empty) return st;
+  const size_t need = bwd_layout(g).total;
+  if (!p->workspace || p->workspace_bytes < need) {
+    mko_set_error("state_update_bwd: workspace of %zu bytes needed, %zu given", need, p->workspace_bytes);
+    return MKO_EWORKSPACE;
+  }
+  return run_bwd(p, stream, static_cast<char*>(p->workspace), g);
+}
+
+extern "C" int mko_state_update_bwd_static(const mko_state_update_params* p, void* stream) {
+  Geo g;
+  bool empty = false;
+  int st = check_bwd(p, &g, &empty);
+  if (st != MKO_OK || empty) return st;
+  const size_t need = bwd_layout(g).total;
+  if (need > MKO_SU_STATIC_SCRATCH_BYTES) {
+    mko_set_error("state_update_bwd_static: this problem needs %zu bytes of partials, more than the %zu-byte "
+                  "static scratch (batch x nheads x (2 dstate + headdim + 2) floats must fit); call "
+                  "mko_state_update_bwd with a workspace instead",
+                  need, static_cast<size_t>(MKO_SU_STATIC_SCRATCH_BYTES));
+    return MKO_EWORKSPACE;
+  }
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    mko_set_error("state_update_bwd_static: no current device");
+    return MKO_ELAUNCH;
+  }
+  if (stream) {
+    int sdev = -1;
+    if (hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev) != hipSuccess || sdev != dev) {
+      mko_set_error("state_update_bwd_static: the stream belongs to device %d, device %d is current", sdev, dev);
+      return MKO_EINVAL;
+    }
+  }
+  void* ws = nullptr;
+  st = scratch_address(&ws);
+  if (st != MKO_OK) return st;
+  return run_bwd(p, stream, static_cast<char*>(ws), g);
 }

@@ -159,7 +159,11 @@ _SIGNATURES = {
                            ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64)], ctypes.c_int),
     "mko_state_update_bwd_workspace_size": ([ctypes.POINTER(StateUpdateParams)], ctypes.c_size_t),
     "mko_state_update_bwd": ([ctypes.POINTER(StateUpdateParams), _vp], ctypes.c_int),
+    "mko_state_update_bwd_static": ([ctypes.POINTER(StateUpdateParams), _vp], ctypes.c_int),
 }
+
+STATIC_SCRATCH_BYTES = 32 << 20
+"""MKO_SU_STATIC_SCRATCH_BYTES: the static partials array of mko_state_update_bwd_static."""
 
 
 def library_path():

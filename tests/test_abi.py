@@ -114,3 +114,19 @@ def test_gated_norm_validation_without_gpu(native):
     assert wide > 0 and (wide - 256 * 4) % (2 * 32768 * 4) == 0
     p.workspace, p.workspace_bytes = None, 0
     assert lib.mko_gated_norm_bwd(ctypes.byref(p), None) == 4
+
+
+def test_static_decode_backward_refuses_an_oversized_problem_on_the_host(native):
+    # Host-side validation only: the size check comes before any pointer is read or any
+    # HIP call is made.
+    lib = native.lib()
+    p = native.StateUpdateParams()
+    p.batch, p.nheads, p.headdim, p.dstate, p.ngroups = 1 << 16, 8, 16, 32, 2
+    p.state_dtype = p.x_dtype = p.dt_dtype = p.bc_dtype = 0
+    for name in ("state", "x", "dt", "A", "B", "C", "grad_state", "dx", "ddt", "dA", "dB", "dC"):
+        setattr(p, name, 256)
+    assert lib.mko_state_update_bwd_workspace_size(ctypes.byref(p)) > native.STATIC_SCRATCH_BYTES
+    assert lib.mko_state_update_bwd_static(ctypes.byref(p), None) == 4  # MKO_EWORKSPACE
+    assert b"static scratch" in lib.mko_last_error()
+    p.dA = None
+    assert lib.mko_state_update_bwd_static(ctypes.byref(p), None) == 1  # a missing output first
