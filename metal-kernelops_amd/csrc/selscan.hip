@@ -796,6 +796,261 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) f
   }
 }
 
+// ---------------------------------------------------------------- backward, lane per (channel, state)
+//
+// The backward in fwd_lane's mapping: a wavefront holds 4 channels x 16 states, lane (c, n), and
+// walks the whole sequence once in reverse, 16 steps a block.  With every (channel, state) chain
+// on its own lane there are enough wavefronts without cutting time into chunks, so the adjoint
+// entering a block is simply carried over from the block to its right: no summary pass, no chain.
+// Per block:
+//   - lane (c, n) loads step t0 + n of its channel's delta, u, z, dout and out and forms that
+//     element's step, du, gy = dout silu(z) and the factor of dz;
+//   - lane (c, n) reads its state's 16 steps of B and of C straight from memory (the 4
+//     channels of the wavefront share them, so the vector L1 serves each row once);
+//   - from the saved state entering the block, the lane recomputes the block's 16 states and
+//     decays a = exp(A delta);
+//   - it walks the 16 steps backwards with the adjoint h_t = gy_t C_t + a_{t+1} h_{t+1}, and per
+//     step writes its state's terms of the two sums over states that du and ddelta need,
+//     h_t B_t and A a_t x_{t-1} h_t, into two LDS transposes, and adds its dA term;
+//   - the dB and dC terms, h_t du_t and gy_t x_t, are summed over the wavefront's 4 channels
+//     (one 16-lane row each) with gfx950's lane swaps: v_permlane32_swap exchanges the
+//     wavefront's halves, so one add sums rows (0 + 2, 1 + 3) of a step's dB terms and, in the
+//     other half, of its dC terms; v_permlane16_swap of two such registers (steps i and i + 1)
+//     exchanges odd and even rows, and one more add leaves dB_i, dB_{i+1}, dC_i and dC_{i+1} as
+//     the four rows of one register: 6 instructions per two steps, in a fixed order;
+//   - lane (c, n) then owns step t0 + n: it sums its rows of the transposes and writes du,
+//     ddelta and dz.  The pre-gate output that dz needs comes back as out / silu(z); a block
+//     where silu(z) is exactly zero somewhere (or out was not given) first sums a transpose
+//     of C x instead;
+//   - the workgroup's 4 wavefronts add their dB/dC blocks in a fixed order and write one
+//     partial per 16 channels (per 4 channels when a group is not a multiple of 16 wide).
+// A block's inputs are requested one block ahead.  Needs dstate <= 16, whole 16-step blocks,
+// channels per group a multiple of 4, fp32 delta and 16-byte aligned rows.
+
+constexpr int kTrPitch = 4 * HS + 4;     // one step's row of 4 channels x 16 states, padded: the
+                                         // 16-byte reads of lanes (c, i..i+7) fall in distinct banks
+constexpr int kTrFloats = HS * kTrPitch;  // one transpose buffer of a wavefront, padded so
+                                              // that the same element of the next buffer is 16
+                                              // banks away (the two terms of a step are written
+                                              // as one pair)
+
+// The value lane I of each 16-lane row holds, in every lane of that row.  Every row and bank
+// is enabled and bound_ctrl is set, so no lane keeps an old value: the move folds into the VALU
+// instruction that consumes it, as its DPP source operand.
+template <int I>
+__device__ __forceinline__ float row_bcast(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + I, 0xf, 0xf, true));
+}
+
+template <class TU, class TB>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
+bwd_lane(Geo g, Ptrs p, int cpb) {
+  // per wavefront: the transposes of h B (t1) and A a x h (t2); in blocks that need it, t1
+  // first transposes C x; the workgroup's dB/dC blocks reuse the t1 buffers
+  __shared__ __align__(16) float lds[4][2][kTrFloats];
+  const int wave = uniform(static_cast<int>(threadIdx.x >> 6));
+  const int lane = threadIdx.x & 63, cl = lane >> 4, n = lane & 15;
+  const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * kLaneChannels;  // first row of the wave
+  const bool active = row0 < g.rows;  // a wavefront's 4 rows are all valid or all past the end
+  const int64_t r = active ? row0 + cl : g.rows - 1;
+  const int64_t bb = r / g.dim, d = r - bb * g.dim;
+  const int64_t bg = uniform(static_cast<int>((active ? row0 : g.rows - 1) / g.dg));  // (batch, group) of the wave
+  const int N = static_cast<int>(g.dstate);
+  const bool sn = n < N;
+  const bool padded = N < HS;  // wave-uniform: states n >= N exist only as zero lanes
+  const float an = sn ? p.A[d * N + n] : 0.0f;
+  const float a2 = an * kLog2e;
+  const float bias = p.bias ? p.bias[d] : 0.0f;
+  const float Dd = p.D ? p.D[d] : 0.0f;
+  const bool has_z = p.z != nullptr;
+  const bool has_out = p.out != nullptr;
+  const int64_t L = g.length;
+  float* t1 = lds[wave][0];
+  float* t2 = lds[wave][1];
+  // Lane offsets in elements (the host keeps every array below 2^31 elements): this lane's
+  // element of a block, its saved state, and its state's row of B and C (read straight from
+  // memory: the wavefront's 4 channels read the same rows, which the vector L1 serves once).
+  // Block offsets are added to wave-uniform base pointers.
+  const uint32_t eoff = static_cast<uint32_t>(r * L + n);
+  const uint32_t soff = static_cast<uint32_t>(ck_index(g, r, 0, sn ? n : 0));
+  const uint32_t boff = static_cast<uint32_t>((bg * N + (sn ? n : 0)) * L);
+  const int tw = cl * HS + n;  // this lane's column in a transpose row
+  const int64_t sstep = g.dim * N;
+  const TU* zsrc = static_cast<const TU*>(has_z ? p.z : p.u);
+  const TU* osrc = static_cast<const TU*>(has_out ? p.out : p.u);
+  // dB/dC partial slot of the wavefront (cpb 4) or workgroup (cpb 16): partial index = first row / cpb
+  float2* pbc = reinterpret_cast<float2*>(p.pbc) +
+                ((cpb == 16 ? row0 - wave * kLaneChannels : row0) / cpb) * L * HS;
+
+  struct In {
+    float dl, xin;
+    TU u, z, go, o;
+    RawRun<TB, HS> b, c;
+  };
+  auto load = [&](int k, In& in) {
+    const int64_t t0 = static_cast<int64_t>(k) * HS;
+    in.dl = (static_cast<const float*>(p.delta) + t0)[eoff];
+    in.u = (static_cast<const TU*>(p.u) + t0)[eoff];
+    in.z = (zsrc + t0)[eoff];
+    in.go = (static_cast<const TU*>(p.dout) + t0)[eoff];
+    in.o = (osrc + t0)[eoff];
+    in.xin = (p.states + k * sstep)[soff];
+    in.b.load(g, static_cast<const TB*>(p.B) + t0, 0, boff, HS);
+    in.c.load(g, static_cast<const TB*>(p.C) + t0, 0, boff, HS);
+  };
+  const int nblk = static_cast<int>(L / HS);
+  In cur;
+  load(nblk - 1, cur);
+  float carry = 0.0f;  // a_{t+1} h_{t+1} entering the block's last step from the right
+  float dA0 = 0.0f, dA1 = 0.0f, dD_acc = 0.0f, db_acc = 0.0f;  // dA in two chains (even, odd steps)
+  const float act = active ? 1.0f : 0.0f;
+
+  for (int k = nblk - 1; k >= 0; --k) {
+    const int64_t t0 = static_cast<int64_t>(k) * HS;
+    // ---- this lane's element: step t0 + n of channel c
+    const float uu = to_f32(cur.u);
+    const float del = step_of(g, cur.dl, bias);
+    const float du = del * uu;
+    float gy = to_f32(cur.go) * act;
+    float dzf = 0.0f, ypre = 0.0f;
+    bool need_y = false;
+    if (has_z) {
+      const float zz = to_f32(cur.z);
+      const float sg = sigmoid(zz);
+      const float gate = zz * sg;
+      dzf = gy * sg * (1.0f + zz * (1.0f - sg));
+      if (has_out && gate != 0.0f) ypre = to_f32(cur.o) * fast_rcp(gate);
+      else need_y = true;
+      gy *= gate;
+    }
+    const bool ty = __ballot(need_y) != 0;  // wave-uniform: transpose C x in this block
+    const float x0 = sn ? cur.xin : 0.0f;
+    float bv[HS], cv[HS];
+    cur.b.get(bv);
+    cur.c.get(cv);
+    if (padded && !sn) {
+#pragma unroll
+      for (int i = 0; i < HS; ++i) bv[i] = cv[i] = 0.0f;
+    }
+    load(k > 0 ? k - 1 : 0, cur);  // the next block's inputs: a block of work to arrive
+    // ---- recompute the block's states from the saved one
+    float xh[HS], ah[HS];
+    auto recompute = [&](auto with_y) {
+      float x = x0;
+      static_for<0, HS>([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        ah[i] = fast_exp2(row_bcast<i>(del) * a2);
+        x = fmaf(ah[i], x, row_bcast<i>(du) * bv[i]);
+        xh[i] = x;
+        if constexpr (decltype(with_y)::value) t1[i * kTrPitch + tw] = cv[i] * x;
+      });
+    };
+    if (ty) {
+      // blocks with a zero gate somewhere: the pre-gate output from the sum of C x
+      recompute(std::true_type{});
+      wave_lds_sync();
+      float v3[HS], c4[4];
+      lds_row<HS>(t1 + n * kTrPitch + cl * HS, v3);
+#pragma unroll
+      for (int m = 0; m < 4; ++m) c4[m] = v3[m];
+#pragma unroll
+      for (int m = 4; m < HS; ++m) c4[m & 3] += v3[m];
+      if (need_y) ypre = fmaf(Dd, uu, (c4[0] + c4[1]) + (c4[2] + c4[3]));
+      wave_lds_sync();
+    } else {
+      recompute(std::false_type{});
+    }
+    // ---- reverse walk
+    float sbc[HS / 2];  // dB/dC of step pairs summed over the wavefront's 4 channels (see below)
+    float rodd = 0.0f;  // the odd step's half-summed register, waiting for its even partner
+    static_for<0, HS>([&](auto jc) {
+      constexpr int i = HS - 1 - decltype(jc)::value;
+      const float h = row_bcast<i>(gy) * cv[i] + carry;
+      t1[i * kTrPitch + tw] = h * bv[i];
+      const float hc = ah[i] * h;
+      const float pr = hc * (i > 0 ? xh[i > 0 ? i - 1 : 0] : x0);
+      t2[i * kTrPitch + tw] = an * pr;
+      if constexpr (i % 2 == 0) dA0 += row_bcast<i>(del) * pr;
+      else dA1 += row_bcast<i>(del) * pr;
+      // dB and dC terms of step i, h du_i and gy_i x_i: rows c0 + c2 and c1 + c3 of each
+      // (a swap of the wavefront's halves), dB in rows 0-1 and dC in rows 2-3 ...
+      const float pb = row_bcast<i>(du) * h, pc = row_bcast<i>(gy) * xh[i];
+      const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(pb), __float_as_uint(pc), false, false);
+      const float rr = __uint_as_float(s32[0]) + __uint_as_float(s32[1]);
+      if constexpr (i % 2 == 1) {
+        rodd = rr;
+      } else {
+        // ... and with the odd step's register, a swap of odd and even rows completes the
+        // channel sums: rows dB_i, dB_{i+1}, dC_i, dC_{i+1}, each over the 16 states
+        const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(rr), __float_as_uint(rodd), false, false);
+        sbc[i / 2] = __uint_as_float(s16[0]) + __uint_as_float(s16[1]);
+      }
+      carry = hc;
+    });
+    wave_lds_sync();
+    // ---- lane (c, n) owns step t0 + n: its rows of the transposes
+    float s1, s2;
+    {
+      float v1[HS], v2[HS];
+      lds_row<HS>(t1 + n * kTrPitch + cl * HS, v1);
+      lds_row<HS>(t2 + n * kTrPitch + cl * HS, v2);
+      float a[4], b[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        a[m] = v1[m];
+        b[m] = v2[m];
+      }
+#pragma unroll
+      for (int m = 4; m < HS; ++m) {
+        a[m & 3] += v1[m];
+        b[m & 3] += v2[m];
+      }
+      s1 = (a[0] + a[1]) + (a[2] + a[3]);
+      s2 = (b[0] + b[1]) + (b[2] + b[3]);
+    }
+    const float duo = fmaf(del, s1, Dd * gy);
+    float dd = fmaf(uu, s1, s2);
+    if (g.softplus) dd *= softplus_grad_from_value(del);
+    dD_acc = fmaf(gy, uu, dD_acc);
+    db_acc = fmaf(dd, act, db_acc);
+    if (active) {
+      (static_cast<TU*>(p.du) + t0)[eoff] = from_f32<TU>(duo);
+      (static_cast<float*>(p.ddelta) + t0)[eoff] = dd;
+      if (has_z && p.dz) (static_cast<TU*>(p.dz) + t0)[eoff] = from_f32<TU>(dzf * ypre);
+    }
+    // ---- dB/dC of the block: register m of lane (row q, state n) holds dB (q < 2) or dC (q >= 2)
+    // of step 2m + (q mod 2)
+    wave_lds_sync();  // every read of t1 is done before it takes the wavefront's dB/dC block
+    const int which = cl >> 1, par = cl & 1;
+    if (cpb == 16) {
+#pragma unroll
+      for (int m = 0; m < HS / 2; ++m) t1[which * HS * HS + (2 * m + par) * HS + n] = sbc[m];
+      __syncthreads();
+      // thread (i, s) adds the 4 wavefronts' (step i, state s) in order
+      const int o = threadIdx.x;
+      float sb = 0.0f, sc = 0.0f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        sb += lds[w][0][o];
+        sc += lds[w][0][HS * HS + o];
+      }
+      (pbc + t0 * HS)[o] = make_float2(sb, sc);
+      __syncthreads();
+    } else if (active) {
+      float* pf = reinterpret_cast<float*>(pbc + t0 * HS) + which;
+#pragma unroll
+      for (int m = 0; m < HS / 2; ++m) pf[((2 * m + par) * HS + n) * 2] = sbc[m];
+    }
+  }
+  if (active && sn) p.dap[static_cast<int64_t>(n) * g.rows + row0 + cl] = dA0 + dA1;
+  dD_acc = row16_sum(dD_acc);
+  db_acc = row16_sum(db_acc);
+  if (active && n == 0) {
+    p.ddp[row0 + cl] = dD_acc;
+    p.dbp[row0 + cl] = db_acc;
+  }
+}
+
 // ---------------------------------------------------------------- backward
 
 template <int NS, bool UNI, class TU>
@@ -1340,14 +1595,33 @@ struct Plan {
   int ns;
   bool uni;
   bool lane;  // forward through fwd_lane (set per call from pointer alignment and shape)
+  bool lane_bwd;  // backward through bwd_lane (likewise)
   size_t off_bt, off_ct, off_bn, off_cn, off_drive, off_sumd, off_adj, off_pbc, off_dap, off_ddp,
       off_dbp;
+  // bwd_lane's workspace: dB/dC partials per cpb channels, dA / dD / ddelta_bias partials per row
+  int cpb;
+  int64_t lncb;
+  size_t loff_pbc, loff_dap, loff_ddp, loff_dbp;
   size_t fwd_bytes, bwd_bytes;
 };
 
 inline size_t align_up(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Rows from which the lane-per-state kernels have enough wavefronts (rows / 4 of them) to fill
+// the chip without time chunks.
+constexpr int64_t kLaneRows = 6144;
+
+// Shapes the lane-per-state forward takes (dtypes and alignment are checked per call).
+static bool lane_shape(const Geo& g, int ns) {
+  return ns == 16 && g.rows >= kLaneRows && g.length % HS == 0 && g.dg % kLaneChannels == 0;
+}
+
+// The backward's too: it also indexes with 32-bit lane offsets.
+static bool lane_bwd_shape(const Geo& g, int ns) {
+  return lane_shape(g, ns) && g.rows * g.length < (static_cast<int64_t>(1) << 31);
+}
 
 static int make_plan(const mko_selscan_params* p, Plan* pl) {
   if (!p) {
@@ -1439,6 +1713,17 @@ static int make_plan(const mko_selscan_params* p, Plan* pl) {
   pl->off_ddp = o; o = align_up(o + rk * 4);
   pl->off_dbp = o; o = align_up(o + rk * 4);
   pl->bwd_bytes = o;
+  // bwd_lane (laid out from offset 0; the workspace is the larger of the two layouts)
+  pl->cpb = (g.dg % 16) == 0 ? 16 : 4;
+  pl->lncb = g.dg / pl->cpb;
+  if (lane_bwd_shape(g, pl->ns)) {
+    size_t q = 0;
+    pl->loff_pbc = q; q = align_up(q + static_cast<size_t>(g.batch * g.ngroups) * pl->lncb * g.length * 16 * 2 * 4);
+    pl->loff_dap = q; q = align_up(q + static_cast<size_t>(g.rows) * 16 * 4);
+    pl->loff_ddp = q; q = align_up(q + static_cast<size_t>(g.rows) * 4);
+    pl->loff_dbp = q; q = align_up(q + static_cast<size_t>(g.rows) * 4);
+    if (q > pl->bwd_bytes) pl->bwd_bytes = q;
+  }
   return MKO_OK;
 }
 
@@ -1493,9 +1778,6 @@ static bool chain_by_wave(const Geo& g) {
   return g.nchunks > 32 && g.rows * g.dstate < 1024 * 256;
 }
 
-// Rows from which the lane-per-state forward has enough wavefronts (rows / 4 of them) to
-// fill the chip without time chunks.
-constexpr int64_t kLaneRows = 6144;
 
 template <class TU>
 static int launch_fwd_lane(const Plan& pl, const Ptrs& q, hipStream_t s) {
@@ -1537,8 +1819,37 @@ static int launch_fwd(const Plan& pl, const Ptrs& q, hipStream_t s) {
   return mko_check_launch("selscan_fwd");
 }
 
+template <class TU>
+static int launch_bwd_lane(const Plan& pl, const Ptrs& q0, const mko_selscan_params* p, hipStream_t s) {
+  Geo g = pl.g;
+  Ptrs q = q0;
+  char* ws = static_cast<char*>(p->workspace);
+  q.pbc = reinterpret_cast<float*>(ws + pl.loff_pbc);
+  q.dap = reinterpret_cast<float*>(ws + pl.loff_dap);
+  q.ddp = reinterpret_cast<float*>(ws + pl.loff_ddp);
+  q.dbp = reinterpret_cast<float*>(ws + pl.loff_dbp);
+  const unsigned grid = static_cast<unsigned>((g.rows + 4 * kLaneChannels - 1) / (4 * kLaneChannels));
+  if (g.bc_dtype == MKO_BF16)
+    MKO_TIMED("selscan_bwd_lane", s, bwd_lane<TU, bf16><<<grid, 256, 0, s>>>(g, q, pl.cpb));
+  else if (g.bc_dtype == MKO_F16)
+    MKO_TIMED("selscan_bwd_lane", s, bwd_lane<TU, _Float16><<<grid, 256, 0, s>>>(g, q, pl.cpb));
+  else
+    MKO_TIMED("selscan_bwd_lane", s, bwd_lane<TU, float><<<grid, 256, 0, s>>>(g, q, pl.cpb));
+  // partials: dB/dC per cpb channels; dA / dD / ddelta_bias per row (one "chunk")
+  g.nchunks = 1;
+  MKO_TIMED("selscan_bwd_reduce", s,
+            reduce_bc<16><<<static_cast<unsigned>(g.batch * g.ngroups * ((g.length + 256 / 16 - 1) / (256 / 16))),
+                            256, 0, s>>>(g, static_cast<int>(pl.lncb), q.pbc, p->dB, p->dC);
+            reduce_params<<<static_cast<unsigned>((g.dstate + 1) * ((g.dim + 63) / 64)), 256, 0, s>>>(
+                g, 16, q.dap, q.ddp, q.dbp, p->dA, p->dD, p->ddelta_bias));
+  return mko_check_launch("selscan_bwd");
+}
+
 template <int NS, bool UNI, class TU>
 static int launch_bwd(const Plan& pl, const Ptrs& q, const mko_selscan_params* p, hipStream_t s) {
+  if constexpr (NS == 16 && !__is_same(TU, Dyn)) {
+    if (pl.lane_bwd) return launch_bwd_lane<TU>(pl, q, p, s);
+  }
   const Geo& g = pl.g;
   const dim3 block(g.wpg * kWave);
   const unsigned gx = static_cast<unsigned>((g.nwr + g.wpg - 1) / g.wpg);
@@ -1620,7 +1931,7 @@ extern "C" int mko_selscan_fwd(const mko_selscan_params* p, void* stream) {
   }
   pl.g.vec = rows_vectorisable(pl.g, {{p->u, p->u_dtype}, {p->delta, p->delta_dtype}, {p->z, p->u_dtype},
                                       {p->out, p->u_dtype}}) ? 1 : 0;
-  pl.lane = pl.ns == 16 && pl.g.rows >= kLaneRows && pl.g.length % HS == 0 && pl.g.dg % kLaneChannels == 0 &&
+  pl.lane = lane_shape(pl.g, pl.ns) &&
             rows_vectorisable(pl.g, {{p->B, p->bc_dtype}, {p->C, p->bc_dtype}});
   Ptrs q = make_ptrs(p, pl);
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -1650,7 +1961,8 @@ extern "C" int mko_selscan_bwd(const mko_selscan_params* p, void* stream) {
   }
   pl.g.vec = rows_vectorisable(pl.g, {{p->u, p->u_dtype}, {p->delta, p->delta_dtype}, {p->z, p->u_dtype},
                                       {p->dout, p->u_dtype}, {p->du, p->u_dtype}, {p->ddelta, p->delta_dtype},
-                                      {p->dz, p->u_dtype}}) ? 1 : 0;
+                                      {p->dz, p->u_dtype}, {p->out, p->u_dtype}}) ? 1 : 0;
+  pl.lane_bwd = lane_bwd_shape(pl.g, pl.ns) && rows_vectorisable(pl.g, {{p->B, p->bc_dtype}, {p->C, p->bc_dtype}});
   Ptrs q = make_ptrs(p, pl);
   hipStream_t s = static_cast<hipStream_t>(stream);
   return dispatch_types(pl, p->u_dtype, p->delta_dtype, [&](auto tag) {

@@ -89,9 +89,11 @@ def _(u, delta, A, B, C, D, z, delta_bias, softplus):
 
 def selscan_bwd_impl(dout: Tensor, u: Tensor, delta: Tensor, A: Tensor, B: Tensor, C: Tensor,
                      D: Optional[Tensor], z: Optional[Tensor], delta_bias: Optional[Tensor],
-                     softplus: bool, states: Tensor
+                     softplus: bool, states: Tensor, out: Optional[Tensor] = None
                      ) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
-    """The backward launch behind ``mko::selscan_bwd`` (see ``selscan_fwd_impl``)."""
+    """The backward launch behind ``mko::selscan_bwd`` (see ``selscan_fwd_impl``).  ``out``, the
+    forward's output, lets the kernels recover the pre-gate output for dz as out / silu(z)
+    instead of summing it over the states again; it is optional."""
     dim = u.shape[1]
     f32 = dict(dtype=torch.float32, device=u.device)
     du, ddelta = torch.empty_like(u), torch.empty_like(delta)
@@ -109,6 +111,7 @@ def selscan_bwd_impl(dout: Tensor, u: Tensor, delta: Tensor, A: Tensor, B: Tenso
     lib = nat.lib()
     p = _params(u, delta, A, B, C, D, z, delta_bias, softplus)
     p.states, p.dout = states.data_ptr(), dout.data_ptr()
+    p.out = nat.ptr(out)
     p.du, p.ddelta, p.dA, p.dB, p.dC = (t.data_ptr() for t in (du, ddelta, dA, dB, dC))
     p.dD = dD.data_ptr() if D is not None else None
     p.dz = dz.data_ptr() if z is not None else None
@@ -123,7 +126,7 @@ _selscan_bwd = torch.library.custom_op("mko::selscan_bwd", selscan_bwd_impl, mut
 
 
 @_selscan_bwd.register_fake
-def _(dout, u, delta, A, B, C, D, z, delta_bias, softplus, states):
+def _(dout, u, delta, A, B, C, D, z, delta_bias, softplus, states, out=None):
     dim = u.shape[1]
     return (torch.empty_like(u), torch.empty_like(delta), A.new_empty(A.shape, dtype=torch.float32),
             torch.empty_like(B), torch.empty_like(C), u.new_empty(dim if D is not None else 0,
@@ -134,7 +137,8 @@ def _(dout, u, delta, A, B, C, D, z, delta_bias, softplus, states):
 
 def _setup(ctx, inputs, output):
     u, delta, A, B, C, D, z, delta_bias, softplus = inputs
-    ctx.save_for_backward(u, delta, A, B, C, D, z, delta_bias, output[1])
+    # the output too: with a gate, the backward reads the pre-gate output back from it
+    ctx.save_for_backward(u, delta, A, B, C, D, z, delta_bias, output[1], output[0] if z is not None else None)
     ctx.softplus = softplus
     # the saved states (the op's second output) never receive a gradient: without this,
     # autograd would fill a zero tensor of their size (335 MB at 4 x 5120 x 4096) per backward
@@ -144,9 +148,9 @@ def _setup(ctx, inputs, output):
 def _backward(ctx, dout, _dstates):
     if dout is None:
         return (None,) * 9
-    u, delta, A, B, C, D, z, bias, states = ctx.saved_tensors
+    u, delta, A, B, C, D, z, bias, states, out = ctx.saved_tensors
     du, ddelta, dA, dB, dC, dD, dz, dbias = torch.ops.mko.selscan_bwd(
-        dout.contiguous(), u, delta, A, B, C, D, z, bias, ctx.softplus, states)
+        dout.contiguous(), u, delta, A, B, C, D, z, bias, ctx.softplus, states, out)
     return (du, ddelta, dA, dB, dC, dD if D is not None else None, dz if z is not None else None,
             dbias if bias is not None else None, None)
 

@@ -165,6 +165,65 @@ def test_lane_forward_shapes_fp32(shape):
     _compare(inputs, dy, True, "lane " + "x".join(map(str, shape)))
 
 
+def _backward_kernels(inputs, dy, softplus=True):
+    """The library's kernels that one backward launches (their timing names)."""
+    from metal_kernelops import _native as nat
+    leaves = {k: (v.to(DEV).requires_grad_(True) if v is not None else None) for k, v in inputs.items()}
+    out = _selective_scan()(**leaves, delta_softplus=softplus)
+    torch.cuda.synchronize()
+    nat.kernel_timing_reset()
+    nat.kernel_timing(True)
+    try:
+        out.backward(dy.to(DEV))
+        torch.cuda.synchronize()
+        return set(nat.kernel_times())
+    finally:
+        nat.kernel_timing(False)
+
+
+@pytest.mark.parametrize("shape", [(2, 3072, 64, 16, 1), (1, 6200, 32, 16, 2), (2, 3072, 48, 12, 3)],
+                         ids=["groups-of-3072", "groups-of-3100", "dstate-12-groups-of-1024"])
+def test_lane_backward_kernel_is_taken_and_deterministic(shape):
+    # 6144+ channel rows, whole 16-step blocks, dstate <= 16 and groups a multiple of 4
+    # channels wide: one lane per (channel, state) walks the sequence backwards. Groups of a
+    # multiple of 16 channels add their dB/dC in 16-channel workgroup partials, others in
+    # 4-channel wavefront partials; both orders are fixed.
+    inputs, dy = _random_problem(*shape, seed=sum(shape) + 1)
+    assert "selscan_bwd_lane" in _backward_kernels(inputs, dy)
+    _compare(inputs, dy, True, "lane bwd " + "x".join(map(str, shape)))
+    runs = [_gpu(inputs, dy, True) for _ in range(2)]
+    for k in NAMES:
+        assert torch.equal(runs[0][1][k], runs[1][1][k]), k
+
+
+def test_lane_backward_where_the_gate_is_zero():
+    # Where silu(z) is exactly zero (z = 0, or z so negative that sigmoid underflows) the
+    # pre-gate output cannot come back from out / silu(z): those blocks sum C x over the
+    # states instead.  Spread such elements over a few blocks and channels.
+    inputs, dy = _random_problem(2, 3072, 64, 16, 1, seed=41, act=torch.bfloat16)
+    z = inputs["z"].clone()
+    z[0, 5, 17] = 0.0
+    z[1, 3000, 63] = -200.0
+    z[0, 100:104, 32:48] = 0.0
+    inputs["z"] = z
+    _compare(inputs, dy, True, "lane bwd, zero gates")
+
+
+def test_lane_backward_without_the_forward_output():
+    # A C-ABI caller may leave out NULL in the backward: dz then comes from the summed C x
+    # in every block, to the same result within rounding.
+    from metal_kernelops.scan import selscan_bwd_impl, selscan_fwd_impl
+    inputs, dy = _random_problem(2, 3072, 32, 16, 1, seed=43)
+    dev = {k: v.to(DEV) for k, v in inputs.items()}
+    args = [dev[k] for k in ("u", "dt", "A", "B", "C", "D", "z", "delta_bias")]
+    out, states = selscan_fwd_impl(*args, True)
+    with_out = selscan_bwd_impl(dy.to(DEV), *args, True, states, out)
+    without = selscan_bwd_impl(dy.to(DEV), *args, True, states, None)
+    for name, a, b in zip(("du", "ddelta", "dA", "dB", "dC", "dD", "dz", "dbias"), with_out, without):
+        e = record("lane bwd with/without out", name, norm_rel(a, b), 1e-5)
+        assert e <= 1e-5, name
+
+
 def test_unaligned_groups_take_the_chunked_forward():
     """Groups of 1550 channels (not a multiple of the 4 a lane-path wavefront shares): the
     chunked forward runs instead, to the same result."""
