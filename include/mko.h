@@ -119,8 +119,8 @@ int mko_selscan_fwd(const mko_selscan_params* p, void* stream);
 
 /* Replaces _Scan.backward (scan.py:257-280) and the autograd of the pre/post
  * ops: given dout and the forward's inputs and states, writes the gradients
- * listed above.  Deterministic when dim/ngroups is a multiple of 64; otherwise
- * dB/dC are accumulated with float atomics. */
+ * listed above.  Every sum (dB/dC over channels, dA/dD/ddelta_bias over batch and
+ * time) runs in a fixed order, so repeated runs are bit-identical. */
 size_t mko_selscan_bwd_workspace_size(const mko_selscan_params* p);
 int mko_selscan_bwd(const mko_selscan_params* p, void* stream);
 

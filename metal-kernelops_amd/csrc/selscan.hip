@@ -1379,10 +1379,14 @@ __global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
           for (int r = 0; r < 32; ++r) sum += trans[(r0 + r) * kTransPitch + col];
           acc[n * kWave + lane] = sum;
         } else {
-          // One sum per (segment, column) over the segment's rows, then one atomic
-          // each: lanes of one group no longer add into the same address one by one.
-          // Inactive lanes hold zeros (act = 0) and sit in the last row's segment.
-          for (int w = lane; w < nseg * 2 * HS; w += kWave) {
+          // One sum per (segment, column) over the segment's rows, stored in the partial
+          // slot of its (batch, group) that belongs to this wavefront: slot k of group bg
+          // is the k-th wavefront its rows [bg dg, (bg + 1) dg) meet, so every slot has one
+          // writer and reduce_bc adds them in slot order.  Inactive lanes hold zeros (act =
+          // 0) and sit in the last row's segment; a wavefront past the last row writes
+          // nothing (its clamped rows would name a slot beyond its group's).
+          const bool live = li.wave_row * kWave < g.rows;  // wave-uniform
+          for (int w = lane; live && w < nseg * 2 * HS; w += kWave) {
             const int sidx = w / (2 * HS), col = w % (2 * HS);
             const int i = col % HS, k = col / HS;
             if (i >= nv) continue;
@@ -1390,7 +1394,8 @@ __global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
             for (int r = seg_first[wave][sidx]; r < seg_first[wave][sidx + 1]; ++r)
               sum += trans[r * kTransPitch + col];
             const int64_t bgs = seg_bg[wave][sidx];
-            atomicAdd(p.pbc + ((bgs * g.length + qs + i) * NS + n) * 2 + k, sum);
+            const int64_t slot = bgs * g.ncb + (li.wave_row - bgs * g.dg / kWave);
+            p.pbc[((slot * g.length + qs + i) * NS + n) * 2 + k] = sum;
           }
         }
         wave_lds_sync();
@@ -1462,13 +1467,16 @@ __global__ void __launch_bounds__(256) bwd_main(Geo g, Ptrs p) {
 // dB/dC (bg, N, L) = sum over channel blocks of the partials (bg, ncb, L, NS, 2).
 // A workgroup covers 256/NS steps x NS states: it reads the partials contiguously
 // (state fastest) and writes through an LDS transpose so the stores run along L.
+// seg_dg != 0 (groups of seg_dg channels, not a multiple of 64 wide): group bg has one
+// partial per wavefront its rows meet, of the ncb slots laid out for each group.
 template <int NS>
-__global__ void __launch_bounds__(256) reduce_bc(Geo g, int ncb, const float* __restrict__ pbc,
+__global__ void __launch_bounds__(256) reduce_bc(Geo g, int ncb, int64_t seg_dg, const float* __restrict__ pbc,
                                                  void* dB, void* dC) {
   constexpr int TT = 256 / NS;
   __shared__ float sb[NS][TT + 1], sc[NS][TT + 1];
   const int64_t nt = (g.length + TT - 1) / TT;
   const int64_t bg = blockIdx.x / nt;
+  const int nsum = seg_dg ? static_cast<int>(((bg + 1) * seg_dg - 1) / kWave - bg * seg_dg / kWave + 1) : ncb;
   const int64_t t0 = (blockIdx.x % nt) * TT;
   const int tid = threadIdx.x;
   {
@@ -1482,7 +1490,7 @@ __global__ void __launch_bounds__(256) reduce_bc(Geo g, int ncb, const float* __
       const float2* src = reinterpret_cast<const float2*>(pbc + ((bg * ncb * g.length + t) * NS + n) * 2);
       const int64_t stride = g.length * NS;  // float2 elements between channel blocks
       int cbk = 0;
-      for (; cbk + PF <= ncb; cbk += PF) {
+      for (; cbk + PF <= nsum; cbk += PF) {
         float2 q[PF];
 #pragma unroll
         for (int j = 0; j < PF; ++j) q[j] = src[(cbk + j) * stride];
@@ -1492,7 +1500,7 @@ __global__ void __launch_bounds__(256) reduce_bc(Geo g, int ncb, const float* __
           vc += q[j].y;
         }
       }
-      for (; cbk < ncb; ++cbk) {
+      for (; cbk < nsum; ++cbk) {
         const float2 q = src[cbk * stride];
         vb += q.x;
         vc += q.y;
@@ -1583,11 +1591,6 @@ __global__ void __launch_bounds__(256) reduce_params(Geo g, int ns, const float*
   }
 }
 
-__global__ void zero_f32(float* p, int64_t n) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = 0.0f;
-}
-
 // ---------------------------------------------------------------- host plan
 
 struct Plan {
@@ -1674,7 +1677,7 @@ static int make_plan(const mko_selscan_params* p, Plan* pl) {
     g.ncb = static_cast<int>(g.dg / (static_cast<int64_t>(g.wpg) * kWave));
   } else {
     g.wpg = 4;
-    g.ncb = 1;
+    g.ncb = static_cast<int>((g.dg + kWave - 1) / kWave + 1);  // wavefronts a group's rows can meet
   }
   // Coarse chunks: about eight wavefronts per SIMD over the chip's 1024 SIMDs
   // (the state-inner loops hide their scalar-load waits with other waves), the
@@ -1839,7 +1842,7 @@ static int launch_bwd_lane(const Plan& pl, const Ptrs& q0, const mko_selscan_par
   g.nchunks = 1;
   MKO_TIMED("selscan_bwd_reduce", s,
             reduce_bc<16><<<static_cast<unsigned>(g.batch * g.ngroups * ((g.length + 256 / 16 - 1) / (256 / 16))),
-                            256, 0, s>>>(g, static_cast<int>(pl.lncb), q.pbc, p->dB, p->dC);
+                            256, 0, s>>>(g, static_cast<int>(pl.lncb), 0, q.pbc, p->dB, p->dC);
             reduce_params<<<static_cast<unsigned>((g.dstate + 1) * ((g.dim + 63) / 64)), 256, 0, s>>>(
                 g, 16, q.dap, q.ddp, q.dbp, p->dA, p->dD, p->ddelta_bias));
   return mko_check_launch("selscan_bwd");
@@ -1867,17 +1870,13 @@ static int launch_bwd(const Plan& pl, const Ptrs& q, const mko_selscan_params* p
               chain_wave<true><<<blocks_for(g.rows * g.dstate, 4), 256, 0, s>>>(g, q.A, q.drive, q.sumd, q.adj));
   else
     MKO_TIMED("selscan_chain", s, chain<true><<<blocks_for(g.rows * g.dstate), 256, 0, s>>>(g, q.A, q.drive, q.sumd, q.adj));
-  if (!UNI) {
-    const int64_t n = bgl * NS * 2;
-    MKO_TIMED("selscan_zero", s, zero_f32<<<blocks_for(n), 256, 0, s>>>(q.pbc, n));
-  }
   if (g.dstate == NS)
     MKO_TIMED("selscan_bwd_main", s, bwd_main<NS, UNI, true><<<dim3(gx, g.nchunks), block, 0, s>>>(g, q));
   else
     MKO_TIMED("selscan_bwd_main", s, bwd_main<NS, UNI, false><<<dim3(gx, g.nchunks), block, 0, s>>>(g, q));
   MKO_TIMED("selscan_bwd_reduce", s,
             reduce_bc<NS><<<static_cast<unsigned>(g.batch * g.ngroups * ((g.length + 256 / NS - 1) / (256 / NS))),
-                            256, 0, s>>>(g, UNI ? g.ncb : 1, q.pbc, p->dB, p->dC);
+                            256, 0, s>>>(g, g.ncb, UNI ? 0 : g.dg, q.pbc, p->dB, p->dC);
             reduce_params<<<static_cast<unsigned>((g.dstate + 1) * ((g.dim + 63) / 64)), 256, 0, s>>>(
                 g, NS, q.dap, q.ddp, q.dbp, p->dA, p->dD, p->ddelta_bias));
   return mko_check_launch("selscan_bwd");

@@ -12,9 +12,9 @@ Public surface, as in dbydd/metal-kernelops ``scan.py:283-329``:
 Differences from the reference, all widenings: the discretisation, the ``D`` skip
 and the ``silu(z)`` gate run inside the kernel instead of as separate torch ops
 (``scan.py:311-319``); u/z/B/C may be float16 or bfloat16 (computed in float32,
-rounded once on the store); B/C/dB/dC are reduced deterministically (the
-reference uses float atomics, ``scan.py:226-227``) whenever ``dim / ngroups`` is a
-multiple of 64.  The backward is once-differentiable, as in the reference
+rounded once on the store); dB/dC are summed over channels in a fixed order (the
+reference adds them with float atomics, ``scan.py:226-227``), so the backward is
+bit-deterministic.  The backward is once-differentiable, as in the reference
 (``scan.py:258``).  Tensors must live on a ROCm GPU; there is no CPU path.
 """
 
@@ -28,11 +28,16 @@ from torch import Tensor
 
 from . import _native as nat
 
-CHUNK = 64
-"""Steps between the scan states the forward saves for the backward."""
+CHUNK = 16
+"""Steps between the scan states the forward saves for the backward, which recomputes each
+16-step block from its saved state (the reference's CHUNK, 64, is its replay chunk and
+per-thread history length)."""
 
-BLOCK = 64
-"""Channels per wavefront: the lanes that share one B_t/C_t and reduce dB/dC together."""
+BLOCK = 16
+"""Channels whose dB/dC terms the backward adds inside one workgroup before it writes a
+partial sum (the lane-per-state backward; groups whose width is not a multiple of 16 use
+4-channel partials).  The reference's BLOCK, 8, plays the same role for its threadgroups.
+Informational: the kernels choose their own reduction widths from the shapes."""
 
 _SOFTPLUS = 1
 _FLOATS = (torch.float32, torch.float16, torch.bfloat16)

@@ -274,12 +274,20 @@ def test_partial_reductions_whole_batches_and_tail():
     _compare(inputs, dy, True, "2x2304x256")
 
 
-def test_deterministic_backward():
-    inputs, dy = _random_problem(2, 256, 300, 16, 1, seed=12)
-    runs = [_gpu(inputs, dy, True) for _ in range(2)]
-    assert torch.equal(runs[0][0], runs[1][0])
-    for k in NAMES:
-        assert torch.equal(runs[0][1][k], runs[1][1][k]), k
+@pytest.mark.parametrize("shape", [(2, 256, 300, 16, 1), (2, 8, 64, 16, 2), (1, 384, 784, 16, 4),
+                                   (3, 24, 77, 20, 3)],
+                         ids=["groups-of-256", "c1-groups-of-4", "groups-of-96", "groups-of-8-dstate-20"])
+def test_deterministic_backward(shape):
+    # Bit-identical reruns for every group width: 64-multiple groups, and groups narrower or
+    # wider than a wavefront whose rows meet several wavefronts (the c1 geometry, 4 channels a
+    # group; the ss2d bench's 96).
+    inputs, dy = _random_problem(*shape, seed=12)
+    runs = [_gpu(inputs, dy, True) for _ in range(3)]
+    for r in runs[1:]:
+        assert torch.equal(runs[0][0], r[0])
+        for k in NAMES:
+            assert torch.equal(runs[0][1][k], r[1][k]), k
+    _compare(inputs, dy, True, "determinism " + "x".join(map(str, shape)))
 
 
 def _layer_channel_subset(case, batch, dim, length, stride):
