@@ -37,6 +37,9 @@ import torch  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, published
 BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, published
+# Vector ALU issue: 256 CUs x 4 SIMDs x 16 lanes x 2.4 GHz, one wave64 instruction per SIMD per
+# 4 cycles (transcendentals take longer, so this is an upper bound for them)
+VALU_PEAK_TLANE_OPS = 256 * 4 * 16 * 2.4e9 / 1e12
 METRIC = "selective-scan fwd+bwd GB/s (% HBM peak); Mamba-2 SSD tokens/s (% MFMA peak)"
 
 
@@ -102,6 +105,23 @@ def load_traffic(name):
         return json.load(f).get(name)
 
 
+def valu_roofline(name, avg_ms):
+    """The dominant kernel against the vector-ALU issue rate: its wave VALU instructions per
+    launch (SQ_INSTS_VALU from a committed PMC summary, profiles/valu.json) x 64 lanes over
+    its measured launch time."""
+    path = os.path.join(ROOT, "profiles", "valu.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        insts = json.load(f).get(name)
+    if insts is None:
+        return None
+    achieved = insts * 64 / (avg_ms * 1e-3) / 1e12
+    return {"bound": "valu", "achieved": round(achieved, 2), "peak": round(VALU_PEAK_TLANE_OPS, 2),
+            "unit": "T lane-ops/s", "frac": round(achieved / VALU_PEAK_TLANE_OPS, 4),
+            "valu_insts_per_launch": insts}
+
+
 # --------------------------------------------------------------------- Mamba-1
 
 
@@ -121,15 +141,19 @@ def mamba1_case(batch, dim, length, steps, warmup, seed=0):
     ms, wall, kernels = timed(step, steps, warmup)
     fwd_b, bwd_b = mamba1_bytes(batch, dim, length, 16, 1)
     name, avg, count = dominant(kernels)
-    per_kernel = {"selscan_bwd_main": bwd_b, "selscan_fwd_replay": fwd_b}
-    roof = roofline(per_kernel.get(name, fwd_b + bwd_b), avg, load_traffic(f"{name}@{batch}x{dim}x{length}"))
+    # each direction's algorithmic bytes belong to its main kernel
+    per_kernel = {"selscan_bwd_lane": bwd_b, "selscan_bwd_main": bwd_b, "selscan_fwd_lane": fwd_b,
+                  "selscan_fwd_replay": fwd_b}
+    tag = f"{name}@{batch}x{dim}x{length}"
+    roof = roofline(per_kernel.get(name, fwd_b + bwd_b), avg, load_traffic(tag))
     roof["kernel"] = name
     roof["algorithmic_bytes"] = per_kernel.get(name, fwd_b + bwd_b)
+    valu = valu_roofline(tag, avg)
     del leaves, dout
     torch.cuda.empty_cache()
     return {
         "ms_per_step": ms, "wall_ms_per_step": wall, "gbs": (fwd_b + bwd_b) / (ms * 1e-3) / 1e9,
-        "bytes_per_step": fwd_b + bwd_b, "roofline": roof,
+        "bytes_per_step": fwd_b + bwd_b, "roofline": roof, "roofline_valu": valu,
         "kernels_ms": {k: round(v[0] / max(v[1], 1), 4) for k, v in sorted(kernels.items())},
     }
 
@@ -675,7 +699,7 @@ def main():
     ap.add_argument("--skip-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--only", choices=["mamba1", "ssd", "decode", "ss2d", "conv1d", "norm", "block", "copy", "all"],
                     default="all",
-                    help="one workload (mamba1 = the config-3 headline alone) or all of them; copy = "
+                    help="one workload (mamba1 = the config-3 headline and config 2) or all of them; copy = "
                          "a plain 1 GiB device copy, the calibration point of the PMC byte counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -731,13 +755,13 @@ def main():
         log("mamba1 config 3 (4x5120x4096) fwd+bwd")
         head = mamba1_case(4, 5120, 4096, args.steps, args.warmup)
         log(f"  {head['ms_per_step']:.3f} ms/step, {head['gbs']:.1f} GB/s; kernels {head['kernels_ms']}")
-    if args.only == "all":
         log("mamba1 config 2 (8x1536x2048) fwd+bwd")
         c2 = mamba1_case(8, 1536, 2048, args.steps, args.warmup)
         also["mamba1_130m_layer_fwd_bwd"] = {
             "value": round(c2["gbs"], 1), "unit": "GB/s", "ms_per_step": round(c2["ms_per_step"], 4),
             "config": {"batch": 8, "dim": 1536, "seqlen": 2048, "dstate": 16, "ngroups": 1},
-            "roofline": c2["roofline"], "kernels_ms": c2["kernels_ms"]}
+            "hbm_frac_whole_step": round(c2["gbs"] / HBM_PEAK_GBS, 4),
+            "roofline": c2["roofline"], "roofline_valu": c2["roofline_valu"], "kernels_ms": c2["kernels_ms"]}
         log(f"  {c2['ms_per_step']:.3f} ms/step, {c2['gbs']:.1f} GB/s")
     if want("decode"):
         log("mamba2 decode config 5 (256x80x64x128), 1024 in-place steps")
@@ -829,6 +853,7 @@ def main():
                    "delta_dtype": "f32", "state_dtype": "f32",
                    "hbm_frac_whole_step": round(head["gbs"] / HBM_PEAK_GBS, 4)},
         "roofline": head["roofline"],
+        "roofline_valu": head["roofline_valu"],
         "cpu_baseline": cpu,
         "kernels_ms": head["kernels_ms"],
         "also": also,
