@@ -176,6 +176,152 @@ __global__ void __launch_bounds__(256) chunk_scan(Geo g, Ptrs p) {
   });
 }
 
+// Stage k of a chunk's schedule: token tile i, then its state stages kk < nnt and its
+// intra stages kk = nnt + j, j = 0 .. i (nnt + i + 1 stages for tile i).
+struct ScanStage {
+  int i, kk;
+};
+constexpr ScanStage scan_stage(int k, int nnt) {
+  int i = 0, base = 0;
+  while (k >= base + nnt + i + 1) {
+    base += nnt + i + 1;
+    ++i;
+  }
+  return ScanStage{i, k - base};
+}
+
+// One workgroup per (b, h, chunk, d_head tile) for all QB 64-token tiles of the chunk
+// (16-bit operands, d_state <= 64 * NNT).  The chunk's u = step x tiles (transposed) and
+// its entering state tiles are staged into LDS once and serve every token tile; only the
+// left operand is staged per stage:
+//   state stages (kk < NNT): C rows of tile i as they are in memory, times S_in; the row
+//     factor e^{cs_l} (at most 1) is applied to the accumulator after the last of them
+//   intra stages (kk = NNT + j, j = 0 .. i): K[l][s] from the C.B^T tile (k_block), times u_j.
+// The schedule is fixed at compile time.  Tile i's x and z rows are requested at its first
+// stage, for its epilogue.
+template <typename TM, bool VEC, int QB, int NNT>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) chunk_scan_mt(Geo g, Ptrs p) {
+  static_assert(sizeof(TM) == 2, "16-bit operands");
+  constexpr int TE = LdsTile<TM>::elems;
+  constexpr int N = QB * NNT + QB * (QB + 1) / 2;
+  constexpr int Q = 64 * QB;
+  __shared__ __align__(16) TM ut[QB][TE];   // u_j^T [p][s]
+  __shared__ __align__(16) TM st[NNT][TE];  // S_in [p][n], n-tile k
+  __shared__ __align__(16) TM ab[2][TE];    // left operand, double-buffered; the epilogue's fp32 tile
+  __shared__ __align__(16) float csc[Q], dlc[Q], ecol[Q], ecs[Q], dcol[64];
+  const WgId id = wg_id(g.nheads, g.npt);
+  const int64_t h = id.x;
+  const int pt = id.y;
+  const int64_t b = id.z / g.nc;
+  const int c = static_cast<int>(id.z % g.nc);
+  const int64_t bh = b * g.nheads + h, gg = h / g.hpg;
+  const int lane = threadIdx.x & 63;
+  int wm, wn;
+  quadrant(threadIdx.x >> 6, wm, wn);
+  const int r0 = blk_r0(), c0 = blk_c0();
+  const int64_t tc = static_cast<int64_t>(c) * Q, pc0 = static_cast<int64_t>(pt) * 64;
+  const TM* X = static_cast<const TM*>(p.x);
+  const TM* Z = p.z ? static_cast<const TM*>(p.z) : X;
+  const TM* Cm = static_cast<const TM*>(p.C);
+  const TM* cbt = static_cast<const TM*>(p.cb) + ((b * g.nc + c) * g.ngroups + gg) * Q * Q;
+  const TM* S = static_cast<const TM*>(p.states) + (bh * g.nc + c) * g.headdim * g.dstate;
+  {
+    // the chunk's x tiles and entering state
+    V8<TM> xr[QB][2], sr[NNT][2];
+#pragma unroll
+    for (int j = 0; j < QB; ++j) load_xw<TM, VEC>(g, X, b, tc + 64 * j, h, pc0, xr[j]);
+#pragma unroll
+    for (int k = 0; k < NNT; ++k) load_sw<TM, VEC>(g, S, pc0, 64 * k, sr[k]);
+    load_chunk_cs(g, p, bh, c, csc, dlc, ecol);
+    if (threadIdx.x < Q) ecs[threadIdx.x] = fast_exp(csc[threadIdx.x]);
+    if (threadIdx.x < 64) {
+      const int64_t pp = pc0 + threadIdx.x;
+      dcol[threadIdx.x] = !p.D ? 0.0f : g.d_per_row ? (pp < g.headdim ? p.D[h * g.headdim + pp] : 0.0f) : p.D[h];
+    }
+    __syncthreads();  // csc, dlc
+#pragma unroll
+    for (int j = 0; j < QB; ++j) {
+      float a[8], bb[8];
+      scale8(xr[j][0], dlc[64 * j + r0], a);
+      scale8(xr[j][1], dlc[64 * j + r0 + 1], bb);
+      put2x8<TM, true>(ut[j], r0, c0, a, bb);  // Bt[p][s] = step_s x_s[p]
+    }
+#pragma unroll
+    for (int k = 0; k < NNT; ++k) put_raw<TM, false>(st[k], r0, c0, sr[k][0], sr[k][1]);  // Bt[p][n] = S_in[p][n]
+  }
+  struct Regs {
+    V8<TM> a[2];
+  };
+  auto fetch = [&](auto kc, Regs& r) {
+    constexpr ScanStage sg = scan_stage(decltype(kc)::value, NNT);
+    if constexpr (sg.kk < NNT)
+      load_bw<TM, VEC>(g, Cm, b, tc + 64 * sg.i, gg, 64 * sg.kk, r.a);  // C rows l
+    else
+      load_win<TM, true>(cbt + (64 * sg.i) * Q + 64 * (sg.kk - NNT), Q, 64, 64, r.a, cbt);  // cb rows l
+  };
+  auto put = [&](auto kc, Regs& r) {
+    constexpr int k = decltype(kc)::value;
+    constexpr ScanStage sg = scan_stage(k, NNT);
+    if constexpr (sg.kk < NNT) {
+      put_raw<TM, false>(ab[k & 1], r0, c0, r.a[0], r.a[1]);  // A[l][n] = C_l[n]
+    } else {
+      float a[8], bb[8];
+      k_block<TM>(r.a[0], r.a[1], csc, ecol, sg.i, sg.kk - NNT, r0, c0, a, bb);
+      put2x8<TM, false>(ab[k & 1], r0, c0, a, bb);  // A[l][s] = K[l][s]
+    }
+  };
+  f32x16 acc;
+  zero(acc);
+  V8<TM> xv[2], zv[2];
+  Regs regs[2];
+  pipeline2_static<N>(regs, fetch, put, [&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    constexpr ScanStage sg = scan_stage(k, NNT);
+    const int64_t tl0 = tc + 64 * sg.i;
+    if constexpr (sg.kk == 0) {  // epilogue inputs of tile i
+      load_xw<TM, VEC>(g, X, b, tl0, h, pc0, xv);
+      load_xw<TM, VEC>(g, Z, b, tl0, h, pc0, zv);
+    }
+    if constexpr (sg.kk < NNT) {
+      mma_tile<TM>(acc, ab[k & 1], st[sg.kk], wm, wn, lane, 64);
+      if constexpr (sg.kk == NNT - 1) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] *= ecs[64 * sg.i + acc_row(wm, lane, r)];
+      }
+    } else {
+      mma_tile<TM>(acc, ab[k & 1], ut[sg.kk - NNT], wm, wn, lane, 64);
+      if constexpr (sg.kk == NNT + sg.i) {
+        // epilogue of tile i: both operand buffers hold the fp32 tile once every wave is done
+        float* red = reinterpret_cast<float*>(&ab[0][0]);
+        __syncthreads();
+        acc_to_lds(red, acc, wm, wn, lane);
+        zero(acc);
+        __syncthreads();
+        float v[2][8];
+        lds_block(red, r0, c0, v[0], v[1]);
+        if (p.yt) store_xw<float, VEC>(g, p.yt, b, tl0, h, pc0, v[0], v[1]);
+        const float4 da = *reinterpret_cast<const float4*>(dcol + c0);
+        const float4 db = *reinterpret_cast<const float4*>(dcol + c0 + 4);
+        const float dv[8] = {da.x, da.y, da.z, da.w, db.x, db.y, db.z, db.w};
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+          float xf[8], zf[8];
+          v8_f32(xv[rr], xf);
+          if (p.z) v8_f32(zv[rr], zf);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            float y = fmaf(dv[e], xf[e], v[rr][e]);
+            if (p.z) y *= zf[e] * sigmoid(zf[e]);
+            v[rr][e] = y;
+          }
+        }
+        store_xw<TM, VEC>(g, static_cast<TM*>(p.y), b, tl0, h, pc0, v[0], v[1]);
+        if constexpr (k + 1 < N) __syncthreads();  // the next stage refills the operand buffers
+      }
+    }
+  });
+}
+
 // ---------------------------------------------------------------- host
 
 int make_geo(const mko_ssd_params* prm, Geo* g) {
@@ -294,6 +440,18 @@ static void launch_fwd_t(const Geo& g, const Ptrs& q, hipStream_t s) {
   MKO_TIMED("ssd_state_pass", s,
             state_pass<TM><<<dim3(static_cast<unsigned>((g.headdim * g.dstate + 2047) / 2048), bh), 256, 0, s>>>(
                 g, q));
+  if constexpr (sizeof(TM) == 2) {
+    const dim3 grid(g.npt * g.nc * bh);
+    if (g.nnt <= 2 && (g.qb == 4 || g.qb == 2 || g.qb == 1)) {
+      if (g.qb == 4 && g.nnt == 2) MKO_TIMED("ssd_chunk_scan", s, chunk_scan_mt<TM, VEC, 4, 2><<<grid, 256, 0, s>>>(g, q));
+      else if (g.qb == 4) MKO_TIMED("ssd_chunk_scan", s, chunk_scan_mt<TM, VEC, 4, 1><<<grid, 256, 0, s>>>(g, q));
+      else if (g.qb == 2 && g.nnt == 2) MKO_TIMED("ssd_chunk_scan", s, chunk_scan_mt<TM, VEC, 2, 2><<<grid, 256, 0, s>>>(g, q));
+      else if (g.qb == 2) MKO_TIMED("ssd_chunk_scan", s, chunk_scan_mt<TM, VEC, 2, 1><<<grid, 256, 0, s>>>(g, q));
+      else if (g.nnt == 2) MKO_TIMED("ssd_chunk_scan", s, chunk_scan_mt<TM, VEC, 1, 2><<<grid, 256, 0, s>>>(g, q));
+      else MKO_TIMED("ssd_chunk_scan", s, chunk_scan_mt<TM, VEC, 1, 1><<<grid, 256, 0, s>>>(g, q));
+      return;
+    }
+  }
   MKO_TIMED("ssd_chunk_scan", s, chunk_scan<TM, VEC><<<dim3(g.qb * g.npt * g.nc * bh), 256, 0, s>>>(g, q));
 }
 

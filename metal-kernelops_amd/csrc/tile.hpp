@@ -265,6 +265,34 @@ __device__ __forceinline__ void pipeline2(int n, Regs& ra, Regs& rb, Fetch&& fet
   }
 }
 
+// f(Int<K>{}) for K = B .. E-1, each call with K a compile-time constant.
+template <int K>
+struct Int {
+  static constexpr int value = K;
+};
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(Int<B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+// pipeline2 over a stage count known at compile time: every stage index is a constant, so
+// a stage schedule that depends only on it compiles to straight-line code.
+template <int N, class Regs, class Fetch, class Put, class Mma>
+__device__ __forceinline__ void pipeline2_static(Regs (&r)[2], Fetch&& fetch, Put&& put, Mma&& mma) {
+  fetch(Int<0>{}, r[0]);
+  if constexpr (N > 1) fetch(Int<1>{}, r[1]);
+  static_for<0, N>([&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    put(kc, r[k & 1]);
+    __syncthreads();
+    if constexpr (k + 2 < N) fetch(Int<k + 2>{}, r[k & 1]);
+    mma(kc);
+  });
+}
+
 // As pipeline2, but the fetches past the last stage load stage n -- the epilogue's
 // inputs -- instead of repeating stage n-1, and epi(regs) is called at the end with the
 // set that holds them (even n: both do; odd n: rb).  Two call sites instead of a select
