@@ -197,8 +197,9 @@ constexpr ScanStage scan_stage(int k, int nnt) {
 //   state stages (kk < NNT): C rows of tile i as they are in memory, times S_in; the row
 //     factor e^{cs_l} (at most 1) is applied to the accumulator after the last of them
 //   intra stages (kk = NNT + j, j = 0 .. i): K[l][s] from the C.B^T tile (k_block), times u_j.
-// The schedule is fixed at compile time.  Tile i's x and z rows are requested at its first
-// stage, for its epilogue.
+// The schedule is fixed at compile time, and each stage's left operand is requested six
+// stages ahead (LDS holds the workgroup to two per CU, so the latency must be hidden by the
+// prefetch).  Tile i's x and z rows are requested at its first stage, for its epilogue.
 template <typename TM, bool VEC, int QB, int NNT>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) chunk_scan_mt(Geo g, Ptrs p) {
   static_assert(sizeof(TM) == 2, "16-bit operands");
@@ -273,8 +274,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) c
   f32x16 acc;
   zero(acc);
   V8<TM> xv[2], zv[2];
-  Regs regs[2];
-  pipeline2_static<N>(regs, fetch, put, [&](auto kc) {
+  constexpr int D = N < 6 ? N : 6;  // stages of prefetch
+  Regs regs[D];
+  pipeline_static<N, D>(regs, fetch, put, [&](auto kc) {
     constexpr int k = decltype(kc)::value;
     constexpr ScanStage sg = scan_stage(k, NNT);
     const int64_t tl0 = tc + 64 * sg.i;

@@ -360,6 +360,183 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) d
   });
 }
 
+// Stage k of du_mt's schedule: s-tile j, then its state stages kk < nnt and its intra
+// stages kk = nnt + m over the l-tiles i = j + m, m = 0 .. qb-1-j (nnt + qb - j stages).
+struct DuStage {
+  int j, kk;
+};
+constexpr DuStage du_stage(int k, int nnt, int qb) {
+  int j = 0, base = 0;
+  while (k >= base + nnt + qb - j) {
+    base += nnt + qb - j;
+    ++j;
+  }
+  return DuStage{j, k - base};
+}
+
+// du for all QB 64-token tiles of one (b, h, chunk, d_head tile), 16-bit operands and
+// d_state <= 64 * NNT:
+//   du[s][p] = e^{T - cs_s} sum_n B_s[n] G[p][n]  +  sum_{l >= s} K[l][s] gy_l[p]
+// gy (transposed) and G of the chunk are staged into LDS once; per stage only the left
+// operand is: B rows as they are in memory for the state stages (the row factor
+// e^{T - cs_s}, at most 1, is applied to the accumulator after the last of them), K^T from
+// the C.B^T tile for the intra stages.  The schedule is fixed at compile time and each
+// left operand is requested six stages ahead.  Per s-tile: tau_s = u_s . du_state_s after
+// the state stages, then dx = step du + D gy and the row sums x.du and u.du.
+template <typename TM, bool VEC, int QB, int NNT>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) du_mt(Geo g, BwdPlan pl, Ptrs p) {
+  static_assert(sizeof(TM) == 2, "16-bit operands");
+  constexpr int TE = LdsTile<TM>::elems;
+  constexpr int N = QB * NNT + QB * (QB + 1) / 2;
+  constexpr int Q = 64 * QB;
+  __shared__ __align__(16) TM gyt[QB][TE];  // gy_l^T [p][l]
+  __shared__ __align__(16) TM gt[NNT][TE];  // G [p][n]
+  __shared__ __align__(16) TM ab[2][TE];    // left operand, double-buffered; the fp32 tile of the epilogues
+  __shared__ __align__(16) float csc[Q], dlc[Q], ecol[Q], ew[Q], dcol[64];
+  const WgId id = wg_id(g.nheads, g.npt);
+  const int64_t h = id.x;
+  const int pt = id.y;
+  const int64_t b = id.z / g.nc;
+  const int c = static_cast<int>(id.z % g.nc);
+  const int64_t bh = b * g.nheads + h, gg = h / g.hpg;
+  const int lane = threadIdx.x & 63;
+  int wm, wn;
+  quadrant(threadIdx.x >> 6, wm, wn);
+  const int r0 = blk_r0(), c0 = blk_c0();
+  const int64_t tc = static_cast<int64_t>(c) * Q, pc0 = static_cast<int64_t>(pt) * 64;
+  const TM* X = static_cast<const TM*>(p.x);
+  const TM* gy = static_cast<const TM*>(p.gy);
+  const TM* Bm = static_cast<const TM*>(p.B);
+  const TM* cbt = static_cast<const TM*>(p.cb) + ((b * g.nc + c) * g.ngroups + gg) * Q * Q;
+  const TM* G = static_cast<const TM*>(p.dstates) + (bh * g.nc + c) * g.headdim * g.dstate;
+  const int64_t so = (bh * g.nc + c) * Q;
+  {
+    V8<TM> gr[QB][2], sr[NNT][2];
+#pragma unroll
+    for (int i = 0; i < QB; ++i) load_xw<TM, VEC>(g, gy, b, tc + 64 * i, h, pc0, gr[i]);
+#pragma unroll
+    for (int k = 0; k < NNT; ++k) load_sw<TM, VEC>(g, G, pc0, 64 * k, sr[k]);
+    load_chunk_cs(g, p, bh, c, csc, dlc, ecol);
+    if (threadIdx.x < Q) ew[threadIdx.x] = fast_exp(p.cs[so + Q - 1] - p.cs[so + threadIdx.x]);
+    if (threadIdx.x < 64) {
+      const int64_t pp = pc0 + threadIdx.x;
+      dcol[threadIdx.x] = !p.D ? 0.0f : g.d_per_row ? (pp < g.headdim ? p.D[h * g.headdim + pp] : 0.0f) : p.D[h];
+    }
+#pragma unroll
+    for (int i = 0; i < QB; ++i) put_raw<TM, true>(gyt[i], r0, c0, gr[i][0], gr[i][1]);  // Bt[p][l] = gy_l[p]
+#pragma unroll
+    for (int k = 0; k < NNT; ++k) put_raw<TM, false>(gt[k], r0, c0, sr[k][0], sr[k][1]);  // Bt[p][n] = G[p][n]
+    __syncthreads();  // csc, dlc, ecol, ew, dcol (the tiles are published by the first stage's barrier)
+  }
+  struct Regs {
+    V8<TM> a[2];
+  };
+  auto fetch = [&](auto kc, Regs& r) {
+    constexpr DuStage sg = du_stage(decltype(kc)::value, NNT, QB);
+    if constexpr (sg.kk < NNT) {
+      load_bw<TM, VEC>(g, Bm, b, tc + 64 * sg.j, gg, 64 * sg.kk, r.a);  // B rows s
+    } else {
+      constexpr int i = sg.j + sg.kk - NNT;
+      load_win<TM, true>(cbt + (64 * i) * Q + 64 * sg.j, Q, 64, 64, r.a, cbt);  // cb rows l
+    }
+  };
+  auto put = [&](auto kc, Regs& r) {
+    constexpr int k = decltype(kc)::value;
+    constexpr DuStage sg = du_stage(k, NNT, QB);
+    if constexpr (sg.kk < NNT) {
+      put_raw<TM, false>(ab[k & 1], r0, c0, r.a[0], r.a[1]);  // A[s][n] = B_s[n]
+    } else {
+      float a[8], bb[8];
+      k_block<TM>(r.a[0], r.a[1], csc, ecol, sg.j + sg.kk - NNT, sg.j, r0, c0, a, bb);
+      put2x8<TM, true>(ab[k & 1], r0, c0, a, bb);  // A[s][l] = K[l][s]
+    }
+  };
+  // x of tile j's rows s = r0, r0+1 and u_s = R(step_s x_s), the rounded input of the forward's products
+  auto u8 = [&](int j, const V8<TM> (&xv)[2], int rr, float (&xf)[8], float (&uf)[8]) {
+    v8_f32(xv[rr], xf);
+    const float d = dlc[64 * j + r0 + rr];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) uf[e] = to_f32(from_f32<TM>(d * xf[e]));
+  };
+  const int64_t po0 = ((bh * g.nc + c) * g.npt + pt) * Q;
+  float* red = reinterpret_cast<float*>(&ab[0][0]);
+  f32x16 acc;
+  zero(acc);
+  V8<TM> xv[2], gv[2];
+  constexpr int D = N < 6 ? N : 6;
+  Regs regs[D];
+  pipeline_static<N, D>(regs, fetch, put, [&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    constexpr DuStage sg = du_stage(k, NNT, QB);
+    constexpr int j = sg.j;
+    const int64_t ts0 = tc + 64 * j;
+    if constexpr (sg.kk == 0) {  // tile j's x (tau, epilogue) and gy (epilogue)
+      load_xw<TM, VEC>(g, X, b, ts0, h, pc0, xv);
+      load_xw<TM, VEC>(g, gy, b, ts0, h, pc0, gv);
+    }
+    if constexpr (sg.kk < NNT) {
+      mma_tile<TM>(acc, ab[k & 1], gt[sg.kk], wm, wn, lane, 64);
+      if constexpr (sg.kk == NNT - 1) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] *= ew[64 * j + acc_row(wm, lane, r)];
+        // tau_s = u_s . du_state_s
+        __syncthreads();
+        acc_to_lds(red, acc, wm, wn, lane);
+        __syncthreads();
+        float v[2][8];
+        lds_block(red, r0, c0, v[0], v[1]);
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+          float xf[8], uf[8];
+          u8(j, xv, rr, xf, uf);
+          float tau = 0.0f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) tau = fmaf(uf[e], v[rr][e], tau);
+          tau = row8_sum(tau);
+          if ((threadIdx.x & 7) == 0) p.tau[po0 + 64 * j + r0 + rr] = tau;
+        }
+        __syncthreads();  // the next stage refills the operand buffers
+      }
+    } else {
+      mma_tile<TM>(acc, ab[k & 1], gyt[j + sg.kk - NNT], wm, wn, lane, 64);
+      if constexpr (j + sg.kk - NNT == QB - 1) {
+        // dx = step du + D gy, and the row sums x.du and u.du of tile j
+        __syncthreads();
+        acc_to_lds(red, acc, wm, wn, lane);
+        zero(acc);
+        __syncthreads();
+        float du[2][8], dxo[2][8];
+        lds_block(red, r0, c0, du[0], du[1]);
+        const float4 da = *reinterpret_cast<const float4*>(dcol + c0);
+        const float4 db = *reinterpret_cast<const float4*>(dcol + c0 + 4);
+        const float dv[8] = {da.x, da.y, da.z, da.w, db.x, db.y, db.z, db.w};
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+          float gf[8], xf[8], uf[8];
+          v8_f32(gv[rr], gf);
+          u8(j, xv, rr, xf, uf);
+          const float d = dlc[64 * j + r0 + rr];
+          float sx = 0.0f, su = 0.0f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            dxo[rr][e] = fmaf(dv[e], gf[e], d * du[rr][e]);
+            sx = fmaf(xf[e], du[rr][e], sx);
+            su = fmaf(uf[e], du[rr][e], su);
+          }
+          sx = row8_sum(sx);
+          su = row8_sum(su);
+          if ((threadIdx.x & 7) == 0) {
+            p.dsx[po0 + 64 * j + r0 + rr] = sx;
+            p.ut[po0 + 64 * j + r0 + rr] = su;
+          }
+        }
+        store_xw<TM, VEC>(g, static_cast<TM*>(p.dx), b, ts0, h, pc0, dxo[0], dxo[1]);
+        if constexpr (k + 1 < N) __syncthreads();  // the next stage refills the operand buffers
+      }
+    }
+  });
+}
+
 // Adjoint of C.B^T for one lower tile (i, j) of a chunk, summed over a block of the
 // group's heads: sum_h (gy_i u_j^T) o e^{cs_l - cs_s}.
 template <typename TM, bool VEC>
@@ -803,6 +980,24 @@ BwdLayout bwd_layout(const Geo& g, const BwdPlan& pl, bool has_z) {
 }
 
 template <typename TM, bool VEC>
+void launch_du(const Geo& g, const BwdPlan& pl, const Ptrs& q, hipStream_t s) {
+  const unsigned bh = static_cast<unsigned>(g.batch * g.nheads);
+  if constexpr (sizeof(TM) == 2) {
+    const dim3 grid(g.npt * g.nc * bh);
+    if (g.nnt <= 2) {
+      if (g.qb == 4 && g.nnt == 2) MKO_TIMED("ssd_du", s, du_mt<TM, VEC, 4, 2><<<grid, 256, 0, s>>>(g, pl, q));
+      else if (g.qb == 4) MKO_TIMED("ssd_du", s, du_mt<TM, VEC, 4, 1><<<grid, 256, 0, s>>>(g, pl, q));
+      else if (g.qb == 2 && g.nnt == 2) MKO_TIMED("ssd_du", s, du_mt<TM, VEC, 2, 2><<<grid, 256, 0, s>>>(g, pl, q));
+      else if (g.qb == 2) MKO_TIMED("ssd_du", s, du_mt<TM, VEC, 2, 1><<<grid, 256, 0, s>>>(g, pl, q));
+      else if (g.nnt == 2) MKO_TIMED("ssd_du", s, du_mt<TM, VEC, 1, 2><<<grid, 256, 0, s>>>(g, pl, q));
+      else MKO_TIMED("ssd_du", s, du_mt<TM, VEC, 1, 1><<<grid, 256, 0, s>>>(g, pl, q));
+      return;
+    }
+  }
+  MKO_TIMED("ssd_du", s, du_kernel<TM, VEC><<<dim3((g.qb + 1) / 2 * g.npt * g.nc * bh), 256, 0, s>>>(g, pl, q));
+}
+
+template <typename TM, bool VEC>
 void launch_bwd_t(const Geo& g, const BwdPlan& pl, const Ptrs& q, hipStream_t s) {
   const unsigned bh = static_cast<unsigned>(g.batch * g.nheads);
   const unsigned ncg = static_cast<unsigned>(g.nc * g.ngroups);
@@ -814,7 +1009,7 @@ void launch_bwd_t(const Geo& g, const BwdPlan& pl, const Ptrs& q, hipStream_t s)
   MKO_TIMED("ssd_chunk_state_bwd", s,
             chunk_state<TM, VEC, true><<<dim3(g.npt * g.nnp * g.nc * bh), 256, 0, s>>>(g, q, q.dstates));
   MKO_TIMED("ssd_state_rev", s, state_rev<TM><<<dim3(pl.nblk, bh), 256, 0, s>>>(g, pl, q));
-  MKO_TIMED("ssd_du", s, du_kernel<TM, VEC><<<dim3((g.qb + 1) / 2 * g.npt * g.nc * bh), 256, 0, s>>>(g, pl, q));
+  launch_du<TM, VEC>(g, pl, q, s);
   MKO_TIMED("ssd_dcb", s, dcb_kernel<TM, VEC><<<dim3(pl.npairs * pl.hb1 * ncg * nb), 256, 0, s>>>(g, pl, q));
   MKO_TIMED("ssd_dbc_state", s,
             dbc_state<TM, VEC><<<dim3(g.qb * g.nnp * 2 * pl.hb2 * ncg * nb), 256, 0, s>>>(g, pl, q));

@@ -293,6 +293,22 @@ __device__ __forceinline__ void pipeline2_static(Regs (&r)[2], Fetch&& fetch, Pu
   });
 }
 
+// The same with D register sets: the loads of stage k + D are issued while stage k is
+// multiplied, so each load has D stages of work to arrive.  For kernels whose occupancy
+// LDS bounds at a few waves per SIMD, the registers are there and the latency is not
+// otherwise hidden.
+template <int N, int D, class Regs, class Fetch, class Put, class Mma>
+__device__ __forceinline__ void pipeline_static(Regs (&r)[D], Fetch&& fetch, Put&& put, Mma&& mma) {
+  static_for<0, (D < N ? D : N)>([&](auto kc) { fetch(kc, r[decltype(kc)::value]); });
+  static_for<0, N>([&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    put(kc, r[k % D]);
+    __syncthreads();
+    if constexpr (k + D < N) fetch(Int<k + D>{}, r[k % D]);
+    mma(kc);
+  });
+}
+
 // As pipeline2, but the fetches past the last stage load stage n -- the epilogue's
 // inputs -- instead of repeating stage n-1, and epi(regs) is called at the end with the
 // set that holds them (even n: both do; odd n: rb).  Two call sites instead of a select
