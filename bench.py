@@ -315,6 +315,8 @@ def ssd_case(steps, warmup, batch=4, length=4096, nheads=64, headdim=64, ngroups
     ms, wall, kernels = timed(step, steps, warmup)
     flops = ssd_flops(batch, length, nheads, headdim, ngroups, dstate, chunk)
     total = sum(flops.values())
+    if "ssd_gate_state" in kernels:  # the fused gate carries the local state adjoint's contraction
+        flops["ssd_gate_state"] = flops.pop("ssd_chunk_state_bwd")
     fwd_b, bwd_b = ssd_bytes(batch, length, nheads, headdim, ngroups, dstate)
     per = {k: v[0] / max(v[1], 1) for k, v in kernels.items()}
     mfma = {}
@@ -325,17 +327,23 @@ def ssd_case(steps, warmup, batch=4, length=4096, nheads=64, headdim=64, ngroups
                        "frac": round(tf / BF16_PEAK_TFLOPS, 4)}
     name = max((k for k in per if k in flops), key=lambda k: per[k])
     achieved = flops[name] / (per[name] * 1e-3) / 1e12
+    traffic = load_traffic(f"{name}@{batch}x{length}x{nheads}x{headdim}x{dstate}")
     roof = {"bound": "mfma", "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
-            "traffic": load_traffic(f"{name}@{batch}x{length}x{nheads}x{headdim}x{dstate}"),
+            "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": traffic,
             "kernel": name, "algorithmic_gflop": round(flops[name] / 1e9, 2)}
+    # the same kernel against HBM: its measured bytes per launch (PMC counters) over its time
+    roof_hbm = None
+    if traffic:
+        gbs = traffic / (per[name] * 1e-3) / 1e9
+        roof_hbm = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": name}
     del leaves, dy, dfinal
     torch.cuda.empty_cache()
     tflops = total / (ms * 1e-3) / 1e12
     return {"ms_per_step": ms, "wall_ms_per_step": wall, "tokens_per_s": batch * length / (ms * 1e-3),
             "gflop_per_step": total / 1e9, "tflops": tflops, "mfma_frac": tflops / BF16_PEAK_TFLOPS,
             "gbs": (fwd_b + bwd_b) / (ms * 1e-3) / 1e9, "bytes_per_step": fwd_b + bwd_b,
-            "roofline": roof, "kernels": mfma,
+            "roofline": roof, "roofline_hbm": roof_hbm, "kernels": mfma,
             "kernels_ms": {k: round(v, 4) for k, v in sorted(per.items())}}
 
 
@@ -746,7 +754,8 @@ def main():
             "hbm_frac_whole_step": round(ssd["gbs"] / HBM_PEAK_GBS, 4),
             "config": {"batch": 4, "seqlen": 4096, "nheads": 64, "headdim": 64, "dstate": 128, "ngroups": 1,
                        "chunk_size": 256, "io_dtype": "bf16", "dt_dtype": "f32"},
-            "roofline": ssd["roofline"], "kernels": ssd["kernels"], "kernels_ms": ssd["kernels_ms"]}
+            "roofline": ssd["roofline"], "roofline_hbm": ssd["roofline_hbm"], "kernels": ssd["kernels"],
+            "kernels_ms": ssd["kernels_ms"]}
         log(f"  {ssd['ms_per_step']:.3f} ms/step, {ssd['tokens_per_s'] / 1e6:.2f} M tokens/s, "
             f"{ssd['tflops']:.1f} TFLOP/s ({100 * ssd['mfma_frac']:.1f}% MFMA), {ssd['gbs']:.0f} GB/s; "
             f"kernels {ssd['kernels_ms']}")

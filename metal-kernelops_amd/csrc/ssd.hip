@@ -389,7 +389,9 @@ SavedLayout saved_layout(const Geo& g) {
   l.dl = o; o = align256(o + bh * g.nc * g.q * 4);
   l.cs = o; o = align256(o + bh * g.nc * g.q * 4);
   l.cb = o; o = align256(o + static_cast<size_t>(g.batch) * g.nc * g.ngroups * g.q * g.q * dtype_size(g.x_dtype));
-  l.yt = o; o = align256(o + (g.save_y ? static_cast<size_t>(g.batch * g.length * g.nheads * g.headdim) * 4 : 0));
+  // the multi-tile backward recomputes the chunk output instead of reading a saved copy
+  const bool yt = g.save_y && !multi_tile(g);
+  l.yt = o; o = align256(o + (yt ? static_cast<size_t>(g.batch * g.length * g.nheads * g.headdim) * 4 : 0));
   l.total = o;
   return l;
 }
@@ -401,7 +403,7 @@ void bind_saved(const Geo& g, void* saved, Ptrs* q) {
   q->dl = reinterpret_cast<float*>(s + l.dl);
   q->cs = reinterpret_cast<float*>(s + l.cs);
   q->cb = s + l.cb;
-  q->yt = g.save_y ? reinterpret_cast<float*>(s + l.yt) : nullptr;
+  q->yt = g.save_y && !multi_tile(g) ? reinterpret_cast<float*>(s + l.yt) : nullptr;
 }
 
 Ptrs base_ptrs(const mko_ssd_params* prm) {
@@ -437,14 +439,15 @@ static void launch_fwd_t(const Geo& g, const Ptrs& q, hipStream_t s) {
   MKO_TIMED("ssd_prep", s, prep<<<dim3(g.nc, g.nheads, g.batch), 256, 0, s>>>(g, q));
   MKO_TIMED("ssd_cb", s,
             cb_kernel<TM, VEC><<<dim3(g.qb * (g.qb + 1) / 2 * g.nc * g.ngroups * g.batch), 256, 0, s>>>(g, q));
-  MKO_TIMED("ssd_chunk_state", s,
-            chunk_state<TM, VEC, false><<<dim3(g.npt * g.nnp * g.nc * bh), 256, 0, s>>>(g, q, q.states));
+  const dim3 cs_grid(g.npt * g.nnp * g.nc * bh);
+  if (g.qb == 4) MKO_TIMED("ssd_chunk_state", s, chunk_state<TM, VEC, false, 4><<<cs_grid, 256, 0, s>>>(g, q, q.states));
+  else MKO_TIMED("ssd_chunk_state", s, chunk_state<TM, VEC, false><<<cs_grid, 256, 0, s>>>(g, q, q.states));
   MKO_TIMED("ssd_state_pass", s,
             state_pass<TM><<<dim3(static_cast<unsigned>((g.headdim * g.dstate + 2047) / 2048), bh), 256, 0, s>>>(
                 g, q));
   if constexpr (sizeof(TM) == 2) {
     const dim3 grid(g.npt * g.nc * bh);
-    if (g.nnt <= 2 && (g.qb == 4 || g.qb == 2 || g.qb == 1)) {
+    if (multi_tile(g)) {
       if (g.qb == 4 && g.nnt == 2) MKO_TIMED("ssd_chunk_scan", s, chunk_scan_mt<TM, VEC, 4, 2><<<grid, 256, 0, s>>>(g, q));
       else if (g.qb == 4) MKO_TIMED("ssd_chunk_scan", s, chunk_scan_mt<TM, VEC, 4, 1><<<grid, 256, 0, s>>>(g, q));
       else if (g.qb == 2 && g.nnt == 2) MKO_TIMED("ssd_chunk_scan", s, chunk_scan_mt<TM, VEC, 2, 2><<<grid, 256, 0, s>>>(g, q));

@@ -88,6 +88,13 @@ struct SavedLayout {
 
 inline size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
+// 16-bit operands with d_state <= 128: one workgroup per (b, h, chunk, d_head tile) runs
+// all of a chunk's token tiles (chunk_scan_mt, gate_state_mt, du_mt), and the backward
+// recomputes the chunk output instead of reading a saved copy.
+inline bool multi_tile(const Geo& g) {
+  return g.x_dtype != MKO_F32 && g.nnt <= 2 && (g.qb == 1 || g.qb == 2 || g.qb == 4);
+}
+
 int make_geo(const mko_ssd_params* prm, Geo* g);
 SavedLayout saved_layout(const Geo& g);
 void bind_saved(const Geo& g, void* saved, Ptrs* q);
@@ -168,7 +175,9 @@ __device__ __forceinline__ void scale8(const V8<TM>& v, float s, float (&f)[8]) 
 // Both operands are token-major in HBM and the contraction runs over tokens, so both
 // are staged transposed.  Double-buffered: the loads of the next 64 tokens are in
 // flight during the products of the current ones.
-template <typename TM, bool VEC, bool BWD>
+// QB > 0: the chunk has QB 64-token tiles (a compile-time stage count, with the loads of
+// up to three stages in flight); QB = 0: qb at run time, two stages in flight.
+template <typename TM, bool VEC, bool BWD, int QB = 0>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(sizeof(TM) == 2 ? 3 : 1)))
 chunk_state(Geo g, Ptrs p, void* out_) {
   constexpr int LD = compact_ld<TM>();  // LDS bounds this kernel: the compact tiles
@@ -195,13 +204,15 @@ chunk_state(Geo g, Ptrs p, void* out_) {
   struct Regs {
     V8<TM> x[2], y0[2], y1[2];
   };
-  auto fetch = [&](int kb, Regs& r) {
+  auto fetch = [&](auto kc, Regs& r) {
+    const int kb = kc;
     const int64_t t0 = static_cast<int64_t>(c) * g.q + 64 * kb;
     load_xw<TM, VEC>(g, X, b, t0, h, pc0, r.x);
     load_bw<TM, VEC>(g, Y, b, t0, gg, nn0, r.y0);
     load_bw<TM, VEC>(g, Y, b, t0, gg, nn0 + 64, r.y1);
   };
-  auto put = [&](int kb, Regs& r) {
+  auto put = [&](auto kc, Regs& r) {
+    const int kb = kc;
     TM* buf = sbuf[kb & 1];
     float a[8], bb[8];
     scale8(r.x[0], s1[64 * kb + r0], a);
@@ -214,12 +225,19 @@ chunk_state(Geo g, Ptrs p, void* out_) {
   zero(acc0);
   zero(acc1);
   __syncthreads();  // s1
-  Regs ra, rb;
-  pipeline2(g.qb, ra, rb, fetch, put, [&](int kb) {
-    TM* buf = sbuf[kb & 1];
+  auto mma = [&](auto kc) {
+    TM* buf = sbuf[static_cast<int>(kc) & 1];
     mma_tile<TM, LD>(acc0, buf, buf + TE, wm, wn, lane, 64);
     mma_tile<TM, LD>(acc1, buf, buf + 2 * TE, wm, wn, lane, 64);
-  });
+  };
+  if constexpr (QB > 0) {
+    constexpr int D = QB < 3 ? QB : 3;
+    Regs regs[D];
+    pipeline_static<QB, D>(regs, fetch, put, mma);
+  } else {
+    Regs ra, rb;
+    pipeline2(g.qb, ra, rb, fetch, put, mma);
+  }
   TM* out = static_cast<TM*>(out_) + (bh * g.nc + c) * g.headdim * g.dstate;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {

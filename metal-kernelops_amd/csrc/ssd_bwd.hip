@@ -146,6 +146,224 @@ __global__ void __launch_bounds__(256) gate(Geo g, BwdPlan pl, Ptrs p) {
   }
 }
 
+// Stage k of gate_state_mt: first the chunk output of each token tile, the tiles in
+// descending order (tile i: nnt state stages, then intra stages over the s-tiles 0 .. i);
+// then qb * nnt stages of the local state adjoint (l-tile i, n-tile kk).
+struct GsStage {
+  bool adj;
+  int i, kk;
+};
+constexpr GsStage gs_stage(int k, int nnt, int qb) {
+  const int ny = qb * nnt + qb * (qb + 1) / 2;
+  if (k >= ny) return GsStage{true, (k - ny) / nnt, (k - ny) % nnt};
+  int ti = 0, base = 0;
+  while (k >= base + nnt + (qb - 1 - ti) + 1) {
+    base += nnt + (qb - 1 - ti) + 1;
+    ++ti;
+  }
+  return GsStage{false, qb - 1 - ti, k - base};
+}
+
+// gate and the local state adjoint in one pass over a (b, h, chunk, d_head tile), 16-bit
+// operands, d_state <= 64 * NNT.  The chunk output before the skip and the gate,
+//   y~[l][p] = sum_{s<=l} K[l][s] u_s[p] + e^{cs_l} sum_n C_l[n] S_in[p][n],
+// is recomputed in fp32 exactly as the forward's multi-tile scan forms it (same operands,
+// same stage order), so the forward saves no copy of it.  Per token tile, from y~: dz, gy =
+// dy silu(z) (stored in the input dtype, which is what the other kernels read), the row
+// sums gy.y~ and the dD column partials.  The tiles run in descending order, so once tile
+// i is done its u slot in LDS is free and takes (e^{cs} gy)^T, the left operand of the
+// local adjoint sum_l e^{cs_l} gy_l (x) C_l that the last stages accumulate.
+template <typename TM, bool VEC, int QB, int NNT>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) gate_state_mt(Geo g, BwdPlan pl,
+                                                                                             Ptrs p) {
+  static_assert(sizeof(TM) == 2, "16-bit operands");
+  constexpr int TE = LdsTile<TM>::elems;
+  constexpr int NY = QB * NNT + QB * (QB + 1) / 2;
+  constexpr int N = NY + QB * NNT;
+  constexpr int Q = 64 * QB;
+  __shared__ __align__(16) TM ut[QB][TE];   // u_j^T [p][s]; after token tile i, slot i holds (e^{cs} gy)^T [p][l]
+  __shared__ __align__(16) TM st[NNT][TE];  // S_in [p][n]
+  __shared__ __align__(16) TM ab[2][TE];    // right/left operand per stage; the epilogue's fp32 tile
+  __shared__ __align__(16) float csc[Q], dlc[Q], ecol[Q], ecs[Q], dcol[64];
+  __shared__ float colred[4][64];
+  const WgId id = wg_id(g.nheads, g.npt);
+  const int64_t h = id.x;
+  const int pt = id.y;
+  const int64_t b = id.z / g.nc;
+  const int c = static_cast<int>(id.z % g.nc);
+  const int64_t bh = b * g.nheads + h, gg = h / g.hpg;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int wm, wn;
+  quadrant(wave, wm, wn);
+  const int r0 = blk_r0(), c0 = blk_c0();
+  const int64_t tc = static_cast<int64_t>(c) * Q, pc0 = static_cast<int64_t>(pt) * 64;
+  const TM* X = static_cast<const TM*>(p.x);
+  const TM* Z = p.z ? static_cast<const TM*>(p.z) : X;
+  const TM* DY = static_cast<const TM*>(p.dy);
+  const TM* Cm = static_cast<const TM*>(p.C);
+  const TM* cbt = static_cast<const TM*>(p.cb) + ((b * g.nc + c) * g.ngroups + gg) * Q * Q;
+  const TM* S = static_cast<const TM*>(p.states) + (bh * g.nc + c) * g.headdim * g.dstate;
+  {
+    V8<TM> xr[QB][2], sr[NNT][2];
+#pragma unroll
+    for (int j = 0; j < QB; ++j) load_xw<TM, VEC>(g, X, b, tc + 64 * j, h, pc0, xr[j]);
+#pragma unroll
+    for (int k = 0; k < NNT; ++k) load_sw<TM, VEC>(g, S, pc0, 64 * k, sr[k]);
+    load_chunk_cs(g, p, bh, c, csc, dlc, ecol);
+    if (threadIdx.x < Q) ecs[threadIdx.x] = fast_exp(csc[threadIdx.x]);
+    if (threadIdx.x < 64) {
+      const int64_t pp = pc0 + threadIdx.x;
+      dcol[threadIdx.x] = !p.D ? 0.0f : g.d_per_row ? (pp < g.headdim ? p.D[h * g.headdim + pp] : 0.0f) : p.D[h];
+    }
+    __syncthreads();  // csc, dlc
+#pragma unroll
+    for (int j = 0; j < QB; ++j) {
+      float a[8], bb[8];
+      scale8(xr[j][0], dlc[64 * j + r0], a);
+      scale8(xr[j][1], dlc[64 * j + r0 + 1], bb);
+      put2x8<TM, true>(ut[j], r0, c0, a, bb);  // Bt[p][s] = step_s x_s[p]
+    }
+#pragma unroll
+    for (int k = 0; k < NNT; ++k) put_raw<TM, false>(st[k], r0, c0, sr[k][0], sr[k][1]);  // Bt[p][n] = S_in[p][n]
+  }
+  struct Regs {
+    V8<TM> a[2];
+  };
+  auto fetch = [&](auto kc, Regs& r) {
+    constexpr GsStage sg = gs_stage(decltype(kc)::value, NNT, QB);
+    if constexpr (sg.adj || sg.kk < NNT)
+      load_bw<TM, VEC>(g, Cm, b, tc + 64 * sg.i, gg, 64 * sg.kk, r.a);  // C rows l
+    else
+      load_win<TM, true>(cbt + (64 * sg.i) * Q + 64 * (sg.kk - NNT), Q, 64, 64, r.a, cbt);  // cb rows l
+  };
+  auto put = [&](auto kc, Regs& r) {
+    constexpr int k = decltype(kc)::value;
+    constexpr GsStage sg = gs_stage(k, NNT, QB);
+    if constexpr (sg.adj) {
+      put_raw<TM, true>(ab[k & 1], r0, c0, r.a[0], r.a[1]);  // Bt[n][l] = C_l[n]
+    } else if constexpr (sg.kk < NNT) {
+      put_raw<TM, false>(ab[k & 1], r0, c0, r.a[0], r.a[1]);  // A[l][n] = C_l[n]
+    } else {
+      float a[8], bb[8];
+      k_block<TM>(r.a[0], r.a[1], csc, ecol, sg.i, sg.kk - NNT, r0, c0, a, bb);
+      put2x8<TM, false>(ab[k & 1], r0, c0, a, bb);  // A[l][s] = K[l][s]
+    }
+  };
+  f32x16 acc, acc1;
+  zero(acc);
+  zero(acc1);
+  V8<TM> xv[2], zv[2], dyv[2];
+  constexpr int D = N < 6 ? N : 6;
+  Regs regs[D];
+  pipeline_static<N, D>(regs, fetch, put, [&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    constexpr GsStage sg = gs_stage(k, NNT, QB);
+    if constexpr (sg.adj) {
+      // A[p][l] = e^{cs_l} gy_l[p] (slot i), Bt[n][l] = C_l[n]
+      mma_tile<TM>(sg.kk == 0 ? acc : acc1, ut[sg.i], ab[k & 1], wm, wn, lane, 64);
+      return;
+    } else {
+      const int i = sg.i;
+      const int64_t tl0 = tc + 64 * i;
+      if constexpr (sg.kk == 0) {  // epilogue inputs of tile i
+        load_xw<TM, VEC>(g, X, b, tl0, h, pc0, xv);
+        load_xw<TM, VEC>(g, Z, b, tl0, h, pc0, zv);
+        load_xw<TM, VEC>(g, DY, b, tl0, h, pc0, dyv);
+      }
+      if constexpr (sg.kk < NNT) {
+        mma_tile<TM>(acc, ab[k & 1], st[sg.kk], wm, wn, lane, 64);
+        if constexpr (sg.kk == NNT - 1) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[r] *= ecs[64 * i + acc_row(wm, lane, r)];
+        }
+        return;
+      }
+      mma_tile<TM>(acc, ab[k & 1], ut[sg.kk - NNT], wm, wn, lane, 64);
+      if constexpr (sg.kk == NNT + sg.i) {
+        float* red = reinterpret_cast<float*>(&ab[0][0]);
+        __syncthreads();
+        acc_to_lds(red, acc, wm, wn, lane);
+        zero(acc);
+        __syncthreads();
+        float yt[2][8];
+        lds_block(red, r0, c0, yt[0], yt[1]);
+        const float4 da = *reinterpret_cast<const float4*>(dcol + c0);
+        const float4 db = *reinterpret_cast<const float4*>(dcol + c0 + 4);
+        const float dv[8] = {da.x, da.y, da.z, da.w, db.x, db.y, db.z, db.w};
+        const int64_t po = ((bh * g.nc + c) * g.npt + pt) * Q + 64 * i;
+        float dd[8], gyo[2][8], dzo[2][8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dd[e] = 0.0f;
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+          float xf[8], gyf[8];
+          v8_f32(xv[rr], xf);
+          v8_f32(dyv[rr], gyf);
+          if (p.z) {
+            float zf[8];
+            v8_f32(zv[rr], zf);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const float sgm = sigmoid(zf[e]);
+              const float ypre = fmaf(dv[e], xf[e], yt[rr][e]);
+              dzo[rr][e] = gyf[e] * ypre * sgm * fmaf(zf[e], 1.0f - sgm, 1.0f);
+              gyf[e] = to_f32(from_f32<TM>(gyf[e] * zf[e] * sgm));  // as stored for the other kernels
+            }
+          }
+          float ya = 0.0f;
+          const float el = ecs[64 * i + r0 + rr];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            ya = fmaf(gyf[e], yt[rr][e], ya);
+            dd[e] = fmaf(gyf[e], xf[e], dd[e]);
+            gyo[rr][e] = gyf[e];
+            yt[rr][e] = gyf[e] * el;  // the adjoint's operand, e^{cs_l} gy_l
+          }
+          ya = row8_sum(ya);
+          if ((threadIdx.x & 7) == 0) p.ya[po + r0 + rr] = ya;
+        }
+        if (p.z) {
+          store_xw<TM, VEC>(g, static_cast<TM*>(p.dz), b, tl0, h, pc0, dzo[0], dzo[1]);
+          store_xw<TM, VEC>(g, static_cast<TM*>(p.gyw), b, tl0, h, pc0, gyo[0], gyo[1]);
+        }
+        put2x8<TM, true>(ut[i], r0, c0, yt[0], yt[1]);  // A[p][l] = e^{cs_l} gy_l[p]
+        if (p.D) {
+          // column sums over the tile's 64 rows: lanes sharing tid % 8, then the 4 wavefronts
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            float v = dd[e];
+            v += __shfl_xor(v, 8);
+            v += __shfl_xor(v, 16);
+            v += __shfl_xor(v, 32);
+            dd[e] = v;
+          }
+          if (lane < 8) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) colred[wave][c0 + e] = dd[e];
+          }
+          __syncthreads();
+          if (threadIdx.x < 64 && pc0 + threadIdx.x < g.headdim) {
+            const int col = threadIdx.x;
+            const float sum = (colred[0][col] + colred[1][col]) + (colred[2][col] + colred[3][col]);
+            p.pdD[(((b * g.nc + c) * g.qb + i) * g.nheads + h) * g.headdim + pc0 + col] = sum;
+          }
+        }
+        __syncthreads();  // the next stage refills the operand buffers; colred is reused
+      }
+    }
+  });
+  TM* out = static_cast<TM*>(p.dstates) + (bh * g.nc + c) * g.headdim * g.dstate;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int64_t pp = pc0 + acc_row(wm, lane, r);
+    const int64_t nn = acc_col(wn, lane);
+    if (pp < g.headdim) {
+      if (nn < g.dstate) out[pp * g.dstate + nn] = from_f32<TM>(acc[r]);
+      if (NNT > 1 && nn + 64 < g.dstate) out[pp * g.dstate + nn + 64] = from_f32<TM>(acc1[r]);
+    }
+  }
+}
+
 // Backwards over the chunks, 8 state elements per thread: G (the adjoint of the
 // state leaving each chunk) over the local adjoints in dstates, e^T <G, S_in> per
 // 2048-element state block, and the adjoint of the initial state.
@@ -979,12 +1197,30 @@ BwdLayout bwd_layout(const Geo& g, const BwdPlan& pl, bool has_z) {
   return l;
 }
 
+// The fused gate and local state adjoint (multi-tile geometries); false if the geometry
+// takes the separate kernels.
+template <typename TM, bool VEC>
+bool launch_gate_state(const Geo& g, const BwdPlan& pl, const Ptrs& q, hipStream_t s) {
+  if constexpr (sizeof(TM) == 2) {
+    if (!multi_tile(g)) return false;
+    const dim3 grid(static_cast<unsigned>(g.npt * g.nc * g.batch * g.nheads));
+    if (g.qb == 4 && g.nnt == 2) MKO_TIMED("ssd_gate_state", s, gate_state_mt<TM, VEC, 4, 2><<<grid, 256, 0, s>>>(g, pl, q));
+    else if (g.qb == 4) MKO_TIMED("ssd_gate_state", s, gate_state_mt<TM, VEC, 4, 1><<<grid, 256, 0, s>>>(g, pl, q));
+    else if (g.qb == 2 && g.nnt == 2) MKO_TIMED("ssd_gate_state", s, gate_state_mt<TM, VEC, 2, 2><<<grid, 256, 0, s>>>(g, pl, q));
+    else if (g.qb == 2) MKO_TIMED("ssd_gate_state", s, gate_state_mt<TM, VEC, 2, 1><<<grid, 256, 0, s>>>(g, pl, q));
+    else if (g.nnt == 2) MKO_TIMED("ssd_gate_state", s, gate_state_mt<TM, VEC, 1, 2><<<grid, 256, 0, s>>>(g, pl, q));
+    else MKO_TIMED("ssd_gate_state", s, gate_state_mt<TM, VEC, 1, 1><<<grid, 256, 0, s>>>(g, pl, q));
+    return true;
+  }
+  return false;
+}
+
 template <typename TM, bool VEC>
 void launch_du(const Geo& g, const BwdPlan& pl, const Ptrs& q, hipStream_t s) {
   const unsigned bh = static_cast<unsigned>(g.batch * g.nheads);
   if constexpr (sizeof(TM) == 2) {
     const dim3 grid(g.npt * g.nc * bh);
-    if (g.nnt <= 2) {
+    if (multi_tile(g)) {
       if (g.qb == 4 && g.nnt == 2) MKO_TIMED("ssd_du", s, du_mt<TM, VEC, 4, 2><<<grid, 256, 0, s>>>(g, pl, q));
       else if (g.qb == 4) MKO_TIMED("ssd_du", s, du_mt<TM, VEC, 4, 1><<<grid, 256, 0, s>>>(g, pl, q));
       else if (g.qb == 2 && g.nnt == 2) MKO_TIMED("ssd_du", s, du_mt<TM, VEC, 2, 2><<<grid, 256, 0, s>>>(g, pl, q));
@@ -1002,12 +1238,17 @@ void launch_bwd_t(const Geo& g, const BwdPlan& pl, const Ptrs& q, hipStream_t s)
   const unsigned bh = static_cast<unsigned>(g.batch * g.nheads);
   const unsigned ncg = static_cast<unsigned>(g.nc * g.ngroups);
   const unsigned nb = static_cast<unsigned>(g.batch);
-  if (q.yt)
-    MKO_TIMED("ssd_gate", s, gate<TM, VEC, true><<<dim3(g.qb * g.npt * g.nc * bh), 256, 0, s>>>(g, pl, q));
-  else
-    MKO_TIMED("ssd_gate", s, gate<TM, VEC, false><<<dim3(g.qb * g.npt * g.nc * bh), 256, 0, s>>>(g, pl, q));
-  MKO_TIMED("ssd_chunk_state_bwd", s,
-            chunk_state<TM, VEC, true><<<dim3(g.npt * g.nnp * g.nc * bh), 256, 0, s>>>(g, q, q.dstates));
+  if (!launch_gate_state<TM, VEC>(g, pl, q, s)) {
+    if (q.yt)
+      MKO_TIMED("ssd_gate", s, gate<TM, VEC, true><<<dim3(g.qb * g.npt * g.nc * bh), 256, 0, s>>>(g, pl, q));
+    else
+      MKO_TIMED("ssd_gate", s, gate<TM, VEC, false><<<dim3(g.qb * g.npt * g.nc * bh), 256, 0, s>>>(g, pl, q));
+    const dim3 cs_grid(g.npt * g.nnp * g.nc * bh);
+    if (g.qb == 4)
+      MKO_TIMED("ssd_chunk_state_bwd", s, chunk_state<TM, VEC, true, 4><<<cs_grid, 256, 0, s>>>(g, q, q.dstates));
+    else
+      MKO_TIMED("ssd_chunk_state_bwd", s, chunk_state<TM, VEC, true><<<cs_grid, 256, 0, s>>>(g, q, q.dstates));
+  }
   MKO_TIMED("ssd_state_rev", s, state_rev<TM><<<dim3(pl.nblk, bh), 256, 0, s>>>(g, pl, q));
   launch_du<TM, VEC>(g, pl, q, s);
   MKO_TIMED("ssd_dcb", s, dcb_kernel<TM, VEC><<<dim3(pl.npairs * pl.hb1 * ncg * nb), 256, 0, s>>>(g, pl, q));

@@ -269,6 +269,7 @@ __device__ __forceinline__ void pipeline2(int n, Regs& ra, Regs& rb, Fetch&& fet
 template <int K>
 struct Int {
   static constexpr int value = K;
+  __device__ constexpr operator int() const { return K; }
 };
 template <int B, int E, class F>
 __device__ __forceinline__ void static_for(F&& f) {
