@@ -170,9 +170,10 @@ constexpr GsStage gs_stage(int k, int nnt, int qb) {
 // is recomputed in fp32 exactly as the forward's multi-tile scan forms it (same operands,
 // same stage order), so the forward saves no copy of it.  Per token tile, from y~: dz, gy =
 // dy silu(z) (stored in the input dtype, which is what the other kernels read), the row
-// sums gy.y~ and the dD column partials.  The tiles run in descending order, so once tile
-// i is done its u slot in LDS is free and takes (e^{cs} gy)^T, the left operand of the
-// local adjoint sum_l e^{cs_l} gy_l (x) C_l that the last stages accumulate.
+// sums gy.y~ and the dD column partials.  The tiles run in descending order, so once tile i
+// is done its u slot in LDS is free and takes (e^{cs} gy)^T, the left operand of the local
+// adjoint sum_l e^{cs_l} gy_l (x) C_l that the last stages accumulate; the adjoint leaves
+// through LDS as 16-byte rows.
 template <typename TM, bool VEC, int QB, int NNT>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) gate_state_mt(Geo g, BwdPlan pl,
                                                                                              Ptrs p) {
@@ -352,15 +353,18 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) g
       }
     }
   });
-  TM* out = static_cast<TM*>(p.dstates) + (bh * g.nc + c) * g.headdim * g.dstate;
+  // the local adjoint [p][n], one 64-wide n-tile at a time through the fp32 tile
+  TM* out = static_cast<TM*>(p.dstates) + (bh * g.nc + c) * g.headdim * g.dstate + pc0 * g.dstate;
+  float* red = reinterpret_cast<float*>(&ab[0][0]);
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int64_t pp = pc0 + acc_row(wm, lane, r);
-    const int64_t nn = acc_col(wn, lane);
-    if (pp < g.headdim) {
-      if (nn < g.dstate) out[pp * g.dstate + nn] = from_f32<TM>(acc[r]);
-      if (NNT > 1 && nn + 64 < g.dstate) out[pp * g.dstate + nn + 64] = from_f32<TM>(acc1[r]);
-    }
+  for (int kk = 0; kk < NNT; ++kk) {
+    __syncthreads();
+    acc_to_lds(red, kk == 0 ? acc : acc1, wm, wn, lane);
+    __syncthreads();
+    float v[2][8];
+    lds_block(red, r0, c0, v[0], v[1]);
+    store_win<TM, VEC>(out + 64 * kk, static_cast<int>(g.dstate), clamp64(g.headdim - pc0),
+                       static_cast<int>(g.dstate - 64 * kk), v[0], v[1]);
   }
 }
 
