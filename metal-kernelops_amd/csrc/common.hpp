@@ -38,6 +38,103 @@ __device__ __forceinline__ bf16 from_f32<bf16>(float v) {
   return r;
 }
 
+// ---- raw words
+// Consecutive elements kept as the 32-bit words they occupy in memory: a 16-bit type holds
+// elements 2i (low half) and 2i + 1 (high half) in word i, fp32 one element per word.  The
+// kernels' vector loads, stores and conversions all go through these.
+
+template <typename T, int NE>
+constexpr int kWordsOf = NE * static_cast<int>(sizeof(T)) / 4;
+
+// W words at p: 16-byte vectors when W is a multiple of 4, else one 8- or 4-byte access.
+template <int W>
+__device__ __forceinline__ void load_words(const void* p, uint32_t (&w)[W]) {
+  if constexpr (W % 4 == 0) {
+    const uint4* q = static_cast<const uint4*>(p);
+#pragma unroll
+    for (int i = 0; i < W / 4; ++i) {
+      const uint4 t = q[i];
+      w[4 * i + 0] = t.x;
+      w[4 * i + 1] = t.y;
+      w[4 * i + 2] = t.z;
+      w[4 * i + 3] = t.w;
+    }
+  } else if constexpr (W == 2) {
+    const uint2 t = *static_cast<const uint2*>(p);
+    w[0] = t.x;
+    w[1] = t.y;
+  } else {
+    static_assert(W == 1, "16-byte vectors, or one 8- or 4-byte access");
+    w[0] = *static_cast<const uint32_t*>(p);
+  }
+}
+
+template <int W>
+__device__ __forceinline__ void store_words(void* p, const uint32_t (&w)[W]) {
+  if constexpr (W % 4 == 0) {
+    uint4* q = static_cast<uint4*>(p);
+#pragma unroll
+    for (int i = 0; i < W / 4; ++i) q[i] = make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
+  } else if constexpr (W == 2) {
+    *static_cast<uint2*>(p) = make_uint2(w[0], w[1]);
+  } else {
+    static_assert(W == 1, "16-byte vectors, or one 8- or 4-byte access");
+    *static_cast<uint32_t*>(p) = w[0];
+  }
+}
+
+// The two 16-bit elements of a word as fp32 (exact).
+template <typename T>
+__device__ __forceinline__ void unpack2(uint32_t w, float& lo, float& hi) {
+  if constexpr (__is_same(T, bf16)) {
+    lo = __uint_as_float(w << 16);
+    hi = __uint_as_float(w & 0xffff0000u);
+  } else {
+    lo = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w & 0xffffu)));
+    hi = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w >> 16)));
+  }
+}
+
+// Two values rounded to nearest even in a 16-bit type, packed low first.
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  if constexpr (__is_same(T, bf16)) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    const bf16x2_t t = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+    return __builtin_bit_cast(uint32_t, t);
+  } else {
+    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+    const f16x2_t t = {static_cast<_Float16>(a), static_cast<_Float16>(b)};
+    return __builtin_bit_cast(uint32_t, t);
+  }
+}
+
+// NE elements of T from their words.
+template <typename T, int NE>
+__device__ __forceinline__ void unpack_words(const uint32_t* w, float (&f)[NE]) {
+  if constexpr (sizeof(T) == 4) {
+#pragma unroll
+    for (int i = 0; i < NE; ++i) f[i] = __uint_as_float(w[i]);
+  } else {
+    static_assert(NE % 2 == 0, "16-bit elements come in word pairs");
+#pragma unroll
+    for (int i = 0; i < NE / 2; ++i) unpack2<T>(w[i], f[2 * i], f[2 * i + 1]);
+  }
+}
+
+// NE fp32 values rounded to T, as words.
+template <typename T, int NE>
+__device__ __forceinline__ void pack_words(const float (&f)[NE], uint32_t* w) {
+  if constexpr (sizeof(T) == 4) {
+#pragma unroll
+    for (int i = 0; i < NE; ++i) w[i] = __float_as_uint(f[i]);
+  } else {
+    static_assert(NE % 2 == 0, "16-bit elements come in word pairs");
+#pragma unroll
+    for (int i = 0; i < NE / 2; ++i) w[i] = pack2<T>(f[2 * i], f[2 * i + 1]);
+  }
+}
+
 // 2^x on the transcendental unit (v_exp_f32).  Underflows to 0 for very negative
 // x, which is the value every decay below wants.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

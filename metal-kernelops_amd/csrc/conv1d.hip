@@ -90,15 +90,7 @@ struct RawBlk {
     const T* q = src + row * g.length + t0;
     if constexpr (VEC) {
       nok = blk < g.nblk ? BS : 0;
-      const uint4* v = reinterpret_cast<const uint4*>(q);
-#pragma unroll
-      for (int i = 0; i < W / 4; ++i) {
-        const uint4 t = v[i];
-        w[4 * i] = t.x;
-        w[4 * i + 1] = t.y;
-        w[4 * i + 2] = t.z;
-        w[4 * i + 3] = t.w;
-      }
+      load_words(q, w);
     } else {
       const int64_t left = g.length - t0;  // at least 1
       nok = blk < g.nblk ? (left < BS ? static_cast<int>(left) : BS) : 0;
@@ -108,22 +100,10 @@ struct RawBlk {
   }
   __device__ __forceinline__ void get(float (&v)[BS]) const {
     float f[BS];
-    if constexpr (!VEC || sizeof(T) == 4) {
-#pragma unroll
-      for (int i = 0; i < BS; ++i) f[i] = __uint_as_float(w[i]);
-    } else if constexpr (__is_same(T, bf16)) {
-#pragma unroll
-      for (int i = 0; i < W; ++i) {
-        f[2 * i] = __uint_as_float(w[i] << 16);
-        f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < W; ++i) {
-        f[2 * i] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w[i] & 0xffffu)));
-        f[2 * i + 1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w[i] >> 16)));
-      }
-    }
+    if constexpr (VEC)
+      unpack_words<T, BS>(w, f);
+    else
+      unpack_words<float, BS>(w, f);  // the scalar path keeps fp32 words
 #pragma unroll
     for (int i = 0; i < BS; ++i) v[i] = i < nok ? f[i] : 0.0f;
   }

@@ -117,11 +117,7 @@ __device__ __forceinline__ void bload_param(__amdgpu_buffer_rsrc_t r, uint32_t o
 template <typename T, int VEC>
 __device__ __forceinline__ void load_raw(const T* p, Raw<T, VEC>& r) {
   if constexpr (VEC * sizeof(T) == 16) {
-    const uint4 v = *reinterpret_cast<const uint4*>(p);
-    r.w[0] = v.x;
-    r.w[1] = v.y;
-    r.w[2] = v.z;
-    r.w[3] = v.w;
+    load_words(p, r.w);
   } else {
     static_assert(VEC == 1, "vectors are 16 bytes or one element");
     if constexpr (sizeof(T) == 4)
@@ -133,26 +129,11 @@ __device__ __forceinline__ void load_raw(const T* p, Raw<T, VEC>& r) {
 
 template <typename T, int VEC>
 __device__ __forceinline__ void unpack(const Raw<T, VEC>& r, float (&o)[VEC]) {
-  if constexpr (sizeof(T) == 4) {
-#pragma unroll
-    for (int i = 0; i < VEC; ++i) o[i] = __uint_as_float(r.w[i]);
-  } else if constexpr (VEC == 1) {
-    if constexpr (__is_same(T, bf16))
-      o[0] = __uint_as_float(r.w[0] << 16);
-    else
-      o[0] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.w[0])));
-  } else if constexpr (__is_same(T, bf16)) {
-#pragma unroll
-    for (int i = 0; i < VEC / 2; ++i) {
-      o[2 * i] = __uint_as_float(r.w[i] << 16);
-      o[2 * i + 1] = __uint_as_float(r.w[i] & 0xffff0000u);
-    }
+  if constexpr (sizeof(T) == 2 && VEC == 1) {
+    float hi;
+    unpack2<T>(r.w[0], o[0], hi);  // one element, in the low half
   } else {
-#pragma unroll
-    for (int i = 0; i < VEC / 2; ++i) {
-      o[2 * i] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.w[i] & 0xffffu)));
-      o[2 * i + 1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.w[i] >> 16)));
-    }
+    unpack_words<T, VEC>(r.w, o);
   }
 }
 
@@ -163,26 +144,12 @@ __device__ __forceinline__ void load_vec(const T* p, float (&o)[VEC]) {
   unpack<T, VEC>(r, o);
 }
 
-__device__ __forceinline__ uint32_t pack2(bf16, float a, float b) {
-  return static_cast<uint32_t>(from_f32<bf16>(a).bits) | (static_cast<uint32_t>(from_f32<bf16>(b).bits) << 16);
-}
-__device__ __forceinline__ uint32_t pack2(_Float16, float a, float b) {
-  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(a))) |
-         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(b))) << 16);
-}
-
 template <typename T, int VEC>
 __device__ __forceinline__ void store_vec(T* p, const float (&v)[VEC]) {
   if constexpr (VEC * sizeof(T) == 16) {
     uint32_t w[4];
-    if constexpr (sizeof(T) == 4) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) w[i] = __float_as_uint(v[i]);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) w[i] = pack2(T{}, v[2 * i], v[2 * i + 1]);
-    }
-    *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+    pack_words<T, VEC>(v, w);
+    store_words(p, w);
   } else {
     p[0] = from_f32<T>(v[0]);
   }
@@ -191,13 +158,9 @@ __device__ __forceinline__ void store_vec(T* p, const float (&v)[VEC]) {
 template <typename T, int VEC>
 __device__ __forceinline__ void bstore(__amdgpu_buffer_rsrc_t r, uint32_t off, const float (&v)[VEC]) {
   if constexpr (VEC * sizeof(T) == 16) {
-    v4u32 w;
-    if constexpr (sizeof(T) == 4) {
-      w = v4u32{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
-    } else {
-      w = v4u32{pack2(T{}, v[0], v[1]), pack2(T{}, v[2], v[3]), pack2(T{}, v[4], v[5]), pack2(T{}, v[6], v[7])};
-    }
-    __builtin_amdgcn_raw_buffer_store_b128(w, r, off, 0, 0);
+    uint32_t u[4];
+    pack_words<T, VEC>(v, u);
+    __builtin_amdgcn_raw_buffer_store_b128(v4u32{u[0], u[1], u[2], u[3]}, r, off, 0, 0);
   } else if constexpr (sizeof(T) == 4) {
     __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[0]), r, off, 0, 0);
   } else {
@@ -267,19 +230,10 @@ __device__ __forceinline__ void load_w(const void* p, int wd, int64_t elem, floa
   }
   const uint16_t* q = static_cast<const uint16_t*>(p) + elem;
   uint32_t w[(VEC + 1) / 2];
-  if constexpr (VEC == 8) {
-    const uint4 v = *reinterpret_cast<const uint4*>(q);
-    w[0] = v.x;
-    w[1] = v.y;
-    w[2] = v.z;
-    w[3] = v.w;
-  } else if constexpr (VEC == 4) {
-    const uint2 v = *reinterpret_cast<const uint2*>(q);
-    w[0] = v.x;
-    w[1] = v.y;
-  } else {
+  if constexpr (VEC >= 4)
+    load_words(q, w);
+  else
     w[0] = q[0];
-  }
   unpack16<VEC>(w, wd == MKO_BF16, o);
 }
 

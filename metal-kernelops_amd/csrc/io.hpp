@@ -12,34 +12,11 @@ template <typename T, int NB>
 __device__ __forceinline__ void load_run_t(const T* __restrict__ p, int nvalid, bool vec,
                                            float (&out)[NB]) {
   if (vec && nvalid >= NB) {
-    constexpr int kWords = NB * static_cast<int>(sizeof(T)) / 4;
+    constexpr int kWords = kWordsOf<T, NB>;
     static_assert(kWords % 4 == 0, "run must be a whole number of 16-byte vectors");
     uint32_t w[kWords];
-    const uint4* q = reinterpret_cast<const uint4*>(p);
-#pragma unroll
-    for (int i = 0; i < kWords / 4; ++i) {
-      const uint4 v = q[i];
-      w[4 * i + 0] = v.x;
-      w[4 * i + 1] = v.y;
-      w[4 * i + 2] = v.z;
-      w[4 * i + 3] = v.w;
-    }
-    if constexpr (sizeof(T) == 4) {
-#pragma unroll
-      for (int i = 0; i < NB; ++i) out[i] = __uint_as_float(w[i]);
-    } else if constexpr (__is_same(T, bf16)) {
-#pragma unroll
-      for (int i = 0; i < kWords; ++i) {
-        out[2 * i] = __uint_as_float(w[i] << 16);
-        out[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < kWords; ++i) {
-        out[2 * i] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w[i] & 0xffffu)));
-        out[2 * i + 1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w[i] >> 16)));
-      }
-    }
+    load_words(p, w);
+    unpack_words<T, NB>(w, out);
   } else {
 #pragma unroll
     for (int i = 0; i < NB; ++i) out[i] = (i < nvalid) ? to_f32(p[i]) : 0.0f;
@@ -50,25 +27,9 @@ template <typename T, int NB>
 __device__ __forceinline__ void store_run_t(T* __restrict__ p, int nvalid, bool vec,
                                             const float (&in)[NB]) {
   if (vec && nvalid >= NB) {
-    constexpr int kWords = NB * static_cast<int>(sizeof(T)) / 4;
-    uint32_t w[kWords];
-    if constexpr (sizeof(T) == 4) {
-#pragma unroll
-      for (int i = 0; i < NB; ++i) w[i] = __float_as_uint(in[i]);
-    } else if constexpr (__is_same(T, bf16)) {
-#pragma unroll
-      for (int i = 0; i < kWords; ++i)
-        w[i] = static_cast<uint32_t>(from_f32<bf16>(in[2 * i]).bits) |
-               (static_cast<uint32_t>(from_f32<bf16>(in[2 * i + 1]).bits) << 16);
-    } else {
-#pragma unroll
-      for (int i = 0; i < kWords; ++i)
-        w[i] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(in[2 * i]))) |
-               (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(in[2 * i + 1]))) << 16);
-    }
-    uint4* q = reinterpret_cast<uint4*>(p);
-#pragma unroll
-    for (int i = 0; i < kWords / 4; ++i) q[i] = make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
+    uint32_t w[kWordsOf<T, NB>];
+    pack_words<T, NB>(in, w);
+    store_words(p, w);
   } else {
 #pragma unroll
     for (int i = 0; i < NB; ++i)

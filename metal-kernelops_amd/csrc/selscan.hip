@@ -308,34 +308,9 @@ struct RawRun {  // NE consecutive elements of a row, raw
   static constexpr int W = NE * static_cast<int>(sizeof(T)) / 4;
   uint32_t w[W];
   __device__ __forceinline__ void load(const Geo&, const void* base, int, int64_t off, int) {
-    const uint4* q = reinterpret_cast<const uint4*>(static_cast<const T*>(base) + off);
-#pragma unroll
-    for (int i = 0; i < W / 4; ++i) {
-      const uint4 t = q[i];
-      w[4 * i] = t.x;
-      w[4 * i + 1] = t.y;
-      w[4 * i + 2] = t.z;
-      w[4 * i + 3] = t.w;
-    }
+    load_words(static_cast<const T*>(base) + off, w);
   }
-  __device__ __forceinline__ void get(float (&f)[NE]) const {
-    if constexpr (sizeof(T) == 4) {
-#pragma unroll
-      for (int i = 0; i < NE; ++i) f[i] = __uint_as_float(w[i]);
-    } else if constexpr (__is_same(T, bf16)) {
-#pragma unroll
-      for (int i = 0; i < W; ++i) {
-        f[2 * i] = __uint_as_float(w[i] << 16);
-        f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < W; ++i) {
-        f[2 * i] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w[i] & 0xffffu)));
-        f[2 * i + 1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w[i] >> 16)));
-      }
-    }
-  }
+  __device__ __forceinline__ void get(float (&f)[NE]) const { unpack_words<T, NE>(w, f); }
 };
 
 template <>

@@ -58,40 +58,16 @@ struct Args {
 
 template <typename T>
 __device__ __forceinline__ void load4(const void* base, int64_t i, float (&v)[4]) {
-  if constexpr (sizeof(T) == 4) {
-    const float4 q = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + i);
-    v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
-  } else {
-    const uint2 q = *reinterpret_cast<const uint2*>(static_cast<const T*>(base) + i);
-    if constexpr (__is_same(T, bf16)) {
-      v[0] = __uint_as_float(q.x << 16); v[1] = __uint_as_float(q.x & 0xffff0000u);
-      v[2] = __uint_as_float(q.y << 16); v[3] = __uint_as_float(q.y & 0xffff0000u);
-    } else {
-      v[0] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(q.x & 0xffffu)));
-      v[1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(q.x >> 16)));
-      v[2] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(q.y & 0xffffu)));
-      v[3] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(q.y >> 16)));
-    }
-  }
+  uint32_t w[kWordsOf<T, 4>];
+  load_words(static_cast<const T*>(base) + i, w);
+  unpack_words<T, 4>(w, v);
 }
 
 template <typename T>
 __device__ __forceinline__ void store4(void* base, int64_t i, const float (&v)[4]) {
-  if constexpr (sizeof(T) == 4) {
-    *reinterpret_cast<float4*>(static_cast<float*>(base) + i) = make_float4(v[0], v[1], v[2], v[3]);
-  } else {
-    uint32_t w0, w1;
-    if constexpr (__is_same(T, bf16)) {
-      w0 = from_f32<bf16>(v[0]).bits | (static_cast<uint32_t>(from_f32<bf16>(v[1]).bits) << 16);
-      w1 = from_f32<bf16>(v[2]).bits | (static_cast<uint32_t>(from_f32<bf16>(v[3]).bits) << 16);
-    } else {
-      w0 = __builtin_bit_cast(uint16_t, static_cast<_Float16>(v[0])) |
-           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(v[1]))) << 16);
-      w1 = __builtin_bit_cast(uint16_t, static_cast<_Float16>(v[2])) |
-           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(v[3]))) << 16);
-    }
-    *reinterpret_cast<uint2*>(static_cast<T*>(base) + i) = make_uint2(w0, w1);
-  }
+  uint32_t w[kWordsOf<T, 4>];
+  pack_words<T, 4>(v, w);
+  store_words(static_cast<T*>(base) + i, w);
 }
 
 template <typename T>

@@ -42,15 +42,7 @@ __device__ __forceinline__ void v8_load(V8<T>& v, const T* p, int n, bool vec) {
   constexpr int W = V8<T>::kWords;
   v.mask = ~0u;
   if (vec && n >= 8) {
-    const uint4* q = reinterpret_cast<const uint4*>(p);
-#pragma unroll
-    for (int i = 0; i < W / 4; ++i) {
-      const uint4 t = q[i];
-      v.w[4 * i + 0] = t.x;
-      v.w[4 * i + 1] = t.y;
-      v.w[4 * i + 2] = t.z;
-      v.w[4 * i + 3] = t.w;
-    }
+    load_words(p, v.w);
   } else {
 #pragma unroll
     for (int i = 0; i < W; ++i) v.w[i] = 0u;
@@ -68,52 +60,19 @@ __device__ __forceinline__ void v8_load(V8<T>& v, const T* p, int n, bool vec) {
 
 template <typename T>
 __device__ __forceinline__ void v8_f32(const V8<T>& v, float (&f)[8]) {
-  if constexpr (sizeof(T) == 4) {
+  uint32_t w[V8<T>::kWords];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) f[e] = __uint_as_float(v.w[e] & v.mask);
-  } else if constexpr (__is_same(T, bf16)) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t w = v.w[i] & v.mask;
-      f[2 * i] = __uint_as_float(w << 16);
-      f[2 * i + 1] = __uint_as_float(w & 0xffff0000u);
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t w = v.w[i] & v.mask;
-      f[2 * i] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w & 0xffffu)));
-      f[2 * i + 1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w >> 16)));
-    }
-  }
-}
-
-// Two values rounded to a 16-bit type, packed low-first into one word.
-template <typename TM>
-__device__ __forceinline__ uint32_t pack2(float a, float b) {
-  if constexpr (__is_same(TM, bf16)) {
-    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-    const bf16x2_t t = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
-    return __builtin_bit_cast(uint32_t, t);
-  } else {
-    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
-    const f16x2_t t = {static_cast<_Float16>(a), static_cast<_Float16>(b)};
-    return __builtin_bit_cast(uint32_t, t);
-  }
+  for (int i = 0; i < V8<T>::kWords; ++i) w[i] = v.w[i] & v.mask;
+  unpack_words<T, 8>(w, f);
 }
 
 // Stores 8 fp32 values as T at p (16-byte aligned when `vec`), or the first n of them.
 template <typename T>
 __device__ __forceinline__ void v8_store(T* p, int n, bool vec, const float (&f)[8]) {
   if (vec && n >= 8) {
-    if constexpr (sizeof(T) == 4) {
-      uint4* q = reinterpret_cast<uint4*>(p);
-      q[0] = make_uint4(__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]), __float_as_uint(f[3]));
-      q[1] = make_uint4(__float_as_uint(f[4]), __float_as_uint(f[5]), __float_as_uint(f[6]), __float_as_uint(f[7]));
-    } else {
-      *reinterpret_cast<uint4*>(p) = make_uint4(pack2<T>(f[0], f[1]), pack2<T>(f[2], f[3]), pack2<T>(f[4], f[5]),
-                                                pack2<T>(f[6], f[7]));
-    }
+    uint32_t w[V8<T>::kWords];
+    pack_words<T, 8>(f, w);
+    store_words(p, w);
   } else {
 #pragma unroll
     for (int e = 0; e < 8; ++e)
@@ -166,16 +125,7 @@ __device__ __forceinline__ void load_win(const T* base, int ld, int nrows, int n
     const int r = r0 + rr;
     if constexpr (VEC) {
       const bool ok = r < nrows && c0 < ncols;
-      const T* p = ok ? base + (r * ld + c0) : safe;
-      const uint4* q = reinterpret_cast<const uint4*>(p);
-#pragma unroll
-      for (int i = 0; i < V8<T>::kWords / 4; ++i) {
-        const uint4 t = q[i];
-        v[rr].w[4 * i + 0] = t.x;
-        v[rr].w[4 * i + 1] = t.y;
-        v[rr].w[4 * i + 2] = t.z;
-        v[rr].w[4 * i + 3] = t.w;
-      }
+      load_words(ok ? base + (r * ld + c0) : safe, v[rr].w);
       v[rr].mask = ok ? ~0u : 0u;
     } else {
       const int n = r < nrows ? ncols - c0 : 0;
