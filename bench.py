@@ -234,10 +234,35 @@ def decode_case(steps=1024, warmup=16):
     roof = roofline(rmw + other, avg, load_traffic(f"{name}@256x80x64x128"))
     roof["kernel"] = name
     roof["algorithmic_bytes"] = rmw + other
-    del state, ring
+
+    # The backward at the same geometry: one step's gradients for every input through
+    # autograd (state, x, dt, A, B, C, D, z, dt_bias), timed as forward+backward steps and by
+    # the backward kernel's own launches.  It reads the state and the adjoint of the new
+    # state and writes the adjoint of the state (fp32), besides the per-token vectors.
+    r = ring[0]
+    leaves = [state.detach().clone(), r["x"], r["dt"], A, r["B"], r["C"], D, r["z"], bias]
+    leaves = [t.detach().clone().requires_grad_(True) for t in leaves]
+    g = torch.Generator().manual_seed(7)
+    dy = torch.randn(256, 80, 64, generator=g).to(dev)
+    dnew = torch.randn(256, 80, 64, 128, generator=g).to(dev)
+    st, x, dt, Ap, Bp, Cp, Dp, zp, bp = leaves
+
+    def bstep():
+        y, ns = mamba2_state_update(st, x, dt, Ap, Bp, Cp, D=Dp, z=zp, dt_bias=bp, dt_softplus=True)
+        torch.autograd.grad((y, ns), leaves, (dy.to(y.dtype), dnew))
+
+    ms_fb, _, kb = timed(bstep, 20, 3)
+    bwd_name = "state_update_bwd"
+    bwd_ms = kb[bwd_name][0] / max(kb[bwd_name][1], 1)
+    bwd_bytes = 3 * state.numel() * 4 + 256 * 80 * 64 * 2 * 5 + 256 * 128 * 2 * 4 + 256 * 80 * 4 * 2
+    bwd = {"ms_per_fwd_bwd_step": round(ms_fb, 4), "bwd_kernel_ms": round(bwd_ms, 4),
+           "bwd_gbs": round(bwd_bytes / (bwd_ms * 1e-3) / 1e9, 1), "bwd_algorithmic_bytes": bwd_bytes,
+           "bwd_hbm_frac": round(bwd_bytes / (bwd_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+           "kernels_ms": {k: round(v[0] / max(v[1], 1), 4) for k, v in sorted(kb.items())}}
+    del state, ring, leaves, dy, dnew
     torch.cuda.empty_cache()
     return {"ms_per_step": ms, "wall_ms_per_step": wall, "steps": steps,
-            "state_rmw_gbs": rmw / (ms * 1e-3) / 1e9, "roofline": roof,
+            "state_rmw_gbs": rmw / (ms * 1e-3) / 1e9, "roofline": roof, "backward": bwd,
             "kernels_ms": {k: round(v[0] / max(v[1], 1), 4) for k, v in sorted(kernels.items())}}
 
 
@@ -780,8 +805,9 @@ def main():
             "ms_per_step": round(dec["ms_per_step"], 5), "steps": dec["steps"],
             "config": {"batch": 256, "nheads": 80, "headdim": 64, "dstate": 128, "ngroups": 1,
                        "state_dtype": "f32", "io_dtype": "bf16"},
-            "roofline": dec["roofline"], "kernels_ms": dec["kernels_ms"]}
-        log(f"  {dec['ms_per_step'] * 1e3:.1f} us/step, {dec['state_rmw_gbs']:.1f} GB/s state RMW")
+            "roofline": dec["roofline"], "kernels_ms": dec["kernels_ms"], "backward": dec["backward"]}
+        log(f"  {dec['ms_per_step'] * 1e3:.1f} us/step, {dec['state_rmw_gbs']:.1f} GB/s state RMW; backward "
+            f"{dec['backward']['bwd_kernel_ms'] * 1e3:.1f} us, {dec['backward']['bwd_gbs']:.1f} GB/s")
     if want("ss2d"):
         log(f"ss2d four-path scan {SS2D_SHAPE} (batch, channels, groups, states, H, W) fwd+bwd, float32")
         s2 = ss2d_case(args.steps, args.warmup)

@@ -8,8 +8,8 @@
 //
 // Backward: the same workgroup recomputes the new state (instead of re-reading it
 // from memory), writes the row-local gradients, and reduces dB/dC over its rows
-// and dA/dD/ddt over its rows in a fixed order; a second kernel sums the
-// per-head partials over heads (dB/dC) or batch (dA/dD/ddt_bias).  Every output
+// and dA/dD/ddt over its rows in a fixed order; two more kernels sum the per-head
+// partials over heads (dB/dC) and over batch (dA/dD/ddt_bias, one workgroup per head).  Every output
 // has one writer, so the backward is bit-deterministic.
 #include <mutex>
 #include <vector>
@@ -281,40 +281,75 @@ __global__ void __launch_bounds__(kThreads) bwd(Args a) {
   }
 }
 
-// Sum the per-head partials: dB/dC over the heads of a group, dA/dD/ddt_bias over batch.
-__global__ void __launch_bounds__(256) reduce(Args a, float* dB, float* dC, float* dA, float* dD,
-                                              float* dbias) {
+// dB/dC: the per-head partials summed over the heads of a group, one thread per (batch,
+// group, state), heads in order.
+__global__ void __launch_bounds__(256) reduce_bc(Args a, float* dB, float* dC) {
   const Geo& g = a.g;
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int64_t N = g.dstate;
   const int64_t hpg = g.nheads / g.ngroups;
-  if (i < g.batch * g.ngroups * N) {
-    const int64_t n = i % N, bgi = i / N;
-    const int64_t b = bgi / g.ngroups, gi = bgi % g.ngroups;
-    float sb = 0.0f, sc = 0.0f;
-    for (int64_t k = 0; k < hpg; ++k) {
-      const int64_t bh = b * g.nheads + gi * hpg + k;
-      sb += a.pb[bh * N + n];
-      sc += a.pc[bh * N + n];
-    }
-    dB[i] = sb;
-    dC[i] = sc;
+  if (i >= g.batch * g.ngroups * N) return;
+  const int64_t n = i % N, bgi = i / N;
+  const int64_t b = bgi / g.ngroups, gi = bgi % g.ngroups;
+  float sb = 0.0f, sc = 0.0f;
+  for (int64_t k = 0; k < hpg; ++k) {
+    const int64_t bh = b * g.nheads + gi * hpg + k;
+    sb += a.pb[bh * N + n];
+    sc += a.pc[bh * N + n];
   }
-  if (i < g.nheads) {
-    float s = 0.0f, t = 0.0f, d = 0.0f;
-    for (int64_t b = 0; b < g.batch; ++b) {
-      s += a.pa[b * g.nheads + i];
-      if (a.pbias) t += a.pbias[b * g.nheads + i];
-      if (a.D && !g.d_per_row) d += a.pd[b * g.nheads + i];
-    }
-    dA[i] = s;
-    if (dbias) dbias[i] = t;
-    if (a.D && !g.d_per_row && dD) dD[i] = d;
+  dB[i] = sb;
+  dC[i] = sc;
+}
+
+// Sum over the workgroup's 256 threads in a fixed order (lane butterflies, then the four
+// wavefronts in order); every thread gets the result.
+__device__ __forceinline__ float block_sum(float v, float* wsum) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+}
+
+// dA, ddt_bias and dD: the per-(batch, head) partials summed over the batch, one workgroup
+// per head.  Thread t adds batches t, t + 256, ... in order; the threads' sums then meet in
+// a fixed tree.  A per-row D takes headdim columns x 4 batch quarters per pass.
+__global__ void __launch_bounds__(256) reduce_heads(Args a, float* dA, float* dD, float* dbias) {
+  __shared__ float wsum[4];
+  __shared__ float part[4][64];
+  const Geo& g = a.g;
+  const int64_t h = blockIdx.x;
+  const int t = threadIdx.x;
+  float s = 0.0f, u = 0.0f, d = 0.0f;
+  for (int64_t b = t; b < g.batch; b += 256) {
+    s += a.pa[b * g.nheads + h];
+    if (a.pbias) u += a.pbias[b * g.nheads + h];
+    if (a.D && !g.d_per_row) d += a.pd[b * g.nheads + h];
   }
-  if (a.D && g.d_per_row && dD && i < g.nheads * g.headdim) {
-    float d = 0.0f;
-    for (int64_t b = 0; b < g.batch; ++b) d += a.pd[b * g.nheads * g.headdim + i];
-    dD[i] = d;
+  s = block_sum(s, wsum);
+  if (t == 0) dA[h] = s;
+  if (dbias) {
+    u = block_sum(u, wsum);
+    if (t == 0) dbias[h] = u;
+  }
+  if (a.D && !g.d_per_row && dD) {
+    d = block_sum(d, wsum);
+    if (t == 0) dD[h] = d;
+  }
+  if (a.D && g.d_per_row && dD) {
+    const int col = t & 63, quarter = t >> 6;
+    for (int64_t p0 = 0; p0 < g.headdim; p0 += 64) {
+      const int64_t pp = p0 + col;
+      float v = 0.0f;
+      if (pp < g.headdim)
+        for (int64_t b = quarter; b < g.batch; b += 4) v += a.pd[(b * g.nheads + h) * g.headdim + pp];
+      __syncthreads();
+      part[quarter][col] = v;
+      __syncthreads();
+      if (quarter == 0 && pp < g.headdim)
+        dD[h * g.headdim + pp] = (part[0][col] + part[1][col]) + (part[2][col] + part[3][col]);
+    }
   }
 }
 
@@ -479,11 +514,11 @@ int run_bwd(const mko_state_update_params* p, void* stream, char* ws, const Geo&
   else if (g.state_dtype == MKO_BF16) launch_bwd_t<bf16>(a, g.vec, s, grid);
   else launch_bwd_t<_Float16>(a, g.vec, s, grid);
   const int64_t nred = g.batch * g.ngroups * g.dstate;
-  int64_t total = nred > g.nheads * g.headdim ? nred : g.nheads * g.headdim;
-  if (total < g.nheads) total = g.nheads;
+  if (nred > 0)
+    MKO_TIMED("state_update_bwd_reduce", s,
+              reduce_bc<<<static_cast<unsigned>((nred + 255) / 256), 256, 0, s>>>(a, p->dB, p->dC));
   MKO_TIMED("state_update_bwd_reduce", s,
-            reduce<<<static_cast<unsigned>((total + 255) / 256), 256, 0, s>>>(a, p->dB, p->dC, p->dA, p->dD,
-                                                                               p->ddt_bias));
+            reduce_heads<<<static_cast<unsigned>(g.nheads), 256, 0, s>>>(a, p->dA, p->dD, p->ddt_bias));
   return mko_check_launch("state_update_bwd");
 }
 
