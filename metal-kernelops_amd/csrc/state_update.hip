@@ -153,7 +153,7 @@ __global__ void __launch_bounds__(kThreads) fwd(Args a) {
 template <typename TS, int VEC>
 __global__ void __launch_bounds__(kThreads) bwd(Args a) {
   __shared__ float red[kThreads * kMaxPerThread];  // [rows_per_pass][dstate] fold buffer
-  __shared__ float rowv[3][kThreads];
+  __shared__ float rowv[3][kThreads];  // per-row dA, dD, ddt terms of the current 256-row window
   const Geo& g = a.g;
   const int64_t bh = blockIdx.x;
   const int64_t b = bh / g.nheads, h = bh % g.nheads;
@@ -238,22 +238,40 @@ __global__ void __launch_bounds__(kThreads) bwd(Args a) {
         }
         const float dD = dyp * xv;
         if (a.D && g.d_per_row) a.pd[row] = dD;
-        rowv[0][slot] = sa * decay * del;  // dA contribution
-        rowv[1][slot] = dD;
-        rowv[2][slot] = dd;
+        const int rw = p % kThreads;  // the row's slot in its window
+        rowv[0][rw] = sa * decay * del;  // dA contribution
+        rowv[1][rw] = dD;
+        rowv[2][rw] = dd;
       }
     }
-    // Fold this pass's per-row values in row order.
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      const int pend = min(static_cast<int>(g.headdim) - p0, rows_per_pass);
-      for (int r = 0; r < pend; ++r) {
-        sum_a += rowv[0][r];
-        sum_d += rowv[1][r];
-        sum_t += rowv[2][r];
+    // At the end of a 256-row window (or of the rows), fold its per-row values: lane r of
+    // the first wavefront adds rows r, r + 64, ... in order, then a fixed butterfly.
+    const int pnext = p0 + rows_per_pass;
+    if (pnext % kThreads == 0 || pnext >= g.headdim) {
+      __syncthreads();
+      if (threadIdx.x < kWave) {
+        const int wbase = p0 - p0 % kThreads;
+        const int nrows = min(static_cast<int>(g.headdim) - wbase, kThreads);
+        float va = 0.0f, vd = 0.0f, vt = 0.0f;
+        for (int r = threadIdx.x; r < nrows; r += kWave) {
+          va += rowv[0][r];
+          vd += rowv[1][r];
+          vt += rowv[2][r];
+        }
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) {
+          va += __shfl_xor(va, m);
+          vd += __shfl_xor(vd, m);
+          vt += __shfl_xor(vt, m);
+        }
+        if (threadIdx.x == 0) {
+          sum_a += va;
+          sum_d += vd;
+          sum_t += vt;
+        }
       }
+      __syncthreads();
     }
-    __syncthreads();
   }
   // dB/dC: fold the lanes' per-state partials over the row slots in a fixed order.
   for (int which = 0; which < 2; ++which) {
