@@ -201,7 +201,9 @@ int mko_state_update_bwd_static(const mko_state_update_params* p, void* stream);
 #define MKO_SSD_D_PER_ROW 2u /* D is (nheads, headdim) instead of (nheads,) */
 #define MKO_SSD_SAVE_Y 4u    /* the forward also saves the chunk output before the skip and
                                 the gate (fp32), so the backward need not recompute it; the
-                                flag must be the same for the forward and its backward */
+                                flag must be the same for the forward and its backward.  16-bit
+                                inputs with dstate <= 128 ignore it: their backward always
+                                recomputes that output, and mko_ssd_saved_bytes leaves it out */
 
 typedef struct mko_ssd_params {
   const void* x;              /* (batch, length, nheads, headdim)  x_dtype            */
