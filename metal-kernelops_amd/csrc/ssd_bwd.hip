@@ -2,8 +2,11 @@
 //
 // With u_s = step_s x_s, K[l][s] = e^{cs_l - cs_s} CB[l][s] (s <= l), gy = dy * silu(z),
 // S_in / S_out the states entering / leaving a chunk and G the adjoint of S_out:
-//   gate        y~ = K u + e^{cs} C S_in^T recomputed; dz; gy; gy.y~ per token; dD partials
+//   gate        y~ = K u + e^{cs} C S_in^T (saved or recomputed); dz; gy; gy.y~ per token;
+//               dD partials
 //   chunk_state local adjoint of S_in: sum_l e^{cs_l} gy_l (x) C_l
+//   (16-bit inputs with d_state <= 128 run gate and chunk_state as one kernel per chunk and
+//   head, gate_state_mt, and du as du_mt; see multi_tile() in ssd.hpp)
 //   state_rev   per state element, backwards over chunks: G, dinitial and e^T <G, S_in>
 //               (the transfer's part of the derivative with respect to the chunk's total decay T)
 //   du          du = K^T gy + e^{T - cs_s} B_s G^T; dx = step du + D gy; per token x.du,
