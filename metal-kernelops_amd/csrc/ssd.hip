@@ -325,6 +325,159 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) c
   });
 }
 
+// The schedule of chunk_scan_cm at qb = 4 and two state tiles (d_state 128).  The chunk's
+// four token tiles run in two halves, {0, 1} and {2, 3}, each with its own two accumulators:
+// the state stages of the half's tiles (right operand: S_in's n-tiles), then its intra
+// pairs (i, j) column by column, u_j staged with the first pair of its column.  Each tile
+// accumulates its terms in chunk_scan_mt's order (state, then j ascending) and runs its
+// epilogue after its diagonal pair.  Two LDS slots hold the right operands: S_in's n-tile
+// k, or u_j, in slot (k or j) & 1; every slot is rewritten at least two stages after its last
+// reader, so the stage barriers cover it.
+struct CmStage {
+  bool state;
+  int i, j;   // state stages: token tile i, n-tile j; pairs: l-tile i, s-tile j
+  int stage;  // this stage's put also stages u_j (pairs) or S_in's n-tile j (state) into slot j & 1, when set
+  int load;   // after this stage's products: 1 = x and z of tile 1, 2 = S_in, 3 = x of tile 1,
+              // 4 = x and z of tile 2, 5 = x and z of tile 3, 6 = x of tile 0
+};
+constexpr CmStage kCmSchedule[18] = {
+    {true, 0, 0, 0, 0},  {true, 0, 1, 0, 0},  {true, 1, 0, 0, 0},  {true, 1, 1, 0, 0},
+    {false, 0, 0, 1, 1}, {false, 1, 0, 0, 2}, {false, 1, 1, 1, 6},
+    {true, 2, 0, 1, 0},  {true, 2, 1, 1, 0},  {true, 3, 0, 0, 0},  {true, 3, 1, 0, 0},
+    {false, 2, 0, 1, 3}, {false, 3, 0, 0, 0}, {false, 2, 1, 1, 4}, {false, 3, 1, 0, 0},
+    {false, 2, 2, 1, 5}, {false, 3, 2, 0, 0}, {false, 3, 3, 1, 0}};
+
+// chunk_scan_mt at qb = 4, d_state 128 with three workgroups per CU (16-bit operands): the same
+// products in the order of kCmSchedule, so that LDS holds two right-operand slots instead of
+// all of a chunk's u tiles, and two accumulators are live instead of one per tile.  Compact
+// 64-element operand tiles; 53.8 KB of LDS.
+template <typename TM, bool VEC>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) chunk_scan_cm(Geo g, Ptrs p) {
+  static_assert(sizeof(TM) == 2, "16-bit operands");
+  constexpr int LD = compact_ld<TM>();
+  constexpr int TE = LdsTile<TM, LD>::elems;
+  constexpr int N = 18;
+  constexpr int Q = 256;
+  __shared__ __align__(16) TM ab[2][TE];  // left operand, double-buffered
+  __shared__ __align__(16) TM ub[2][TE];  // right operand slots
+  __shared__ __align__(16) float red[64 * 65];
+  __shared__ __align__(16) float csc[Q], dlc[Q], ecol[Q], ecs[Q], dcol[64];
+  const WgId id = wg_id(g.nheads, g.npt);
+  const int64_t h = id.x;
+  const int pt = id.y;
+  const int64_t b = id.z / g.nc;
+  const int c = static_cast<int>(id.z % g.nc);
+  const int64_t bh = b * g.nheads + h, gg = h / g.hpg;
+  const int lane = threadIdx.x & 63;
+  int wm, wn;
+  quadrant(threadIdx.x >> 6, wm, wn);
+  const int r0 = blk_r0(), c0 = blk_c0();
+  const int64_t tc = static_cast<int64_t>(c) * Q, pc0 = static_cast<int64_t>(pt) * 64;
+  const TM* X = static_cast<const TM*>(p.x);
+  const TM* Z = p.z ? static_cast<const TM*>(p.z) : X;
+  const TM* Cm = static_cast<const TM*>(p.C);
+  const TM* cbt = static_cast<const TM*>(p.cb) + ((b * g.nc + c) * g.ngroups + gg) * Q * Q;
+  const TM* S = static_cast<const TM*>(p.states) + (bh * g.nc + c) * g.headdim * g.dstate;
+  V8<TM> xv[2], zv[2];  // x and z rows of the tile whose u is staged next
+  V8<TM> sv[2][2];      // S_in's n-tiles, for the second half
+  {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) load_sw<TM, VEC>(g, S, pc0, 64 * k, sv[k]);
+    load_xw<TM, VEC>(g, X, b, tc, h, pc0, xv);
+    load_xw<TM, VEC>(g, Z, b, tc, h, pc0, zv);
+    load_chunk_cs(g, p, bh, c, csc, dlc, ecol);
+    if (threadIdx.x < Q) ecs[threadIdx.x] = fast_exp(csc[threadIdx.x]);
+    if (threadIdx.x < 64) {
+      const int64_t pp = pc0 + threadIdx.x;
+      dcol[threadIdx.x] = !p.D ? 0.0f : g.d_per_row ? (pp < g.headdim ? p.D[h * g.headdim + pp] : 0.0f) : p.D[h];
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) put_raw<TM, false, LD>(ub[k], r0, c0, sv[k][0], sv[k][1]);  // Bt[p][n] = S_in[p][n]
+  }
+  struct Regs {
+    V8<TM> a[2];
+  };
+  auto fetch = [&](auto kc, Regs& r) {
+    constexpr CmStage sg = kCmSchedule[decltype(kc)::value];
+    if constexpr (sg.state)
+      load_bw<TM, VEC>(g, Cm, b, tc + 64 * sg.i, gg, 64 * sg.j, r.a);  // C rows l
+    else
+      load_win<TM, true>(cbt + (64 * sg.i) * Q + 64 * sg.j, Q, 64, 64, r.a, cbt);  // cb rows l
+  };
+  auto put = [&](auto kc, Regs& r) {
+    constexpr int k = decltype(kc)::value;
+    constexpr CmStage sg = kCmSchedule[k];
+    if constexpr (sg.state) {
+      put_raw<TM, false, LD>(ab[k & 1], r0, c0, r.a[0], r.a[1]);  // A[l][n] = C_l[n]
+      if constexpr (sg.stage) put_raw<TM, false, LD>(ub[sg.j & 1], r0, c0, sv[sg.j][0], sv[sg.j][1]);
+    } else {
+      float a[8], bb[8];
+      k_block<TM>(r.a[0], r.a[1], csc, ecol, sg.i, sg.j, r0, c0, a, bb);
+      put2x8<TM, false, LD>(ab[k & 1], r0, c0, a, bb);  // A[l][s] = K[l][s]
+      if constexpr (sg.stage) {
+        scale8(xv[0], dlc[64 * sg.j + r0], a);
+        scale8(xv[1], dlc[64 * sg.j + r0 + 1], bb);
+        put2x8<TM, true, LD>(ub[sg.j & 1], r0, c0, a, bb);  // Bt[p][s] = step_s x_s[p]
+      }
+    }
+  };
+  f32x16 acc[2];
+  zero(acc[0]);
+  zero(acc[1]);
+  constexpr int D = 2;
+  Regs regs[D];
+  __syncthreads();  // csc, dlc, S_in
+  pipeline_static<N, D>(regs, fetch, put, [&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    constexpr CmStage sg = kCmSchedule[k];
+    f32x16& ac = acc[sg.i & 1];
+    if constexpr (sg.state) {
+      mma_tile<TM, LD>(ac, ab[k & 1], ub[sg.j & 1], wm, wn, lane, 64);
+      if constexpr (sg.j == 1) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) ac[r] *= ecs[64 * sg.i + acc_row(wm, lane, r)];
+      }
+    } else {
+      mma_tile<TM, LD>(ac, ab[k & 1], ub[sg.j & 1], wm, wn, lane, 64);
+      if constexpr (sg.i == sg.j) {
+        // tile i is complete
+        const int64_t tl0 = tc + 64 * sg.i;
+        acc_to_lds(red, ac, wm, wn, lane);
+        zero(ac);
+        __syncthreads();
+        float v[2][8];
+        lds_block(red, r0, c0, v[0], v[1]);
+        const float4 da = *reinterpret_cast<const float4*>(dcol + c0);
+        const float4 db = *reinterpret_cast<const float4*>(dcol + c0 + 4);
+        const float dv[8] = {da.x, da.y, da.z, da.w, db.x, db.y, db.z, db.w};
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+          float xf[8], zf[8];
+          v8_f32(xv[rr], xf);
+          if (p.z) v8_f32(zv[rr], zf);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            float y = fmaf(dv[e], xf[e], v[rr][e]);
+            if (p.z) y *= zf[e] * sigmoid(zf[e]);
+            v[rr][e] = y;
+          }
+        }
+        store_xw<TM, VEC>(g, static_cast<TM*>(p.y), b, tl0, h, pc0, v[0], v[1]);
+      }
+    }
+    if constexpr (sg.load == 1 || sg.load == 4 || sg.load == 5) {
+      constexpr int t = sg.load == 1 ? 1 : sg.load == 4 ? 2 : 3;
+      load_xw<TM, VEC>(g, X, b, tc + 64 * t, h, pc0, xv);
+      load_xw<TM, VEC>(g, Z, b, tc + 64 * t, h, pc0, zv);
+    } else if constexpr (sg.load == 2) {
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) load_sw<TM, VEC>(g, S, pc0, 64 * kk, sv[kk]);
+    } else if constexpr (sg.load == 3 || sg.load == 6) {
+      load_xw<TM, VEC>(g, X, b, tc + (sg.load == 3 ? 64 : 0), h, pc0, xv);  // u_1, u_0 again
+    }
+  });
+}
+
 // ---------------------------------------------------------------- host
 
 int make_geo(const mko_ssd_params* prm, Geo* g) {
@@ -448,6 +601,10 @@ static void launch_fwd_t(const Geo& g, const Ptrs& q, hipStream_t s) {
                 g, q));
   if constexpr (sizeof(TM) == 2) {
     const dim3 grid(g.npt * g.nc * bh);
+    if (multi_tile(g) && g.qb == 4 && g.nnt == 2 && g.dstate == 128) {
+      MKO_TIMED("ssd_chunk_scan", s, chunk_scan_cm<TM, VEC><<<grid, 256, 0, s>>>(g, q));
+      return;
+    }
     if (multi_tile(g)) {
       if (g.qb == 4 && g.nnt == 2) MKO_TIMED("ssd_chunk_scan", s, chunk_scan_mt<TM, VEC, 4, 2><<<grid, 256, 0, s>>>(g, q));
       else if (g.qb == 4) MKO_TIMED("ssd_chunk_scan", s, chunk_scan_mt<TM, VEC, 4, 1><<<grid, 256, 0, s>>>(g, q));

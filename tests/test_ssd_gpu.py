@@ -51,6 +51,7 @@ SHAPES = [
     (1, 5, 2, 2, 1, 3),
     (2, 300, 4, 64, 1, 128),   # two 128-token chunks, ragged tail
     (1, 1100, 2, 80, 2, 72),   # 256-token chunks, P and N not multiples of 64
+    (1, 1100, 3, 64, 1, 128),  # 256-token chunks at the c4 head shape, ragged tail
 ]
 
 
