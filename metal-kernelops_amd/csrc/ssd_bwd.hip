@@ -762,6 +762,197 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) d
   });
 }
 
+// The schedule of du_cm at qb = 4 and two state tiles (d_state 128).  The output tiles run in
+// two halves, {3, 2} and {1, 0}, each with its own two accumulators: the half's state stages
+// (right operand: G's n-tiles; tau after a tile's last one), then its intra pairs (l-tile i,
+// s-tile j) by l-tile in descending order, gy_i staged with the first pair of its l-tile.  A
+// tile is complete after its pair with i = j, where its epilogue runs.  Two LDS slots hold the
+// right operands: G's n-tile k in slot k, gy_i in slot (i + 1) & 1; every slot is rewritten at
+// least two stages after its last reader, so the stage barriers cover it.
+struct DuCmStage {
+  bool state;
+  int i, j;   // state stages: i = output tile, j = n-tile; pairs: l-tile i, s-tile j
+  int stage;  // this stage's put also stages gy_i (pairs) or G's n-tile j (state), when set
+  int load;   // after this stage's products: 1 = gy_2, 2 = gy_3, x_1 and x_0, 3 = gy_2,
+              // 4 = gy_1, 5 = gy_0 (G's n-tiles stay in registers from the start)
+};
+constexpr DuCmStage kDuCmSchedule[18] = {
+    {true, 3, 0, 0, 0},  {true, 2, 0, 0, 0},  {true, 3, 1, 0, 0},  {true, 2, 1, 0, 0},
+    {false, 3, 3, 1, 1}, {false, 3, 2, 0, 6}, {false, 2, 2, 1, 2},
+    {true, 1, 0, 1, 0},  {true, 0, 0, 0, 0},  {true, 1, 1, 1, 0},  {true, 0, 1, 0, 0},
+    {false, 3, 1, 1, 3}, {false, 3, 0, 0, 0}, {false, 2, 1, 1, 4}, {false, 2, 0, 0, 0},
+    {false, 1, 1, 1, 5}, {false, 1, 0, 0, 0}, {false, 0, 0, 1, 0}};
+
+// du_mt at qb = 4, d_state 128 with three workgroups per CU (16-bit operands): the same
+// products in the order of kDuCmSchedule, two right-operand slots in LDS instead of all of a
+// chunk's gy tiles and G, two accumulators live instead of one per tile.  Compact 64-element
+// operand tiles; 53.8 KB of LDS.
+template <typename TM, bool VEC>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) du_cm(Geo g, BwdPlan pl, Ptrs p) {
+  static_assert(sizeof(TM) == 2, "16-bit operands");
+  constexpr int LD = compact_ld<TM>();
+  constexpr int TE = LdsTile<TM, LD>::elems;
+  constexpr int N = 18;
+  constexpr int Q = 256;
+  __shared__ __align__(16) TM ab[2][TE];  // left operand, double-buffered
+  __shared__ __align__(16) TM ub[2][TE];  // right operand slots
+  __shared__ __align__(16) float red[64 * 65];
+  __shared__ __align__(16) float csc[Q], dlc[Q], ecol[Q], ew[Q], dcol[64];
+  const WgId id = wg_id(g.nheads, g.npt);
+  const int64_t h = id.x;
+  const int pt = id.y;
+  const int64_t b = id.z / g.nc;
+  const int c = static_cast<int>(id.z % g.nc);
+  const int64_t bh = b * g.nheads + h, gg = h / g.hpg;
+  const int lane = threadIdx.x & 63;
+  int wm, wn;
+  quadrant(threadIdx.x >> 6, wm, wn);
+  const int r0 = blk_r0(), c0 = blk_c0();
+  const int64_t tc = static_cast<int64_t>(c) * Q, pc0 = static_cast<int64_t>(pt) * 64;
+  const TM* X = static_cast<const TM*>(p.x);
+  const TM* gy = static_cast<const TM*>(p.gy);
+  const TM* Bm = static_cast<const TM*>(p.B);
+  const TM* cbt = static_cast<const TM*>(p.cb) + ((b * g.nc + c) * g.ngroups + gg) * Q * Q;
+  const TM* G = static_cast<const TM*>(p.dstates) + (bh * g.nc + c) * g.headdim * g.dstate;
+  const int64_t so = (bh * g.nc + c) * Q;
+  V8<TM> xs[2][2];  // x rows of the output tiles, tile j in set j & 1
+  V8<TM> gv[2];     // gy rows of the l-tile staged next (its epilogue's too when i = j)
+  V8<TM> sv[2][2];  // G's n-tiles, for the second half
+  {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) load_sw<TM, VEC>(g, G, pc0, 64 * k, sv[k]);
+    load_xw<TM, VEC>(g, X, b, tc + 192, h, pc0, xs[1]);
+    load_xw<TM, VEC>(g, X, b, tc + 128, h, pc0, xs[0]);
+    load_xw<TM, VEC>(g, gy, b, tc + 192, h, pc0, gv);
+    load_chunk_cs(g, p, bh, c, csc, dlc, ecol);
+    if (threadIdx.x < Q) ew[threadIdx.x] = fast_exp(p.cs[so + Q - 1] - p.cs[so + threadIdx.x]);
+    if (threadIdx.x < 64) {
+      const int64_t pp = pc0 + threadIdx.x;
+      dcol[threadIdx.x] = !p.D ? 0.0f : g.d_per_row ? (pp < g.headdim ? p.D[h * g.headdim + pp] : 0.0f) : p.D[h];
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) put_raw<TM, false, LD>(ub[k], r0, c0, sv[k][0], sv[k][1]);  // Bt[p][n] = G[p][n]
+  }
+  struct Regs {
+    V8<TM> a[2];
+  };
+  auto fetch = [&](auto kc, Regs& r) {
+    constexpr DuCmStage sg = kDuCmSchedule[decltype(kc)::value];
+    if constexpr (sg.state)
+      load_bw<TM, VEC>(g, Bm, b, tc + 64 * sg.i, gg, 64 * sg.j, r.a);  // B rows s
+    else
+      load_win<TM, true>(cbt + (64 * sg.i) * Q + 64 * sg.j, Q, 64, 64, r.a, cbt);  // cb rows l
+  };
+  auto put = [&](auto kc, Regs& r) {
+    constexpr int k = decltype(kc)::value;
+    constexpr DuCmStage sg = kDuCmSchedule[k];
+    if constexpr (sg.state) {
+      put_raw<TM, false, LD>(ab[k & 1], r0, c0, r.a[0], r.a[1]);  // A[s][n] = B_s[n]
+      if constexpr (sg.stage) put_raw<TM, false, LD>(ub[sg.j], r0, c0, sv[sg.j][0], sv[sg.j][1]);
+    } else {
+      float a[8], bb[8];
+      k_block<TM>(r.a[0], r.a[1], csc, ecol, sg.i, sg.j, r0, c0, a, bb);
+      put2x8<TM, true, LD>(ab[k & 1], r0, c0, a, bb);  // A[s][l] = K[l][s]
+      if constexpr (sg.stage) put_raw<TM, true, LD>(ub[(sg.i + 1) & 1], r0, c0, gv[0], gv[1]);  // Bt[p][l] = gy_l[p]
+    }
+  };
+  // x of tile j's rows s and u_s = R(step_s x_s), the rounded input of the forward's products
+  auto u8 = [&](int j, const V8<TM> (&xv)[2], int rr, float (&xf)[8], float (&uf)[8]) {
+    v8_f32(xv[rr], xf);
+    const float d = dlc[64 * j + r0 + rr];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) uf[e] = to_f32(from_f32<TM>(d * xf[e]));
+  };
+  const int64_t po0 = ((bh * g.nc + c) * g.npt + pt) * Q;
+  f32x16 acc[2];
+  zero(acc[0]);
+  zero(acc[1]);
+  constexpr int D = 2;
+  Regs regs[D];
+  __syncthreads();  // csc, dlc, ecol, ew, dcol, G
+  pipeline_static<N, D>(regs, fetch, put, [&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    constexpr DuCmStage sg = kDuCmSchedule[k];
+    if constexpr (sg.state) {
+      constexpr int j = sg.i;
+      f32x16& ac = acc[j & 1];
+      mma_tile<TM, LD>(ac, ab[k & 1], ub[sg.j], wm, wn, lane, 64);
+      if constexpr (sg.j == 1) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) ac[r] *= ew[64 * j + acc_row(wm, lane, r)];
+        // tau_s = u_s . du_state_s
+        acc_to_lds(red, ac, wm, wn, lane);
+        __syncthreads();
+        float v[2][8];
+        lds_block(red, r0, c0, v[0], v[1]);
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+          float xf[8], uf[8];
+          u8(j, xs[j & 1], rr, xf, uf);
+          float tau = 0.0f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) tau = fmaf(uf[e], v[rr][e], tau);
+          tau = row8_sum(tau);
+          if ((threadIdx.x & 7) == 0) p.tau[po0 + 64 * j + r0 + rr] = tau;
+        }
+      }
+    } else {
+      constexpr int j = sg.j;
+      f32x16& ac = acc[j & 1];
+      mma_tile<TM, LD>(ac, ab[k & 1], ub[(sg.i + 1) & 1], wm, wn, lane, 64);
+      if constexpr (sg.i == sg.j) {
+        // dx = step du + D gy, and the row sums x.du and u.du of tile j
+        const int64_t ts0 = tc + 64 * j;
+        acc_to_lds(red, ac, wm, wn, lane);
+        zero(ac);
+        __syncthreads();
+        float du[2][8], dxo[2][8];
+        lds_block(red, r0, c0, du[0], du[1]);
+        const float4 da = *reinterpret_cast<const float4*>(dcol + c0);
+        const float4 db = *reinterpret_cast<const float4*>(dcol + c0 + 4);
+        const float dv[8] = {da.x, da.y, da.z, da.w, db.x, db.y, db.z, db.w};
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+          float gf[8], xf[8], uf[8];
+          v8_f32(gv[rr], gf);
+          u8(j, xs[j & 1], rr, xf, uf);
+          const float d = dlc[64 * j + r0 + rr];
+          float sx = 0.0f, su = 0.0f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            dxo[rr][e] = fmaf(dv[e], gf[e], d * du[rr][e]);
+            sx = fmaf(xf[e], du[rr][e], sx);
+            su = fmaf(uf[e], du[rr][e], su);
+          }
+          sx = row8_sum(sx);
+          su = row8_sum(su);
+          if ((threadIdx.x & 7) == 0) {
+            p.dsx[po0 + 64 * j + r0 + rr] = sx;
+            p.ut[po0 + 64 * j + r0 + rr] = su;
+          }
+        }
+        store_xw<TM, VEC>(g, static_cast<TM*>(p.dx), b, ts0, h, pc0, dxo[0], dxo[1]);
+      }
+    }
+    if constexpr (sg.load == 1) {
+      load_xw<TM, VEC>(g, gy, b, tc + 128, h, pc0, gv);
+    } else if constexpr (sg.load == 2) {
+      load_xw<TM, VEC>(g, gy, b, tc + 192, h, pc0, gv);
+      load_xw<TM, VEC>(g, X, b, tc + 64, h, pc0, xs[1]);
+      load_xw<TM, VEC>(g, X, b, tc, h, pc0, xs[0]);
+    } else if constexpr (sg.load == 3) {
+      load_xw<TM, VEC>(g, gy, b, tc + 128, h, pc0, gv);
+    } else if constexpr (sg.load == 4) {
+      load_xw<TM, VEC>(g, gy, b, tc + 64, h, pc0, gv);
+    } else if constexpr (sg.load == 5) {
+      load_xw<TM, VEC>(g, gy, b, tc, h, pc0, gv);
+    } else if constexpr (sg.load == 6) {
+#pragma unroll
+      for (int k = 0; k < 2; ++k) load_sw<TM, VEC>(g, G, pc0, 64 * k, sv[k]);
+    }
+  });
+}
+
 // Adjoint of C.B^T for one lower tile (i, j) of a chunk, summed over a block of the
 // group's heads: sum_h (gy_i u_j^T) o e^{cs_l - cs_s}.
 template <typename TM, bool VEC>
@@ -1227,6 +1418,10 @@ void launch_du(const Geo& g, const BwdPlan& pl, const Ptrs& q, hipStream_t s) {
   const unsigned bh = static_cast<unsigned>(g.batch * g.nheads);
   if constexpr (sizeof(TM) == 2) {
     const dim3 grid(g.npt * g.nc * bh);
+    if (multi_tile(g) && g.qb == 4 && g.nnt == 2 && g.dstate == 128) {
+      MKO_TIMED("ssd_du", s, du_cm<TM, VEC><<<grid, 256, 0, s>>>(g, pl, q));
+      return;
+    }
     if (multi_tile(g)) {
       if (g.qb == 4 && g.nnt == 2) MKO_TIMED("ssd_du", s, du_mt<TM, VEC, 4, 2><<<grid, 256, 0, s>>>(g, pl, q));
       else if (g.qb == 4) MKO_TIMED("ssd_du", s, du_mt<TM, VEC, 4, 1><<<grid, 256, 0, s>>>(g, pl, q));
