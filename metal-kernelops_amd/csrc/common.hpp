@@ -83,6 +83,26 @@ __device__ __forceinline__ void store_words(void* p, const uint32_t (&w)[W]) {
   }
 }
 
+// p advanced by off bytes.  With a wave-uniform p the access compiles to the scalar-base
+// form of the global loads and stores (64-bit base in SGPRs, one 32-bit offset VGPR per
+// lane) instead of a 64-bit address pair per lane.
+template <typename T>
+__device__ __forceinline__ T* at_bytes(T* p, uint32_t off) {
+  return reinterpret_cast<T*>(reinterpret_cast<char*>(p) + off);
+}
+template <typename T>
+__device__ __forceinline__ const T* at_bytes(const T* p, uint32_t off) {
+  return reinterpret_cast<const T*>(reinterpret_cast<const char*>(p) + off);
+}
+
+// v, unchanged, as a value the optimiser cannot see through.  A byte offset passed through it
+// stays a 32-bit value in one VGPR (the scalar-base form of at_bytes), where a select or a
+// mask folded into it would otherwise be widened to a 64-bit address per lane.
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+  asm("" : "+v"(v));
+  return v;
+}
+
 // The two 16-bit elements of a word as fp32 (exact).
 template <typename T>
 __device__ __forceinline__ void unpack2(uint32_t w, float& lo, float& hi) {

@@ -325,32 +325,35 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) c
   });
 }
 
-// The schedule of chunk_scan_cm at qb = 4 and two state tiles (d_state 128).  The chunk's
-// four token tiles run in two halves, {0, 1} and {2, 3}, each with its own two accumulators:
-// the state stages of the half's tiles (right operand: S_in's n-tiles), then its intra
-// pairs (i, j) column by column, u_j staged with the first pair of its column.  Each tile
-// accumulates its terms in chunk_scan_mt's order (state, then j ascending) and runs its
-// epilogue after its diagonal pair.  Two LDS slots hold the right operands: S_in's n-tile
-// k, or u_j, in slot (k or j) & 1; every slot is rewritten at least two stages after its last
-// reader, so the stage barriers cover it.
+// The three-workgroups-per-CU schedule of a chunk's output at qb = 4 and two state tiles
+// (d_state 128).  The chunk's four token tiles run in two halves, {0, 1} and {2, 3}, each with
+// its own two accumulators: the state stages of the half's tiles (right operand: S_in's
+// n-tiles), then its intra pairs (i, j) column by column, u_j staged with the first pair of
+// its column.  Each tile accumulates its terms in chunk_scan_mt's order (state, then j
+// ascending) and runs its epilogue after its diagonal pair.  Two LDS slots hold the right
+// operands: S_in's n-tile k, or u_j, in slot (k or j) & 1; every slot is rewritten at least
+// two stages after its last reader, so the stage barriers cover it.  Register operands are
+// requested one or two stages before their use.
 struct CmStage {
   bool state;
   int i, j;   // state stages: token tile i, n-tile j; pairs: l-tile i, s-tile j
   int stage;  // this stage's put also stages u_j (pairs) or S_in's n-tile j (state) into slot j & 1, when set
-  int load;   // after this stage's products: 1 = x and z of tile 1, 2 = S_in, 3 = x of tile 1,
-              // 4 = x and z of tile 2, 5 = x and z of tile 3, 6 = x of tile 0
+  // requested after this stage's products (-1: none): x rows of token tile x (for u_x), z rows
+  // of tile z (the epilogue's inputs), S_in's n-tile s
+  int x, z, s;
 };
 constexpr CmStage kCmSchedule[18] = {
-    {true, 0, 0, 0, 0},  {true, 0, 1, 0, 0},  {true, 1, 0, 0, 0},  {true, 1, 1, 0, 0},
-    {false, 0, 0, 1, 1}, {false, 1, 0, 0, 2}, {false, 1, 1, 1, 6},
-    {true, 2, 0, 1, 0},  {true, 2, 1, 1, 0},  {true, 3, 0, 0, 0},  {true, 3, 1, 0, 0},
-    {false, 2, 0, 1, 3}, {false, 3, 0, 0, 0}, {false, 2, 1, 1, 4}, {false, 3, 1, 0, 0},
-    {false, 2, 2, 1, 5}, {false, 3, 2, 0, 0}, {false, 3, 3, 1, 0}};
+    {true, 0, 0, 0, -1, -1, -1},  {true, 0, 1, 0, -1, -1, -1},  {true, 1, 0, 0, -1, 0, -1},
+    {true, 1, 1, 0, -1, -1, -1},  {false, 0, 0, 1, 1, 1, -1},   {false, 1, 0, 0, -1, -1, 0},
+    {false, 1, 1, 1, 0, -1, 1},   {true, 2, 0, 1, -1, -1, -1},  {true, 2, 1, 1, -1, -1, -1},
+    {true, 3, 0, 0, -1, -1, -1},  {true, 3, 1, 0, -1, -1, -1},  {false, 2, 0, 1, 1, -1, -1},
+    {false, 3, 0, 0, -1, -1, -1}, {false, 2, 1, 1, 2, 2, -1},   {false, 3, 1, 0, -1, -1, -1},
+    {false, 2, 2, 1, 3, 3, -1},   {false, 3, 2, 0, -1, -1, -1}, {false, 3, 3, 1, -1, -1, -1}};
 
 // chunk_scan_mt at qb = 4, d_state 128 with three workgroups per CU (16-bit operands): the same
-// products in the order of kCmSchedule, so that LDS holds two right-operand slots instead of
-// all of a chunk's u tiles, and two accumulators are live instead of one per tile.  Compact
-// 64-element operand tiles; 53.8 KB of LDS.
+// sums, bit for bit, in the order of kCmSchedule, so that LDS holds two right-operand slots
+// instead of all of a chunk's u tiles, and two accumulators are live instead of one per tile.
+// Compact 64-element operand tiles; 53.8 KB of LDS.
 template <typename TM, bool VEC>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) chunk_scan_cm(Geo g, Ptrs p) {
   static_assert(sizeof(TM) == 2, "16-bit operands");
@@ -378,13 +381,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) c
   const TM* Cm = static_cast<const TM*>(p.C);
   const TM* cbt = static_cast<const TM*>(p.cb) + ((b * g.nc + c) * g.ngroups + gg) * Q * Q;
   const TM* S = static_cast<const TM*>(p.states) + (bh * g.nc + c) * g.headdim * g.dstate;
-  V8<TM> xv[2], zv[2];  // x and z rows of the tile whose u is staged next
-  V8<TM> sv[2][2];      // S_in's n-tiles, for the second half
+  V8<TM> xv[2];     // x rows of the tile whose u is staged next (and whose epilogue is next)
+  V8<TM> zv[2];     // z rows of the tile whose epilogue is next
+  V8<TM> sv[2][2];  // S_in's n-tiles
   {
 #pragma unroll
     for (int k = 0; k < 2; ++k) load_sw<TM, VEC>(g, S, pc0, 64 * k, sv[k]);
     load_xw<TM, VEC>(g, X, b, tc, h, pc0, xv);
-    load_xw<TM, VEC>(g, Z, b, tc, h, pc0, zv);
     load_chunk_cs(g, p, bh, c, csc, dlc, ecol);
     if (threadIdx.x < Q) ecs[threadIdx.x] = fast_exp(csc[threadIdx.x]);
     if (threadIdx.x < 64) {
@@ -441,7 +444,6 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) c
       mma_tile<TM, LD>(ac, ab[k & 1], ub[sg.j & 1], wm, wn, lane, 64);
       if constexpr (sg.i == sg.j) {
         // tile i is complete
-        const int64_t tl0 = tc + 64 * sg.i;
         acc_to_lds(red, ac, wm, wn, lane);
         zero(ac);
         __syncthreads();
@@ -462,19 +464,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) c
             v[rr][e] = y;
           }
         }
-        store_xw<TM, VEC>(g, static_cast<TM*>(p.y), b, tl0, h, pc0, v[0], v[1]);
+        store_xw<TM, VEC>(g, static_cast<TM*>(p.y), b, tc + 64 * sg.i, h, pc0, v[0], v[1]);
       }
     }
-    if constexpr (sg.load == 1 || sg.load == 4 || sg.load == 5) {
-      constexpr int t = sg.load == 1 ? 1 : sg.load == 4 ? 2 : 3;
-      load_xw<TM, VEC>(g, X, b, tc + 64 * t, h, pc0, xv);
-      load_xw<TM, VEC>(g, Z, b, tc + 64 * t, h, pc0, zv);
-    } else if constexpr (sg.load == 2) {
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) load_sw<TM, VEC>(g, S, pc0, 64 * kk, sv[kk]);
-    } else if constexpr (sg.load == 3 || sg.load == 6) {
-      load_xw<TM, VEC>(g, X, b, tc + (sg.load == 3 ? 64 : 0), h, pc0, xv);  // u_1, u_0 again
-    }
+    if constexpr (sg.x >= 0) load_xw<TM, VEC>(g, X, b, tc + 64 * sg.x, h, pc0, xv);
+    if constexpr (sg.z >= 0) load_xw<TM, VEC>(g, Z, b, tc + 64 * sg.z, h, pc0, zv);
+    if constexpr (sg.s >= 0) load_sw<TM, VEC>(g, S, pc0, 64 * sg.s, sv[sg.s]);
   });
 }
 
@@ -516,6 +511,7 @@ int make_geo(const mko_ssd_params* prm, Geo* g) {
   g->npt = static_cast<int>((g->headdim + 63) / 64);
   g->nnt = static_cast<int>((g->dstate + 63) / 64);
   g->nnp = (g->nnt + 1) / 2;
+  // row strides below 2^24 keep every lane's byte offset in a 64-row window within 32 bits
   if (g->nheads * g->headdim >= (int64_t(1) << 24) || g->ngroups * g->dstate >= (int64_t(1) << 24)) {
     mko_set_error("ssd: nheads * headdim and ngroups * dstate must be below 2^24");
     return MKO_EUNSUPPORTED;

@@ -132,6 +132,12 @@ __device__ __forceinline__ void store_xw(const Geo& g, TM* dst, int64_t b, int64
   store_win<TM, VEC>(dst + xidx(g, b, t0, h, pc0), static_cast<int>(g.nheads * g.headdim), clamp64(g.length - t0),
                      static_cast<int>(g.headdim - pc0), a, bb);
 }
+template <typename TM, bool VEC>
+__device__ __forceinline__ void store_xw_row(const Geo& g, TM* dst, int64_t b, int64_t t0, int64_t h, int64_t pc0,
+                                             int rr, const float (&a)[8]) {
+  store_win_row<TM, VEC>(dst + xidx(g, b, t0, h, pc0), static_cast<int>(g.nheads * g.headdim),
+                         clamp64(g.length - t0), static_cast<int>(g.headdim - pc0), rr, a);
+}
 //   B/C-like (b, L, G, N): rows = tokens t0 .., columns = d_state nn0 ..
 template <typename TM, bool VEC>
 __device__ __forceinline__ void load_bw(const Geo& g, const TM* src, int64_t b, int64_t t0, int64_t gg, int64_t nn0,
@@ -395,7 +401,6 @@ __device__ __forceinline__ void load_d8(const Geo& g, const Ptrs& p, int64_t h, 
     d[k] = v;
   }
 }
-
 
 }  // namespace ssd
 }  // namespace mko

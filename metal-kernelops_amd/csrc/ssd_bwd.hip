@@ -48,6 +48,64 @@ __device__ __forceinline__ float block_sum(float v, float* wsum) {
   return (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
 }
 
+// The gate's backward on row r0 + rr and columns c0 .. c0 + 7 of the token tile at tl0, from
+// yt = that row of the chunk output before the skip and the gate, y~.  With z: dz = dy (D x +
+// y~) d silu(z) and gy = dy silu(z) rounded to the storage type (the value the other kernels
+// read), both stored; without z, gy = dy.  gy gets gy, ya[po + r0 + rr] the row sum gy . y~,
+// and dd accumulates the column partials gy x.
+template <typename TM, bool VEC>
+__device__ __forceinline__ void gate_row(const Geo& g, const Ptrs& p, int rr, const float (&yt)[8], const V8<TM>& xv,
+                                         const V8<TM>& zv, const V8<TM>& dyv, const float (&dv)[8], int64_t b,
+                                         int64_t tl0, int64_t h, int64_t pc0, int64_t po, float (&gy)[8],
+                                         float (&dd)[8]) {
+  float xf[8];
+  v8_f32(xv, xf);
+  v8_f32(dyv, gy);
+  if (p.z) {
+    float zf[8], dz[8];
+    v8_f32(zv, zf);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float sgm = sigmoid(zf[e]);
+      const float ypre = fmaf(dv[e], xf[e], yt[e]);
+      dz[e] = gy[e] * ypre * sgm * fmaf(zf[e], 1.0f - sgm, 1.0f);
+      gy[e] = to_f32(from_f32<TM>(gy[e] * zf[e] * sgm));
+    }
+    store_xw_row<TM, VEC>(g, static_cast<TM*>(p.dz), b, tl0, h, pc0, rr, dz);
+    store_xw_row<TM, VEC>(g, static_cast<TM*>(p.gyw), b, tl0, h, pc0, rr, gy);
+  }
+  float ya = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    ya = fmaf(gy[e], yt[e], ya);
+    dd[e] = fmaf(gy[e], xf[e], dd[e]);
+  }
+  ya = row8_sum(ya);
+  if ((threadIdx.x & 7) == 0) p.ya[po + blk_r0() + rr] = ya;
+}
+
+// Column sums of the threads' dd over a tile's 64 rows (lanes sharing tid % 8, then the four
+// wavefronts in a fixed order through colred, 256 floats of LDS) into out[col] for col <
+// ncol.  colred must be free on entry; it is read by the first 64 threads on exit.
+__device__ __forceinline__ void dd_columns(float (&dd)[8], float* colred, float* out, int ncol) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, c0 = blk_c0();
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float v = dd[e];
+    v += __shfl_xor(v, 8);
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    dd[e] = v;
+  }
+  if (lane < 8) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) colred[64 * wave + c0 + e] = dd[e];
+  }
+  __syncthreads();
+  const int col = threadIdx.x;
+  if (col < 64 && col < ncol) out[col] = (colred[col] + colred[64 + col]) + (colred[128 + col] + colred[192 + col]);
+}
+
 // SAVED: the forward saved the chunk output (p.yt); otherwise it is recomputed here.
 template <typename TM, bool VEC, bool SAVED>
 __global__ void __launch_bounds__(256) gate(Geo g, BwdPlan pl, Ptrs p) {
@@ -91,62 +149,16 @@ __global__ void __launch_bounds__(256) gate(Geo g, BwdPlan pl, Ptrs p) {
     __syncthreads();
     lds_block(red, r0, c0, yt[0], yt[1]);
   }
-  float dd[8], gyo[2][8], dzo[2][8];
-#pragma unroll
-  for (int k = 0; k < 8; ++k) dd[k] = 0.0f;
   const int64_t po = ((bh * g.nc + c) * g.npt + pt) * g.q + 64 * i;
+  float dd[8] = {};
 #pragma unroll
   for (int rr = 0; rr < 2; ++rr) {
-    float xf[8], gyf[8];
-    v8_f32(xv[rr], xf);
-    v8_f32(dyv[rr], gyf);
-    if (p.z) {
-      float zf[8];
-      v8_f32(zv[rr], zf);
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const float sg = sigmoid(zf[k]);
-        float ypre = yt[rr][k];
-        ypre = fmaf(dv[k], xf[k], ypre);
-        dzo[rr][k] = gyf[k] * ypre * sg * fmaf(zf[k], 1.0f - sg, 1.0f);
-        gyf[k] = to_f32(from_f32<TM>(gyf[k] * zf[k] * sg));  // as stored for the other kernels
-        gyo[rr][k] = gyf[k];
-      }
-    }
-    float ya = 0.0f;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      ya = fmaf(gyf[k], yt[rr][k], ya);
-      dd[k] = fmaf(gyf[k], xf[k], dd[k]);
-    }
-    ya = row8_sum(ya);
-    if ((threadIdx.x & 7) == 0) p.ya[po + r0 + rr] = ya;
+    float gy[8];
+    gate_row<TM, VEC>(g, p, rr, yt[rr], xv[rr], zv[rr], dyv[rr], dv, b, tl0, h, pc0, po, gy, dd);
   }
-  if (p.z) {
-    store_xw<TM, VEC>(g, static_cast<TM*>(p.dz), b, tl0, h, pc0, dzo[0], dzo[1]);
-    store_xw<TM, VEC>(g, static_cast<TM*>(p.gyw), b, tl0, h, pc0, gyo[0], gyo[1]);
-  }
-  if (p.D) {
-    // column sums over the 64 rows: lanes sharing tid%8 (xor 8, 16, 32), then the 4 wavefronts
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      float v = dd[k];
-      v += __shfl_xor(v, 8);
-      v += __shfl_xor(v, 16);
-      v += __shfl_xor(v, 32);
-      dd[k] = v;
-    }
-    if (lane < 8) {
-#pragma unroll
-      for (int k = 0; k < 8; ++k) colred[wave][c0 + k] = dd[k];
-    }
-    __syncthreads();
-    if (threadIdx.x < 64 && pc0 + threadIdx.x < g.headdim) {
-      const int col = threadIdx.x;
-      const float sum = (colred[0][col] + colred[1][col]) + (colred[2][col] + colred[3][col]);
-      p.pdD[(((b * g.nc + c) * g.qb + i) * g.nheads + h) * g.headdim + pc0 + col] = sum;
-    }
-  }
+  if (p.D)
+    dd_columns(dd, &colred[0][0], p.pdD + (((b * g.nc + c) * g.qb + i) * g.nheads + h) * g.headdim + pc0,
+               clamp64(g.headdim - pc0));
 }
 
 // Stage k of gate_state_mt: first the chunk output of each token tile, the tiles in
@@ -295,63 +307,19 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) g
         const float4 db = *reinterpret_cast<const float4*>(dcol + c0 + 4);
         const float dv[8] = {da.x, da.y, da.z, da.w, db.x, db.y, db.z, db.w};
         const int64_t po = ((bh * g.nc + c) * g.npt + pt) * Q + 64 * i;
-        float dd[8], gyo[2][8], dzo[2][8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) dd[e] = 0.0f;
+        float dd[8] = {};
 #pragma unroll
         for (int rr = 0; rr < 2; ++rr) {
-          float xf[8], gyf[8];
-          v8_f32(xv[rr], xf);
-          v8_f32(dyv[rr], gyf);
-          if (p.z) {
-            float zf[8];
-            v8_f32(zv[rr], zf);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              const float sgm = sigmoid(zf[e]);
-              const float ypre = fmaf(dv[e], xf[e], yt[rr][e]);
-              dzo[rr][e] = gyf[e] * ypre * sgm * fmaf(zf[e], 1.0f - sgm, 1.0f);
-              gyf[e] = to_f32(from_f32<TM>(gyf[e] * zf[e] * sgm));  // as stored for the other kernels
-            }
-          }
-          float ya = 0.0f;
+          float gy[8];
+          gate_row<TM, VEC>(g, p, rr, yt[rr], xv[rr], zv[rr], dyv[rr], dv, b, tl0, h, pc0, po, gy, dd);
           const float el = ecs[64 * i + r0 + rr];
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            ya = fmaf(gyf[e], yt[rr][e], ya);
-            dd[e] = fmaf(gyf[e], xf[e], dd[e]);
-            gyo[rr][e] = gyf[e];
-            yt[rr][e] = gyf[e] * el;  // the adjoint's operand, e^{cs_l} gy_l
-          }
-          ya = row8_sum(ya);
-          if ((threadIdx.x & 7) == 0) p.ya[po + r0 + rr] = ya;
-        }
-        if (p.z) {
-          store_xw<TM, VEC>(g, static_cast<TM*>(p.dz), b, tl0, h, pc0, dzo[0], dzo[1]);
-          store_xw<TM, VEC>(g, static_cast<TM*>(p.gyw), b, tl0, h, pc0, gyo[0], gyo[1]);
+          for (int e = 0; e < 8; ++e) yt[rr][e] = gy[e] * el;  // the adjoint's operand, e^{cs_l} gy_l
         }
         put2x8<TM, true>(ut[i], r0, c0, yt[0], yt[1]);  // A[p][l] = e^{cs_l} gy_l[p]
-        if (p.D) {
-          // column sums over the tile's 64 rows: lanes sharing tid % 8, then the 4 wavefronts
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            float v = dd[e];
-            v += __shfl_xor(v, 8);
-            v += __shfl_xor(v, 16);
-            v += __shfl_xor(v, 32);
-            dd[e] = v;
-          }
-          if (lane < 8) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) colred[wave][c0 + e] = dd[e];
-          }
-          __syncthreads();
-          if (threadIdx.x < 64 && pc0 + threadIdx.x < g.headdim) {
-            const int col = threadIdx.x;
-            const float sum = (colred[0][col] + colred[1][col]) + (colred[2][col] + colred[3][col]);
-            p.pdD[(((b * g.nc + c) * g.qb + i) * g.nheads + h) * g.headdim + pc0 + col] = sum;
-          }
-        }
+        if (p.D)
+          dd_columns(dd, &colred[0][0], p.pdD + (((b * g.nc + c) * g.qb + i) * g.nheads + h) * g.headdim + pc0,
+                     clamp64(g.headdim - pc0));
         __syncthreads();  // the next stage refills the operand buffers; colred is reused
       }
     }

@@ -111,21 +111,25 @@ __device__ __forceinline__ void put2x8(TM* dst, int r0, int c0, const float (&a)
 }
 
 // Loads the thread's 2x8 block of a 64x64 window of a row-major view: window element
-// (r, c) is base[r * ld + c] (base and ld uniform, r * ld < 2^31); rows >= nrows and
+// (r, c) is base[r * ld + c] (base and ld uniform, (63 * ld + 63) * sizeof(T) < 2^32, so
+// each lane's byte offset is one 32-bit value added to the scalar base); rows >= nrows and
 // columns >= ncols read as zero.  VEC: whole 8-element runs, 16-byte aligned, and the
-// loads are unconditional (a lane outside the window reads `safe`, any valid aligned
-// address, and discards it), so the number of loads in flight is static and the
-// compiler can wait for exactly the ones it needs.
+// loads are unconditional (a lane outside the window reads at offset 0 of the window, or
+// of `safe`, any valid aligned address, when the window is empty, and discards it), so the
+// number of loads in flight is static and the compiler can wait for exactly the ones it
+// needs.
 template <typename T, bool VEC>
 __device__ __forceinline__ void load_win(const T* base, int ld, int nrows, int ncols, V8<T> (&v)[2],
                                          const T* safe) {
   const int r0 = blk_r0(), c0 = blk_c0();
+  // a window with no element starts anywhere: its lanes all read `safe`
+  const T* wb = nrows > 0 && ncols > 0 ? base : safe;
 #pragma unroll
   for (int rr = 0; rr < 2; ++rr) {
     const int r = r0 + rr;
     if constexpr (VEC) {
       const bool ok = r < nrows && c0 < ncols;
-      load_words(ok ? base + (r * ld + c0) : safe, v[rr].w);
+      load_words(at_bytes(wb, opaque(ok ? static_cast<uint32_t>((r * ld + c0) * sizeof(T)) : 0u)), v[rr].w);
       v[rr].mask = ok ? ~0u : 0u;
     } else {
       const int n = r < nrows ? ncols - c0 : 0;
@@ -138,14 +142,23 @@ __device__ __forceinline__ void load_win(const T* base, int ld, int nrows, int n
 }
 
 // Stores the thread's block (rows r0, r0+1 of a 64x64 window at base with row stride
-// ld) as T, inside nrows x ncols.
+// ld, under load_win's offset bound) as T, inside nrows x ncols.
 template <typename T, bool VEC>
 __device__ __forceinline__ void store_win(T* base, int ld, int nrows, int ncols, const float (&a)[8],
                                           const float (&b)[8]) {
   const int r0 = blk_r0(), c0 = blk_c0();
   const int n = ncols - c0;
-  if (r0 < nrows && n > 0) v8_store(base + (r0 * ld + c0), n, VEC, a);
-  if (r0 + 1 < nrows && n > 0) v8_store(base + ((r0 + 1) * ld + c0), n, VEC, b);
+  if (r0 < nrows && n > 0) v8_store(at_bytes(base, static_cast<uint32_t>((r0 * ld + c0) * sizeof(T))), n, VEC, a);
+  if (r0 + 1 < nrows && n > 0)
+    v8_store(at_bytes(base, static_cast<uint32_t>(((r0 + 1) * ld + c0) * sizeof(T))), n, VEC, b);
+}
+
+// Stores row r0 + rr of the thread's block only.
+template <typename T, bool VEC>
+__device__ __forceinline__ void store_win_row(T* base, int ld, int nrows, int ncols, int rr, const float (&a)[8]) {
+  const int r = blk_r0() + rr, c0 = blk_c0();
+  const int n = ncols - c0;
+  if (r < nrows && n > 0) v8_store(at_bytes(base, static_cast<uint32_t>((r * ld + c0) * sizeof(T))), n, VEC, a);
 }
 
 // Writes the thread's raw block (rows a, b) into an LDS operand tile without conversion.
