@@ -662,6 +662,13 @@ __device__ __forceinline__ float row_newbcast(float v) {
 
 constexpr int kLaneChannels = 4;  // channels per wavefront in the lane-per-state kernels
 
+// One 16-step block of B and C staged through LDS for a wavefront of the lane-per-state
+// kernels, whose 4 channels share one (batch, group): lane l fetches 8 values of it (matrix
+// l / 32, state (l / 2) mod 16, steps 8 (l mod 2) ..), stages them as float32 (zeros for
+// padded states), and lane (c, n) reads its state's 16 steps back.  Rows are kBcRow floats:
+// 16-byte aligned, and the 16 rows' reads fall in distinct banks.
+constexpr int kBcRow = 20;
+
 template <class TU, class TB>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) fwd_lane(Geo g, Ptrs p) {
   constexpr int kRow = HS + 1;   // a step's 16 states, padded so the transposed reads miss no bank
@@ -690,11 +697,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) f
   const int64_t sstep = g.dim * N;  // one saved state further
   float* sw = sy[wave] + cl * kCS;
   // The wavefront's 4 channels share one (batch, group), so one 16-step block of B and C
-  // serves all of them: lane l fetches 8 values of it (matrix l / 32, state (l / 2) mod 16,
-  // steps 8 (l mod 2) ..), stages them in LDS as float32 (zeros for padded states), and
-  // lane (c, n) reads its state's 16 steps back.  Rows are 20 floats: 16-byte aligned, and
-  // the 16 rows' reads fall in distinct banks.
-  constexpr int kBcRow = 20;
+  // serves all of them, staged through LDS (kBcRow).
   __shared__ __align__(16) float sbc[4][2][HS][kBcRow];
   const int sm = lane >> 5, sst = (lane >> 1) & 15, shf = lane & 1;
   const bool sok = sst < N;
@@ -780,8 +783,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) f
 // Per block:
 //   - lane (c, n) loads step t0 + n of its channel's delta, u, z, dout and out and forms that
 //     element's step, du, gy = dout silu(z) and the factor of dz;
-//   - lane (c, n) reads its state's 16 steps of B and of C straight from memory (the 4
-//     channels of the wavefront share them, so the vector L1 serves each row once);
+//   - B and C of the block come through LDS as in fwd_lane (kBcRow), lane (c, n) reading its
+//     state's 16 steps of each;
 //   - from the saved state entering the block, the lane recomputes the block's 16 states and
 //     decays a = exp(A delta);
 //   - it walks the 16 steps backwards with the adjoint h_t = gy_t C_t + a_{t+1} h_{t+1}, and per
@@ -823,6 +826,7 @@ bwd_lane(Geo g, Ptrs p, int cpb) {
   // per wavefront: the transposes of h B (t1) and A a x h (t2); in blocks that need it, t1
   // first transposes C x; the workgroup's dB/dC blocks reuse the t1 buffers
   __shared__ __align__(16) float lds[4][2][kTrFloats];
+  __shared__ __align__(16) float sbc[4][2][HS][kBcRow];  // B and C of the block (kBcRow)
   const int wave = uniform(static_cast<int>(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63, cl = lane >> 4, n = lane & 15;
   const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * kLaneChannels;  // first row of the wave
@@ -831,8 +835,7 @@ bwd_lane(Geo g, Ptrs p, int cpb) {
   const int64_t bb = r / g.dim, d = r - bb * g.dim;
   const int64_t bg = uniform(static_cast<int>((active ? row0 : g.rows - 1) / g.dg));  // (batch, group) of the wave
   const int N = static_cast<int>(g.dstate);
-  const bool sn = n < N;
-  const bool padded = N < HS;  // wave-uniform: states n >= N exist only as zero lanes
+  const bool sn = n < N;  // states n >= N exist only as zero lanes
   const float an = sn ? p.A[d * N + n] : 0.0f;
   const float a2 = an * kLog2e;
   const float bias = p.bias ? p.bias[d] : 0.0f;
@@ -848,7 +851,13 @@ bwd_lane(Geo g, Ptrs p, int cpb) {
   // Block offsets are added to wave-uniform base pointers.
   const uint32_t eoff = static_cast<uint32_t>(r * L + n);
   const uint32_t soff = static_cast<uint32_t>(ck_index(g, r, 0, sn ? n : 0));
-  const uint32_t boff = static_cast<uint32_t>((bg * N + (sn ? n : 0)) * L);
+  const int sm = lane >> 5, sst = (lane >> 1) & 15, shf = lane & 1;  // this lane's share of the B/C block
+  const bool sok = sst < N;
+  const uint32_t bcoff = static_cast<uint32_t>((bg * N + (sok ? sst : 0)) * L + 8 * shf);
+  const TB* bcsrc = static_cast<const TB*>(sm ? p.C : p.B);
+  float* stg = &sbc[wave][sm][sst][8 * shf];
+  const float* brow = &sbc[wave][0][n][0];
+  const float* crow = &sbc[wave][1][n][0];
   const int tw = cl * HS + n;  // this lane's column in a transpose row
   const int64_t sstep = g.dim * N;
   const TU* zsrc = static_cast<const TU*>(has_z ? p.z : p.u);
@@ -860,7 +869,7 @@ bwd_lane(Geo g, Ptrs p, int cpb) {
   struct In {
     float dl, xin;
     TU u, z, go, o;
-    RawRun<TB, HS> b, c;
+    RawRun<TB, 8> bc;
   };
   auto load = [&](int k, In& in) {
     const int64_t t0 = static_cast<int64_t>(k) * HS;
@@ -870,8 +879,7 @@ bwd_lane(Geo g, Ptrs p, int cpb) {
     in.go = (static_cast<const TU*>(p.dout) + t0)[eoff];
     in.o = (osrc + t0)[eoff];
     in.xin = (p.states + k * sstep)[soff];
-    in.b.load(g, static_cast<const TB*>(p.B) + t0, 0, boff, HS);
-    in.c.load(g, static_cast<const TB*>(p.C) + t0, 0, boff, HS);
+    in.bc.load(g, bcsrc + t0, 0, bcoff, 8);
   };
   const int nblk = static_cast<int>(L / HS);
   In cur;
@@ -900,14 +908,21 @@ bwd_lane(Geo g, Ptrs p, int cpb) {
     }
     const bool ty = __ballot(need_y) != 0;  // wave-uniform: transpose C x in this block
     const float x0 = sn ? cur.xin : 0.0f;
-    float bv[HS], cv[HS];
-    cur.b.get(bv);
-    cur.c.get(cv);
-    if (padded && !sn) {
+    {
+      float sv[8];
+      cur.bc.get(sv);
+      if (!sok) {  // a padded state adds nothing
 #pragma unroll
-      for (int i = 0; i < HS; ++i) bv[i] = cv[i] = 0.0f;
+        for (int i = 0; i < 8; ++i) sv[i] = 0.0f;
+      }
+      reinterpret_cast<float4*>(stg)[0] = make_float4(sv[0], sv[1], sv[2], sv[3]);
+      reinterpret_cast<float4*>(stg)[1] = make_float4(sv[4], sv[5], sv[6], sv[7]);
     }
     load(k > 0 ? k - 1 : 0, cur);  // the next block's inputs: a block of work to arrive
+    wave_lds_sync();
+    float bv[HS], cv[HS];
+    lds_row<HS>(brow, bv);
+    lds_row<HS>(crow, cv);
     // ---- recompute the block's states from the saved one
     float xh[HS], ah[HS];
     auto recompute = [&](auto with_y) {
