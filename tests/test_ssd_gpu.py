@@ -52,6 +52,7 @@ SHAPES = [
     (2, 300, 4, 64, 1, 128),   # two 128-token chunks, ragged tail
     (1, 1100, 2, 80, 2, 72),   # 256-token chunks, P and N not multiples of 64
     (1, 1100, 3, 64, 1, 128),  # 256-token chunks at the c4 head shape, ragged tail
+    (1, 1030, 4, 60, 2, 128),  # 256-token chunks at d_state 128 with element-wise d_head rows
 ]
 
 
