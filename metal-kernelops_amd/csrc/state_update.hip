@@ -82,11 +82,11 @@ __device__ __forceinline__ float ld_any(const void* base, int dtype, int64_t i) 
 }
 
 // Elements of a row handled by lane j of its TPR lanes: vector chunks j, j+TPR, ...
-// (VEC = 4) or single elements (VEC = 1).
-template <int VEC, typename F>
+// (VEC = 4) or single elements (VEC = 1), at most SPL of them.
+template <int VEC, int SPL = kMaxPerThread, typename F>
 __device__ __forceinline__ void for_row_chunks(int n_states, int tpr, int j, F&& f) {
 #pragma unroll
-  for (int k = 0; k < kMaxPerThread / VEC; ++k) {
+  for (int k = 0; k < SPL / VEC; ++k) {
     const int n0 = (j + k * tpr) * VEC;
     if (n0 < n_states) f(k, n0);
   }
@@ -150,9 +150,12 @@ __global__ void __launch_bounds__(kThreads) fwd(Args a) {
   }
 }
 
-template <typename TS, int VEC>
+// SPL: states per lane (tpr * SPL >= dstate).  With 4 (one vector per lane and row) the
+// dB/dC accumulators take 8 registers instead of 32, so twice the waves share a SIMD and
+// more rows' loads are in flight; each pass covers fewer rows.
+template <typename TS, int VEC, int SPL>
 __global__ void __launch_bounds__(kThreads) bwd(Args a) {
-  __shared__ float red[kThreads * kMaxPerThread];  // [rows_per_pass][dstate] fold buffer
+  __shared__ float red[kThreads * SPL];  // [rows_per_pass][tpr * SPL] fold buffer
   __shared__ float rowv[3][kThreads];  // per-row dA, dD, ddt terms of the current 256-row window
   const Geo& g = a.g;
   const int64_t bh = blockIdx.x;
@@ -165,15 +168,70 @@ __global__ void __launch_bounds__(kThreads) bwd(Args a) {
   const int rows_per_pass = kThreads / tpr;
   const float Ah = a.A[h];
   const float bias = a.dt_bias ? a.dt_bias[h] : 0.0f;
-  float pb[kMaxPerThread], pc[kMaxPerThread];
+  float pb[SPL], pc[SPL];
 #pragma unroll
-  for (int k = 0; k < kMaxPerThread; ++k) pb[k] = pc[k] = 0.0f;
+  for (int k = 0; k < SPL; ++k) pb[k] = pc[k] = 0.0f;
   float sum_a = 0.0f, sum_d = 0.0f, sum_t = 0.0f;  // thread 0: per-head folds
+
+  // This lane's elements of a row (chunk k of VEC at n0 = (j + k tpr) VEC, present when
+  // n0 < N): B and C are the same for every row of the head and are loaded once; a row's
+  // state and new-state adjoint are requested a pass ahead when a lane holds one vector.
+  constexpr bool kAhead = SPL == VEC;
+  float bvs[SPL], cvs[SPL];
+  struct Row {
+    float s[SPL], dn[SPL];
+  };
+  for_row_chunks<VEC, SPL>(N, tpr, j, [&](int k, int n0) {
+    float* bv = bvs + k * VEC;
+    float* cv = cvs + k * VEC;
+    if constexpr (VEC == 4) {
+      float b4[4], c4[4];
+      if (g.bc_dtype == MKO_F32) { load4<float>(a.B, bg * N + n0, b4); load4<float>(a.C, bg * N + n0, c4); }
+      else if (g.bc_dtype == MKO_BF16) { load4<bf16>(a.B, bg * N + n0, b4); load4<bf16>(a.C, bg * N + n0, c4); }
+      else { load4<_Float16>(a.B, bg * N + n0, b4); load4<_Float16>(a.C, bg * N + n0, c4); }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        bv[e] = b4[e];
+        cv[e] = c4[e];
+      }
+    } else {
+      bv[0] = ld_any(a.B, g.bc_dtype, bg * N + n0);
+      cv[0] = ld_any(a.C, g.bc_dtype, bg * N + n0);
+    }
+  });
+  auto fetch = [&](int p, Row& r) {
+    if (p >= g.headdim) return;
+    const int64_t row = bh * g.headdim + p;
+    for_row_chunks<VEC, SPL>(N, tpr, j, [&](int k, int n0) {
+      float* s = r.s + k * VEC;
+      float* dn = r.dn + k * VEC;
+      if constexpr (VEC == 4) {
+        float s4[4], d4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        load4<TS>(a.state, row * N + n0, s4);
+        if (a.dnew) load4<float>(a.dnew, row * N + n0, d4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          s[e] = s4[e];
+          dn[e] = d4[e];
+        }
+      } else {
+        s[0] = ld<TS>(a.state, row * N + n0);
+        dn[0] = a.dnew ? a.dnew[row * N + n0] : 0.0f;
+      }
+    });
+  };
+  Row cur, nxt;
+  if constexpr (kAhead) fetch(slot, cur);
 
   // Passes are uniform over the workgroup (every thread runs every pass), so the
   // barriers below are reached by all threads.
   for (int p0 = 0; p0 < g.headdim; p0 += rows_per_pass) {
     const int p = p0 + slot;
+    if constexpr (kAhead) {
+      fetch(p + rows_per_pass, nxt);
+    } else {
+      fetch(p, cur);
+    }
     if (p < g.headdim) {
       const int64_t row = bh * g.headdim + p;
       const float raw = ld_any(a.dt, g.dt_dtype, g.dt_per_row ? row : bh) + bias;
@@ -191,21 +249,12 @@ __global__ void __launch_bounds__(kThreads) bwd(Args a) {
       }
       const float dyp = dyv * gate;  // grad of the pre-gate output
       float sx = 0.0f, sa = 0.0f, sy = 0.0f;
-      for_row_chunks<VEC>(N, tpr, j, [&](int k, int n0) {
-        float s[VEC], bv[VEC], cv[VEC], dn[VEC], gs[VEC];
-        if constexpr (VEC == 4) {
-          load4<TS>(a.state, row * N + n0, s);
-          if (g.bc_dtype == MKO_F32) { load4<float>(a.B, bg * N + n0, bv); load4<float>(a.C, bg * N + n0, cv); }
-          else if (g.bc_dtype == MKO_BF16) { load4<bf16>(a.B, bg * N + n0, bv); load4<bf16>(a.C, bg * N + n0, cv); }
-          else { load4<_Float16>(a.B, bg * N + n0, bv); load4<_Float16>(a.C, bg * N + n0, cv); }
-          if (a.dnew) load4<float>(a.dnew, row * N + n0, dn);
-          else { dn[0] = dn[1] = dn[2] = dn[3] = 0.0f; }
-        } else {
-          s[0] = ld<TS>(a.state, row * N + n0);
-          bv[0] = ld_any(a.B, g.bc_dtype, bg * N + n0);
-          cv[0] = ld_any(a.C, g.bc_dtype, bg * N + n0);
-          dn[0] = a.dnew ? a.dnew[row * N + n0] : 0.0f;
-        }
+      for_row_chunks<VEC, SPL>(N, tpr, j, [&](int k, int n0) {
+        const float* s = cur.s + k * VEC;
+        const float* dn = cur.dn + k * VEC;
+        const float* bv = bvs + k * VEC;
+        const float* cv = cvs + k * VEC;
+        float gs[VEC];
 #pragma unroll
         for (int e = 0; e < VEC; ++e) {
           const float nv = fmaf(decay, s[e], dxv * bv[e]);
@@ -272,12 +321,13 @@ __global__ void __launch_bounds__(kThreads) bwd(Args a) {
       }
       __syncthreads();
     }
+    if constexpr (kAhead) cur = nxt;
   }
   // dB/dC: fold the lanes' per-state partials over the row slots in a fixed order.
   for (int which = 0; which < 2; ++which) {
     float* src = which == 0 ? pb : pc;
 #pragma unroll
-    for (int k = 0; k < kMaxPerThread; ++k) red[slot * kMaxPerThread * tpr + k * tpr + j] = src[k];
+    for (int k = 0; k < SPL; ++k) red[slot * SPL * tpr + k * tpr + j] = src[k];
     __syncthreads();
     for (int n = threadIdx.x; n < N; n += kThreads) {
       // state n lives at chunk k = n / (tpr*VEC), lane j = (n / VEC) % tpr, element e = n % VEC
@@ -286,7 +336,7 @@ __global__ void __launch_bounds__(kThreads) bwd(Args a) {
       const int e = n % VEC;
       float s = 0.0f;
       const int nslots = min(rows_per_pass, static_cast<int>(g.headdim));
-      for (int r = 0; r < nslots; ++r) s += red[r * kMaxPerThread * tpr + (k * VEC + e) * tpr + jj];
+      for (int r = 0; r < nslots; ++r) s += red[r * SPL * tpr + (k * VEC + e) * tpr + jj];
       (which == 0 ? a.pb : a.pc)[bh * N + n] = s;
     }
     __syncthreads();
@@ -438,11 +488,25 @@ void launch_fwd_t(const Args& a, int vec, hipStream_t s, unsigned grid) {
             else fwd<TS, 1><<<grid, kThreads, 0, s>>>(a));
 }
 
+// Lanes per row for one 4-element vector per lane, when a row has at most 64 of them.
+static int tpr_one_vector(const Geo& g) {
+  int tpr = 1;
+  while (tpr < 64 && tpr * 4 < g.dstate) tpr <<= 1;
+  return tpr * 4 >= g.dstate ? tpr : 0;
+}
+
 template <typename TS>
 void launch_bwd_t(const Args& a, int vec, hipStream_t s, unsigned grid) {
-  MKO_TIMED("state_update_bwd", s,
-            if (vec == 4) bwd<TS, 4><<<grid, kThreads, 0, s>>>(a);
-            else bwd<TS, 1><<<grid, kThreads, 0, s>>>(a));
+  const int tpr4 = tpr_one_vector(a.g);
+  if (vec == 4 && tpr4) {
+    Args b = a;
+    b.g.tpr = tpr4;
+    MKO_TIMED("state_update_bwd", s, bwd<TS, 4, 4><<<grid, kThreads, 0, s>>>(b));
+  } else {
+    MKO_TIMED("state_update_bwd", s,
+              if (vec == 4) bwd<TS, 4, kMaxPerThread><<<grid, kThreads, 0, s>>>(a);
+              else bwd<TS, 1, kMaxPerThread><<<grid, kThreads, 0, s>>>(a));
+  }
 }
 
 Args base_args(const mko_state_update_params* p, const Geo& g) {
