@@ -8,7 +8,8 @@
 //   state_pass  per (b, h), element-wise over P x N, sequential over chunks:
 //               entering state of every chunk, and the final state
 //   chunk_scan  per (b, h, chunk, 64-token tile), or per (b, h, chunk) for 16-bit inputs
-//               with d_state <= 128 (chunk_scan_mt):
+//               with d_state <= 128 (chunk_scan_mt; chunk_scan_cm at 256-token chunks with
+//               d_state 128):
 //               y = tril(e^{cs_l - cs_s} CB) (step x) + e^{cs_l} C S_in^T + D x, * silu(z)
 // The backward mirrors these (see ssd_bwd.hip).  Operands of the products are
 // rounded to the input dtype (bf16/f16 products on the bf16/f16 matrix cores,

@@ -89,7 +89,8 @@ struct SavedLayout {
 inline size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
 // 16-bit operands with d_state <= 128: one workgroup per (b, h, chunk, d_head tile) runs
-// all of a chunk's token tiles (chunk_scan_mt, gate_state_mt, du_mt), and the backward
+// all of a chunk's token tiles (chunk_scan_mt, gate_state_mt, du_mt; at 256-token chunks
+// with d_state 128 the scan and du run as chunk_scan_cm and du_cm), and the backward
 // recomputes the chunk output instead of reading a saved copy.
 inline bool multi_tile(const Geo& g) {
   return g.x_dtype != MKO_F32 && g.nnt <= 2 && (g.qb == 1 || g.qb == 2 || g.qb == 4);

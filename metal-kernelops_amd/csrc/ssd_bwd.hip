@@ -6,7 +6,8 @@
 //               dD partials
 //   chunk_state local adjoint of S_in: sum_l e^{cs_l} gy_l (x) C_l
 //   (16-bit inputs with d_state <= 128 run gate and chunk_state as one kernel per chunk and
-//   head, gate_state_mt, and du as du_mt; see multi_tile() in ssd.hpp)
+//   head, gate_state_mt, and du as du_mt, or du_cm at 256-token chunks with d_state 128; see
+//   multi_tile() in ssd.hpp)
 //   state_rev   per state element, backwards over chunks: G, dinitial and e^T <G, S_in>
 //               (the transfer's part of the derivative with respect to the chunk's total decay T)
 //   du          du = K^T gy + e^{T - cs_s} B_s G^T; dx = step du + D gy; per token x.du,
