@@ -150,9 +150,9 @@ __global__ void __launch_bounds__(kThreads) fwd(Args a) {
   }
 }
 
-// SPL: states per lane (tpr * SPL >= dstate).  With 4 (one vector per lane and row) the
-// dB/dC accumulators take 8 registers instead of 32, so twice the waves share a SIMD and
-// more rows' loads are in flight; each pass covers fewer rows.
+// SPL: states per lane (tpr * SPL >= dstate).  With 8 (two 4-element vectors per lane and
+// row) the dB/dC accumulators take 16 registers instead of 32, so more waves share a SIMD,
+// and each pass's rows are requested a pass ahead.
 template <typename TS, int VEC, int SPL>
 __global__ void __launch_bounds__(kThreads) bwd(Args a) {
   __shared__ float red[kThreads * SPL];  // [rows_per_pass][tpr * SPL] fold buffer
@@ -175,8 +175,8 @@ __global__ void __launch_bounds__(kThreads) bwd(Args a) {
 
   // This lane's elements of a row (chunk k of VEC at n0 = (j + k tpr) VEC, present when
   // n0 < N): B and C are the same for every row of the head and are loaded once; a row's
-  // state and new-state adjoint are requested a pass ahead when a lane holds one vector.
-  constexpr bool kAhead = SPL == VEC;
+  // state and new-state adjoint are requested a pass ahead when a lane holds at most 8.
+  constexpr bool kAhead = SPL <= 8;
   float bvs[SPL], cvs[SPL];
   struct Row {
     float s[SPL], dn[SPL];
@@ -488,20 +488,20 @@ void launch_fwd_t(const Args& a, int vec, hipStream_t s, unsigned grid) {
             else fwd<TS, 1><<<grid, kThreads, 0, s>>>(a));
 }
 
-// Lanes per row for one 4-element vector per lane, when a row has at most 64 of them.
-static int tpr_one_vector(const Geo& g) {
+// Lanes per row for two 4-element vectors per lane, when a row needs at most 64 lanes.
+static int tpr_two_vectors(const Geo& g) {
   int tpr = 1;
-  while (tpr < 64 && tpr * 4 < g.dstate) tpr <<= 1;
-  return tpr * 4 >= g.dstate ? tpr : 0;
+  while (tpr < 64 && tpr * 8 < g.dstate) tpr <<= 1;
+  return tpr * 8 >= g.dstate ? tpr : 0;
 }
 
 template <typename TS>
 void launch_bwd_t(const Args& a, int vec, hipStream_t s, unsigned grid) {
-  const int tpr4 = tpr_one_vector(a.g);
-  if (vec == 4 && tpr4) {
+  const int tpr8 = tpr_two_vectors(a.g);
+  if (vec == 4 && tpr8) {
     Args b = a;
-    b.g.tpr = tpr4;
-    MKO_TIMED("state_update_bwd", s, bwd<TS, 4, 4><<<grid, kThreads, 0, s>>>(b));
+    b.g.tpr = tpr8;
+    MKO_TIMED("state_update_bwd", s, bwd<TS, 4, 8><<<grid, kThreads, 0, s>>>(b));
   } else {
     MKO_TIMED("state_update_bwd", s,
               if (vec == 4) bwd<TS, 4, kMaxPerThread><<<grid, kThreads, 0, s>>>(a);

@@ -60,8 +60,8 @@ CASES = [
     ("f16", torch.float16, (2, 4, 16, 32, 2), {}),
     ("bf16", torch.bfloat16, (2, 4, 16, 32, 2), {}),
     ("bf16-decode", torch.bfloat16, (1, 16, 128, 128, 1), {}),
-    ("dstate-320", torch.float32, (2, 4, 8, 320, 2), dict(softplus=True)),  # 16 states per lane
-    ("dstate-24", torch.float32, (2, 4, 40, 24, 2), {}),  # one vector per lane, 8 lanes per row
+    ("dstate-640", torch.float32, (2, 4, 8, 640, 2), dict(softplus=True)),  # 16 states per lane
+    ("dstate-24", torch.float32, (2, 4, 40, 24, 2), {}),  # two vectors per lane, 4 lanes per row
 ]
 
 
