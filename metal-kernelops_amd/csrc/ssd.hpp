@@ -245,15 +245,19 @@ chunk_state(Geo g, Ptrs p, void* out_) {
     Regs ra, rb;
     pipeline2(g.qb, ra, rb, fetch, put, mma);
   }
-  TM* out = static_cast<TM*>(out_) + (bh * g.nc + c) * g.headdim * g.dstate;
+  // the [p][n] tile leaves through LDS as 16-byte row runs, one 64-wide n-tile at a time
+  TM* out = static_cast<TM*>(out_) + (bh * g.nc + c) * g.headdim * g.dstate + pc0 * g.dstate + nn0;
+  float* red = reinterpret_cast<float*>(&sbuf[0][0]);
+  static_assert(sizeof(sbuf) >= 64 * 65 * sizeof(float), "the fp32 tile fits the operand buffers");
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int64_t pp = pc0 + acc_row(wm, lane, r);
-    const int64_t nn = nn0 + acc_col(wn, lane);
-    if (pp < g.headdim) {
-      if (nn < g.dstate) out[pp * g.dstate + nn] = from_f32<TM>(acc0[r]);
-      if (nn + 64 < g.dstate) out[pp * g.dstate + nn + 64] = from_f32<TM>(acc1[r]);
-    }
+  for (int kk = 0; kk < 2; ++kk) {
+    __syncthreads();  // the last stage's products (kk 0), or the reads of the previous tile, are done
+    acc_to_lds(red, kk == 0 ? acc0 : acc1, wm, wn, lane);
+    __syncthreads();
+    float v[2][8];
+    lds_block(red, blk_r0(), blk_c0(), v[0], v[1]);
+    store_win<TM, VEC>(out + 64 * kk, static_cast<int>(g.dstate), clamp64(g.headdim - pc0),
+                       static_cast<int>(g.dstate - nn0 - 64 * kk), v[0], v[1]);
   }
 }
 
