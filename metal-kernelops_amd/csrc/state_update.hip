@@ -349,24 +349,50 @@ __global__ void __launch_bounds__(kThreads) bwd(Args a) {
   }
 }
 
-// dB/dC: the per-head partials summed over the heads of a group, one thread per (batch,
-// group, state), heads in order.
+// dB/dC: the per-head partials summed over the heads of a group.  A workgroup takes 64 states
+// of one (batch, group); its four wavefronts each add a quarter of the group's heads in order
+// (the loads issued eight at a time), and the quarters meet in a fixed order.
 __global__ void __launch_bounds__(256) reduce_bc(Args a, float* dB, float* dC) {
+  __shared__ float qs[2][4][64];
   const Geo& g = a.g;
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int64_t N = g.dstate;
   const int64_t hpg = g.nheads / g.ngroups;
-  if (i >= g.batch * g.ngroups * N) return;
-  const int64_t n = i % N, bgi = i / N;
+  const int64_t ntile = (N + 63) / 64;
+  const int64_t bgi = blockIdx.x / ntile;
   const int64_t b = bgi / g.ngroups, gi = bgi % g.ngroups;
+  const int nl = threadIdx.x & 63, q = threadIdx.x >> 6;
+  const int64_t n = (blockIdx.x % ntile) * 64 + nl;
+  const int64_t k0 = q * hpg / 4, k1 = (q + 1) * hpg / 4;
   float sb = 0.0f, sc = 0.0f;
-  for (int64_t k = 0; k < hpg; ++k) {
-    const int64_t bh = b * g.nheads + gi * hpg + k;
-    sb += a.pb[bh * N + n];
-    sc += a.pc[bh * N + n];
+  if (n < N) {
+    const int64_t base = (b * g.nheads + gi * hpg) * N + n;
+    int64_t k = k0;
+    for (; k + 8 <= k1; k += 8) {
+      float vb[8], vc[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        vb[e] = a.pb[base + (k + e) * N];
+        vc[e] = a.pc[base + (k + e) * N];
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        sb += vb[e];
+        sc += vc[e];
+      }
+    }
+    for (; k < k1; ++k) {
+      sb += a.pb[base + k * N];
+      sc += a.pc[base + k * N];
+    }
   }
-  dB[i] = sb;
-  dC[i] = sc;
+  qs[0][q][nl] = sb;
+  qs[1][q][nl] = sc;
+  __syncthreads();
+  if (q == 0 && n < N) {
+    const int64_t i = bgi * N + n;
+    dB[i] = (qs[0][0][nl] + qs[0][1][nl]) + (qs[0][2][nl] + qs[0][3][nl]);
+    dC[i] = (qs[1][0][nl] + qs[1][1][nl]) + (qs[1][2][nl] + qs[1][3][nl]);
+  }
 }
 
 // Sum over the workgroup's 256 threads in a fixed order (lane butterflies, then the four
@@ -595,10 +621,10 @@ int run_bwd(const mko_state_update_params* p, void* stream, char* ws, const Geo&
   if (g.state_dtype == MKO_F32) launch_bwd_t<float>(a, g.vec, s, grid);
   else if (g.state_dtype == MKO_BF16) launch_bwd_t<bf16>(a, g.vec, s, grid);
   else launch_bwd_t<_Float16>(a, g.vec, s, grid);
-  const int64_t nred = g.batch * g.ngroups * g.dstate;
+  const int64_t nred = g.batch * g.ngroups * ((g.dstate + 63) / 64);
   if (nred > 0)
     MKO_TIMED("state_update_bwd_reduce", s,
-              reduce_bc<<<static_cast<unsigned>((nred + 255) / 256), 256, 0, s>>>(a, p->dB, p->dC));
+              reduce_bc<<<static_cast<unsigned>(nred), 256, 0, s>>>(a, p->dB, p->dC));
   MKO_TIMED("state_update_bwd_reduce", s,
             reduce_heads<<<static_cast<unsigned>(g.nheads), 256, 0, s>>>(a, p->dA, p->dD, p->ddt_bias));
   return mko_check_launch("state_update_bwd");
