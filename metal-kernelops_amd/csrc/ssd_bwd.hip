@@ -1294,21 +1294,29 @@ __global__ void __launch_bounds__(256) reduce_params(Geo g, BwdPlan pl, Ptrs p) 
   float hsum = 0.0f;
   for (int pt = 0; pt < g.npt; ++pt) {
     const int64_t pc = static_cast<int64_t>(pt) * 64 + col;
-    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+    // rows grp, grp + 4, ... in 16 chains, so that 16 loads are in flight per thread
+    float sv[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) sv[e] = 0.0f;
     if (pc < g.headdim) {
       const float* q = p.pdD + h * g.headdim + pc;
       const int64_t stride = g.nheads * g.headdim;
       int64_t k = grp;
-      for (; k + 12 < nrow; k += 16) {
-        s0 += q[k * stride];
-        s1 += q[(k + 4) * stride];
-        s2 += q[(k + 8) * stride];
-        s3 += q[(k + 12) * stride];
+      for (; k + 60 < nrow; k += 64) {
+        float v[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) v[e] = q[(k + 4 * e) * stride];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sv[e] += v[e];
       }
-      for (; k < nrow; k += 4) s0 += q[k * stride];
+      for (; k < nrow; k += 4) sv[0] += q[k * stride];
     }
+#pragma unroll
+    for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+      for (int e = 0; e < w; ++e) sv[e] += sv[e + w];
     __syncthreads();
-    part[grp][col] = (s0 + s1) + (s2 + s3);
+    part[grp][col] = sv[0];
     __syncthreads();
     if (tid < 64 && pc < g.headdim) {
       const float tot = (part[0][col] + part[1][col]) + (part[2][col] + part[3][col]);
