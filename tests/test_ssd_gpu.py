@@ -253,8 +253,10 @@ def test_backward_each_option(case):
     _compare(got, ref, 1e-4, str(case))
 
 
-def test_backward_deterministic_and_graph_free_outputs():
-    shape = (2, 300, 8, 64, 2, 64)
+@pytest.mark.parametrize("shape", [(2, 300, 8, 64, 2, 64),     # 128-token chunks, one d_state tile
+                                   (1, 1100, 4, 64, 1, 128)],  # 256-token chunks at d_state 128
+                         ids=lambda s: "x".join(map(str, s)))
+def test_backward_deterministic_and_graph_free_outputs(shape):
     inputs, dy, dfinal = _inputs(shape, seed=9)
     a = _gpu_grads(inputs, dy, dfinal, True, torch.bfloat16)
     b = _gpu_grads(inputs, dy, dfinal, True, torch.bfloat16)
