@@ -789,14 +789,16 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) f
 //     decays a = exp(A delta);
 //   - it walks the 16 steps backwards with the adjoint h_t = gy_t C_t + a_{t+1} h_{t+1}, and per
 //     step writes its state's terms of the two sums over states that du and ddelta need,
-//     h_t B_t and A a_t x_{t-1} h_t, into two LDS transposes, and adds its dA term;
+//     h_t B_t and A a_t x_{t-1} h_t, as one pair into the wavefront's LDS transpose, and adds its
+//     dA term (the adjoint and dA multiply-adds take their step's gy and delta as a DPP row
+//     broadcast, fmac_row);
 //   - the dB and dC terms, h_t du_t and gy_t x_t, are summed over the wavefront's 4 channels
 //     (one 16-lane row each) with gfx950's lane swaps: v_permlane32_swap exchanges the
 //     wavefront's halves, so one add sums rows (0 + 2, 1 + 3) of a step's dB terms and, in the
 //     other half, of its dC terms; v_permlane16_swap of two such registers (steps i and i + 1)
 //     exchanges odd and even rows, and one more add leaves dB_i, dB_{i+1}, dC_i and dC_{i+1} as
 //     the four rows of one register: 6 instructions per two steps, in a fixed order;
-//   - lane (c, n) then owns step t0 + n: it sums its rows of the transposes and writes du,
+//   - lane (c, n) then owns step t0 + n: it sums its row of the transpose and writes du,
 //     ddelta and dz.  The pre-gate output that dz needs comes back as out / silu(z); a block
 //     where silu(z) is exactly zero somewhere (or out was not given) first sums a transpose
 //     of C x instead;
@@ -805,12 +807,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) f
 // A block's inputs are requested one block ahead.  Needs dstate <= 16, whole 16-step blocks,
 // channels per group a multiple of 4, fp32 delta and 16-byte aligned rows.
 
-constexpr int kTrPitch = 4 * HS + 4;     // one step's row of 4 channels x 16 states, padded: the
-                                         // 16-byte reads of lanes (c, i..i+7) fall in distinct banks
-constexpr int kTrFloats = HS * kTrPitch;  // one transpose buffer of a wavefront, padded so
-                                              // that the same element of the next buffer is 16
-                                              // banks away (the two terms of a step are written
-                                              // as one pair)
+// The transposes of a wavefront hold, per step, a row of 4 channels x 16 states of pairs
+// (h B, A a x h): a step's two terms leave a lane as one 8-byte write at an immediate offset
+// from one base address.  Rows are padded to 4 mod 32 floats, so the 16-byte reads of lanes
+// (c, i..i+7), which read rows i..i+7, fall in distinct banks.
+constexpr int kTrPitch = 2 * 4 * HS + 4;
+constexpr int kTrFloats = HS * kTrPitch;  // one wavefront's transpose block
 
 // The value lane I of each 16-lane row holds, in every lane of that row.  Every row and bank
 // is enabled and bound_ctrl is set, so no lane keeps an old value: the move folds into the VALU
@@ -820,12 +822,29 @@ __device__ __forceinline__ float row_bcast(float v) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + I, 0xf, 0xf, true));
 }
 
+// acc + (the value lane I of each 16-lane row holds in v) * m, as one v_fmac_f32 with the row
+// broadcast as its DPP source (the compiler folds DPP into multiplies but not into fmac, and
+// would otherwise spend a v_mov_b32_dpp on it).  A DPP source written by the instruction just
+// before needs two wait states, which the compiler does not insert for inline assembly: with
+// kGuard the instruction carries them itself; without it v must have been written well before
+// (every caller's v is formed before the block's recompute, dozens of instructions earlier).
+template <int I, bool kGuard = false>
+__device__ __forceinline__ float fmac_row(float acc, float v, float m) {
+  if constexpr (kGuard)
+    asm("s_nop 1\n\tv_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+        : "+v"(acc) : "v"(v), "v"(m), "i"(I));
+  else
+    asm("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+        : "+v"(acc) : "v"(v), "v"(m), "i"(I));
+  return acc;
+}
+
 template <class TU, class TB>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
 bwd_lane(Geo g, Ptrs p, int cpb) {
-  // per wavefront: the transposes of h B (t1) and A a x h (t2); in blocks that need it, t1
-  // first transposes C x; the workgroup's dB/dC blocks reuse the t1 buffers
-  __shared__ __align__(16) float lds[4][2][kTrFloats];
+  // per wavefront: the transposes of the pairs (h B, A a x h); in blocks that need it, the
+  // first terms first transpose C x; the workgroup's dB/dC blocks reuse the buffers
+  __shared__ __align__(16) float lds[4][kTrFloats];
   __shared__ __align__(16) float sbc[4][2][HS][kBcRow];  // B and C of the block (kBcRow)
   const int wave = uniform(static_cast<int>(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63, cl = lane >> 4, n = lane & 15;
@@ -843,8 +862,7 @@ bwd_lane(Geo g, Ptrs p, int cpb) {
   const bool has_z = p.z != nullptr;
   const bool has_out = p.out != nullptr;
   const int64_t L = g.length;
-  float* t1 = lds[wave][0];
-  float* t2 = lds[wave][1];
+  float* tr = lds[wave];
   // Lane offsets in elements (the host keeps every array below 2^31 elements): this lane's
   // element of a block, its saved state, and its state's row of B and C (read straight from
   // memory: the wavefront's 4 channels read the same rows, which the vector L1 serves once).
@@ -932,19 +950,19 @@ bwd_lane(Geo g, Ptrs p, int cpb) {
         ah[i] = fast_exp2(row_bcast<i>(del) * a2);
         x = fmaf(ah[i], x, row_bcast<i>(du) * bv[i]);
         xh[i] = x;
-        if constexpr (decltype(with_y)::value) t1[i * kTrPitch + tw] = cv[i] * x;
+        if constexpr (decltype(with_y)::value) tr[i * kTrPitch + 2 * tw] = cv[i] * x;
       });
     };
     if (ty) {
       // blocks with a zero gate somewhere: the pre-gate output from the sum of C x
       recompute(std::true_type{});
       wave_lds_sync();
-      float v3[HS], c4[4];
-      lds_row<HS>(t1 + n * kTrPitch + cl * HS, v3);
+      float v3[2 * HS], c4[4];
+      lds_row<2 * HS>(tr + n * kTrPitch + 2 * cl * HS, v3);
 #pragma unroll
-      for (int m = 0; m < 4; ++m) c4[m] = v3[m];
+      for (int m = 0; m < 4; ++m) c4[m] = v3[2 * m];
 #pragma unroll
-      for (int m = 4; m < HS; ++m) c4[m & 3] += v3[m];
+      for (int m = 4; m < HS; ++m) c4[m & 3] += v3[2 * m];
       if (need_y) ypre = fmaf(Dd, uu, (c4[0] + c4[1]) + (c4[2] + c4[3]));
       wave_lds_sync();
     } else {
@@ -955,13 +973,12 @@ bwd_lane(Geo g, Ptrs p, int cpb) {
     float rodd = 0.0f;  // the odd step's half-summed register, waiting for its even partner
     static_for<0, HS>([&](auto jc) {
       constexpr int i = HS - 1 - decltype(jc)::value;
-      const float h = row_bcast<i>(gy) * cv[i] + carry;
-      t1[i * kTrPitch + tw] = h * bv[i];
+      const float h = fmac_row<i, i == HS - 1>(carry, gy, cv[i]);
       const float hc = ah[i] * h;
       const float pr = hc * (i > 0 ? xh[i > 0 ? i - 1 : 0] : x0);
-      t2[i * kTrPitch + tw] = an * pr;
-      if constexpr (i % 2 == 0) dA0 += row_bcast<i>(del) * pr;
-      else dA1 += row_bcast<i>(del) * pr;
+      *reinterpret_cast<float2*>(tr + i * kTrPitch + 2 * tw) = make_float2(h * bv[i], an * pr);
+      if constexpr (i % 2 == 0) dA0 = fmac_row<i>(dA0, del, pr);
+      else dA1 = fmac_row<i>(dA1, del, pr);
       // dB and dC terms of step i, h du_i and gy_i x_i: rows c0 + c2 and c1 + c3 of each
       // (a swap of the wavefront's halves), dB in rows 0-1 and dC in rows 2-3 ...
       const float pb = row_bcast<i>(du) * h, pc = row_bcast<i>(gy) * xh[i];
@@ -981,19 +998,18 @@ bwd_lane(Geo g, Ptrs p, int cpb) {
     // ---- lane (c, n) owns step t0 + n: its rows of the transposes
     float s1, s2;
     {
-      float v1[HS], v2[HS];
-      lds_row<HS>(t1 + n * kTrPitch + cl * HS, v1);
-      lds_row<HS>(t2 + n * kTrPitch + cl * HS, v2);
+      float v[2 * HS];
+      lds_row<2 * HS>(tr + n * kTrPitch + 2 * cl * HS, v);
       float a[4], b[4];
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
-        a[m] = v1[m];
-        b[m] = v2[m];
+        a[m] = v[2 * m];
+        b[m] = v[2 * m + 1];
       }
 #pragma unroll
       for (int m = 4; m < HS; ++m) {
-        a[m & 3] += v1[m];
-        b[m & 3] += v2[m];
+        a[m & 3] += v[2 * m];
+        b[m & 3] += v[2 * m + 1];
       }
       s1 = (a[0] + a[1]) + (a[2] + a[3]);
       s2 = (b[0] + b[1]) + (b[2] + b[3]);
@@ -1010,19 +1026,19 @@ bwd_lane(Geo g, Ptrs p, int cpb) {
     }
     // ---- dB/dC of the block: register m of lane (row q, state n) holds dB (q < 2) or dC (q >= 2)
     // of step 2m + (q mod 2)
-    wave_lds_sync();  // every read of t1 is done before it takes the wavefront's dB/dC block
+    wave_lds_sync();  // every read of the transposes is done before they take the dB/dC block
     const int which = cl >> 1, par = cl & 1;
     if (cpb == 16) {
 #pragma unroll
-      for (int m = 0; m < HS / 2; ++m) t1[which * HS * HS + (2 * m + par) * HS + n] = sbc[m];
+      for (int m = 0; m < HS / 2; ++m) tr[which * HS * HS + (2 * m + par) * HS + n] = sbc[m];
       __syncthreads();
       // thread (i, s) adds the 4 wavefronts' (step i, state s) in order
       const int o = threadIdx.x;
       float sb = 0.0f, sc = 0.0f;
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        sb += lds[w][0][o];
-        sc += lds[w][0][HS * HS + o];
+        sb += lds[w][o];
+        sc += lds[w][HS * HS + o];
       }
       (pbc + t0 * HS)[o] = make_float2(sb, sc);
       __syncthreads();
