@@ -827,7 +827,8 @@ __device__ __forceinline__ float row_bcast(float v) {
 // would otherwise spend a v_mov_b32_dpp on it).  A DPP source written by the instruction just
 // before needs two wait states, which the compiler does not insert for inline assembly: with
 // kGuard the instruction carries them itself; without it v must have been written well before
-// (every caller's v is formed before the block's recompute, dozens of instructions earlier).
+// (every caller's v is formed before the block's recompute, dozens of instructions earlier;
+// tests/test_isa_hazards.py checks the built code).
 template <int I, bool kGuard = false>
 __device__ __forceinline__ float fmac_row(float acc, float v, float m) {
   if constexpr (kGuard)
@@ -995,7 +996,7 @@ bwd_lane(Geo g, Ptrs p, int cpb) {
       carry = hc;
     });
     wave_lds_sync();
-    // ---- lane (c, n) owns step t0 + n: its rows of the transposes
+    // ---- lane (c, n) owns step t0 + n: its row of the transpose
     float s1, s2;
     {
       float v[2 * HS];
