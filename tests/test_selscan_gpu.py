@@ -140,6 +140,7 @@ LANE_SHAPES = [
     (2, 3072, 64, 16, 1),   # the smallest lane-path problem
     (2, 3072, 48, 12, 2),   # dstate 12 (lanes 12..15 idle), two groups
     (1, 6200, 32, 16, 2),   # a ragged last workgroup, two groups of 3100 channels
+    (2, 3072, 16, 16, 1),   # one 16-step block: the backward's load ahead re-reads block 0
 ]
 
 
