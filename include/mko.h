@@ -124,6 +124,13 @@ int mko_selscan_fwd(const mko_selscan_params* p, void* stream);
 size_t mko_selscan_bwd_workspace_size(const mko_selscan_params* p);
 int mko_selscan_bwd(const mko_selscan_params* p, void* stream);
 
+/* Which mapping each direction takes for this geometry, from the sizes alone (a call
+ * still falls back to the lane-per-channel kernels when B/C rows are not 16-byte
+ * aligned): 1 for the lane-per-(channel, state) kernels, 0 for the lane-per-channel ones.
+ * Host only, no launch; pointers are not read.  No reference counterpart (the reference
+ * has one Metal mapping). */
+int mko_selscan_plan(const mko_selscan_params* p, int* fwd_lane, int* bwd_lane);
+
 /* ======================================================================== */
 /* Mamba-2 decode state update                                                */
 /* ======================================================================== */

@@ -4,7 +4,8 @@ Usage: ``python metal-kernelops_amd/build.py [--verbose]``.  Compiles every
 ``csrc/*.hip`` to an object in parallel with hipcc for gfx950, then links the
 shared library into ``metal_kernelops/_lib/libmko.so`` (in-tree, so it travels
 with the source tree to the GPU host).  Packed-FP32 instructions are disabled for
-all device code.
+all device code.  After linking, the DPP wait states of the Mamba-1 backward's inline
+assembly are checked on the built code object (``isa_check.py``); a problem fails the build.
 """
 
 from __future__ import annotations
@@ -24,6 +25,8 @@ OBJDIR = os.path.join(HERE, "_build")
 LIBDIR = os.path.join(HERE, "metal_kernelops", "_lib")
 LIB = os.path.join(LIBDIR, "libmko.so")
 ARCH = "gfx950"
+if HERE not in sys.path:
+    sys.path.insert(0, HERE)
 
 DEVICE_FLAGS = [
     "-std=c++17", "-O3", "-fPIC", f"--offload-arch={ARCH}",
@@ -70,6 +73,12 @@ def build(verbose=False, jobs=None):
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
     os.replace(tmp, LIB)
+    # the inline-assembly DPP multiply-adds of the Mamba-1 backward rely on the schedule around
+    # them; a build whose schedule breaks their wait states must not ship
+    import isa_check
+    n = isa_check.check_object(os.path.join(OBJDIR, "selscan.o"))
+    if verbose:
+        print(f"DPP wait states checked: {n} v_fmac_f32_dpp in selscan.o", flush=True)
     return LIB
 
 

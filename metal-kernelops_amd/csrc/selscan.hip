@@ -864,7 +864,8 @@ bwd_lane(Geo g, Ptrs p, int cpb) {
   const bool has_out = p.out != nullptr;
   const int64_t L = g.length;
   float* tr = lds[wave];
-  // Lane offsets in elements (the host keeps every array below 2^31 elements): this lane's
+  // Lane offsets in elements (lane_bwd_shape keeps the per-row arrays and B/C below 2^31
+  // elements each): this lane's
   // element of a block, its saved state, and its state's row of B and C (read straight from
   // memory: the wavefront's 4 channels read the same rows, which the vector L1 serves once).
   // Block offsets are added to wave-uniform base pointers.
@@ -1628,9 +1629,13 @@ static bool lane_shape(const Geo& g, int ns) {
   return ns == 16 && g.rows >= kLaneRows && g.length % HS == 0 && g.dg % kLaneChannels == 0;
 }
 
-// The backward's too: it also indexes with 32-bit lane offsets.
+// The backward's too.  It indexes the per-row arrays (u, delta, z, dout, out, du, ddelta, dz,
+// the saved states) and B/C with 32-bit lane offsets from a 64-bit base, so each of them must
+// hold fewer than 2^31 elements: rows x length for the rows, and batch x groups x 16 states x
+// length for B and C (four times the rows' count when a group is 4 channels wide).
 static bool lane_bwd_shape(const Geo& g, int ns) {
-  return lane_shape(g, ns) && g.rows * g.length < (static_cast<int64_t>(1) << 31);
+  constexpr int64_t kLimit = static_cast<int64_t>(1) << 31;
+  return lane_shape(g, ns) && g.rows * g.length < kLimit && g.batch * g.ngroups * HS * g.length < kLimit;
 }
 
 static int make_plan(const mko_selscan_params* p, Plan* pl) {
@@ -1920,6 +1925,15 @@ extern "C" size_t mko_selscan_bwd_workspace_size(const mko_selscan_params* p) {
   Plan pl;
   if (make_plan(p, &pl) != MKO_OK) return 0;
   return pl.bwd_bytes;
+}
+
+extern "C" int mko_selscan_plan(const mko_selscan_params* p, int* fwd_lane, int* bwd_lane) {
+  Plan pl;
+  const int st = make_plan(p, &pl);
+  if (st != MKO_OK) return st;
+  if (fwd_lane) *fwd_lane = lane_shape(pl.g, pl.ns) ? 1 : 0;
+  if (bwd_lane) *bwd_lane = lane_bwd_shape(pl.g, pl.ns) ? 1 : 0;
+  return MKO_OK;
 }
 
 extern "C" int mko_selscan_fwd(const mko_selscan_params* p, void* stream) {

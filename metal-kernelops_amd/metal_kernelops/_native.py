@@ -151,6 +151,8 @@ _SIGNATURES = {
     "mko_selscan_fwd": ([ctypes.POINTER(SelscanParams), _vp], ctypes.c_int),
     "mko_selscan_bwd_workspace_size": ([ctypes.POINTER(SelscanParams)], ctypes.c_size_t),
     "mko_selscan_bwd": ([ctypes.POINTER(SelscanParams), _vp], ctypes.c_int),
+    "mko_selscan_plan": ([ctypes.POINTER(SelscanParams), ctypes.POINTER(ctypes.c_int),
+                          ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
     "mko_state_update_fwd": ([ctypes.POINTER(StateUpdateParams), _vp], ctypes.c_int),
     "mko_profile_enable": ([ctypes.c_int], ctypes.c_int),
     "mko_profile_reset": ([], None),

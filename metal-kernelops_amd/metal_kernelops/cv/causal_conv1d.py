@@ -222,41 +222,43 @@ def causal_conv1d_ref(x, weight, bias=None, activation=None, initial_state=None,
     return out
 
 
+def _check_prefill(x, weight, bias, initial_state):
+    """The prefill contract, rule by rule: x is 3-d with weight's channel count, bias is
+    one value per channel, the initial state spans K-1 steps of every (batch, channel)."""
+    rules = Rules("causal_conv1d_fn")
+    rules.dims("x", x, 3, "(batch, channels, length)")
+    channels, width = weight.shape
+    rules.require(x.shape[1] == channels, f"x carries {x.shape[1]} channels against {channels} in weight")
+    rules.require(bias is None or (bias.dim() == 1 and bias.shape[0] == channels),
+                  f"bias should hold one value per channel, ({channels},); its shape is "
+                  f"{None if bias is None else tuple(bias.shape)}")
+    rules.shape("initial_state", initial_state, (x.shape[0], channels, width - 1))
+    return rules
+
+
 def causal_conv1d_fn(x, weight, bias=None, activation=None, initial_state=None, return_final_state=False):
-    """Causal depthwise conv1d over a whole sequence on the ROCm GPU.
+    """Prefill: the causal depthwise convolution of a whole sequence, on the ROCm GPU.
 
-    Args:
-        x: ``(batch, channels, length)``.
-        weight: ``(channels, 1, K)`` depthwise, or ``(channels, K)``; ``K <= 32``.
-        bias: ``(channels,)`` or ``None``.
-        activation: ``None``, ``"silu"`` or ``"swish"``.
-        initial_state: ``(batch, channels, K-1)`` entering the sequence.
-        return_final_state: also return the state leaving the sequence.
+    ``x`` is ``(batch, channels, length)``; ``weight`` holds K taps per channel, either as
+    the ``(channels, 1, K)`` weight of a depthwise ``nn.Conv1d`` or as a ``(channels, K)``
+    matrix, with K at most 32.  ``bias`` adds one value per channel.  ``activation`` is
+    ``None`` (identity) or SiLU, spelled ``"silu"`` or ``"swish"``.  ``initial_state``,
+    ``(batch, channels, K-1)``, stands for the K-1 steps before the sequence (zeros when
+    absent).
 
-    Returns:
-        ``(batch, channels, length)`` in ``x.dtype``, or ``(out, final_state)`` with
-        ``final_state`` of shape ``(batch, channels, K-1)``.
+    The result has ``x``'s shape and dtype.  With ``return_final_state`` the call returns
+    ``(out, final_state)``, the last K-1 steps of ``cat(initial_state, x)``, shaped like
+    ``initial_state``.
     """
     weight = _as_depthwise(weight)
     _check_activation(activation)
-    if x.dim() != 3:
-        raise ValueError(f"x must be (batch, channels, length), got {tuple(x.shape)}")
-    channels, width = weight.shape
-    if x.shape[1] != channels:
-        raise ValueError(f"x has {x.shape[1]} channels, weight has {channels}")
-    if bias is not None and (bias.dim() != 1 or bias.shape[0] != channels):
-        raise ValueError(f"bias must be ({channels},), got {tuple(bias.shape)}")
-    if initial_state is not None:
-        expected = (x.shape[0], channels, width - 1)
-        if tuple(initial_state.shape) != expected:
-            raise ValueError(f"initial_state must be {expected}, got {tuple(initial_state.shape)}")
-    for name, t in (("x", x), ("weight", weight), ("bias", bias), ("initial_state", initial_state)):
+    rules = _check_prefill(x, weight, bias, initial_state)
+    width = weight.shape[1]
+    for t in (x, weight, bias, initial_state):
         if t is not None:
             _require_gpu(t)
-    if weight.dtype not in _FLOATS:
-        raise ValueError(f"causal_conv1d_fn computes in weight.dtype; float32, float16 or bfloat16, got {weight.dtype}")
-    if width > _MAX_WIDTH:
-        raise ValueError(f"the kernel width must be at most {_MAX_WIDTH}, got {width}")
+    rules.dtype_in(_FLOATS, weight=weight)
+    rules.require(width <= _MAX_WIDTH, f"at most {_MAX_WIDTH} taps run on the kernels; weight has {width}")
 
     compute = weight.dtype
     work = x.to(compute).contiguous()
@@ -276,51 +278,56 @@ def causal_conv1d_fn(x, weight, bias=None, activation=None, initial_state=None, 
     return out, final.to(x.dtype)
 
 
+def _check_update(x, state, weight, bias):
+    """The decode contract: x is (batch, channels, q) with weight's channels; the state
+    covers the same (batch, channel) pairs with at least K-1 unit-stride columns."""
+    rules = Rules("causal_conv1d_update")
+    rules.dims("x", x, 3, "(batch, channels) or (batch, channels, q)")
+    channels, width = weight.shape
+    taps = width - 1
+    batch = x.shape[0]
+    rules.require(x.shape[1] == channels, f"x carries {x.shape[1]} channels against {channels} in weight")
+    rules.require(state.dim() == 3 and tuple(state.shape[:2]) == (batch, channels),
+                  f"state should be ({batch}, {channels}, s) with s >= {taps}; its shape is {tuple(state.shape)}")
+    rules.require(state.shape[-1] >= taps,
+                  f"state should keep at least K-1 = {taps} columns; it keeps {state.shape[-1]}")
+    rules.require(state.stride(-1) == 1,
+                  f"state should have stride 1 in its last dimension (a cache slice may be strided elsewhere); "
+                  f"its strides are {state.stride()}")
+    rules.require(bias is None or (bias.dim() == 1 and bias.shape[0] == channels),
+                  f"bias should hold one value per channel, ({channels},); its shape is "
+                  f"{None if bias is None else tuple(bias.shape)}")
+    return rules
+
+
 def causal_conv1d_update(x, state, weight, bias=None, activation=None):
-    """Advance the causal convolution by ``q`` tokens, updating ``state`` in place.
+    """Decode: convolve q new tokens against a rolling state, which advances in place.
 
-    Args:
-        x: ``(batch, channels)`` or ``(batch, channels, q)``.
-        state: ``(batch, channels, s)``, ``s >= K-1``, last stride 1 (it may be a slice of a
-            larger cache), overwritten with ``cat(state, x)[..., -s:]``.
-        weight: ``(channels, 1, K)`` or ``(channels, K)``.
-        bias: ``(channels,)`` or ``None``.
-        activation: ``None``, ``"silu"`` or ``"swish"``.
+    ``x`` is ``(batch, channels)`` for one token or ``(batch, channels, q)``.  ``state``
+    is ``(batch, channels, s)`` with ``s >= K-1`` and unit stride along its last axis (it
+    may be a slice of a larger cache); afterwards it holds the last ``s`` columns of
+    ``cat(state, x)``.  ``weight``, ``bias`` and ``activation`` are as in
+    :func:`causal_conv1d_fn`.
 
-    Returns:
-        ``(batch, channels)`` or ``(batch, channels, q)``, matching the rank of ``x``.  The
-        decode path carries no autograd (``cv/causal_conv1d.py:690-756``).
+    Returns the outputs of the q new tokens, with ``x``'s rank.  This path is for
+    inference: inputs that require grad raise ``RuntimeError``
+    (``cv/causal_conv1d.py:690-756``).
     """
     weight = _as_depthwise(weight)
     _check_activation(activation)
     squeezed = x.dim() == 2
     if squeezed:
         x = x.unsqueeze(-1)
-    if x.dim() != 3:
-        raise ValueError(f"x must be (batch, channels) or (batch, channels, q), got {tuple(x.shape)}")
-    channels, width = weight.shape
-    taps = width - 1
-    batch, xchannels, _ = x.shape
-    if xchannels != channels:
-        raise ValueError(f"x has {xchannels} channels, weight has {channels}")
-    if state.dim() != 3 or state.shape[0] != batch or state.shape[1] != channels:
-        raise ValueError(f"state must be ({batch}, {channels}, s) with s >= {taps}, got {tuple(state.shape)}")
-    span = state.shape[-1]
-    if span < taps:
-        raise ValueError(f"state must hold at least K-1 = {taps} columns, got {span}")
-    if state.stride(-1) != 1:
-        raise ValueError(f"state must have stride 1 in its last dimension, got {state.stride()}")
-    if bias is not None and (bias.dim() != 1 or bias.shape[0] != channels):
-        raise ValueError(f"bias must be ({channels},), got {tuple(bias.shape)}")
+    rules = _check_update(x, state, weight, bias)
     if x.requires_grad or weight.requires_grad or state.requires_grad:
-        raise RuntimeError("causal_conv1d_update is the decode path and carries no autograd")
+        raise RuntimeError("causal_conv1d_update: the decode update carries no autograd; call it under "
+                           "torch.no_grad() or on detached tensors")
     for t in (x, state, weight, bias):
         if t is not None:
             _require_gpu(t)
-    if state.dtype not in _FLOATS:
-        raise ValueError(f"state must be float32, float16 or bfloat16, got {state.dtype}")
-    if width > _MAX_WIDTH:
-        raise ValueError(f"the kernel width must be at most {_MAX_WIDTH}, got {width}")
+    rules.dtype_in(_FLOATS, state=state)
+    width = weight.shape[1]
+    rules.require(width <= _MAX_WIDTH, f"at most {_MAX_WIDTH} taps run on the kernels; weight has {width}")
     # the kernel reads and writes every tensor in the state's dtype, computing in float32
     dtype = state.dtype
     work = x.to(dtype).contiguous()

@@ -235,19 +235,18 @@ def scan_mps(u, dt, A, B, C):
 
 
 def selective_scan(u, dt, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False):
-    """Drop-in selective scan matching mamba_ssm's ``selective_scan_fn``.
+    """The Mamba-1 selective scan with mamba_ssm's ``selective_scan_fn`` call signature.
 
-    Args:
-        u, dt: (batch, dim, length)
-        A: (dim, dstate), negative; dstate <= 32
-        B, C: (batch, groups, dstate, length), groups dividing dim
-        D: (dim,) skip connection
-        z: (batch, dim, length) gate, applied as ``out * silu(z)``
-        delta_bias: (dim,) added to dt
-        delta_softplus: apply softplus (threshold 20) to dt + delta_bias
+    ``u`` and the step sizes ``dt`` are ``(batch, dim, length)``.  ``A`` is the
+    ``(dim, dstate)`` state matrix (negative entries; at most 32 states).  ``B`` and ``C``
+    are ``(batch, groups, dstate, length)``, each group shared by ``dim / groups``
+    consecutive channels.  Optional: ``D``, a ``(dim,)`` skip weight on ``u``; ``z``, a
+    ``(batch, dim, length)`` gate that multiplies the result by ``silu(z)``;
+    ``delta_bias``, ``(dim,)``, added to ``dt``; ``delta_softplus``, which passes
+    ``dt + delta_bias`` through softplus (threshold 20) before the scan.
 
-    Returns:
-        (batch, dim, length) in u's dtype.
+    Returns the ``(batch, dim, length)`` output in ``u``'s dtype, differentiable in
+    every tensor argument.
     """
     return _run(u, dt, A, B, C, D, z, delta_bias, delta_softplus)
 

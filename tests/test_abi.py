@@ -130,3 +130,29 @@ def test_static_decode_backward_refuses_an_oversized_problem_on_the_host(native)
     assert b"static scratch" in lib.mko_last_error()
     p.dA = None
     assert lib.mko_state_update_bwd_static(ctypes.byref(p), None) == 1  # a missing output first
+
+
+def test_lane_backward_refused_past_its_32_bit_offsets(native):
+    """The lane-per-state backward addresses B/C with 32-bit lane offsets.  With groups of
+    4 channels B/C hold four times as many elements as u, so a geometry whose rows x length
+    still fits 2^31 while batch x groups x 16 x length does not must plan the
+    lane-per-channel backward; the forward (64-bit offsets) keeps its lane mapping."""
+    lib = native.lib()
+
+    def plan(batch, dim, length, groups):
+        p = native.SelscanParams()
+        p.batch, p.dim, p.length, p.dstate, p.ngroups = batch, dim, length, 16, groups
+        fwd, bwd = ctypes.c_int(-1), ctypes.c_int(-1)
+        assert lib.mko_selscan_plan(ctypes.byref(p), ctypes.byref(fwd), ctypes.byref(bwd)) == 0
+        return fwd.value, bwd.value
+
+    # c3's geometry takes the lane kernels both ways
+    assert plan(4, 5120, 4096, 1) == (1, 1)
+    # 4-channel groups: B/C = 4 * rows * length elements; rows * length = 2^29
+    assert plan(1, 8192, 65536, 2048) == (1, 0)
+    # one step shorter per 16: B/C just under 2^31 elements, the lane backward again
+    assert plan(1, 8192, 65536 - 16, 2048) == (1, 1)
+    # 16-channel groups at the same sizes: B/C = rows * length, inside the bound
+    assert plan(1, 8192, 65536, 512) == (1, 1)
+    # rows * length itself at 2^31
+    assert plan(1, 8192, 262144, 1) == (1, 0)

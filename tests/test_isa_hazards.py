@@ -1,96 +1,25 @@
-"""Wait states around the inline-assembly DPP multiply-adds of the Mamba-1 lane backward.
+"""The wait-state check of the inline-assembly DPP multiply-adds in the Mamba-1 backward.
 
-`fmac_row` in csrc/selscan.hip issues `v_fmac_f32_dpp` (a row broadcast as the DPP source)
-from inline assembly, because the compiler folds DPP into multiplies but not into fmac.  The
-hardware needs two wait states between a vector write of a register and a DPP read of it, and
-the compiler inserts none for inline assembly: the code is correct only while every such
-instruction's DPP source was written at least two instructions earlier (or the instruction
-carries its own `s_nop 1`).  This test disassembles the gfx950 code object of the selscan.o
-that `build()` produced (this build's own code) and checks every one of them, so a compiler
-that schedules differently fails here on the CPU instead of giving wrong gradients on a GPU.
+`metal-kernelops_amd/isa_check.py` holds the check; `build()` runs it on the built
+selscan.o and fails the build on a problem.  Here the checker itself is tested on small
+listings (so that a regression of the checker cannot let a bad schedule through), and the
+built object is checked again when it is present.
 """
 import os
-import re
-import shutil
-import subprocess
+import sys
 
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-OBJ = os.path.join(ROOT, "metal-kernelops_amd", "_build", "selscan.o")
-OBJDUMP = "/opt/rocm/llvm/bin/llvm-objdump"
+PKG = os.path.join(ROOT, "metal-kernelops_amd")
+if PKG not in sys.path:
+    sys.path.insert(0, PKG)
 
-INSN = re.compile(r"^\s+([a-z_0-9]+)(.*?)\s*//\s*([0-9A-F]+):")
-FUNC = re.compile(r"^([0-9a-f]+) <([^>]+)>:")
-TARGET = re.compile(r"<([^>+]+)\+0x([0-9a-f]+)>")
+import isa_check  # noqa: E402
 
-
-def _disassemble(tmp_path):
-    if not os.path.exists(OBJ):
-        pytest.skip("selscan.o not built (run __graft_entry__.build() first)")
-    if not os.path.exists(OBJDUMP):
-        pytest.skip("llvm-objdump not available")
-    obj = tmp_path / "selscan.o"
-    shutil.copy(OBJ, obj)
-    subprocess.run([OBJDUMP, "--offloading", str(obj)], check=True, capture_output=True, cwd=tmp_path)
-    dev = [p for p in tmp_path.iterdir() if "amdgcn" in p.name and "gfx950" in p.name]
-    assert dev, "no gfx950 code object in selscan.o"
-    out = subprocess.run([OBJDUMP, "-d", "--mcpu=gfx950", str(dev[0])], check=True, capture_output=True, text=True)
-    return out.stdout.splitlines()
-
-
-def _written(mnemonic, operands):
-    """Vector registers an instruction writes (its first operand, for vector ALU ops)."""
-    if not mnemonic.startswith("v_") or mnemonic.startswith(("v_cmp", "v_readlane", "v_readfirstlane")):
-        return set()
-    dst = operands.split(",")[0].strip()
-    m = re.fullmatch(r"v(\d+)", dst)
-    if m:
-        return {int(m.group(1))}
-    m = re.fullmatch(r"v\[(\d+):(\d+)\]", dst)
-    if m:
-        return set(range(int(m.group(1)), int(m.group(2)) + 1))
-    return set()
-
-
-def _problems(lines):
-    """(number of v_fmac_f32_dpp checked, the ones whose DPP source may not have settled)."""
-    funcs, insns = {}, []
-    for line in lines:
-        m = FUNC.match(line)
-        if m:
-            funcs[m.group(2)] = int(m.group(1), 16)
-            continue
-        m = INSN.match(line)
-        if m:
-            insns.append((int(m.group(3), 16), m.group(1), m.group(2), line))
-    targets = set()
-    for _, mn, _, line in insns:
-        if mn.startswith(("s_branch", "s_cbranch")):
-            t = TARGET.search(line)
-            if t and t.group(1) in funcs:
-                targets.add(funcs[t.group(1)] + int(t.group(2), 16))
-    checked, problems = 0, []
-    for i, (addr, mn, ops, line) in enumerate(insns):
-        if mn != "v_fmac_f32_dpp":
-            continue
-        checked += 1
-        src = int(re.match(r"\s*v\d+,\s*v(\d+),", ops).group(1))
-        if addr in targets:
-            problems.append(f"branch target at {line.strip()}")
-            continue
-        waits, j = 0, i - 1
-        while waits < 2 and j >= 0:
-            a, m2, o2, l2 = insns[j]
-            if src in _written(m2, o2):
-                problems.append(f"v{src} written {waits} wait states before: {l2.strip()} -> {line.strip()}")
-                break
-            waits += int(o2.split()[0]) + 1 if m2 == "s_nop" else 1
-            if waits < 2 and a in targets:
-                problems.append(f"branch target inside the window: {l2.strip()} -> {line.strip()}")
-                break
-            j -= 1
-    return checked, problems
+OBJ = os.path.join(PKG, "_build", "selscan.o")
+LIB = os.path.join(PKG, "metal_kernelops", "_lib", "libmko.so")
+FMAC = "v_fmac_f32_dpp v10, v4, v5 row_newbcast:3 row_mask:0xf bank_mask:0xf bound_ctrl:1"
 
 
 def _listing(body):
@@ -100,20 +29,49 @@ def _listing(body):
     return out
 
 
+def _bad(body):
+    return bool(isa_check.problems(_listing(body))[1])
+
+
 def test_checker_finds_an_unsettled_source():
-    """The check itself: a source written one instruction before the DPP read is reported, the
-    same source behind s_nop 1 or two other instructions is not, and a branch landing between
-    the write and the read makes the read unverifiable."""
-    fmac = "v_fmac_f32_dpp v10, v4, v5 row_newbcast:3 row_mask:0xf bank_mask:0xf bound_ctrl:1"
-    bad = _listing(["v_mul_f32_e32 v4, v1, v2", "v_add_f32_e32 v7, v1, v2", fmac])
-    nop = _listing(["v_mul_f32_e32 v4, v1, v2", "s_nop 1", fmac])
-    far = _listing(["v_mul_f32_e32 v4, v1, v2", "v_add_f32_e32 v7, v1, v2", "v_add_f32_e32 v8, v1, v2", fmac])
-    jump = _listing(["s_branch 1 <k+0xc>", "v_mul_f32_e32 v4, v1, v2", "v_add_f32_e32 v7, v1, v2", fmac])
-    assert _problems(bad)[1] and not _problems(nop)[1] and not _problems(far)[1]
-    assert _problems(jump)[1] and _problems(far)[0] == 1
+    """The DPP source written one instruction before is reported; behind s_nop 1 or two other
+    instructions it is not; a branch landing between write and read makes it unverifiable."""
+    assert _bad(["v_mul_f32_e32 v4, v1, v2", "v_add_f32_e32 v7, v1, v2", FMAC])
+    assert not _bad(["v_mul_f32_e32 v4, v1, v2", "s_nop 1", FMAC])
+    far = ["v_mul_f32_e32 v4, v1, v2", "v_add_f32_e32 v7, v1, v2", "v_add_f32_e32 v8, v1, v2", FMAC]
+    assert not _bad(far) and isa_check.problems(_listing(far))[0] == 1
+    assert _bad(["s_branch 1 <k+0xc>", "v_mul_f32_e32 v4, v1, v2", "v_add_f32_e32 v7, v1, v2", FMAC])
 
 
-def test_dpp_fmac_sources_are_settled(tmp_path):
-    checked, problems = _problems(_disassemble(tmp_path))
-    assert checked > 0, "no v_fmac_f32_dpp found: fmac_row is no longer used, drop this test"
-    assert not problems, "\n".join(problems[:10])
+def test_checker_covers_every_input_and_exec():
+    """The multiplier and the tied accumulator need the same two wait states as the DPP
+    source; both outputs of a lane swap count as writes; a loaded register too; and a
+    v_cmpx (it writes EXEC) needs five."""
+    pad = "v_add_f32_e32 v7, v1, v2"
+    assert _bad(["v_mul_f32_e32 v5, v1, v2", pad, FMAC])  # multiplier
+    assert _bad(["v_mov_b32_e32 v10, v1", pad, FMAC])  # accumulator
+    assert _bad(["v_permlane32_swap_b32_e32 v9, v4", pad, FMAC])  # second output of a swap
+    assert _bad(["v_permlane16_swap_b32_e32 v5, v9", FMAC])  # first output of a swap
+    assert _bad(["v_lshlrev_b64 v[4:5], 1, v[0:1]", pad, FMAC])  # a register pair
+    assert _bad(["ds_read_b32 v4, v2", pad, FMAC])  # a load's destination
+    assert not _bad(["ds_write_b32 v4, v5", pad, FMAC])  # a store reads its operands
+    assert _bad(["v_cmpx_gt_f32_e32 vcc, v1, v2", pad, pad, pad, pad, FMAC])  # EXEC, 4 wait states
+    assert not _bad(["v_cmpx_gt_f32_e32 vcc, v1, v2", pad, pad, pad, pad, pad, FMAC])
+    assert not _bad(["v_cmp_gt_f32_e32 vcc, v4, v5", FMAC])  # a compare into VCC writes no VGPR
+    assert not _bad(["v_mul_f32_e32 v4, v1, v2", "s_nop 0", pad, FMAC])
+    # a loop head three instructions before: settled VGPRs, and the paths into it (the fall-
+    # through and the back branch) carry no v_cmpx; one that does is reported
+    loop = ["s_nop 4", "s_waitcnt lgkmcnt(0)", pad, pad, FMAC, "s_cbranch_scc1 1 <k+0x4>"]
+    assert not _bad(loop)
+    assert _bad(["s_nop 4", "s_waitcnt lgkmcnt(0)", pad, pad, FMAC, "v_cmpx_gt_f32_e32 vcc, v1, v2",
+                 "s_cbranch_scc1 1 <k+0x4>"])
+
+
+def test_dpp_fmac_inputs_are_settled_in_the_built_object():
+    """The object `build()` produced.  Where the library exists, its objects must be there to
+    check: a missing object fails rather than skips."""
+    if not os.path.exists(OBJ):
+        if os.path.exists(LIB) and os.path.isdir(os.path.join(PKG, "_build")):
+            pytest.fail(f"{LIB} exists but {OBJ} is missing: rebuild with __graft_entry__.build()")
+        pytest.skip("selscan.o not built here (run __graft_entry__.build() first)")
+    assert isa_check.check_object(OBJ) > 0

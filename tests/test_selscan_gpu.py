@@ -182,8 +182,9 @@ def _backward_kernels(inputs, dy, softplus=True):
         nat.kernel_timing(False)
 
 
-@pytest.mark.parametrize("shape", [(2, 3072, 64, 16, 1), (1, 6200, 32, 16, 2), (2, 3072, 48, 12, 3)],
-                         ids=["groups-of-3072", "groups-of-3100", "dstate-12-groups-of-1024"])
+@pytest.mark.parametrize("shape", [(2, 3072, 64, 16, 1), (1, 6200, 32, 16, 2), (2, 3072, 48, 12, 3),
+                                   (2, 3072, 16, 16, 1)],
+                         ids=["groups-of-3072", "groups-of-3100", "dstate-12-groups-of-1024", "one-16-step-block"])
 def test_lane_backward_kernel_is_taken_and_deterministic(shape):
     # 6144+ channel rows, whole 16-step blocks, dstate <= 16 and groups a multiple of 4
     # channels wide: one lane per (channel, state) walks the sequence backwards. Groups of a
