@@ -122,6 +122,41 @@ def valu_roofline(name, avg_ms):
             "valu_insts_per_launch": insts}
 
 
+def copy_floor(gib=1.0, runs=20):
+    """The part's read-and-write streaming rate in this run: libmko's streaming copy
+    (mko_stream_copy) of ``gib`` GiB, with the nontemporal hint (as the decode kernels
+    access their state) and without it, ``runs`` timed copies each after 3 warm-ups."""
+    from metal_kernelops import _native as nat
+    n = int(gib * (1 << 30)) // 4
+    src = torch.empty(n, dtype=torch.float32, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    out = {"kernel": "mko_stream_copy", "bytes_read": n * 4, "bytes_written": n * 4, "runs": runs}
+    for key, nt in (("nontemporal", True), ("plain", False)):
+        for _ in range(3):
+            nat.stream_copy(src, dst, nt)
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(runs):
+            nat.stream_copy(src, dst, nt)
+        t1.record()
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / runs
+        gbs = 2 * n * 4 / (ms * 1e-3) / 1e9
+        out[key] = {"us": round(ms * 1e3, 1), "gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+    if not torch.equal(src, dst):
+        raise RuntimeError("mko_stream_copy: the copy differs from its source")
+    del src, dst
+    torch.cuda.empty_cache()
+    out["gbs"] = max(out["nontemporal"]["gbs"], out["plain"]["gbs"])
+    return out
+
+
+def of_copy(gbs, floor):
+    """A streaming rate as a fraction of the run's copy floor."""
+    return None if floor is None else round(gbs / floor["gbs"], 4)
+
+
 # --------------------------------------------------------------------- Mamba-1
 
 
@@ -255,9 +290,13 @@ def decode_case(steps=1024, warmup=16):
     bwd_name = "state_update_bwd"
     bwd_ms = kb[bwd_name][0] / max(kb[bwd_name][1], 1)
     bwd_bytes = 3 * state.numel() * 4 + 256 * 80 * 64 * 2 * 5 + 256 * 128 * 2 * 4 + 256 * 80 * 4 * 2
+    broof = roofline(bwd_bytes, bwd_ms, load_traffic(f"{bwd_name}@256x80x64x128"))
+    broof["kernel"] = bwd_name
+    broof["algorithmic_bytes"] = bwd_bytes
     bwd = {"ms_per_fwd_bwd_step": round(ms_fb, 4), "bwd_kernel_ms": round(bwd_ms, 4),
            "bwd_gbs": round(bwd_bytes / (bwd_ms * 1e-3) / 1e9, 1), "bwd_algorithmic_bytes": bwd_bytes,
            "bwd_hbm_frac": round(bwd_bytes / (bwd_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+           "roofline": broof,
            "kernels_ms": {k: round(v[0] / max(v[1], 1), 4) for k, v in sorted(kb.items())}}
     del state, ring, leaves, dy, dnew
     torch.cuda.empty_cache()
@@ -745,26 +784,14 @@ def main():
     torch.backends.cuda.matmul.allow_tf32 = False
 
     if args.only == "copy":
-        # A device-to-device copy of 1 GiB, three times: under rocprofv3 --pmc its
-        # FETCH_SIZE / WRITE_SIZE per dispatch calibrate the counters against a known
-        # 1 GiB read and 1 GiB write.
-        # The timed copies give the practical read+write bandwidth of the part.
-        src = torch.empty(1 << 28, dtype=torch.float32, device="cuda").fill_(1.0)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        t0.record()
-        for _ in range(10):
-            dst.copy_(src)
-        t1.record()
-        torch.cuda.synchronize()
-        ms = t0.elapsed_time(t1) / 10
-        nbytes = src.numel() * 4
-        print(json.dumps({"copy_bytes_read": nbytes, "copy_bytes_written": nbytes, "copy_ms": round(ms, 4),
-                          "copy_gbs": round(2 * nbytes / ms / 1e6, 1)}), flush=True)
+        # Under rocprofv3 --pmc, FETCH_SIZE / WRITE_SIZE per dispatch of these copies calibrate
+        # the byte counters against a known 1 GiB read and 1 GiB write (23 dispatches each of
+        # the plain and the nontemporal form); the timed copies give the part's streaming rate.
+        print(json.dumps(copy_floor()), flush=True)
         return
+    log("copy floor: libmko streaming copy of 1 GiB")  # every run measures the floor it is compared with
+    floor = copy_floor()
+    log(f"  nontemporal {floor['nontemporal']['gbs']:.0f} GB/s, plain {floor['plain']['gbs']:.0f} GB/s")
     also = {}
     want = (lambda w: args.only in (w, "all"))
     if want("ssd"):
@@ -805,7 +832,9 @@ def main():
             "ms_per_step": round(dec["ms_per_step"], 5), "steps": dec["steps"],
             "config": {"batch": 256, "nheads": 80, "headdim": 64, "dstate": 128, "ngroups": 1,
                        "state_dtype": "f32", "io_dtype": "bf16"},
-            "roofline": dec["roofline"], "kernels_ms": dec["kernels_ms"], "backward": dec["backward"]}
+            "roofline": dec["roofline"], "kernels_ms": dec["kernels_ms"], "backward": dec["backward"],
+            "of_copy_floor": of_copy(dec["roofline"]["achieved"], floor),
+            "backward_of_copy_floor": of_copy(dec["backward"]["roofline"]["achieved"], floor)}
         log(f"  {dec['ms_per_step'] * 1e3:.1f} us/step, {dec['state_rmw_gbs']:.1f} GB/s state RMW; backward "
             f"{dec['backward']['bwd_kernel_ms'] * 1e3:.1f} us, {dec['backward']['bwd_gbs']:.1f} GB/s")
     if want("ss2d"):
@@ -850,6 +879,7 @@ def main():
             f"2.7B layer {bl['mamba2_2.7b_layer']['ms_per_step']:.3f} ms/step, "
             f"{bl['mamba2_2.7b_layer']['value'] / 1e6:.2f} M tokens/s; kernels {bl['mamba2_2.7b_layer']['kernels_ms']}")
     if head is None:  # a single non-headline workload: print its own record
+        also["copy_floor"] = floor
         print(json.dumps(also), flush=True)
         return
     cpu = None
@@ -889,6 +919,7 @@ def main():
                    "hbm_frac_whole_step": round(head["gbs"] / HBM_PEAK_GBS, 4)},
         "roofline": head["roofline"],
         "roofline_valu": head["roofline_valu"],
+        "copy_floor": floor,
         "cpu_baseline": cpu,
         "kernels_ms": head["kernels_ms"],
         "also": also,

@@ -63,6 +63,16 @@ void mko_profile_reset(void);
 int mko_profile_count(void);      /* number of distinct kernels timed */
 int mko_profile_entry(int index, char* name, size_t name_len, double* total_ms, int64_t* launches);
 
+/* Streaming device copy (measurement).  No reference counterpart: the reference's
+ * verifiers time a state-sized torch copy as their floor (benchmarks/verify_mamba2_state.py:
+ * 398-401, 431-445); this is the library's own, tuned for this part, so that the state
+ * read-modify-write kernels are measured against the rate a read-and-write stream reaches
+ * here.  Copies `bytes` from src to dst (16-byte aligned, not overlapping) on `stream`.
+ * MKO_STREAM_NONTEMPORAL reads and writes with the nontemporal hint, as the decode kernels
+ * read and write their state. */
+#define MKO_STREAM_NONTEMPORAL 1u
+int mko_stream_copy(const void* src, void* dst, size_t bytes, uint32_t flags, void* stream);
+
 /* ======================================================================== */
 /* Mamba-1 selective scan                                                     */
 /* ======================================================================== */

@@ -83,6 +83,53 @@ __device__ __forceinline__ void store_words(void* p, const uint32_t (&w)[W]) {
   }
 }
 
+// The same accesses with the nontemporal hint (global_load/store ... nt): for streams that are
+// read or written once and not reused from the caches, such as a decode step's state.  On
+// this part a read-and-write stream runs about 8% faster with them (6.2 against 5.7 TB/s for
+// a device copy at four 16-byte vectors per lane).
+typedef uint32_t mko_u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t mko_u32x2 __attribute__((ext_vector_type(2)));
+
+template <int W>
+__device__ __forceinline__ void load_words_nt(const void* p, uint32_t (&w)[W]) {
+  if constexpr (W % 4 == 0) {
+    const mko_u32x4* q = static_cast<const mko_u32x4*>(p);
+#pragma unroll
+    for (int i = 0; i < W / 4; ++i) {
+      const mko_u32x4 t = __builtin_nontemporal_load(q + i);
+      w[4 * i + 0] = t.x;
+      w[4 * i + 1] = t.y;
+      w[4 * i + 2] = t.z;
+      w[4 * i + 3] = t.w;
+    }
+  } else if constexpr (W == 2) {
+    const mko_u32x2 t = __builtin_nontemporal_load(static_cast<const mko_u32x2*>(p));
+    w[0] = t.x;
+    w[1] = t.y;
+  } else {
+    static_assert(W == 1, "16-byte vectors, or one 8- or 4-byte access");
+    w[0] = __builtin_nontemporal_load(static_cast<const uint32_t*>(p));
+  }
+}
+
+template <int W>
+__device__ __forceinline__ void store_words_nt(void* p, const uint32_t (&w)[W]) {
+  if constexpr (W % 4 == 0) {
+    mko_u32x4* q = static_cast<mko_u32x4*>(p);
+#pragma unroll
+    for (int i = 0; i < W / 4; ++i) {
+      const mko_u32x4 t = {w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]};
+      __builtin_nontemporal_store(t, q + i);
+    }
+  } else if constexpr (W == 2) {
+    const mko_u32x2 t = {w[0], w[1]};
+    __builtin_nontemporal_store(t, static_cast<mko_u32x2*>(p));
+  } else {
+    static_assert(W == 1, "16-byte vectors, or one 8- or 4-byte access");
+    __builtin_nontemporal_store(w[0], static_cast<uint32_t*>(p));
+  }
+}
+
 // p advanced by off bytes.  With a wave-uniform p the access compiles to the scalar-base
 // form of the global loads and stores (64-bit base in SGPRs, one 32-bit offset VGPR per
 // lane) instead of a 64-bit address pair per lane.

@@ -81,6 +81,26 @@ __device__ __forceinline__ float ld_any(const void* base, int dtype, int64_t i) 
   return to_f32(static_cast<const _Float16*>(base)[i]);
 }
 
+// Element i of a float32, float16 or bfloat16 array chosen at run time, read without a branch
+// and converted later: two 16-bit loads (the element's low half, and for float32 its high
+// half; a 16-bit element is read twice rather than reading past it), and the conversion by
+// selects.  A load under a run-time dtype branch makes the compiler wait at the join for every
+// load in flight, and converting each value right after its load serialises the loads.
+struct RawAny {
+  uint32_t lo, hi;
+};
+__device__ __forceinline__ RawAny load_any_raw(const void* base, int dtype, int64_t i) {
+  const bool f32 = dtype == MKO_F32;
+  const uint16_t* p = reinterpret_cast<const uint16_t*>(static_cast<const char*>(base) + i * (f32 ? 4 : 2));
+  return {p[0], p[f32 ? 1 : 0]};
+}
+__device__ __forceinline__ float raw_any_f32(RawAny r, int dtype) {
+  const float as_f32 = __uint_as_float(r.lo | (r.hi << 16));
+  const float as_bf16 = __uint_as_float(r.lo << 16);
+  const float as_f16 = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.lo)));
+  return dtype == MKO_F32 ? as_f32 : (dtype == MKO_BF16 ? as_bf16 : as_f16);
+}
+
 // Elements of a row handled by lane j of its TPR lanes: vector chunks j, j+TPR, ...
 // (VEC = 4) or single elements (VEC = 1), at most SPL of them.
 template <int VEC, int SPL = kMaxPerThread, typename F>
@@ -97,7 +117,126 @@ __device__ __forceinline__ float row_sum(float v, int tpr) {
   return v;
 }
 
-template <typename TS, int VEC>
+template <typename T>
+__device__ __forceinline__ void load4_nt(const void* base, int64_t i, float (&v)[4]) {
+  uint32_t w[kWordsOf<T, 4>];
+  load_words_nt(static_cast<const T*>(base) + i, w);
+  unpack_words<T, 4>(w, v);
+}
+
+template <typename T>
+__device__ __forceinline__ void store4_nt(void* base, int64_t i, const float (&v)[4]) {
+  uint32_t w[kWordsOf<T, 4>];
+  pack_words<T, 4>(v, w);
+  store_words_nt(static_cast<T*>(base) + i, w);
+}
+
+// Passes (of kThreads / tpr rows) per forward workgroup: a workgroup streams 2 x 4 KB of an
+// fp32 state.  One workgroup per whole (batch, head) (8 passes at d_state 128) streamed at
+// 5.4 TB/s; two passes with their state rows requested before any arithmetic and the state
+// read and written with the nontemporal hint, at 5.9 TB/s.
+constexpr int kFwdPasses = 2;
+
+// Sum over the tpr lanes of a row (tpr a power of two <= 64, uniform): an unrolled butterfly.
+__device__ __forceinline__ float row_sum_pow2(float v, int tpr) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1)
+    if (off < tpr) v += __shfl_xor(v, off);
+  return v;
+}
+
+// The forward when one 4-element vector per lane covers a row (tpr * 4 >= dstate).  Grid (row
+// blocks of kFwdPasses passes, nheads, batch), so the head and batch need no division; lane
+// arithmetic is shifts and masks of the power-of-two tpr; every array is addressed from a
+// wave-uniform 64-bit base with a 32-bit lane offset.  Every load is issued unconditionally,
+// from a clamped row and state (a lane past the row's states reads chunk 0, a pass past the
+// head's rows reads its first row) and masked at use, and the per-row scalars are read
+// without a dtype branch (load_any_raw): a load under a run-time condition makes the compiler
+// wait for each load before the next, and 64-bit index division cost several hundred
+// instructions per workgroup.  At c5 this runs at 5.9 TB/s against 5.4 TB/s for one
+// workgroup per (batch, head).
+template <typename TS, typename TB>
+__global__ void __launch_bounds__(kThreads) fwd_v4(Args a, int tpr_shift) {
+  const Geo& g = a.g;
+  const int h = static_cast<int>(blockIdx.y), b = static_cast<int>(blockIdx.z);
+  const int H = static_cast<int>(g.nheads), P = static_cast<int>(g.headdim), N = static_cast<int>(g.dstate);
+  const int gg = g.ngroups == 1 ? 0 : h / (H / static_cast<int>(g.ngroups));
+  const int tpr = 1 << tpr_shift;
+  const int j = static_cast<int>(threadIdx.x) & (tpr - 1);
+  const int rows_per_pass = kThreads >> tpr_shift;
+  const int prow0 = static_cast<int>(blockIdx.x) * kFwdPasses * rows_per_pass;  // the block's first row
+  const int slot = static_cast<int>(threadIdx.x) >> tpr_shift;
+  const int64_t head_row0 = (static_cast<int64_t>(b) * H + h) * P;  // the head's first row
+  const bool nok = 4 * j < N;
+  const int n0 = nok ? 4 * j : 0;
+  const TB* Bb = static_cast<const TB*>(a.B) + (static_cast<int64_t>(b) * g.ngroups + gg) * N;
+  const TB* Cb = static_cast<const TB*>(a.C) + (static_cast<int64_t>(b) * g.ngroups + gg) * N;
+  const TS* sb = static_cast<const TS*>(a.state) + (head_row0 + prow0) * N;
+  TS* nb = static_cast<TS*>(a.new_state) + (head_row0 + prow0) * N;
+  float bv[4], cv[4];
+  load4<TB>(Bb, n0, bv);
+  load4<TB>(Cb, n0, cv);
+  int prel[kFwdPasses];  // the pass's row within the block, clamped to a row of the head
+  float sv[kFwdPasses][4];
+#pragma unroll
+  for (int q = 0; q < kFwdPasses; ++q) {
+    const int r = q * rows_per_pass + slot;
+    prel[q] = prow0 + r < P ? r : -prow0;
+    load4_nt<TS>(sb, static_cast<uint32_t>(prel[q] * N + n0), sv[q]);
+  }
+  // the per-row scalars: every raw load issued before any of them is converted
+  // (D as well: loaded in the epilogue it would wait for the previous pass's stores too, which
+  // the vector memory counter also counts)
+  const void* zsrc = a.z ? a.z : a.x;
+  const float* dsrc = a.D ? a.D : a.A;
+  RawAny rdt[kFwdPasses], rx[kFwdPasses], rz[kFwdPasses];
+  float dv[kFwdPasses];
+#pragma unroll
+  for (int q = 0; q < kFwdPasses; ++q) {
+    const int64_t row = head_row0 + prow0 + prel[q];
+    rdt[q] = load_any_raw(a.dt, g.dt_dtype, g.dt_per_row ? row : static_cast<int64_t>(b) * H + h);
+    rx[q] = load_any_raw(a.x, g.x_dtype, row);
+    rz[q] = load_any_raw(zsrc, g.x_dtype, row);
+    dv[q] = dsrc[a.D && g.d_per_row ? h * P + prow0 + prel[q] : h];
+  }
+  const float Ah = a.A[h];
+  const float bias = a.dt_bias ? a.dt_bias[h] : 0.0f;
+  float decay[kFwdPasses], dx[kFwdPasses], xv[kFwdPasses], zv[kFwdPasses];
+#pragma unroll
+  for (int q = 0; q < kFwdPasses; ++q) {
+    float del = raw_any_f32(rdt[q], g.dt_dtype) + bias;
+    if (g.softplus) del = softplus(del);
+    decay[q] = expf(Ah * del);
+    xv[q] = raw_any_f32(rx[q], g.x_dtype);
+    dx[q] = del * xv[q];
+    zv[q] = raw_any_f32(rz[q], g.x_dtype);
+  }
+#pragma unroll
+  for (int q = 0; q < kFwdPasses; ++q) {
+    const int r = q * rows_per_pass + slot;
+    const bool pok = prow0 + r < P;
+    float nv[4];
+    float acc = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      nv[e] = fmaf(decay[q], sv[q][e], dx[q] * bv[e]);
+      acc = fmaf(nv[e], cv[e], acc);
+    }
+    if (pok && nok) store4_nt<TS>(nb, static_cast<uint32_t>(r * N + n0), nv);
+    acc = row_sum_pow2(nok ? acc : 0.0f, tpr);
+    if (pok && j == 0) {
+      const int p = prow0 + r;
+      float out = acc;
+      if (a.D) out = fmaf(dv[q], xv[q], out);
+      if (a.z) out *= zv[q] * sigmoid(zv[q]);
+      static_cast<TS*>(a.y)[head_row0 + p] = from_f32<TS>(out);
+    }
+  }
+}
+
+// Grid (batch * nheads, row blocks of kFwdPasses passes).  SPL: states per lane (tpr * SPL
+// >= dstate); 4 when one 4-element vector per lane covers a row.
+template <typename TS, int VEC, int SPL>
 __global__ void __launch_bounds__(kThreads) fwd(Args a) {
   const Geo& g = a.g;
   const int64_t bh = blockIdx.x;
@@ -107,9 +246,49 @@ __global__ void __launch_bounds__(kThreads) fwd(Args a) {
   const int tpr = g.tpr;
   const int j = threadIdx.x % tpr;
   const int rows_per_pass = kThreads / tpr;
+  const int pfirst = static_cast<int>(blockIdx.y) * kFwdPasses * rows_per_pass + static_cast<int>(threadIdx.x) / tpr;
   const float Ah = a.A[h];
   const float bias = a.dt_bias ? a.dt_bias[h] : 0.0f;
-  for (int p = threadIdx.x / tpr; p < g.headdim; p += rows_per_pass) {
+  // this lane's B and C: the same for every row of the head
+  float bvs[SPL], cvs[SPL];
+  for_row_chunks<VEC, SPL>(N, tpr, j, [&](int k, int n0) {
+    if constexpr (VEC == 4) {
+      float b4[4], c4[4];
+      if (g.bc_dtype == MKO_F32) { load4<float>(a.B, bg * N + n0, b4); load4<float>(a.C, bg * N + n0, c4); }
+      else if (g.bc_dtype == MKO_BF16) { load4<bf16>(a.B, bg * N + n0, b4); load4<bf16>(a.C, bg * N + n0, c4); }
+      else { load4<_Float16>(a.B, bg * N + n0, b4); load4<_Float16>(a.C, bg * N + n0, c4); }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        bvs[k * 4 + e] = b4[e];
+        cvs[k * 4 + e] = c4[e];
+      }
+    } else {
+      bvs[k] = ld_any(a.B, g.bc_dtype, bg * N + n0);
+      cvs[k] = ld_any(a.C, g.bc_dtype, bg * N + n0);
+    }
+  });
+  // the state rows of every pass, requested before any arithmetic
+  float sv[kFwdPasses][SPL];
+#pragma unroll
+  for (int q = 0; q < kFwdPasses; ++q) {
+    const int p = pfirst + q * rows_per_pass;
+    if (p >= g.headdim) continue;
+    const int64_t row = bh * g.headdim + p;
+    for_row_chunks<VEC, SPL>(N, tpr, j, [&](int k, int n0) {
+      if constexpr (VEC == 4) {
+        float s4[4];
+        load4_nt<TS>(a.state, row * N + n0, s4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sv[q][k * 4 + e] = s4[e];
+      } else {
+        sv[q][k] = ld<TS>(a.state, row * N + n0);
+      }
+    });
+  }
+#pragma unroll
+  for (int q = 0; q < kFwdPasses; ++q) {
+    const int p = pfirst + q * rows_per_pass;
+    if (p >= g.headdim) continue;  // uniform over the row's tpr lanes (a row is whole in a wavefront)
     const int64_t row = bh * g.headdim + p;
     float del = ld_any(a.dt, g.dt_dtype, g.dt_per_row ? row : bh) + bias;
     if (g.softplus) del = softplus(del);
@@ -117,24 +296,19 @@ __global__ void __launch_bounds__(kThreads) fwd(Args a) {
     const float xv = ld_any(a.x, g.x_dtype, row);
     const float dx = del * xv;
     float acc = 0.0f;
-    for_row_chunks<VEC>(N, tpr, j, [&](int, int n0) {
+    for_row_chunks<VEC, SPL>(N, tpr, j, [&](int k, int n0) {
       if constexpr (VEC == 4) {
-        float s[4], bv[4], cv[4], nv[4];
-        load4<TS>(a.state, row * N + n0, s);
-        if (g.bc_dtype == MKO_F32) { load4<float>(a.B, bg * N + n0, bv); load4<float>(a.C, bg * N + n0, cv); }
-        else if (g.bc_dtype == MKO_BF16) { load4<bf16>(a.B, bg * N + n0, bv); load4<bf16>(a.C, bg * N + n0, cv); }
-        else { load4<_Float16>(a.B, bg * N + n0, bv); load4<_Float16>(a.C, bg * N + n0, cv); }
+        float nv[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          nv[e] = fmaf(decay, s[e], dx * bv[e]);
-          acc = fmaf(nv[e], cv[e], acc);
+          nv[e] = fmaf(decay, sv[q][k * 4 + e], dx * bvs[k * 4 + e]);
+          acc = fmaf(nv[e], cvs[k * 4 + e], acc);
         }
-        store4<TS>(a.new_state, row * N + n0, nv);
+        store4_nt<TS>(a.new_state, row * N + n0, nv);
       } else {
-        const float s = ld<TS>(a.state, row * N + n0);
-        const float nv = fmaf(decay, s, dx * ld_any(a.B, g.bc_dtype, bg * N + n0));
+        const float nv = fmaf(decay, sv[q][k], dx * bvs[k]);
         static_cast<TS*>(a.new_state)[row * N + n0] = from_f32<TS>(nv);
-        acc = fmaf(nv, ld_any(a.C, g.bc_dtype, bg * N + n0), acc);
+        acc = fmaf(nv, cvs[k], acc);
       }
     });
     acc = row_sum(acc, tpr);
@@ -158,14 +332,17 @@ __global__ void __launch_bounds__(kThreads) bwd(Args a) {
   __shared__ float red[kThreads * SPL];  // [rows_per_pass][tpr * SPL] fold buffer
   __shared__ float rowv[3][kThreads];  // per-row dA, dD, ddt terms of the current 256-row window
   const Geo& g = a.g;
-  const int64_t bh = blockIdx.x;
-  const int64_t b = bh / g.nheads, h = bh % g.nheads;
-  const int64_t bg = b * g.ngroups + h / (g.nheads / g.ngroups);
+  // 32-bit index arithmetic (the grid is batch * nheads < 2^31 workgroups; tpr is a power of two)
+  const uint32_t bh32 = blockIdx.x, H32 = static_cast<uint32_t>(g.nheads);
+  const int64_t bh = bh32;
+  const int64_t b = bh32 / H32, h = bh32 - static_cast<uint32_t>(b) * H32;
+  const int64_t bg = b * g.ngroups + (g.ngroups == 1 ? 0 : static_cast<uint32_t>(h) / (H32 / static_cast<uint32_t>(g.ngroups)));
   const int N = static_cast<int>(g.dstate);
   const int tpr = g.tpr;
-  const int j = threadIdx.x % tpr;
-  const int slot = threadIdx.x / tpr;
-  const int rows_per_pass = kThreads / tpr;
+  const int tpr_shift = __builtin_ctz(static_cast<unsigned>(tpr));
+  const int j = static_cast<int>(threadIdx.x) & (tpr - 1);
+  const int slot = static_cast<int>(threadIdx.x) >> tpr_shift;
+  const int rows_per_pass = kThreads >> tpr_shift;
   const float Ah = a.A[h];
   const float bias = a.dt_bias ? a.dt_bias[h] : 0.0f;
   float pb[SPL], pc[SPL];
@@ -199,6 +376,7 @@ __global__ void __launch_bounds__(kThreads) bwd(Args a) {
       cv[0] = ld_any(a.C, g.bc_dtype, bg * N + n0);
     }
   });
+  // The state and the new-state adjoint stream through once, read with the nontemporal hint.
   auto fetch = [&](int p, Row& r) {
     if (p >= g.headdim) return;
     const int64_t row = bh * g.headdim + p;
@@ -207,8 +385,8 @@ __global__ void __launch_bounds__(kThreads) bwd(Args a) {
       float* dn = r.dn + k * VEC;
       if constexpr (VEC == 4) {
         float s4[4], d4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        load4<TS>(a.state, row * N + n0, s4);
-        if (a.dnew) load4<float>(a.dnew, row * N + n0, d4);
+        load4_nt<TS>(a.state, row * N + n0, s4);
+        if (a.dnew) load4_nt<float>(a.dnew, row * N + n0, d4);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           s[e] = s4[e];
@@ -267,14 +445,14 @@ __global__ void __launch_bounds__(kThreads) bwd(Args a) {
           sy = fmaf(nv, cv[e], sy);
         }
         if constexpr (VEC == 4) {
-          *reinterpret_cast<float4*>(a.gstate + row * N + n0) = make_float4(gs[0], gs[1], gs[2], gs[3]);
+          store4_nt<float>(a.gstate, row * N + n0, gs);
         } else {
           a.gstate[row * N + n0] = gs[0];
         }
       });
-      sx = row_sum(sx, tpr);
-      sa = row_sum(sa, tpr);
-      sy = row_sum(sy, tpr);
+      sx = row_sum_pow2(sx, tpr);
+      sa = row_sum_pow2(sa, tpr);
+      sy = row_sum_pow2(sy, tpr);
       if (j == 0) {
         a.dx[row] = fmaf(del, sx, dyp * dv);
         // delta enters through the drive (del x B) and the decay (exp(A del)).
@@ -464,6 +642,10 @@ static int make_geo(const mko_state_update_params* p, Geo* g) {
     mko_set_error("state_update: bad sizes");
     return MKO_EINVAL;
   }
+  if (g->headdim > 65535 * 8) {  // the forward's row blocks of at least 8 rows are a grid axis
+    mko_set_error("state_update: headdim=%lld > %d is not supported", (long long)g->headdim, 65535 * 8);
+    return MKO_EUNSUPPORTED;
+  }
   if (g->dstate > kMaxPerThread * 64) {
     mko_set_error("state_update: dstate=%lld > %d is not supported", (long long)g->dstate, kMaxPerThread * 64);
     return MKO_EUNSUPPORTED;
@@ -507,11 +689,35 @@ using namespace mko::su;
 
 namespace {
 
+// Lanes per row for one 4-element vector per lane, when a row needs at most 64 lanes.
+static int tpr_one_vector(const Geo& g) {
+  int tpr = 1;
+  while (tpr < 64 && tpr * 4 < g.dstate) tpr <<= 1;
+  return tpr * 4 >= g.dstate ? tpr : 0;
+}
+
 template <typename TS>
-void launch_fwd_t(const Args& a, int vec, hipStream_t s, unsigned grid) {
+void launch_fwd_t(const Args& a, int vec, hipStream_t s, unsigned bh) {
+  const int tpr4 = tpr_one_vector(a.g);
+  Args f = a;
+  // fwd_v4's grid has the heads and the batch as its y and z axes
+  const bool v4 = vec == 4 && tpr4 && a.g.nheads <= 65535 && a.g.batch <= 65535;
+  if (v4) f.g.tpr = tpr4;
+  const int64_t rows_per_wg = static_cast<int64_t>(kFwdPasses) * (kThreads / f.g.tpr);
+  const unsigned nrb = static_cast<unsigned>((a.g.headdim + rows_per_wg - 1) / rows_per_wg);
+  if (v4) {
+    const dim3 grid(nrb, static_cast<unsigned>(a.g.nheads), static_cast<unsigned>(a.g.batch));
+    const int shift = __builtin_ctz(static_cast<unsigned>(tpr4));
+    MKO_TIMED("state_update_fwd", s,
+              if (a.g.bc_dtype == MKO_F32) fwd_v4<TS, float><<<grid, kThreads, 0, s>>>(f, shift);
+              else if (a.g.bc_dtype == MKO_BF16) fwd_v4<TS, bf16><<<grid, kThreads, 0, s>>>(f, shift);
+              else fwd_v4<TS, _Float16><<<grid, kThreads, 0, s>>>(f, shift));
+    return;
+  }
+  const dim3 grid(bh, nrb);
   MKO_TIMED("state_update_fwd", s,
-            if (vec == 4) fwd<TS, 4><<<grid, kThreads, 0, s>>>(a);
-            else fwd<TS, 1><<<grid, kThreads, 0, s>>>(a));
+            if (vec == 4) fwd<TS, 4, kMaxPerThread><<<grid, kThreads, 0, s>>>(f);
+            else fwd<TS, 1, kMaxPerThread><<<grid, kThreads, 0, s>>>(f));
 }
 
 // Lanes per row for two 4-element vectors per lane, when a row needs at most 64 lanes.

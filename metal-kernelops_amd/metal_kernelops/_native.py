@@ -151,6 +151,7 @@ _SIGNATURES = {
     "mko_selscan_fwd": ([ctypes.POINTER(SelscanParams), _vp], ctypes.c_int),
     "mko_selscan_bwd_workspace_size": ([ctypes.POINTER(SelscanParams)], ctypes.c_size_t),
     "mko_selscan_bwd": ([ctypes.POINTER(SelscanParams), _vp], ctypes.c_int),
+    "mko_stream_copy": ([_vp, _vp, ctypes.c_size_t, ctypes.c_uint32, _vp], ctypes.c_int),
     "mko_selscan_plan": ([ctypes.POINTER(SelscanParams), ctypes.POINTER(ctypes.c_int),
                           ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
     "mko_state_update_fwd": ([ctypes.POINTER(StateUpdateParams), _vp], ctypes.c_int),
@@ -225,6 +226,20 @@ def kernel_times():
         if handle.mko_profile_entry(i, name, 128, ctypes.byref(total), ctypes.byref(count)) == 0:
             out[name.value.decode()] = (total.value, count.value)
     return out
+
+
+STREAM_NONTEMPORAL = 1
+"""MKO_STREAM_NONTEMPORAL."""
+
+
+def stream_copy(src, dst, nontemporal=True):
+    """Copies ``src`` into ``dst`` (same byte count, 16-byte aligned) with the library's
+    streaming copy kernel on the current stream."""
+    nbytes = src.numel() * src.element_size()
+    if dst.numel() * dst.element_size() != nbytes:
+        raise ValueError("stream_copy: src and dst differ in size")
+    check(lib().mko_stream_copy(src.data_ptr(), dst.data_ptr(), nbytes, STREAM_NONTEMPORAL if nontemporal else 0,
+                                stream_of(src.device)), "mko_stream_copy")
 
 
 def exported_symbols():
