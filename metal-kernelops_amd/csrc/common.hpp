@@ -130,6 +130,24 @@ __device__ __forceinline__ void store_words_nt(void* p, const uint32_t (&w)[W]) 
   }
 }
 
+// One element (2 or 4 bytes) with the nontemporal hint.
+template <typename T>
+__device__ __forceinline__ T load_nt(const T* p) {
+  static_assert(sizeof(T) == 2 || sizeof(T) == 4, "16- or 32-bit elements");
+  if constexpr (sizeof(T) == 2)
+    return __builtin_bit_cast(T, __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(p)));
+  else
+    return __builtin_bit_cast(T, __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p)));
+}
+template <typename T>
+__device__ __forceinline__ void store_nt(T* p, T v) {
+  static_assert(sizeof(T) == 2 || sizeof(T) == 4, "16- or 32-bit elements");
+  if constexpr (sizeof(T) == 2)
+    __builtin_nontemporal_store(__builtin_bit_cast(uint16_t, v), reinterpret_cast<uint16_t*>(p));
+  else
+    __builtin_nontemporal_store(__builtin_bit_cast(uint32_t, v), reinterpret_cast<uint32_t*>(p));
+}
+
 // p advanced by off bytes.  With a wave-uniform p the access compiles to the scalar-base
 // form of the global loads and stores (64-bit base in SGPRs, one 32-bit offset VGPR per
 // lane) instead of a 64-bit address pair per lane.

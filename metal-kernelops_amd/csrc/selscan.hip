@@ -1042,7 +1042,13 @@ bwd_lane(Geo g, Ptrs p, int cpb) {
         sb += lds[w][o];
         sc += lds[w][HS * HS + o];
       }
-      (pbc + t0 * HS)[o] = make_float2(sb, sc);
+      {
+        // whole 2 KB runs that only reduce_bc reads back: written with the nontemporal hint
+        // (the per-lane element streams above keep plain accesses: a wavefront covers half a
+        // line of each per block, and the next block uses the other half)
+        const mko_u32x2 w = {__float_as_uint(sb), __float_as_uint(sc)};
+        __builtin_nontemporal_store(w, reinterpret_cast<mko_u32x2*>(pbc + t0 * HS) + o);
+      }
       __syncthreads();
     } else if (active) {
       float* pf = reinterpret_cast<float*>(pbc + t0 * HS) + which;
