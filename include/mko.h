@@ -12,8 +12,9 @@
  * behind mko_state_update_bwd_static, comes with the code object).  Inputs are
  * never written.
  * All tensors are dense row-major (contiguous) in the layouts documented per
- * field.  dtype fields take MKO_F32 / MKO_F16 / MKO_BF16; every kernel computes
- * in float32 and rounds once when it stores a 16-bit output.
+ * field.  dtype fields take MKO_F32 / MKO_F16 / MKO_BF16 (and MKO_F64 for the SSD); every
+ * kernel computes in float32 (float64 for float64 SSD inputs) and rounds once when it stores a
+ * 16-bit output.
  *
  * The reference (dbydd/metal-kernelops) has no native ABI: its Python launches
  * Metal kernels through torch.mps.compile_shader.  Each entry point below names
@@ -31,7 +32,9 @@ extern "C" {
 
 #define MKO_ABI_VERSION 1
 
-enum mko_dtype { MKO_F32 = 0, MKO_F16 = 1, MKO_BF16 = 2 };
+/* MKO_F64 is taken by the SSD entry points only (mko_ssd_*), where every floating-point
+ * array of the parameter block is then float64; the other entry points refuse it. */
+enum mko_dtype { MKO_F32 = 0, MKO_F16 = 1, MKO_BF16 = 2, MKO_F64 = 3 };
 
 enum mko_status {
   MKO_OK = 0,
@@ -264,7 +267,11 @@ size_t mko_ssd_saved_bytes(const mko_ssd_params* p);
  * (cv/mamba2_chunk.py:447-533, 568-614, 617-678): y and the final state of the SSD
  * recurrence, computed in chunks with the intra-chunk, chunk-state and
  * state-to-output contractions on the matrix cores.  The result does not depend
- * on the caller's chunk_size; the kernels pick their own chunk (64 to 256). */
+ * on the caller's chunk_size; the kernels pick their own chunk (64 to 256).
+ * float64 (x_dtype MKO_F64, which the reference's composition takes,
+ * cv/mamba2_chunk.py:439-440): x, dt, B, C, z, initial_states and the outputs are float64
+ * and so are A, D and dt_bias (and dA, dD, ddt_bias in the backward) despite the float*
+ * field types; the per-token recurrence runs on the fp64 vector units, d_state <= 256. */
 size_t mko_ssd_fwd_workspace_size(const mko_ssd_params* p);
 int mko_ssd_fwd(const mko_ssd_params* p, void* stream);
 

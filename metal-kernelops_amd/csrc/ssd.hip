@@ -15,6 +15,7 @@
 // rounded to the input dtype (bf16/f16 products on the bf16/f16 matrix cores,
 // fp32 inputs on the fp32 ones); accumulation, decays and states are fp32.
 #include "ssd.hpp"
+#include "ssd64.hpp"
 
 namespace mko {
 namespace ssd {
@@ -628,18 +629,21 @@ using namespace mko;
 using namespace mko::ssd;
 
 extern "C" size_t mko_ssd_saved_bytes(const mko_ssd_params* prm) {
+  if (prm && prm->x_dtype == MKO_F64) return ssd64_saved_bytes(prm);
   Geo g;
   if (make_geo(prm, &g) != MKO_OK) return 0;
   return saved_layout(g).total;
 }
 
 extern "C" size_t mko_ssd_fwd_workspace_size(const mko_ssd_params* prm) {
+  if (prm && prm->x_dtype == MKO_F64) return 0;
   Geo g;
   if (make_geo(prm, &g) != MKO_OK) return 0;
   return 0;
 }
 
 extern "C" int mko_ssd_fwd(const mko_ssd_params* prm, void* stream) {
+  if (prm && prm->x_dtype == MKO_F64) return ssd64_fwd(prm, static_cast<hipStream_t>(stream));
   Geo g;
   int st = make_geo(prm, &g);
   if (st != MKO_OK) return st;

@@ -25,6 +25,7 @@
 #include <algorithm>
 
 #include "ssd.hpp"
+#include "ssd64.hpp"
 
 namespace mko {
 namespace ssd {
@@ -1456,12 +1457,14 @@ using namespace mko;
 using namespace mko::ssd;
 
 extern "C" size_t mko_ssd_bwd_workspace_size(const mko_ssd_params* prm) {
+  if (prm && prm->x_dtype == MKO_F64) return ssd64_bwd_workspace_size(prm);
   Geo g;
   if (make_geo(prm, &g) != MKO_OK) return 0;
   return bwd_layout(g, make_plan(g), prm->z != nullptr).total;
 }
 
 extern "C" int mko_ssd_bwd(const mko_ssd_params* prm, void* stream) {
+  if (prm && prm->x_dtype == MKO_F64) return ssd64_bwd(prm, static_cast<hipStream_t>(stream));
   Geo g;
   int st = make_geo(prm, &g);
   if (st != MKO_OK) return st;

@@ -17,8 +17,8 @@ import torch
 
 ABI_VERSION = 1
 
-F32, F16, BF16 = 0, 1, 2
-_DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
+F32, F16, BF16, F64 = 0, 1, 2, 3  # MKO_F64: the SSD entry points only
+_DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16, torch.float64: F64}
 
 _LIB_PATH = os.environ.get(
     "MKO_LIBRARY", os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libmko.so"))

@@ -20,7 +20,9 @@ Kernels (``libmko.so``): the block factorisation of the SSD paper with the
 intra-chunk product, the chunk states and the state-to-output product on the
 matrix cores (bf16/f16 operands for bf16/f16 inputs, fp32 operands for fp32
 inputs; fp32 accumulation, decays and states), and an O(nchunks) sequential
-state pass instead of the reference's O(nchunks^2) transfer matrix.  The chunk
+state pass instead of the reference's O(nchunks^2) transfer matrix.  float64
+inputs, which the reference's composition also takes, run the per-token
+recurrence in float64 on the vector units (d_state <= 256).  The chunk
 length is the kernels' own choice: ``chunk_size`` is accepted for signature
 parity and, as in the reference, does not change the result.  The backward is a
 hand-written set of kernels (the reference differentiates its torch
@@ -41,6 +43,7 @@ from .._contract import Rules
 __all__ = ["mamba2_chunk_scan", "mamba2_chunk_scan_reference", "last_path"]
 
 _FLOATS = (torch.float32, torch.float16, torch.bfloat16)
+_X_FLOATS = _FLOATS + (torch.float64,)
 _SOFTPLUS, _D_PER_ROW, _SAVE_Y = 1, 2, 4
 
 _path = "none"
@@ -71,9 +74,8 @@ def _initial_layout(rules, states, batch, nheads, headdim, dstate):
 def _check(x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size):
     """The reference's argument rules (``cv/mamba2_chunk.py:398-444``), in its order.
 
-    Returns the sizes and ``initial_states`` in the kernels' layout.  float64 ``x``, which
-    the reference's torch composition takes, is refused here: the kernels compute in
-    float32 with float32 or 16-bit operands."""
+    Returns the sizes and ``initial_states`` in the kernels' layout.  ``x`` may be float32,
+    float16, bfloat16 or float64, as in the reference."""
     rules = Rules("mamba2_chunk_scan")
     rules.require(chunk_size >= 1, f"chunk_size must be at least 1 (got {chunk_size})")
     rules.dims("x", x, 4, "(batch, length, nheads, headdim)")
@@ -93,9 +95,9 @@ def _check(x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size):
     rules.shape("dt_bias", dt_bias, (nheads,))
     if initial_states is not None:
         initial_states = _initial_layout(rules, initial_states, batch, nheads, headdim, dstate)
-    rules.dtype_in(_FLOATS, x=x)
+    rules.dtype_in(_X_FLOATS, x=x)
     rules.same_device(x.device, dt=dt, A=A, B=B, C=C)
-    rules.dtype_in(_FLOATS, dt=dt, B=B, C=C, z=z, D=D, dt_bias=dt_bias, initial_states=initial_states, A=A)
+    rules.dtype_in(_X_FLOATS, dt=dt, B=B, C=C, z=z, D=D, dt_bias=dt_bias, initial_states=initial_states, A=A)
     return batch, length, nheads, headdim, ngroups, dstate, initial_states
 
 
@@ -139,7 +141,8 @@ def _ssd_bwd(dy: Tensor, dfinal: Optional[Tensor], x: Tensor, dt: Tensor, A: Ten
              C: Tensor, D: Optional[Tensor], z: Optional[Tensor], dt_bias: Optional[Tensor],
              initial_states: Optional[Tensor], softplus: bool, save_y: bool, saved: Tensor
              ) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
-    f32 = dict(dtype=torch.float32, device=x.device)
+    # the parameters' gradients in the arithmetic's precision: float64 for float64 inputs
+    f32 = dict(dtype=torch.float64 if x.dtype == torch.float64 else torch.float32, device=x.device)
     dx, ddt = torch.empty_like(x), torch.empty_like(dt)
     dA = torch.empty(A.shape, **f32)
     dB, dC = torch.empty_like(B), torch.empty_like(C)
@@ -164,7 +167,7 @@ def _ssd_bwd(dy: Tensor, dfinal: Optional[Tensor], x: Tensor, dt: Tensor, A: Ten
 @_ssd_bwd.register_fake
 def _(dy, dfinal, x, dt, A, B, C, D, z, dt_bias, initial_states, softplus, save_y, saved):
     def f(shape):
-        return x.new_empty(shape, dtype=torch.float32)
+        return x.new_empty(shape, dtype=torch.float64 if x.dtype == torch.float64 else torch.float32)
     return (torch.empty_like(x), torch.empty_like(dt), f(A.shape), torch.empty_like(B),
             torch.empty_like(C), f(D.shape if D is not None else (0,)),
             torch.empty_like(z) if z is not None else x.new_empty(0),
@@ -194,8 +197,8 @@ def _backward(ctx, dy, dfinal, _dsaved):
 torch.library.register_autograd("mko::ssd_fwd", _backward, setup_context=_setup)
 
 
-def _f32(t):
-    return None if t is None else (t if t.dtype == torch.float32 else t.float()).contiguous()
+def _as(t, dtype):
+    return None if t is None else (t if t.dtype == dtype else t.to(dtype)).contiguous()
 
 
 def mamba2_chunk_scan(x, dt, A, B, C, chunk_size=64, D=None, z=None, dt_bias=None,
@@ -210,8 +213,8 @@ def mamba2_chunk_scan(x, dt, A, B, C, chunk_size=64, D=None, z=None, dt_bias=Non
     argument                  shape                           meaning
     ========================  ==============================  ==============================
     ``x``                     (b, L, H, P)                    input; its dtype (float32,
-                                                              float16, bfloat16) is the
-                                                              operand and output dtype
+                                                              float16, bfloat16, float64) is
+                                                              the operand and output dtype
     ``dt``                    (b, L, H)                       step sizes before the optional
                                                               bias and softplus
     ``A``                     (H,)                            per-head log decay (negative)
@@ -235,15 +238,19 @@ def mamba2_chunk_scan(x, dt, A, B, C, chunk_size=64, D=None, z=None, dt_bias=Non
                          f"got {x.device}")
     batch, length, nheads, headdim, ngroups, dstate, initial_states = _check(
         x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size)
-    x, dt = x.contiguous(), dt.contiguous()
+    x = x.contiguous()
     # B and C take x's dtype: every contraction runs with x.dtype operands (as the
-    # reference's composition does); autograd casts their gradients back.
+    # reference's composition does); autograd casts their gradients back.  The step sizes
+    # and the per-head parameters are float32, or float64 for float64 x (the reference
+    # computes in float64 then, cv/mamba2_chunk.py:447-462).
+    acc = torch.float64 if x.dtype == torch.float64 else torch.float32
+    dt = dt.contiguous() if acc == torch.float32 else _as(dt, acc)
     B, C = B.to(x.dtype).contiguous(), C.to(x.dtype).contiguous()
     if z is not None:
         z = (z if z.dtype == x.dtype else z.to(x.dtype)).contiguous()
     if initial_states is not None:
         initial_states = initial_states.to(x.dtype).contiguous()
-    A, D, dt_bias = _f32(A), _f32(D), _f32(dt_bias)
+    A, D, dt_bias = _as(A, acc), _as(D, acc), _as(dt_bias, acc)
     _path = "hip"
     # The forward keeps its chunk output for the backward only when a gradient will be taken.
     save_y = torch.is_grad_enabled() and any(

@@ -303,3 +303,106 @@ def test_config4_backward_prefix():
             gk = gk[:1, :cut]
         err = record("c4 bwd prefix 384", "d" + k, norm_rel(gk, v.grad), 2e-2)
         assert err <= 2e-2, f"d{k} {err:.3e}"
+
+
+def _composition_grads(inputs, dy, dfinal, softplus, dtype):
+    """float64 gradients of the oracle's chunked composition (pinned to the recurrence by
+    tests/test_oracle.py) on the inputs rounded to the kernel's activation dtype: the
+    recurrence's autograd would hold a state per token, too much at these head counts."""
+    leaves = _leaves({k: (v.to(dtype) if k in ACTS else v).double() for k, v in inputs.items()}, "cpu")
+    fn = lambda x, dt, A, B, C, **kw: oracle.mamba2_chunk_scan_composition(x, dt, A, B, C, 256, **kw)
+    return _run_grad(fn, leaves, dy, dfinal, softplus)
+
+
+# Many heads: at least 256 (batch, head, 64-wide d_head tile) pairs of 16-bit inputs with
+# 256-token chunks, two d_head tiles, a ragged state tile, grouped heads and a ragged tail.
+MANY_HEAD_SHAPES = [
+    (1, 1100, 128, 128, 2, 96),
+    (2, 1024, 128, 64, 1, 128),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
+@pytest.mark.parametrize("shape", MANY_HEAD_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_backward_many_heads(shape, dtype):
+    """Every option with the initial-state and final-state gradients at head counts past the
+    small matrix, against float64 autograd of the composition; bit-identical run to run."""
+    inputs, dy, dfinal = _inputs(shape, seed=sum(shape) + 5, d_row=shape[3] == 64)
+    got = _gpu_grads(inputs, dy, dfinal, True, dtype)
+    ref = _composition_grads(inputs, dy, dfinal, True, dtype)
+    _compare(got, ref, GRAD_TOL[dtype], f"many heads {shape} {dtype}")
+    again = _gpu_grads(inputs, dy, dfinal, True, dtype)
+    for k in got:
+        assert torch.equal(got[k], again[k]), k
+
+
+# ---------------------------------------------------------------- float64
+
+F64_TOL = 1e-10  # both sides compute in float64; the sums differ only in their order
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_float64_forward_and_backward(shape):
+    """float64 inputs, which the reference's composition takes (cv/mamba2_chunk.py:439-440):
+    every option, forward and every gradient against the float64 recurrence at 1e-10."""
+    inputs, dy, dfinal = _inputs(shape, seed=sum(shape) + 7, d_row=shape[3] % 2 == 0)
+    inputs = {k: v.double() for k, v in inputs.items()}
+    leaves = _leaves(inputs, DEV)
+    kw = {k: leaves[k] for k in leaves if k not in NAMES}
+    y, s = _api()(*(leaves[k] for k in NAMES), 64, **kw, dt_softplus=True)
+    assert y.dtype == torch.float64 and s.dtype == torch.float64
+    ref_leaves = _leaves(inputs, "cpu")
+    rkw = {k: ref_leaves[k] for k in ref_leaves if k not in NAMES}
+    yr, sr = oracle.mamba2_chunk_scan_recurrence(*(ref_leaves[k] for k in NAMES), **rkw, dt_softplus=True)
+    what = f"{shape} float64"
+    assert record(what, "y", max_rel(y, yr), F64_TOL) <= F64_TOL
+    assert record(what, "final_state", max_rel(s, sr), F64_TOL) <= F64_TOL
+    ((y * dy.to(DEV)).sum() + (s * dfinal.to(DEV)).sum()).backward()
+    ((yr * dy).sum() + (sr * dfinal).sum()).backward()
+    for k in leaves:
+        g, r = leaves[k].grad, ref_leaves[k].grad
+        assert g.dtype == torch.float64, k
+        err = record(what, "d" + k, norm_rel(g, r), F64_TOL)
+        assert err <= F64_TOL, f"{what}: d{k} {err:.3e}"
+
+
+def test_float64_ssd_minimal():
+    """The reference verifier's float64 case (benchmarks/verify_mamba2_chunk.py:214-233):
+    the scan against the literal ssd_minimal_discrete, chunk 4, with an initial state."""
+    import torch.nn.functional as F
+    batch, length, nheads, headdim, ngroups, dstate = 1, 16, 2, 3, 1, 4
+    g = lambda s: torch.Generator().manual_seed(s)
+    x = torch.randn(batch, length, nheads, headdim, generator=g(5), dtype=torch.float64)
+    dt = F.softplus(torch.randn(batch, length, nheads, generator=g(6), dtype=torch.float64) - 2)
+    A = -torch.exp(torch.rand(nheads, generator=g(7), dtype=torch.float64))
+    B = torch.randn(batch, length, ngroups, dstate, generator=g(8), dtype=torch.float64)
+    C = torch.randn(batch, length, ngroups, dstate, generator=g(9), dtype=torch.float64)
+    init = torch.randn(batch, nheads, headdim, dstate, generator=g(10), dtype=torch.float64) * 0.1
+    y_min, s_min = oracle.ssd_minimal_discrete(x * dt.unsqueeze(-1), A * dt, B, C, 4, init[:, None])
+    y, s = _api()(*(t.to(DEV) for t in (x, dt, A, B, C)), 4, initial_states=init.to(DEV))
+    assert record("ssd_minimal float64", "y", max_rel(y, y_min), F64_TOL) <= F64_TOL
+    assert record("ssd_minimal float64", "final_state", max_rel(s, s_min), F64_TOL) <= F64_TOL
+
+
+def test_float64_errors_and_empty():
+    """float64 x takes float64 step sizes and parameters (the wrapper converts them), refuses
+    d_state above 256, and an empty sequence returns the initial state."""
+    x, dt, A, B, C = (t.double().to(DEV) for t in _problem(1, 8, 2, 4, 1, 300))
+    with pytest.raises(RuntimeError, match="d_state"):
+        _api()(x, dt, A, B, C)
+    x, dt, A, B, C = (t.double().to(DEV) for t in _problem(2, 0, 2, 4, 1, 8))
+    init = torch.randn(2, 2, 4, 8, dtype=torch.float64, device=DEV)
+    y, s = _api()(x, dt.float(), A.float(), B, C, initial_states=init)
+    assert y.shape == x.shape and torch.equal(s, init)
+
+
+def test_double_backward_is_refused():
+    """The backward is hand-written: a second derivative through it raises RuntimeError
+    (the reference differentiates its composition, which allows it)."""
+    inputs, dy, dfinal = _inputs((1, 40, 2, 8, 1, 8), seed=3)
+    leaves = _leaves(inputs, DEV, torch.float32)
+    kw = {k: leaves[k] for k in leaves if k not in NAMES}
+    y, s = _api()(*(leaves[k] for k in NAMES), 64, **kw, dt_softplus=True)
+    (gx,) = torch.autograd.grad((y * dy.to(DEV).float()).sum(), leaves["x"], create_graph=True)
+    with pytest.raises(RuntimeError):
+        gx.sum().backward()
