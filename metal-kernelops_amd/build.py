@@ -4,8 +4,9 @@ Usage: ``python metal-kernelops_amd/build.py [--verbose]``.  Compiles every
 ``csrc/*.hip`` to an object in parallel with hipcc for gfx950, then links the
 shared library into ``metal_kernelops/_lib/libmko.so`` (in-tree, so it travels
 with the source tree to the GPU host).  Packed-FP32 instructions are disabled for
-all device code.  After linking, the DPP wait states of the Mamba-1 backward's inline
-assembly are checked on the built code object (``isa_check.py``); a problem fails the build.
+all device code.  After linking, the built code objects are checked (``isa_check.py``): the
+DPP wait states of the Mamba-1 backward's inline assembly, and that no kernel rounds a product
+to float16 in one step; a problem fails the build.
 """
 
 from __future__ import annotations
@@ -79,6 +80,10 @@ def build(verbose=False, jobs=None):
     n = isa_check.check_object(os.path.join(OBJDIR, "selscan.o"))
     if verbose:
         print(f"DPP wait states checked: {n} v_fmac_f32_dpp in selscan.o", flush=True)
+    # one rounding of float16 results in every kernel: the SSD backward's cancelling sums
+    # assume that all of its kernels round the same products alike
+    for obj in objs:
+        isa_check.check_f16_rounding(obj)
     return LIB
 
 

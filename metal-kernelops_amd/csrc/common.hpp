@@ -24,12 +24,24 @@ __device__ __forceinline__ float to_f32(bf16 v) {
   return __uint_as_float(static_cast<uint32_t>(v.bits) << 16);
 }
 
+// v as a finished fp32 value.  Every rounding to float16 in these kernels goes through it: it
+// is rounded to fp32 first, then to float16.  Without it the compiler folds a product of
+// a float16 and an fp32 value into one mixed-precision multiply-add (v_fma_mixlo_f16) that
+// rounds the exact product once, and does so in some kernels and not in others.  The two
+// roundings differ by one float16 unit where the fp32 product falls on a float16 tie, so the
+// SSD backward's row and column sums that must cancel (gy . y~ against u . du, from the same
+// rounded u, K and gy) would then not.
+__device__ __forceinline__ float fp32_value(float v) {
+  asm("" : "+v"(v));
+  return v;
+}
+
 template <typename T>
 __device__ __forceinline__ T from_f32(float v);
 template <>
 __device__ __forceinline__ float from_f32<float>(float v) { return v; }
 template <>
-__device__ __forceinline__ _Float16 from_f32<_Float16>(float v) { return static_cast<_Float16>(v); }
+__device__ __forceinline__ _Float16 from_f32<_Float16>(float v) { return static_cast<_Float16>(fp32_value(v)); }
 template <>
 __device__ __forceinline__ bf16 from_f32<bf16>(float v) {
   // Round to nearest even (v_cvt_pk_bf16_f32); NaN stays NaN.
@@ -189,7 +201,7 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
     return __builtin_bit_cast(uint32_t, t);
   } else {
     typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
-    const f16x2_t t = {static_cast<_Float16>(a), static_cast<_Float16>(b)};
+    const f16x2_t t = {static_cast<_Float16>(fp32_value(a)), static_cast<_Float16>(fp32_value(b))};
     return __builtin_bit_cast(uint32_t, t);
   }
 }

@@ -1,4 +1,5 @@
-"""Wait-state check of the inline-assembly DPP multiply-adds in the built Mamba-1 backward.
+"""Checks of the built device code: the wait states of the Mamba-1 backward's inline-assembly
+DPP multiply-adds, and the one rounding convention for float16 results.
 
 ``fmac_row`` in csrc/selscan.hip issues ``v_fmac_f32_dpp`` (a row broadcast as the DPP
 source) from inline assembly, because the compiler folds DPP into multiplies but not into
@@ -15,6 +16,13 @@ gfx9-family parts (the ones LLVM's hazard recognizer enforces for compiled DPP):
 produced (``_build/selscan.o``, whose device code is what ``libmko.so`` carries) with ROCm's
 ``llvm-objdump`` and checks every ``v_fmac_f32_dpp`` in it.  ``build.py`` runs it after
 compiling and fails the build on a problem; ``tests/test_isa_hazards.py`` checks the checker.
+
+``check_f16_rounding`` fails an object that holds a mixed-precision multiply-add with a
+float16 result (``v_fma_mixlo_f16`` / ``v_fma_mixhi_f16``, and the ``v_mad_mix`` forms).  Such an
+instruction rounds an exact product once to float16, where the kernels' convention (every
+float16 value is an fp32 value rounded to float16, ``from_f32`` and ``pack2`` in
+csrc/common.hpp) rounds twice; the SSD backward's cancelling row and column sums need every
+kernel to round the same products the same way.
 """
 
 from __future__ import annotations
@@ -150,8 +158,9 @@ def problems(lines):
     return checked, found
 
 
-def disassemble(obj):
-    """The gfx950 disassembly of the device code object embedded in ``obj``."""
+def disassemble(obj, required=True):
+    """The gfx950 disassembly of the device code object embedded in ``obj`` (no lines for an
+    object without one, unless ``required``)."""
     if not os.path.exists(OBJDUMP):
         raise RuntimeError(f"{OBJDUMP} not found: the DPP wait states of {obj} cannot be checked")
     with tempfile.TemporaryDirectory() as tmp:
@@ -160,6 +169,8 @@ def disassemble(obj):
         subprocess.run([OBJDUMP, "--offloading", local], check=True, capture_output=True, cwd=tmp)
         dev = [p for p in os.listdir(tmp) if "amdgcn" in p and "gfx950" in p]
         if not dev:
+            if not required:
+                return []
             raise RuntimeError(f"no gfx950 code object in {obj}")
         out = subprocess.run([OBJDUMP, "-d", "--mcpu=gfx950", os.path.join(tmp, dev[0])], check=True,
                              capture_output=True, text=True)
@@ -175,3 +186,28 @@ def check_object(obj):
     if found:
         raise RuntimeError(f"{len(found)} DPP hazard(s) in {obj}:\n" + "\n".join(found[:10]))
     return checked
+
+
+MIX16 = re.compile(r"\sv_(?:fma|mad)_mix(?:lo|hi)_f16\b")
+
+
+def f16_rounding_problems(lines):
+    """The functions of a disassembly that hold a mixed-precision multiply-add with a float16
+    result, with the count of such instructions in each."""
+    found, func = {}, None
+    for line in lines:
+        m = FUNC.match(line)
+        if m:
+            func = m.group(2)
+            continue
+        if MIX16.search(line):
+            found[func] = found.get(func, 0) + 1
+    return found
+
+
+def check_f16_rounding(obj):
+    """Raises RuntimeError when ``obj`` rounds a product to float16 in one step."""
+    found = f16_rounding_problems(disassemble(obj, required=False))
+    if found:
+        raise RuntimeError(f"float16 results of mixed-precision multiply-adds in {obj} (route the value "
+                           "through from_f32 / pack2): " + ", ".join(f"{k} ({v})" for k, v in list(found.items())[:5]))

@@ -1,9 +1,10 @@
-"""The wait-state check of the inline-assembly DPP multiply-adds in the Mamba-1 backward.
+"""The checks of the built device code: the wait states of the inline-assembly DPP
+multiply-adds in the Mamba-1 backward, and the single rounding convention for float16 results.
 
-`metal-kernelops_amd/isa_check.py` holds the check; `build()` runs it on the built
-selscan.o and fails the build on a problem.  Here the checker itself is tested on small
-listings (so that a regression of the checker cannot let a bad schedule through), and the
-built object is checked again when it is present.
+`metal-kernelops_amd/isa_check.py` holds the checks; `build()` runs them on the built objects
+and fails the build on a problem.  Here the checkers themselves are tested on small listings
+(so that a regression of a checker cannot let bad code through), and the built objects are
+checked again when they are present.
 """
 import os
 import sys
@@ -75,3 +76,28 @@ def test_dpp_fmac_inputs_are_settled_in_the_built_object():
             pytest.fail(f"{LIB} exists but {OBJ} is missing: rebuild with __graft_entry__.build()")
         pytest.skip("selscan.o not built here (run __graft_entry__.build() first)")
     assert isa_check.check_object(OBJ) > 0
+
+
+def test_f16_rounding_checker():
+    """A mixed-precision multiply-add with a float16 result (one rounding of the exact product)
+    is reported, with its function; one with an fp32 result, and fp32-to-float16 conversions,
+    are not."""
+    assert isa_check.f16_rounding_problems(_listing(["v_fma_mixlo_f16 v3, v1, v2, 0 op_sel_hi:[1,0,0]"])) == {"k": 1}
+    assert isa_check.f16_rounding_problems(_listing(["v_fma_mixhi_f16 v3, v1, v2, v4"])) == {"k": 1}
+    assert isa_check.f16_rounding_problems(_listing(["v_mad_mixlo_f16 v3, v1, v2, v4"])) == {"k": 1}
+    assert isa_check.f16_rounding_problems(_listing(["v_fma_mix_f32 v3, v1, v2, v4 op_sel_hi:[1,0,0]",
+                                                     "v_cvt_pk_f16_f32 v5, v6, v7", "v_cvt_f16_f32_e32 v8, v9"])) == {}
+
+
+@pytest.mark.parametrize("name", ["ssd.o", "ssd_bwd.o", "selscan.o", "state_update.o", "conv1d.o", "gated_norm.o"])
+def test_built_objects_round_float16_results_one_way(name):
+    """Every fp32-to-float16 rounding in the built kernels is a conversion of a finished fp32
+    value.  The SSD backward's dA / ddt_bias depend on it: the gate kernel's row sums gy . y~
+    and the du kernels' column sums u . du cancel only when both take u = step x rounded the
+    same way, and a fused single rounding in one of them left float16 dA errors of 1e-2."""
+    obj = os.path.join(PKG, "_build", name)
+    if not os.path.exists(obj):
+        if os.path.exists(LIB):
+            pytest.fail(f"{LIB} exists but {obj} does not: rebuild with build()")
+        pytest.skip("library not built")
+    isa_check.check_f16_rounding(obj)
