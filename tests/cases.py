@@ -71,6 +71,33 @@ def ssd_problem(batch, length, nheads, headdim, ngroups, dstate, seed=0, act=tor
                 dt_bias=dt_bias, initial_states=None if initial is None else initial.to(act))
 
 
+def ssd_matrix_inputs(shape, seed, options=("D", "z", "dt_bias", "initial_states"), d_row=False):
+    """The SSD option/shape matrix's inputs (the reference verifier's ``_problem`` draws,
+    benchmarks/verify_mamba2_chunk.py:113-147): x, dt, A = -exp(U), B, C ~ N(0, 1); D, z,
+    dt_bias (x0.1) and initial states (x0.1) from a second generator; the upstream gradients
+    dy and d final_state (float64) from a third."""
+    batch, length, nheads, headdim, ngroups, dstate = shape
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(batch, length, nheads, headdim, generator=g)
+    dt = torch.randn(batch, length, nheads, generator=g)
+    A = -torch.exp(torch.rand(nheads, generator=g))
+    B = torch.randn(batch, length, ngroups, dstate, generator=g)
+    C = torch.randn(batch, length, ngroups, dstate, generator=g)
+    inputs = dict(x=x, dt=dt, A=A, B=B, C=C)
+    g = torch.Generator().manual_seed(seed + 10)
+    opt = dict(D=torch.randn(nheads, generator=g),
+               z=torch.randn(batch, length, nheads, headdim, generator=g),
+               dt_bias=torch.randn(nheads, generator=g) * 0.1,
+               initial_states=torch.randn(batch, nheads, headdim, dstate, generator=g) * 0.1)
+    if d_row:
+        opt["D"] = torch.randn(nheads, headdim, generator=torch.Generator().manual_seed(seed + 20))
+    inputs.update({k: opt[k] for k in options})
+    g = torch.Generator().manual_seed(seed + 30)
+    dy = torch.randn(batch, length, nheads, headdim, generator=g, dtype=torch.float64)
+    dfinal = torch.randn(batch, nheads, headdim, dstate, generator=g, dtype=torch.float64)
+    return inputs, dy, dfinal
+
+
 def decode_problem(batch, nheads, headdim, dstate, ngroups, seed=0, act=torch.bfloat16,
                    state_dtype=torch.float32, dt_per_row=False):
     """Config 5 draws: state=0.1*N(0,1), x, dt, dt_bias, A=-U(1,16), B, C, D=ones, z."""

@@ -7,13 +7,15 @@ Tolerances (reference and north star): fp32 1e-5, fp16 2e-3, bf16 2e-2 max
 relative error; gradient norms 1e-4 (fp32).
 """
 
+import json
+import math
 import numpy as np
 import os
 import pytest
 import torch
 
 import oracle
-from cases import max_rel, norm_rel, record, ssd_problem
+from cases import max_rel, norm_rel, record, ssd_matrix_inputs, ssd_problem
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -172,17 +174,7 @@ def _gpu_grads(inputs, dy, dfinal, softplus, dtype):
 
 
 def _inputs(shape, seed, options=("D", "z", "dt_bias", "initial_states"), d_row=False):
-    batch, length, nheads, headdim, ngroups, dstate = shape
-    x, dt, A, B, C = _problem(*shape, seed=seed)
-    inputs = dict(x=x, dt=dt, A=A, B=B, C=C)
-    opt = _options(batch, length, nheads, headdim, dstate, seed=seed + 10)
-    if d_row:
-        opt["D"] = torch.randn(nheads, headdim, generator=torch.Generator().manual_seed(seed + 20))
-    inputs.update({k: opt[k] for k in options})
-    g = torch.Generator().manual_seed(seed + 30)
-    dy = torch.randn(batch, length, nheads, headdim, generator=g, dtype=torch.float64)
-    dfinal = torch.randn(batch, nheads, headdim, dstate, generator=g, dtype=torch.float64)
-    return inputs, dy, dfinal
+    return ssd_matrix_inputs(shape, seed, options, d_row)
 
 
 def _compare(got, ref, tol, what):
@@ -198,13 +190,58 @@ def _compare(got, ref, tol, what):
         assert err <= tol, f"{what}: d{k} norm-relative error {err:.3e} > {tol}"
 
 
+# The 16-bit gradient bars come from the reference's own arithmetic: the norm-relative error of
+# its bf16 / fp16 torch composition's autograd (oracle.mamba2_chunk_scan_composition) against
+# float64 on the same rounded inputs, measured by tests/golden/make_ssd_half_bars.py.  Each
+# gradient of a 16-bit case is held to 1.5x that error.  On the matrix's small cases a
+# gradient has few elements (dA one per head, ddt 72 on 2x9x4), so one case's error is a noisy
+# sample (the composition's bf16 dA spans 0.8e-3 to 6e-3 over the rows): there the bar is 1.5x
+# the larger of the case's error and the root-mean-square error of that gradient over the
+# matrix's rows of the dtype.  The config-4 cases are held to their own error, except dA: the
+# kernels round u = step x, C.B^T and K = C.B^T e^{cs_l - cs_s} to the input dtype for the
+# matrix cores, where the composition keeps its decays and C.B^T products in fp32 and folds
+# the step into one rounded score, and with 64 heads that shows in dA.  The fixture holds the
+# dA error those rounding points imply (make_ssd_half_bars.kernel_rounding_dA, a float64
+# restatement of where the kernels round, which the GPU's own per-token sums match): 3.9e-3
+# on the causal prefix and 8.1e-3 on batch 0, against the composition's 1.9e-3 and 2.3e-3.
+# The config-4 dA is held to 1.1x that, so it must do exactly what its rounding design says.
+C4_DA_FACTOR = 1.1
+HALF_BARS = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "ssd_half_composition_errors.json")))["cases"]
+HALF_NAME = {torch.bfloat16: "bf16", torch.float16: "fp16"}
+
+
+def _half_bars(case, dtype, quantities):
+    name = HALF_NAME[dtype]
+    own = HALF_BARS[case]
+    rows = [v for k, v in HALF_BARS.items() if k.startswith(f"matrix {name} ")]
+    bars = {}
+    for q in quantities:
+        if q not in own:
+            continue
+        base = own[q]
+        if case.startswith("matrix "):
+            vals = [v[q] for v in rows if q in v]
+            base = max(base, math.sqrt(sum(e * e for e in vals) / len(vals)))
+        if q == "dA" and not case.startswith("matrix "):
+            bars[q] = C4_DA_FACTOR * own["dA kernel rounding"]
+        else:
+            bars[q] = 1.5 * base
+    return bars
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16], ids=str)
 @pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
 def test_backward_option_matrix(shape, dtype):
     inputs, dy, dfinal = _inputs(shape, seed=sum(shape) + 3)
     ref = _oracle_grads(inputs, dy, dfinal, True, dtype)
     got = _gpu_grads(inputs, dy, dfinal, True, dtype)
-    _compare(got, ref, GRAD_TOL[dtype], f"{shape} {dtype}")
+    if dtype == torch.float32:
+        _compare(got, ref, GRAD_TOL[dtype], f"{shape} {dtype}")
+        return
+    case = f"matrix {HALF_NAME[dtype]} " + "x".join(map(str, shape))
+    bars = _half_bars(case, dtype, ["d" + k for k in ref])
+    for k, r in ref.items():
+        _compare({k: got[k]}, {k: r}, bars.get("d" + k, 0.0), f"{shape} {dtype}")
 
 
 def test_reference_gradient_case():
@@ -296,14 +333,55 @@ def test_config4_backward_prefix():
         pre["x"], pre["dt"], pre["A"], pre["B"], pre["C"], chunk_size=128, D=pre["D"], z=pre["z"],
         dt_bias=pre["dt_bias"], dt_softplus=True)
     (yr * dy[:1, :cut]).sum().backward()
+    bars = _half_bars("c4 prefix 384", torch.bfloat16, ["d" + k for k in pre])
+    over = []
     for k, v in pre.items():
         gk = got[k]
         if k in ("x", "dt", "B", "C", "z"):
             assert torch.count_nonzero(gk[:, cut:]) == 0 and torch.count_nonzero(gk[1:]) == 0, k
             gk = gk[:1, :cut]
-        err = record("c4 bwd prefix 384", "d" + k, norm_rel(gk, v.grad), 2e-2)
-        assert err <= 2e-2, f"d{k} {err:.3e}"
+        err = record("c4 bwd prefix 384", "d" + k, norm_rel(gk, v.grad), bars["d" + k])
+        if err > bars["d" + k]:
+            over.append(f"d{k} {err:.3e} > {bars['d' + k]:.3e}")
+    assert not over, over
 
+
+def test_config4_backward_full():
+    """Config 4 (b4 L4096 H64 P64 N128, bf16) with the upstream gradient on batch 0 over all
+    4096 tokens and a final-state gradient: the whole state-adjoint chain over the 16 chunks
+    and the d_final path, against float64 autograd of the composition on batch 0 (batches are
+    independent, so the other batches' per-token gradients must be exactly zero and A, D and
+    dt_bias take only batch 0's terms)."""
+    batch, length, nheads, headdim, ngroups, dstate = 4, 4096, 64, 64, 1, 128
+    p = ssd_problem(batch, length, nheads, headdim, ngroups, dstate, seed=4, act=torch.bfloat16, init=False)
+    p.pop("initial_states")
+    g = torch.Generator().manual_seed(45)
+    dy = torch.zeros(batch, length, nheads, headdim, dtype=torch.float64)
+    dfinal = torch.zeros(batch, nheads, headdim, dstate, dtype=torch.float64)
+    dy[:1] = torch.randn(1, length, nheads, headdim, generator=g, dtype=torch.float64)
+    dfinal[:1] = torch.randn(1, nheads, headdim, dstate, generator=g, dtype=torch.float64)
+    leaves = {k: v.detach().to(DEV).requires_grad_(True) for k, v in p.items()}
+    kw = {k: leaves[k] for k in ("D", "z", "dt_bias")}
+    y, s = _api()(leaves["x"], leaves["dt"], leaves["A"], leaves["B"], leaves["C"], 256, **kw, dt_softplus=True)
+    ((y.double() * dy.to(DEV)).sum() + (s.double() * dfinal.to(DEV)).sum()).backward()
+    got = {k: v.grad for k, v in leaves.items()}
+    one = {k: (v[:1] if k in ("x", "dt", "B", "C", "z") else v).detach().double().requires_grad_(True)
+           for k, v in p.items()}
+    yr, sr = oracle.mamba2_chunk_scan_composition(
+        one["x"], one["dt"], one["A"], one["B"], one["C"], chunk_size=256, D=one["D"], z=one["z"],
+        dt_bias=one["dt_bias"], dt_softplus=True)
+    ((yr * dy[:1]).sum() + (sr * dfinal[:1]).sum()).backward()
+    bars = _half_bars("c4 batch 0", torch.bfloat16, ["d" + k for k in one])
+    over = []
+    for k, v in one.items():
+        gk = got[k]
+        if k in ("x", "dt", "B", "C", "z"):
+            assert torch.count_nonzero(gk[1:]) == 0, k
+            gk = gk[:1]
+        err = record("c4 bwd batch 0 full", "d" + k, norm_rel(gk, v.grad), bars["d" + k])
+        if err > bars["d" + k]:
+            over.append(f"d{k} {err:.3e} > {bars['d' + k]:.3e}")
+    assert not over, over
 
 def _composition_grads(inputs, dy, dfinal, softplus, dtype):
     """float64 gradients of the oracle's chunked composition (pinned to the recurrence by

@@ -1,8 +1,9 @@
 """Mamba-2 decode state update: HIP kernels against the float64 CPU oracle.
 
 Case list, contracts, adjoint-None checks and determinism follow the reference
-verifier (benchmarks/verify_mamba2_state.py:552-570, 196-302); tolerances are the
-reference's decode tolerances: 1e-5 fp32, 5e-3 fp16, 3e-2 bf16.
+verifier (benchmarks/verify_mamba2_state.py:552-570, 196-302).  Tolerances: the reference's
+decode tolerances for fp32 and fp16 (1e-5, 5e-3); bf16 is held to 2e-2, tighter than the
+reference's 3e-2, since the kernels' bf16 errors measure under 1e-2 on every case here.
 """
 
 import pytest
@@ -14,7 +15,7 @@ from cases import decode_problem, max_rel, norm_rel, record
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
 NAMES = ("state", "x", "dt", "A", "B", "C", "D", "z", "dt_bias")
-TOL = {torch.float32: 1e-5, torch.float16: 5e-3, torch.bfloat16: 3e-2}
+TOL = {torch.float32: 1e-5, torch.float16: 5e-3, torch.bfloat16: 2e-2}
 
 
 def _api():
@@ -87,12 +88,14 @@ def test_case(tag, dtype, shape, opts):
     fwd_err = max((y.detach().double().cpu() - want_y.detach()).abs().max().item(),
                   (s.detach().double().cpu() - want_s.detach()).abs().max().item())
     scale = max(want_y.abs().max().item(), want_s.abs().max().item())
-    assert fwd_err <= TOL[dtype] * max(scale, 1.0), f"{tag}: forward |err| {fwd_err:.3e}"
+    fwd_bar = TOL[dtype] * max(scale, 1.0)
+    record(f"decode {tag}", "y, new_state (max abs)", fwd_err, fwd_bar)
+    assert fwd_err <= fwd_bar, f"{tag}: forward |err| {fwd_err:.3e}"
     for name, t, w in zip(NAMES, got, truth):
         if t is None:
             continue
         assert t.grad is not None and t.grad.dtype == dtype, name
-        e = norm_rel(t.grad, w.grad)
+        e = record(f"decode {tag}", "d" + name, norm_rel(t.grad, w.grad), TOL[dtype])
         assert e <= TOL[dtype], f"{tag}: grad {name} rel {e:.3e}"
 
 
