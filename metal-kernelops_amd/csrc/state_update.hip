@@ -355,8 +355,16 @@ __global__ void __launch_bounds__(kThreads) bwd(Args a) {
   // state and new-state adjoint are requested a pass ahead when a lane holds at most 8.
   constexpr bool kAhead = SPL <= 8;
   float bvs[SPL], cvs[SPL];
+  // A pass's inputs: the state and new-state adjoint rows, and the row's raw scalars.  They are
+  // all loaded unconditionally (from the last row for a slot past the head's rows, from chunk 0
+  // for a chunk past the row's states; an absent optional input is read from an array of the
+  // same shape and masked at use): a load under a run-time condition, or a scalar load issued
+  // after the next pass's rows, makes the compiler wait for every load issued before it, which
+  // drains the look-ahead.
   struct Row {
     float s[SPL], dn[SPL];
+    RawAny dt, x, z;
+    float dy, dv;
   };
   for_row_chunks<VEC, SPL>(N, tpr, j, [&](int k, int n0) {
     float* bv = bvs + k * VEC;
@@ -376,27 +384,34 @@ __global__ void __launch_bounds__(kThreads) bwd(Args a) {
       cv[0] = ld_any(a.C, g.bc_dtype, bg * N + n0);
     }
   });
+  const int P = static_cast<int>(g.headdim);
+  const void* zsrc = a.z ? a.z : a.x;                // same shape and dtype as z
+  const float* dysrc = a.dy ? a.dy : a.dx;           // same shape as dy (an output; masked)
+  const float* dnsrc = a.dnew ? a.dnew : a.gstate;   // same shape as dnew (an output; masked)
+  const float* dsrc = a.D ? a.D : a.A;
   // The state and the new-state adjoint stream through once, read with the nontemporal hint.
   auto fetch = [&](int p, Row& r) {
-    if (p >= g.headdim) return;
-    const int64_t row = bh * g.headdim + p;
-    for_row_chunks<VEC, SPL>(N, tpr, j, [&](int k, int n0) {
+    const int pc = p < P ? p : P - 1;
+    const int64_t row = bh * g.headdim + pc;
+    r.dt = load_any_raw(a.dt, g.dt_dtype, g.dt_per_row ? row : bh);
+    r.x = load_any_raw(a.x, g.x_dtype, row);
+    r.z = load_any_raw(zsrc, g.x_dtype, row);
+    r.dy = dysrc[row];
+    r.dv = dsrc[a.D ? (g.d_per_row ? h * g.headdim + pc : h) : 0];
+#pragma unroll
+    for (int k = 0; k < SPL / VEC; ++k) {
+      const int n0 = (j + k * tpr) * VEC;
+      const int nc = n0 < N ? n0 : 0;
       float* s = r.s + k * VEC;
       float* dn = r.dn + k * VEC;
       if constexpr (VEC == 4) {
-        float s4[4], d4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        load4_nt<TS>(a.state, row * N + n0, s4);
-        if (a.dnew) load4_nt<float>(a.dnew, row * N + n0, d4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          s[e] = s4[e];
-          dn[e] = d4[e];
-        }
+        load4_nt<TS>(a.state, row * N + nc, *reinterpret_cast<float(*)[4]>(s));
+        load4_nt<float>(dnsrc, row * N + nc, *reinterpret_cast<float(*)[4]>(dn));
       } else {
-        s[0] = ld<TS>(a.state, row * N + n0);
-        dn[0] = a.dnew ? a.dnew[row * N + n0] : 0.0f;
+        s[0] = ld<TS>(a.state, row * N + nc);
+        dn[0] = dnsrc[row * N + nc];
       }
-    });
+    }
   };
   Row cur, nxt;
   if constexpr (kAhead) fetch(slot, cur);
@@ -412,16 +427,16 @@ __global__ void __launch_bounds__(kThreads) bwd(Args a) {
     }
     if (p < g.headdim) {
       const int64_t row = bh * g.headdim + p;
-      const float raw = ld_any(a.dt, g.dt_dtype, g.dt_per_row ? row : bh) + bias;
+      const float raw = raw_any_f32(cur.dt, g.dt_dtype) + bias;
       const float del = g.softplus ? softplus(raw) : raw;
       const float decay = expf(Ah * del);
-      const float xv = ld_any(a.x, g.x_dtype, row);
+      const float xv = raw_any_f32(cur.x, g.x_dtype);
       const float dxv = del * xv;
-      const float dv = a.D ? (g.d_per_row ? a.D[h * g.headdim + p] : a.D[h]) : 0.0f;
-      const float dyv = a.dy ? a.dy[row] : 0.0f;
+      const float dv = a.D ? cur.dv : 0.0f;
+      const float dyv = a.dy ? cur.dy : 0.0f;
       float zv = 0.0f, sg = 1.0f, gate = 1.0f;
       if (a.z) {
-        zv = ld_any(a.z, g.x_dtype, row);
+        zv = raw_any_f32(cur.z, g.x_dtype);
         sg = sigmoid(zv);
         gate = zv * sg;
       }
@@ -429,7 +444,9 @@ __global__ void __launch_bounds__(kThreads) bwd(Args a) {
       float sx = 0.0f, sa = 0.0f, sy = 0.0f;
       for_row_chunks<VEC, SPL>(N, tpr, j, [&](int k, int n0) {
         const float* s = cur.s + k * VEC;
-        const float* dn = cur.dn + k * VEC;
+        float dn[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) dn[e] = a.dnew ? cur.dn[k * VEC + e] : 0.0f;
         const float* bv = bvs + k * VEC;
         const float* cv = cvs + k * VEC;
         float gs[VEC];
