@@ -121,10 +121,10 @@ __device__ __forceinline__ void acc_to_lds(float* red, const V& v, int wm, int w
 // 64x64 windows of the problem's tensors; the base is uniform, each lane adds a
 // 32-bit offset (load_win / store_win).
 //   x-like (b, L, H, P): rows = tokens t0 .., columns = d_head pc0 ..
-template <typename TM, bool VEC>
+template <typename TM, bool VEC, bool NT = false>
 __device__ __forceinline__ void load_xw(const Geo& g, const TM* src, int64_t b, int64_t t0, int64_t h, int64_t pc0,
                                         V8<TM> (&v)[2]) {
-  load_win<TM, VEC>(src + xidx(g, b, t0, h, pc0), static_cast<int>(g.nheads * g.headdim), clamp64(g.length - t0),
+  load_win<TM, VEC, NT>(src + xidx(g, b, t0, h, pc0), static_cast<int>(g.nheads * g.headdim), clamp64(g.length - t0),
                     static_cast<int>(g.headdim - pc0), v, src);
 }
 template <typename TM, bool VEC>
@@ -140,10 +140,10 @@ __device__ __forceinline__ void store_xw_row(const Geo& g, TM* dst, int64_t b, i
                          clamp64(g.length - t0), static_cast<int>(g.headdim - pc0), rr, a);
 }
 //   B/C-like (b, L, G, N): rows = tokens t0 .., columns = d_state nn0 ..
-template <typename TM, bool VEC>
+template <typename TM, bool VEC, bool NT = false>
 __device__ __forceinline__ void load_bw(const Geo& g, const TM* src, int64_t b, int64_t t0, int64_t gg, int64_t nn0,
                                         V8<TM> (&v)[2]) {
-  load_win<TM, VEC>(src + bcidx(g, b, t0, gg, nn0), static_cast<int>(g.ngroups * g.dstate), clamp64(g.length - t0),
+  load_win<TM, VEC, NT>(src + bcidx(g, b, t0, gg, nn0), static_cast<int>(g.ngroups * g.dstate), clamp64(g.length - t0),
                     static_cast<int>(g.dstate - nn0), v, src);
 }
 template <typename TM, bool VEC>
@@ -153,9 +153,9 @@ __device__ __forceinline__ void store_bw(const Geo& g, TM* dst, int64_t b, int64
                      static_cast<int>(g.dstate - nn0), a, bb);
 }
 //   a (P, N) state matrix: rows = d_head pc0 .., columns = d_state nn0 ..
-template <typename TM, bool VEC>
+template <typename TM, bool VEC, bool NT = false>
 __device__ __forceinline__ void load_sw(const Geo& g, const TM* st, int64_t pc0, int64_t nn0, V8<TM> (&v)[2]) {
-  load_win<TM, VEC>(st + pc0 * g.dstate + nn0, static_cast<int>(g.dstate), clamp64(g.headdim - pc0),
+  load_win<TM, VEC, NT>(st + pc0 * g.dstate + nn0, static_cast<int>(g.dstate), clamp64(g.headdim - pc0),
                     static_cast<int>(g.dstate - nn0), v, st);
 }
 

@@ -1076,10 +1076,11 @@ dbc_state(Geo g, BwdPlan pl, Ptrs p) {
     const int hh = k / g.npt, pt = k % g.npt;
     const int64_t h = h0 + hh, bh = b * g.nheads + h;
     const int64_t so = (bh * g.nc + c) * g.q;
-    load_xw<TM, VEC>(g, src, b, tl0, h, pt * 64, r.src);  // rows l
+    // x / gy and the states stream through once (no later kernel reads them again): nontemporal
+    load_xw<TM, VEC, true>(g, src, b, tl0, h, pt * 64, r.src);  // rows l
     const TM* st = stm + (bh * g.nc + c) * g.headdim * g.dstate;
-    load_sw<TM, VEC>(g, st, pt * 64, nn0, r.s0);  // rows p
-    load_sw<TM, VEC>(g, st, pt * 64, nn0 + 64, r.s1);
+    load_sw<TM, VEC, true>(g, st, pt * 64, nn0, r.s0);  // rows p
+    load_sw<TM, VEC, true>(g, st, pt * 64, nn0 + 64, r.s1);
 #pragma unroll
     for (int rr = 0; rr < 2; ++rr) {
       r.cl[rr] = p.cs[so + 64 * tt + r0 + rr];

@@ -117,8 +117,8 @@ __device__ __forceinline__ void put2x8(TM* dst, int r0, int c0, const float (&a)
 // loads are unconditional (a lane outside the window reads at offset 0 of the window, or
 // of `safe`, any valid aligned address, when the window is empty, and discards it), so the
 // number of loads in flight is static and the compiler can wait for exactly the ones it
-// needs.
-template <typename T, bool VEC>
+// needs.  NT: with the nontemporal hint, for a window that no other workgroup reads again.
+template <typename T, bool VEC, bool NT = false>
 __device__ __forceinline__ void load_win(const T* base, int ld, int nrows, int ncols, V8<T> (&v)[2],
                                          const T* safe) {
   const int r0 = blk_r0(), c0 = blk_c0();
@@ -129,7 +129,11 @@ __device__ __forceinline__ void load_win(const T* base, int ld, int nrows, int n
     const int r = r0 + rr;
     if constexpr (VEC) {
       const bool ok = r < nrows && c0 < ncols;
-      load_words(at_bytes(wb, opaque(ok ? static_cast<uint32_t>((r * ld + c0) * sizeof(T)) : 0u)), v[rr].w);
+      const T* at = at_bytes(wb, opaque(ok ? static_cast<uint32_t>((r * ld + c0) * sizeof(T)) : 0u));
+      if constexpr (NT)
+        load_words_nt(at, v[rr].w);
+      else
+        load_words(at, v[rr].w);
       v[rr].mask = ok ? ~0u : 0u;
     } else {
       const int n = r < nrows ? ncols - c0 : 0;
