@@ -1498,26 +1498,28 @@ __global__ void __launch_bounds__(256) reduce_bc(Geo g, int ncb, int64_t seg_dg,
     const int64_t t = t0 + tl;
     float vb = 0.0f, vc = 0.0f;
     if (t < g.length) {
-      // channel blocks in order: whole batches of eight issue their loads together,
-      // the rest one at a time
-      constexpr int PF = 8;
-      const float2* src = reinterpret_cast<const float2*>(pbc + ((bg * ncb * g.length + t) * NS + n) * 2);
-      const int64_t stride = g.length * NS;  // float2 elements between channel blocks
+      // channel blocks in order: whole batches of sixteen issue their loads together, the
+      // rest one at a time; the partials are read once, with the nontemporal hint (eight at a
+      // time without it: 0.135 ms at c3; sixteen with it: 0.107 ms, thirty-two the same)
+      constexpr int PF = 16;
+      const float* src = pbc + ((bg * ncb * g.length + t) * NS + n) * 2;
+      const int64_t stride = g.length * NS * 2;  // floats between channel blocks
       int cbk = 0;
       for (; cbk + PF <= nsum; cbk += PF) {
-        float2 q[PF];
+        uint32_t q[PF][2];
 #pragma unroll
-        for (int j = 0; j < PF; ++j) q[j] = src[(cbk + j) * stride];
+        for (int j = 0; j < PF; ++j) load_words_nt(src + (cbk + j) * stride, q[j]);
 #pragma unroll
         for (int j = 0; j < PF; ++j) {
-          vb += q[j].x;
-          vc += q[j].y;
+          vb += __uint_as_float(q[j][0]);
+          vc += __uint_as_float(q[j][1]);
         }
       }
       for (; cbk < nsum; ++cbk) {
-        const float2 q = src[cbk * stride];
-        vb += q.x;
-        vc += q.y;
+        uint32_t q[2];
+        load_words_nt(src + cbk * stride, q);
+        vb += __uint_as_float(q[0]);
+        vc += __uint_as_float(q[1]);
       }
     }
     sb[n][tl] = vb;
