@@ -731,7 +731,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) f
   float x = 0.0f;
   auto block = [&](int k, In& in) {
     const int64_t t0 = static_cast<int64_t>(k) * HS;
-    if (active && sn) sp[k * sstep] = x;
+    if (active && sn) __builtin_nontemporal_store(x, sp + k * sstep);  // whole lines, read once by the backward
     const float uu = to_f32(in.u);
     const float zz = to_f32(in.z);
     const float del = step_of(g, in.dl, bias);
@@ -898,7 +898,7 @@ bwd_lane(Geo g, Ptrs p, int cpb) {
     in.z = (zsrc + t0)[eoff];
     in.go = (static_cast<const TU*>(p.dout) + t0)[eoff];
     in.o = (osrc + t0)[eoff];
-    in.xin = (p.states + k * sstep)[soff];
+    in.xin = __builtin_nontemporal_load(p.states + k * sstep + soff);  // whole lines, read once
     in.bc.load(g, bcsrc + t0, 0, bcoff, 8);
   };
   const int nblk = static_cast<int>(L / HS);
