@@ -134,7 +134,7 @@ __device__ __forceinline__ void store4_nt(void* base, int64_t i, const float (&v
 // Passes (of kThreads / tpr rows) per forward workgroup: a workgroup streams 2 x 4 KB of an
 // fp32 state.  One workgroup per whole (batch, head) (8 passes at d_state 128) streamed at
 // 5.4 TB/s; two passes with their state rows requested before any arithmetic and the state
-// read and written with the nontemporal hint, at 5.9 TB/s.
+// read and written with the nontemporal hint, at 6.3 TB/s.
 constexpr int kFwdPasses = 2;
 
 // Sum over the tpr lanes of a row (tpr a power of two <= 64, uniform): an unrolled butterfly.
@@ -153,8 +153,8 @@ __device__ __forceinline__ float row_sum_pow2(float v, int tpr) {
 // head's rows reads its first row) and masked at use, and the per-row scalars are read
 // without a dtype branch (load_any_raw): a load under a run-time condition makes the compiler
 // wait for each load before the next, and 64-bit index division cost several hundred
-// instructions per workgroup.  At c5 this runs at 5.9 TB/s against 5.4 TB/s for one
-// workgroup per (batch, head).
+// instructions per workgroup.  At c5 this runs at 6.3 TB/s, the rate of a nontemporal device
+// copy, against 5.4 TB/s for one workgroup per (batch, head).
 template <typename TS, typename TB>
 __global__ void __launch_bounds__(kThreads) fwd_v4(Args a, int tpr_shift) {
   const Geo& g = a.g;
