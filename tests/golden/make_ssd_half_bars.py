@@ -8,8 +8,8 @@ dtype with float32 step sizes, decay exponents and C.B^T (``cv/mamba2_chunk.py:4
 takes its gradients by autograd through it (``:653-678``).  ``oracle.mamba2_chunk_scan_composition`` is
 that composition, restated and pinned to the float64 recurrence by ``tests/test_oracle.py``.
 For each 16-bit gradient case of ``tests/test_ssd_gpu.py`` -- the bf16 and fp16 rows of the
-option / shape matrix, the config-4 causal prefix, and config 4's batch 0 over all 4096 tokens
-with a final-state gradient -- this runs the composition in the 16-bit dtype on the case's
+option / shape matrix, one case without the gate, the config-4 causal prefix, and config 4's
+batch 0 over all 4096 tokens with a final-state gradient -- this runs the composition in the 16-bit dtype on the case's
 inputs (rounded to it where the kernels take it) and records the norm-relative error of every
 gradient against float64 autograd on the same rounded inputs: of the recurrence, or at config
 4's full length of the float64 composition (which tests/test_oracle.py pins to the
@@ -47,6 +47,9 @@ MATRIX = [
     (1, 1100, 3, 64, 1, 128),
     (1, 1030, 4, 60, 2, 128),
 ]
+
+
+NOGATE = (1, 1100, 2, 80, 2, 72)
 
 
 def _grads(fn, inputs, dy, dfinal):
@@ -159,6 +162,14 @@ def main():
             key = f"matrix {name} " + "x".join(map(str, shape))
             table[key] = errors(inputs, dy, dfinal, 64, dtype)
             print(key, table[key], flush=True)
+    # without the gate (test_backward_without_gate): gy is dy itself, the case whose float16 dA a
+    # kernel rounding u differently on the two sides of the d cs cancellation put at 50x this error
+    for dtype, name in ((torch.bfloat16, "bf16"), (torch.float16, "fp16")):
+        shape = NOGATE
+        inputs, dy, dfinal = ssd_matrix_inputs(shape, seed=sum(shape) + 3, options=("D", "dt_bias", "initial_states"))
+        key = f"nogate {name} " + "x".join(map(str, shape))
+        table[key] = errors(inputs, dy, dfinal, 64, dtype)
+        print(key, table[key], flush=True)
     # the config-4 causal prefix of test_config4_backward_prefix: batch 0, 384 tokens
     p = ssd_problem(4, 4096, 64, 64, 1, 128, seed=4, act=torch.bfloat16, init=False)
     p.pop("initial_states")
