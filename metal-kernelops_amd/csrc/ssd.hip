@@ -175,7 +175,7 @@ __global__ void __launch_bounds__(256) chunk_scan(Geo g, Ptrs p) {
         v[rr][k] = y;
       }
     }
-    store_xw<TM, VEC>(g, static_cast<TM*>(p.y), b, tl0, h, pc0, v[0], v[1]);
+    store_xw<TM, VEC, true>(g, static_cast<TM*>(p.y), b, tl0, h, pc0, v[0], v[1]);
   });
 }
 
@@ -320,7 +320,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) c
             v[rr][e] = y;
           }
         }
-        store_xw<TM, VEC>(g, static_cast<TM*>(p.y), b, tl0, h, pc0, v[0], v[1]);
+        store_xw<TM, VEC, true>(g, static_cast<TM*>(p.y), b, tl0, h, pc0, v[0], v[1]);
         if constexpr (k + 1 < N) __syncthreads();  // the next stage refills the operand buffers
       }
     }
@@ -466,7 +466,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) c
             v[rr][e] = y;
           }
         }
-        store_xw<TM, VEC>(g, static_cast<TM*>(p.y), b, tc + 64 * sg.i, h, pc0, v[0], v[1]);
+        store_xw<TM, VEC, true>(g, static_cast<TM*>(p.y), b, tc + 64 * sg.i, h, pc0, v[0], v[1]);
       }
     }
     if constexpr (sg.x >= 0) load_xw<TM, VEC>(g, X, b, tc + 64 * sg.x, h, pc0, xv);

@@ -127,16 +127,16 @@ __device__ __forceinline__ void load_xw(const Geo& g, const TM* src, int64_t b, 
   load_win<TM, VEC, NT>(src + xidx(g, b, t0, h, pc0), static_cast<int>(g.nheads * g.headdim), clamp64(g.length - t0),
                     static_cast<int>(g.headdim - pc0), v, src);
 }
-template <typename TM, bool VEC>
+template <typename TM, bool VEC, bool NT = false>
 __device__ __forceinline__ void store_xw(const Geo& g, TM* dst, int64_t b, int64_t t0, int64_t h, int64_t pc0,
                                          const float (&a)[8], const float (&bb)[8]) {
-  store_win<TM, VEC>(dst + xidx(g, b, t0, h, pc0), static_cast<int>(g.nheads * g.headdim), clamp64(g.length - t0),
+  store_win<TM, VEC, NT>(dst + xidx(g, b, t0, h, pc0), static_cast<int>(g.nheads * g.headdim), clamp64(g.length - t0),
                      static_cast<int>(g.headdim - pc0), a, bb);
 }
-template <typename TM, bool VEC>
+template <typename TM, bool VEC, bool NT = false>
 __device__ __forceinline__ void store_xw_row(const Geo& g, TM* dst, int64_t b, int64_t t0, int64_t h, int64_t pc0,
                                              int rr, const float (&a)[8]) {
-  store_win_row<TM, VEC>(dst + xidx(g, b, t0, h, pc0), static_cast<int>(g.nheads * g.headdim),
+  store_win_row<TM, VEC, NT>(dst + xidx(g, b, t0, h, pc0), static_cast<int>(g.nheads * g.headdim),
                          clamp64(g.length - t0), static_cast<int>(g.headdim - pc0), rr, a);
 }
 //   B/C-like (b, L, G, N): rows = tokens t0 .., columns = d_state nn0 ..

@@ -73,7 +73,7 @@ __device__ __forceinline__ void gate_row(const Geo& g, const Ptrs& p, int rr, co
       dz[e] = gy[e] * ypre * sgm * fmaf(zf[e], 1.0f - sgm, 1.0f);
       gy[e] = to_f32(from_f32<TM>(gy[e] * zf[e] * sgm));
     }
-    store_xw_row<TM, VEC>(g, static_cast<TM*>(p.dz), b, tl0, h, pc0, rr, dz);
+    store_xw_row<TM, VEC, true>(g, static_cast<TM*>(p.dz), b, tl0, h, pc0, rr, dz);
     store_xw_row<TM, VEC>(g, static_cast<TM*>(p.gyw), b, tl0, h, pc0, rr, gy);
   }
   float ya = 0.0f;
@@ -535,7 +535,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) d
         p.ut[po0 + 64 * j + r0 + rr] = su;
       }
     }
-    store_xw<TM, VEC>(g, static_cast<TM*>(p.dx), b, tc + 64 * j, h, pc0, dxo[0], dxo[1]);
+    store_xw<TM, VEC, true>(g, static_cast<TM*>(p.dx), b, tc + 64 * j, h, pc0, dxo[0], dxo[1]);
     if (j != jb) load_xw<TM, VEC>(g, static_cast<const TM*>(p.x), b, tc + 64 * jb, h, pc0, xv);
     __syncthreads();  // red is refilled by the next stage
   };
@@ -725,7 +725,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) d
             p.ut[po0 + 64 * j + r0 + rr] = su;
           }
         }
-        store_xw<TM, VEC>(g, static_cast<TM*>(p.dx), b, ts0, h, pc0, dxo[0], dxo[1]);
+        store_xw<TM, VEC, true>(g, static_cast<TM*>(p.dx), b, ts0, h, pc0, dxo[0], dxo[1]);
         if constexpr (k + 1 < N) __syncthreads();  // the next stage refills the operand buffers
       }
     }
@@ -901,7 +901,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) d
             p.ut[po0 + 64 * j + r0 + rr] = su;
           }
         }
-        store_xw<TM, VEC>(g, static_cast<TM*>(p.dx), b, ts0, h, pc0, dxo[0], dxo[1]);
+        store_xw<TM, VEC, true>(g, static_cast<TM*>(p.dx), b, ts0, h, pc0, dxo[0], dxo[1]);
       }
     }
     if constexpr (sg.load == 1) {

@@ -67,12 +67,15 @@ __device__ __forceinline__ void v8_f32(const V8<T>& v, float (&f)[8]) {
 }
 
 // Stores 8 fp32 values as T at p (16-byte aligned when `vec`), or the first n of them.
-template <typename T>
+template <typename T, bool NT = false>
 __device__ __forceinline__ void v8_store(T* p, int n, bool vec, const float (&f)[8]) {
   if (vec && n >= 8) {
     uint32_t w[V8<T>::kWords];
     pack_words<T, 8>(f, w);
-    store_words(p, w);
+    if constexpr (NT)
+      store_words_nt(p, w);
+    else
+      store_words(p, w);
   } else {
 #pragma unroll
     for (int e = 0; e < 8; ++e)
@@ -147,22 +150,22 @@ __device__ __forceinline__ void load_win(const T* base, int ld, int nrows, int n
 
 // Stores the thread's block (rows r0, r0+1 of a 64x64 window at base with row stride
 // ld, under load_win's offset bound) as T, inside nrows x ncols.
-template <typename T, bool VEC>
+template <typename T, bool VEC, bool NT = false>
 __device__ __forceinline__ void store_win(T* base, int ld, int nrows, int ncols, const float (&a)[8],
                                           const float (&b)[8]) {
   const int r0 = blk_r0(), c0 = blk_c0();
   const int n = ncols - c0;
-  if (r0 < nrows && n > 0) v8_store(at_bytes(base, static_cast<uint32_t>((r0 * ld + c0) * sizeof(T))), n, VEC, a);
+  if (r0 < nrows && n > 0) v8_store<T, NT>(at_bytes(base, static_cast<uint32_t>((r0 * ld + c0) * sizeof(T))), n, VEC, a);
   if (r0 + 1 < nrows && n > 0)
-    v8_store(at_bytes(base, static_cast<uint32_t>(((r0 + 1) * ld + c0) * sizeof(T))), n, VEC, b);
+    v8_store<T, NT>(at_bytes(base, static_cast<uint32_t>(((r0 + 1) * ld + c0) * sizeof(T))), n, VEC, b);
 }
 
 // Stores row r0 + rr of the thread's block only.
-template <typename T, bool VEC>
+template <typename T, bool VEC, bool NT = false>
 __device__ __forceinline__ void store_win_row(T* base, int ld, int nrows, int ncols, int rr, const float (&a)[8]) {
   const int r = blk_r0() + rr, c0 = blk_c0();
   const int n = ncols - c0;
-  if (r < nrows && n > 0) v8_store(at_bytes(base, static_cast<uint32_t>((r * ld + c0) * sizeof(T))), n, VEC, a);
+  if (r < nrows && n > 0) v8_store<T, NT>(at_bytes(base, static_cast<uint32_t>((r * ld + c0) * sizeof(T))), n, VEC, a);
 }
 
 // Writes the thread's raw block (rows a, b) into an LDS operand tile without conversion.
