@@ -276,7 +276,12 @@ size_t mko_ssd_fwd_workspace_size(const mko_ssd_params* p);
 int mko_ssd_fwd(const mko_ssd_params* p, void* stream);
 
 /* Replaces the torch autograd of that composition (the reference has no
- * hand-written SSD backward): gradients of every differentiable input. */
+ * hand-written SSD backward): gradients of every differentiable input.  For 16-bit and
+ * float32 inputs part of the work runs on a second stream of the current device that the
+ * library creates on first use (non-blocking, default priority, kept until the process
+ * ends); `stream` waits for it before the call's last kernel, so the outputs and the
+ * workspace are ordered on `stream` alone.  While `stream` is being captured into a graph
+ * everything runs on `stream`.  The stream must belong to the current device. */
 size_t mko_ssd_bwd_workspace_size(const mko_ssd_params* p);
 int mko_ssd_bwd(const mko_ssd_params* p, void* stream);
 

@@ -21,8 +21,12 @@
 // sides use the same rounded operands (gy and u as the matrix cores see them) and
 // the cancellation between them is exact up to fp32 accumulation.
 //   reduce      dA, ddt_bias, dD
-// Every partial sum is reduced in a fixed order: the backward is deterministic.
+// Every partial sum is reduced in a fixed order: the backward is deterministic.  dcb runs on
+// a second stream beside state_rev, du, dbc_state, finish and reduce (launch_bwd_t), and
+// dbc_final, which reads its partials, runs last.
 #include <algorithm>
+#include <mutex>
+#include <vector>
 
 #include "ssd.hpp"
 #include "ssd64.hpp"
@@ -1417,8 +1421,72 @@ void launch_du(const Geo& g, const BwdPlan& pl, const Ptrs& q, hipStream_t s) {
   MKO_TIMED("ssd_du", s, du_kernel<TM, VEC><<<dim3((g.qb + 1) / 2 * g.npt * g.nc * bh), 256, 0, s>>>(g, pl, q));
 }
 
+// The backward's second stream on each device: one non-blocking stream at the default
+// priority and its events, created on first use and kept until the process ends.
+struct SideStream {
+  hipStream_t stream = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+std::mutex g_side_mu;  // guards g_side and keeps each call's event records next to their waits
+std::vector<SideStream> g_side;  // per device ordinal
+
+// The current device's side stream in *out (created on first use), or null while s is being
+// captured into a graph, where creating it is not allowed: the caller then runs everything
+// on s.  Call with g_side_mu held.
+int side_stream(hipStream_t s, SideStream** out) {
+  *out = nullptr;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  hipError_t err = hipStreamIsCapturing(s, &cap);
+  if (err != hipSuccess) {
+    mko_set_error("ssd_bwd: stream capture status: %s", hipGetErrorString(err));
+    return MKO_ELAUNCH;
+  }
+  if (cap != hipStreamCaptureStatusNone) return MKO_OK;
+  int dev = -1;
+  err = hipGetDevice(&dev);
+  if (err != hipSuccess || dev < 0) {
+    mko_set_error("ssd_bwd: no current device: %s", hipGetErrorString(err));
+    return MKO_ELAUNCH;
+  }
+  if (static_cast<size_t>(dev) >= g_side.size()) g_side.resize(dev + 1);
+  SideStream& sd = g_side[dev];
+  if (!sd.stream) {
+    SideStream made;
+    err = hipStreamCreateWithFlags(&made.stream, hipStreamNonBlocking);
+    for (hipEvent_t* e : {&made.fork, &made.join})
+      if (err == hipSuccess) err = hipEventCreateWithFlags(e, hipEventDisableTiming);
+    if (err != hipSuccess) {
+      mko_set_error("ssd_bwd: second stream on device %d: %s", dev, hipGetErrorString(err));
+      return MKO_ELAUNCH;
+    }
+    sd = made;
+  }
+  *out = &sd;
+  return MKO_OK;
+}
+
+// Makes `to` wait for the work queued on `from` so far, through event e.
+int stream_wait(hipStream_t from, hipStream_t to, hipEvent_t e) {
+  hipError_t err = hipEventRecord(e, from);
+  if (err == hipSuccess) err = hipStreamWaitEvent(to, e, 0);
+  if (err != hipSuccess) {
+    mko_set_error("ssd_bwd: ordering of the two streams: %s", hipGetErrorString(err));
+    return MKO_ELAUNCH;
+  }
+  return MKO_OK;
+}
+
+// The kernels after the gate, in two streams.  dcb reads only gy and the forward's inputs
+// and writes only partials that dbc_final reads, so the side stream runs it as soon as the
+// gate is done, beside state_rev, du, dbc_state, finish and reduce_params on s, and s waits
+// for it just before dbc_final.  Alone at 4 x 4096 tokens and 64 heads, dcb's 640 long
+// workgroups leave about 40% of the workgroup slots empty for 0.12 ms.  (dbc_state, which
+// could follow it there once state_rev is done, is faster on s: it then no longer competes
+// with du.)  Calls from several host threads share the side stream: the lock keeps each fork
+// record next to its wait, and a join that waits for a later call's work on the same stream
+// also waits for its own.
 template <typename TM, bool VEC>
-void launch_bwd_t(const Geo& g, const BwdPlan& pl, const Ptrs& q, hipStream_t s) {
+int launch_bwd_t(const Geo& g, const BwdPlan& pl, const Ptrs& q, hipStream_t s) {
   const unsigned bh = static_cast<unsigned>(g.batch * g.nheads);
   const unsigned ncg = static_cast<unsigned>(g.nc * g.ngroups);
   const unsigned nb = static_cast<unsigned>(g.batch);
@@ -1433,21 +1501,48 @@ void launch_bwd_t(const Geo& g, const BwdPlan& pl, const Ptrs& q, hipStream_t s)
     else
       MKO_TIMED("ssd_chunk_state_bwd", s, chunk_state<TM, VEC, true><<<cs_grid, 256, 0, s>>>(g, q, q.dstates));
   }
+  auto dcb = [&](hipStream_t st) {
+    MKO_TIMED("ssd_dcb", st, dcb_kernel<TM, VEC><<<dim3(pl.npairs * pl.hb1 * ncg * nb), 256, 0, st>>>(g, pl, q));
+  };
+  hipEvent_t join = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_side_mu);
+    SideStream* sd = nullptr;
+    int err = side_stream(s, &sd);
+    if (err != MKO_OK) return err;
+    if (sd) {
+      if ((err = stream_wait(s, sd->stream, sd->fork)) != MKO_OK) return err;
+      dcb(sd->stream);
+      const hipError_t e = hipEventRecord(sd->join, sd->stream);
+      if (e != hipSuccess) {
+        mko_set_error("ssd_bwd: join event of the second stream: %s", hipGetErrorString(e));
+        return MKO_ELAUNCH;
+      }
+      join = sd->join;
+    }
+  }
   MKO_TIMED("ssd_state_rev", s, state_rev<TM><<<dim3(pl.nblk, bh), 256, 0, s>>>(g, pl, q));
   launch_du<TM, VEC>(g, pl, q, s);
-  MKO_TIMED("ssd_dcb", s, dcb_kernel<TM, VEC><<<dim3(pl.npairs * pl.hb1 * ncg * nb), 256, 0, s>>>(g, pl, q));
+  if (!join) dcb(s);
   MKO_TIMED("ssd_dbc_state", s,
             dbc_state<TM, VEC><<<dim3(g.qb * g.nnp * 2 * pl.hb2 * ncg * nb), 256, 0, s>>>(g, pl, q));
-  MKO_TIMED("ssd_dbc_final", s, dbc_final<TM, VEC><<<dim3(g.qb * g.nnp * 2 * ncg * nb), 256, 0, s>>>(g, pl, q));
   MKO_TIMED("ssd_finish", s,
             finish<<<dim3(g.nc, static_cast<unsigned>(g.nheads), nb), 256, 0, s>>>(g, pl, q));
   MKO_TIMED("ssd_reduce", s, reduce_params<<<dim3(static_cast<unsigned>(g.nheads)), 256, 0, s>>>(g, pl, q));
+  if (join) {
+    const hipError_t e = hipStreamWaitEvent(s, join, 0);
+    if (e != hipSuccess) {
+      mko_set_error("ssd_bwd: join of the second stream: %s", hipGetErrorString(e));
+      return MKO_ELAUNCH;
+    }
+  }
+  MKO_TIMED("ssd_dbc_final", s, dbc_final<TM, VEC><<<dim3(g.qb * g.nnp * 2 * ncg * nb), 256, 0, s>>>(g, pl, q));
+  return MKO_OK;
 }
 
 template <typename TM>
-void launch_bwd_t(const Geo& g, const BwdPlan& pl, const Ptrs& q, hipStream_t s) {
-  if (g.vec) launch_bwd_t<TM, true>(g, pl, q, s);
-  else launch_bwd_t<TM, false>(g, pl, q, s);
+int launch_bwd_t(const Geo& g, const BwdPlan& pl, const Ptrs& q, hipStream_t s) {
+  return g.vec ? launch_bwd_t<TM, true>(g, pl, q, s) : launch_bwd_t<TM, false>(g, pl, q, s);
 }
 
 }  // namespace
@@ -1504,9 +1599,10 @@ extern "C" int mko_ssd_bwd(const mko_ssd_params* prm, void* stream) {
   q.pbias = reinterpret_cast<float*>(ws + lay.pbias);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (tokens) {
-    if (g.x_dtype == MKO_F32) launch_bwd_t<float>(g, pl, q, s);
-    else if (g.x_dtype == MKO_BF16) launch_bwd_t<bf16>(g, pl, q, s);
-    else launch_bwd_t<_Float16>(g, pl, q, s);
+    if (g.x_dtype == MKO_F32) st = launch_bwd_t<float>(g, pl, q, s);
+    else if (g.x_dtype == MKO_BF16) st = launch_bwd_t<bf16>(g, pl, q, s);
+    else st = launch_bwd_t<_Float16>(g, pl, q, s);
+    if (st != MKO_OK) return st;
   } else {
     // no tokens: dinitial = dfinal (zero without it); the parameter gradients are zero
     if (g.batch > 0 && q.dinit) {

@@ -301,6 +301,76 @@ def test_backward_deterministic_and_graph_free_outputs(shape):
         assert torch.equal(a[k], b[k]), k
 
 
+TWO_STREAM_SHAPES = [(2, 300, 8, 64, 2, 64), (1, 1100, 4, 64, 1, 128)]
+
+
+def test_backward_from_two_host_threads():
+    """Two host threads run the backward at once, each on its own torch stream, three times
+    each.  They share the library's second stream of the device (the C.B^T adjoint runs there),
+    and every run matches that problem's single-thread gradients bit for bit."""
+    import threading
+    cases = [_inputs(s, seed=20 + i) for i, s in enumerate(TWO_STREAM_SHAPES)]
+    serial = [_gpu_grads(*c, True, torch.bfloat16) for c in cases]
+    torch.cuda.synchronize()
+    results, errors = [None, None], []
+
+    def work(i):
+        try:
+            st = torch.cuda.Stream()
+            with torch.cuda.stream(st):
+                runs = [_gpu_grads(*cases[i], True, torch.bfloat16) for _ in range(3)]
+            st.synchronize()
+            results[i] = runs
+        except Exception as e:  # reported by the main thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=work, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=100)
+    assert not errors, errors
+    for i, runs in enumerate(results):
+        assert runs is not None, f"thread {i} did not finish"
+        for r, got in enumerate(runs):
+            for k, v in serial[i].items():
+                assert torch.equal(got[k], v), f"{TWO_STREAM_SHAPES[i]} run {r}: d{k}"
+
+
+def test_backward_under_graph_capture():
+    """A forward and backward captured into a graph: under capture the library keeps the whole
+    backward on the capturing stream.  Each of three replays, with eager runs of the same step
+    in between, gives the eager gradients bit for bit."""
+    inputs, dy, dfinal = _inputs(TWO_STREAM_SHAPES[1], seed=11)
+    leaves = _leaves(inputs, DEV, torch.bfloat16)
+    dyd, dfd = dy.to(DEV).to(torch.bfloat16), dfinal.to(DEV).to(torch.bfloat16)
+    kw = {k: v for k, v in leaves.items() if k not in NAMES}
+    order = list(leaves.values())
+
+    def step():
+        y, s = _api()(*(leaves[k] for k in NAMES), 64, **kw, dt_softplus=True)
+        return torch.autograd.grad((y, s), order, (dyd, dfd))
+
+    eager = [g.clone() for g in step()]
+    warm = torch.cuda.Stream()
+    warm.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(warm):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(warm)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = step()
+    for r in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        again = step()
+        torch.cuda.synchronize()
+        for name, g, e, a in zip(leaves, captured, eager, again):
+            assert torch.equal(g, e), f"replay {r}: d{name}"
+            assert torch.equal(a, e), f"eager run after replay {r}: d{name}"
+
+
 def test_backward_empty_sequence():
     inputs, dy, dfinal = _inputs((2, 0, 4, 6, 2, 5), seed=1)
     got = _gpu_grads(inputs, dy, dfinal, True, torch.float32)
