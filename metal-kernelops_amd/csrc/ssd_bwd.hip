@@ -1457,6 +1457,9 @@ int side_stream(hipStream_t s, SideStream** out) {
       if (err == hipSuccess) err = hipEventCreateWithFlags(e, hipEventDisableTiming);
     if (err != hipSuccess) {
       mko_set_error("ssd_bwd: second stream on device %d: %s", dev, hipGetErrorString(err));
+      for (hipEvent_t e : {made.fork, made.join})
+        if (e) (void)hipEventDestroy(e);
+      if (made.stream) (void)hipStreamDestroy(made.stream);
       return MKO_ELAUNCH;
     }
     sd = made;
@@ -1480,9 +1483,9 @@ int stream_wait(hipStream_t from, hipStream_t to, hipEvent_t e) {
 // and writes only partials that dbc_final reads, so the side stream runs it as soon as the
 // gate is done, beside state_rev, du, dbc_state, finish and reduce_params on s, and s waits
 // for it just before dbc_final.  Alone at 4 x 4096 tokens and 64 heads, dcb's 640 long
-// workgroups leave about 40% of the workgroup slots empty for 0.12 ms.  (dbc_state, which
-// could follow it there once state_rev is done, is faster on s: it then no longer competes
-// with du.)  Calls from several host threads share the side stream: the lock keeps each fork
+// workgroups leave about 40% of the workgroup slots empty for 0.12 ms.  (dbc_state could
+// follow it there once state_rev is done; it runs faster on s, where it does not compete with
+// du.)  Calls from several host threads share the side stream: the lock keeps each fork
 // record next to its wait, and a join that waits for a later call's work on the same stream
 // also waits for its own.
 template <typename TM, bool VEC>
