@@ -153,6 +153,23 @@ def test_ssd_composition_matches_recurrence(shape, chunk):
     assert max_rel(s, s_ref) < 1e-12
 
 
+@pytest.mark.parametrize("shape", [(1, 1030, 4, 60, 2, 128), (1, 1100, 3, 64, 1, 128), (2, 300, 4, 64, 1, 128)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_fp32_composition_error_grows_with_the_chunk(shape):
+    """The reference's fp32 chunk composition errs in its forward through the in-chunk exponent
+    differences (cumulative sums of step x A, rounded to fp32), which grow with the chunk.  On
+    config-4 draws (A = -U(1, 16)) it stays below 2.5e-6 max-relative at 64-token chunks, the
+    kernels' chunk for fp32 inputs (measured 1.0-1.8e-6), and is at least twice that at 256
+    (measured 3.5-8.3e-6): the scale of error an fp32 chunked forward carries by construction."""
+    p = ssd_problem(*shape, seed=7, act=torch.float32)
+    p = {k: v for k, v in p.items() if v is not None}
+    y_ref, _ = oracle.mamba2_chunk_scan_recurrence(**{k: v.double() for k, v in p.items()}, dt_softplus=True)
+    e64, e256 = (max_rel(oracle.mamba2_chunk_scan_composition(chunk_size=q, **p, dt_softplus=True)[0], y_ref)
+                 for q in (64, 256))
+    assert e64 < 2.5e-6, f"64-token chunks: {e64:.2e}"
+    assert e256 > 2 * e64, f"256-token chunks: {e256:.2e} against {e64:.2e}"
+
+
 def test_ssd_minimal_matches_recurrence():
     g = _g(11)
     b, length, h, pdim, grp, n = 1, 16, 2, 3, 1, 4
